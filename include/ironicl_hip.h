@@ -1,0 +1,217 @@
+/*
+ * ironicl_hip.h - C ABI of the MI355X (gfx950) TabICLv2 FP32 forward backend.
+ *
+ * The library, libironicl_hip.so, replaces Ironicl's CUDA backend at its
+ * plugin point: the `Device` enum (src/models/tabicl_v2/mod.rs:15-41) and the
+ * `cuda` module surface (src/models/tabicl_v2/cuda/mod.rs:47-52). A thin Rust
+ * FFI crate wraps these entry points into a `rocm` module with the same
+ * surface; INTEGRATION.md shows that binding.
+ *
+ * Conventions
+ *   - Every entry point returns an irx_status. On failure the calling thread's
+ *     irx_last_error() holds a message. Nothing panics or aborts across the ABI.
+ *   - Host buffers passed in are borrowed for the duration of the call; output
+ *     buffers are allocated by the caller.
+ *   - All tensors are FP32, row-major, in the reference's logical layouts.
+ *   - Weights are reference counted and shared by every predictor of a model.
+ *   - Calls on one predictor serialize (an internal mutex); different
+ *     predictors may run concurrently, each on its own HIP stream.
+ */
+#ifndef IRONICL_HIP_H
+#define IRONICL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IRX_ABI_VERSION 1
+
+/* Result codes. The Rust wrapper maps them onto `Error` like gpu_error /
+ * out_of_memory (src/kernels/cuda/mod.rs:61-68): DEVICE_ERROR and
+ * OUT_OF_MEMORY become Error::UnsupportedBackend("ROCm: ..."),
+ * INVALID_ARGUMENT becomes Error::InvalidArgument, INTERRUPTED carries the
+ * progress hook's error (src/progress.rs:29-72). */
+typedef enum irx_status {
+    IRX_OK = 0,
+    IRX_NO_DEVICE = 1,        /* no usable GPU, or IRONICL_NO_ROCM is set: Device::new() -> None */
+    IRX_OUT_OF_MEMORY = 2,
+    IRX_INVALID_ARGUMENT = 3, /* shape or pointer mismatch */
+    IRX_DEVICE_ERROR = 4,     /* a HIP call failed */
+    IRX_INTERRUPTED = 5,      /* the progress hook returned non-zero */
+    IRX_DOES_NOT_FIT = 6,     /* the context does not fit the device: the caller falls back to the CPU */
+    IRX_NOT_FINITE = 7,       /* a cached key or value is not finite (cuda/build.rs:340-350) */
+    IRX_UNSUPPORTED = 8       /* e.g. a grouped all-missing (-100) triple in build inputs */
+} irx_status;
+
+/* Precision of the products. Only FP32 (optimize="safe",
+ * Precision::Fp32 in src/models/tabicl_v2/cuda/mod.rs:71-92) exists here. */
+typedef enum irx_precision { IRX_PRECISION_FP32 = 0 } irx_precision;
+
+typedef enum irx_task { IRX_TASK_CLASSIFIER = 0, IRX_TASK_REGRESSOR = 1 } irx_task;
+
+/* Progress stages (src/progress.rs: Stage::Build, Stage::Predict). */
+typedef enum irx_stage { IRX_STAGE_BUILD = 0, IRX_STAGE_PREDICT = 1 } irx_stage;
+
+/* Estimators B, features H, training rows N, decoder outputs per row
+ * (workspace::Shape, src/models/tabicl_v2/cuda/workspace.rs:25). */
+typedef struct irx_shape {
+    size_t ensembles;
+    size_t features;
+    size_t rows;
+    size_t outputs;
+} irx_shape;
+
+typedef struct irx_device irx_device;
+typedef struct irx_weights irx_weights;
+typedef struct irx_built_cache irx_built_cache;
+typedef struct irx_predictor irx_predictor;
+
+/* Looks up an official tensor by checkpoint name (src/format/model.rs:772-867):
+ * returns 0 and a borrowed view valid for the duration of the call, non-zero
+ * when absent. Replaces the `|name| self.tensor(name)` closure passed to
+ * ModelWeights::new (src/models/tabicl_v2/cuda/weights.rs:299). */
+typedef int (*irx_tensor_lookup)(void *user, const char *name, const float **data, size_t *len);
+
+/* Progress hook (src/progress.rs:29-72): called on the calling thread between
+ * groups and passes; a non-zero return stops the work with IRX_INTERRUPTED. */
+typedef int (*irx_progress_fn)(void *user, int stage, size_t done, size_t total);
+
+/* The ICL keys and values of one block on the host, `[B, 8, N, 64]` each
+ * (IclSource::block, src/models/tabicl_v2/cuda/cache.rs:61-64). */
+typedef int (*irx_icl_source)(void *user, size_t block, const float **keys, const float **values);
+
+/* Message of the last failure on this thread; never NULL. */
+const char *irx_last_error(void);
+int irx_abi_version(void);
+
+/* ---- Device: Device::new / free_memory (src/kernels/cuda/mod.rs:116-209) ---- */
+
+/* Opens GPU `ordinal`. IRX_NO_DEVICE when there is none or IRONICL_NO_ROCM is
+ * set (the CPU path then runs); an error only when a device exists but fails. */
+int irx_device_open(int ordinal, irx_device **out);
+void irx_device_close(irx_device *device);
+int irx_device_free_memory(irx_device *device, size_t *bytes);
+/* Number of compute units (for launch sizing by callers and tests). */
+int irx_device_compute_units(irx_device *device, int *units);
+
+/* ---- Weights: ModelWeights::new / budget (src/models/tabicl_v2/cuda/weights.rs:286-342) ---- */
+
+/* Uploads every official tensor once. The regressor's absent LayerNorm biases
+ * are zero-filled (src/format/model.rs:273-280). The device stays open while
+ * any weights hold it. */
+int irx_weights_upload(irx_device *device, int task, irx_tensor_lookup lookup, void *user,
+                       irx_weights **out);
+void irx_weights_retain(irx_weights *weights);
+void irx_weights_release(irx_weights *weights);
+size_t irx_weights_bytes(const irx_weights *weights);
+/* Free device memory, capped by device_limit minus the weights (0 = no limit). */
+int irx_weights_budget(const irx_weights *weights, uint64_t device_limit, size_t *budget);
+
+/* ---- Build: fits / build (src/models/tabicl_v2/cuda/build.rs:42-212) ---- */
+
+/* Bytes per cached ICL key or value at `precision` (context_bytes, build.rs:92-97). */
+size_t irx_context_bytes(int precision);
+/* Whether a context of `shape` builds on the device within `budget` bytes
+ * (fits, build.rs:158-160). */
+int irx_build_fits(size_t budget, int precision, const irx_shape *shape);
+
+/* BuildInputs (build.rs:42-63). */
+typedef struct irx_build_inputs {
+    irx_shape shape;
+    const float *x;                    /* [B, N, H] preprocessed training rows */
+    const float *column_labels;        /* [B, N, 128] column-stage label embeddings */
+    const float *icl_labels;           /* [B, N, 512] ICL label embeddings */
+    const float *inducing_queries[3];  /* per column block: norm1, q-proj and QASSMax of the inducing points, [128, 128] */
+    const float *base_scales[12];      /* per ICL block: QASSMax base scale for N sources, [512] */
+    const float *rope_frequencies;     /* [8] */
+    const float *cls_tokens;           /* [4, 128] */
+    size_t budget;                     /* device bytes the build may use */
+    irx_progress_fn progress;          /* may be NULL */
+    void *progress_user;
+} irx_build_inputs;
+
+/* BuildOutputs (build.rs:66-74), host buffers owned by the caller. A NULL
+ * pointer skips that tensor's download (the context then lives in HBM only,
+ * through `keep`). The reserved CLS streams of the column tensors are left as
+ * they are. */
+typedef struct irx_build_outputs {
+    float *column_keys[3];   /* [B, H+4, 8, 128, 16] */
+    float *column_values[3];
+    float *icl_keys[12];     /* [B, 8, N, 64] */
+    float *icl_values[12];
+} irx_build_outputs;
+
+/* Builds a context: the training rows' pass through the column ISAB, the row
+ * transformer and the ICL self-attention, keeping every block's K/V. With
+ * keep != NULL the ICL and column K/V stay resident in HBM and *keep owns them
+ * until passed to irx_predictor_new or irx_built_cache_free (BuiltCache,
+ * src/models/tabicl_v2/cuda/cache.rs:137). */
+int irx_build(irx_weights *weights, int precision, const irx_build_inputs *inputs,
+              irx_build_outputs *outputs, irx_built_cache **keep);
+void irx_built_cache_free(irx_built_cache *cache);
+
+/* ---- Predictor (src/models/tabicl_v2/cuda/predictor.rs:57-271) ---- */
+
+/* ContextTensors (predictor.rs:57-72). */
+typedef struct irx_context_tensors {
+    irx_shape shape;
+    const float *column_keys[3];    /* [B, H+4, 8, 128, 16]; may be NULL when adopting a built cache */
+    const float *column_values[3];
+    irx_icl_source icl;             /* may be NULL when adopting a built cache */
+    void *icl_user;
+    const float *base_scales[12];   /* [512] each */
+    const float *rope_frequencies;  /* [8] */
+    const float *cls_tokens;        /* [4, 128] */
+    size_t budget;
+} irx_context_tensors;
+
+/* Uploads the context's caches, or adopts `adopt` (ownership transfers, also
+ * on failure). IRX_DOES_NOT_FIT when the context cannot stay on the device:
+ * the caller predicts on the CPU (Predictor::new -> None). */
+int irx_predictor_new(irx_weights *weights, int precision, const irx_context_tensors *context,
+                      irx_built_cache *adopt, irx_predictor **out);
+void irx_predictor_free(irx_predictor *predictor);
+/* Whether the ICL cache streams from the host (always 0: on a 288 GB MI355X
+ * the cache stays resident). */
+int irx_predictor_streamed(const irx_predictor *predictor);
+/* Query rows per pass. */
+size_t irx_predictor_pass_rows(const irx_predictor *predictor);
+/* Sets the query rows per pass (a multiple of 32, at least 32). */
+int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows);
+
+/* Predictor::predict (predictor.rs:224-271): x [B, Q, H] on the host, logits
+ * [B, Q, outputs] on the host. cpu_rows, when not NULL, gets Q flags: 1 for a
+ * row with a grouped all-missing (-100) triple, which the caller predicts on
+ * the CPU (its logits are left unspecified). */
+int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, float *logits,
+                          uint8_t *cpu_rows, irx_progress_fn progress, void *progress_user);
+/* The same with x and logits already in device memory (HBM-resident inputs).
+ * Returns when the logits are written. */
+int irx_predictor_predict_device(irx_predictor *predictor, const float *x_device, size_t q,
+                                 float *logits_device, uint8_t *cpu_rows);
+
+/* ---- Kernel harness (cuda/testing.rs:27-207): one kernel family on host data ---- */
+
+/* softmax(q k^T / 8) v for `pairs` (estimator, head) pairs: q [pairs, query_rows, 64],
+ * k and v [pairs, rows, 64]; out [pairs, query_rows, 64]. */
+int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v,
+                           size_t pairs, size_t query_rows, size_t rows, float *out);
+/* first = gelu(x w1^T + b1); second = first w2^T + b2 (+ first when width2 == width).
+ * x [rows, depth], w1 [width, depth], w2 [width2, width]. */
+int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1,
+                      const float *w2, const float *b2, size_t rows, size_t width, size_t depth,
+                      size_t width2, float *first, float *second);
+/* LayerNorm over width (128 or 512), eps 1e-5. */
+int irx_test_layer_norm(irx_device *device, const float *x, const float *weight, const float *bias,
+                        size_t rows, size_t width, float *out);
+/* 16-wide-head attention: q [heads, query_rows, 16], k and v [heads, rows, 16]. */
+int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v,
+                             size_t heads, size_t query_rows, size_t rows, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

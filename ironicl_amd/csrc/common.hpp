@@ -1,0 +1,162 @@
+// Shared definitions of the gfx950 TabICLv2 backend: model constants, error
+// plumbing, wave64 reductions and the launchers every translation unit uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace irx {
+
+// Architecture constants (src/models/tabicl_v2/cpu.rs:40-54).
+constexpr int kColumnDim = 128;
+constexpr int kIclDim = 512;
+constexpr int kHeads = 8;
+constexpr int kInducing = 128;
+constexpr int kColumnBlocks = 3;
+constexpr int kRowBlocks = 3;
+constexpr int kIclBlocks = 12;
+constexpr int kReserved = 4;
+constexpr int kFfnHidden = 1024;
+constexpr int kColumnHead = kColumnDim / kHeads;  // 16
+constexpr int kIclHead = kIclDim / kHeads;         // 64
+// One column's cached inducing K (or V): 8 heads x 128 points x 16 dims.
+constexpr int kColumnCache = kHeads * kInducing * kColumnHead;
+
+// A failed HIP call or argument check. The C ABI turns it into a status code
+// and the thread's last-error message.
+struct Failure {
+    int status;
+    std::string message;
+};
+
+[[noreturn]] void fail(int status, const std::string &message);
+void check_hip(hipError_t err, const char *what);
+
+#define IRX_HIP(call) ::irx::check_hip((call), #call)
+
+// ---- device helpers ----
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int offset = 32; offset >= 1; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int offset = 32; offset >= 1; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
+    return v;
+}
+
+// Exact GELU, 0.5 x (1 + erf(x / sqrt 2)) (src/kernels/reference.rs:52-54).
+__device__ __forceinline__ float gelu_erf(float x) {
+    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+inline unsigned ceil_div(size_t a, size_t b) { return static_cast<unsigned>((a + b - 1) / b); }
+
+// ---- launchers (defined in the kernel translation units) ----
+
+// Where a product writes element (m, n): segments of `col_seg` columns go to
+// head-major planes, rows to groups. A plain row-major [M, N] output is
+// col_seg = N, heads = 1, rows_per_group >= M, strides 0, ldc = row stride.
+struct OutMap {
+    int col_seg;
+    int heads;
+    long long plane_stride;
+    long long head_stride;
+    int rows_per_group;
+    long long group_stride;
+    long long ldc;
+    static OutMap row_major(int n, long long ldc) { return {n, 1, 0, 0, 1 << 30, 0, ldc}; }
+    // [heads, rows, hd] head-major (and a second plane after `plane_stride`
+    // for columns past heads * hd, e.g. keys then values).
+    static OutMap head_major(int hd, int heads, long long rows, long long plane_stride) {
+        return {hd, heads, plane_stride, rows * hd, 1 << 30, 0, hd};
+    }
+};
+
+enum Epilogue : int {
+    kEpiNone = 0,
+    kEpiGelu = 1,      // gelu(acc + bias)
+    kEpiResidual = 2,  // acc + bias + residual[m, n]
+    kEpiQass = 4,      // residual[m, n] * base[(m / qass_rows) * N + n] * (1 + tanh(acc + bias))
+};
+
+struct GemmArgs {
+    const float *a;         // [M, K], row stride lda
+    long long lda;
+    const float *w;         // [N, K] row-major (PyTorch Linear layout)
+    const float *bias;      // [N] or null
+    const float *residual;  // [M, N] row-major with stride ldr, or null
+    long long ldr;
+    const float *qass_base; // kEpiQass: [8 * N], head (row / qass_rows) % 8
+    int qass_rows;          // kEpiQass: rows per head
+    float *c;
+    OutMap out;
+    int m, n, k;
+    int epilogue;
+};
+
+// C = epilogue(A W^T + bias) on FP32 MFMA. K must be a multiple of 16.
+void gemm(const GemmArgs &args, hipStream_t stream);
+
+// LayerNorm over `width` (128 or 512), eps 1e-5, two passes (reference.rs:223-252).
+void layer_norm(const float *x, long long ldx, const float *weight, const float *bias, float *y,
+                long long ldy, long long rows, int width, hipStream_t stream);
+
+// Attention of 16-wide heads with online softmax. Element (seq, head, row, d)
+// of Q is at q + qoff(seq) + row * q_row + head * q_head + d, where qoff(seq) =
+// (seq / group) * q_group + (seq % group) * q_seq; likewise K, V, O.
+struct SmallAttention {
+    const float *q, *k, *v;
+    float *o;
+    long long q_seq, q_group, q_row, q_head;
+    long long k_seq, k_group, k_row, k_head;
+    long long v_seq, v_group, v_row, v_head;
+    long long o_seq, o_group, o_row, o_head;
+    int group;           // sequences per group (>= 1)
+    int seqs, heads;
+    int q_rows, kv_rows;
+    float scale;         // 1/sqrt(16)
+    const float *rope_cos, *rope_sin;  // [positions, 16] tables or null
+};
+void small_attention(const SmallAttention &args, hipStream_t stream);
+
+// ICL attention of 64-wide heads: Q [pairs, q_rows, 64] (head-major, q_stride
+// between pairs), K and V [pairs, kv_rows, 64]; the output goes to tokens
+// [b * q_rows + row, head * 64 + d] with pair = b * 8 + head, row stride ldo.
+// Split-K partials use `partial` (floats) when splits > 1.
+struct IclAttention {
+    const float *q;
+    long long q_pair_stride;
+    const float *k, *v;
+    long long kv_pair_stride;
+    float *o;
+    long long ldo;
+    int pairs, q_rows, kv_rows;
+    float *partial;       // [splits, pairs, q_rows_padded, 65] or null
+    size_t partial_floats;
+    int compute_units;
+};
+// Splits the ICL attention would use, and the partial floats it needs.
+int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units);
+size_t icl_attention_partial_floats(int pairs, int q_rows, int splits);
+void icl_attention(const IclAttention &args, hipStream_t stream);
+
+// Glue kernels (glue.hip).
+void column_input(const float *x, long long x_estimator_stride, int b, int rows, int h, const float *in_w, const float *in_b,
+                  const float *labels, float *state, uint8_t *missing_rows, hipStream_t stream);
+void build_rows(const float *state, int b, int rows, int h, const float *cls, float *seq,
+                hipStream_t stream);
+void gather_cls(const float *seq, long long seqs, int len, float *cls, hipStream_t stream);
+void add_inplace(float *y, const float *x, long long count, hipStream_t stream);
+void repeat_rows(const float *src, long long src_floats, long long copies, float *dst,
+                 hipStream_t stream);
+void count_nonfinite(const float *x, long long count, unsigned *counter, hipStream_t stream);
+void fill_zero(float *x, long long count, hipStream_t stream);
+
+}  // namespace irx

@@ -1,0 +1,211 @@
+// LayerNorm and the bandwidth-bound glue of the forward pass.
+//
+// LayerNorm (src/kernels/reference.rs:223-252): one wave per row, two passes
+// over registers (mean, then centred variance), eps 1e-5, population
+// variance. Glue kernels restate the data movement of the reference's CUDA
+// backend (column_input, build_rows, gather_cls, repeat, add_labels;
+// src/kernels/cuda/kernels.rs:475-718) in this backend's layouts:
+//   column states   [B*H, rows, 128]   (column c = b*H + f)
+//   row sequences   [B*rows, H+4, 128] (4 CLS tokens, then the features)
+#include "common.hpp"
+
+namespace irx {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+template <int W>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, long long ldx, const float *w,
+                                                         const float *b, float *y, long long ldy,
+                                                         long long rows) {
+    constexpr int PER = W / 64;
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const float *xr = x + row * ldx + lane * PER;
+    float v[PER];
+    if constexpr (PER == 2) {
+        f32x2 t = *reinterpret_cast<const f32x2 *>(xr);
+        v[0] = t[0], v[1] = t[1];
+    } else {
+#pragma unroll
+        for (int c = 0; c < PER / 4; ++c) {
+            f32x4 t = *reinterpret_cast<const f32x4 *>(xr + 4 * c);
+            v[4 * c] = t[0], v[4 * c + 1] = t[1], v[4 * c + 2] = t[2], v[4 * c + 3] = t[3];
+        }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) s += v[i];
+    const float mean = wave_sum(s) / (float)W;
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        float d = v[i] - mean;
+        sq = fmaf(d, d, sq);
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)W + 1e-5f);
+    float *yr = y + row * ldy + lane * PER;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int c = lane * PER + i;
+        v[i] = (v[i] - mean) * rstd * w[c] + (b ? b[c] : 0.f);
+    }
+    if constexpr (PER == 2) {
+        *reinterpret_cast<f32x2 *>(yr) = f32x2{v[0], v[1]};
+    } else {
+#pragma unroll
+        for (int c = 0; c < PER / 4; ++c)
+            *reinterpret_cast<f32x4 *>(yr + 4 * c) = f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+    }
+}
+
+// Grouped features (f+1, f+2, f+4) mod H through the 3 -> 128 input affine
+// (cpu.rs:1144-1157, 2461-2473), the -100 all-missing marker, and the
+// column-stage label embeddings of training rows.
+__global__ __launch_bounds__(256) void column_input_kernel(const float *x, long long xs, int b, int rows, int h,
+                                                           const float *in_w, const float *in_b,
+                                                           const float *labels, float *state,
+                                                           uint8_t *missing) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = (long long)b * h * rows * kColumnDim;
+    if (idx >= total) return;
+    const int ch = idx & (kColumnDim - 1);
+    const long long cr = idx >> 7;
+    const int r = (int)(cr % rows);
+    const int c = (int)(cr / rows);
+    const int e = c / h, f = c - e * h;
+    const float *xr = x + (long long)e * xs + (long long)r * h;
+    const float s0 = xr[(f + 1) % h], s1 = xr[(f + 2) % h], s2 = xr[(f + 4) % h];
+    float v = fmaf(in_w[ch * 3 + 0], s0, in_b[ch]);
+    v = fmaf(in_w[ch * 3 + 1], s1, v);
+    v = fmaf(in_w[ch * 3 + 2], s2, v);
+    if (s0 == -100.0f && s1 == -100.0f && s2 == -100.0f) {
+        v = -100.0f;
+        if (missing && ch == 0) missing[(long long)e * rows + r] = 1;
+    }
+    if (labels) v += labels[((long long)e * rows + r) * kColumnDim + ch];
+    state[idx] = v;
+}
+
+// Row sequences: the 4 CLS tokens, then feature f's column state (cpu.rs:1226-1231).
+__global__ __launch_bounds__(256) void build_rows_kernel(const float *state, int b, int rows, int h,
+                                                         const float *cls, float *seq) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int len = h + kReserved;
+    const long long total = (long long)b * rows * len * kColumnDim;
+    if (idx >= total) return;
+    const int ch = idx & (kColumnDim - 1);
+    const long long st = idx >> 7;
+    const int t = (int)(st % len);
+    const long long s = st / len;
+    const int r = (int)(s % rows);
+    const int e = (int)(s / rows);
+    float v;
+    if (t < kReserved)
+        v = cls[t * kColumnDim + ch];
+    else
+        v = state[(((long long)e * h + (t - kReserved)) * rows + r) * kColumnDim + ch];
+    seq[idx] = v;
+}
+
+__global__ __launch_bounds__(256) void gather_cls_kernel(const float *seq, long long seqs, int len, float *cls) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = seqs * kReserved * kColumnDim;
+    if (idx >= total) return;
+    const long long s = idx / (kReserved * kColumnDim);
+    const int within = (int)(idx - s * (kReserved * kColumnDim));
+    cls[idx] = seq[s * len * kColumnDim + within];
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float *y, const float *x, long long count) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx < count) y[idx] += x[idx];
+}
+
+__global__ __launch_bounds__(256) void repeat_kernel(const float *src, long long src_floats, long long copies,
+                                                     float *dst) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx < src_floats * copies) dst[idx] = src[idx % src_floats];
+}
+
+__global__ __launch_bounds__(256) void nonfinite_kernel(const float *x, long long count, unsigned *counter) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    bool bad = idx < count && !isfinite(x[idx]);
+    if (__any(bad) && (threadIdx.x & 63) == 0) atomicAdd(counter, 1u);
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(float *x, long long count) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx < count) x[idx] = 0.f;
+}
+
+}  // namespace
+
+void layer_norm(const float *x, long long ldx, const float *weight, const float *bias, float *y, long long ldy,
+                long long rows, int width, hipStream_t stream) {
+    if (rows <= 0) return;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(y) & 15) || (ldx & 3) || (ldy & 3))
+        fail(3, "layer norm operands must be 16-byte aligned");
+    dim3 grid(ceil_div(rows, 4));
+    if (width == 128)
+        hipLaunchKernelGGL(layer_norm_kernel<128>, grid, dim3(256), 0, stream, x, ldx, weight, bias, y, ldy, rows);
+    else if (width == 512)
+        hipLaunchKernelGGL(layer_norm_kernel<512>, grid, dim3(256), 0, stream, x, ldx, weight, bias, y, ldy, rows);
+    else
+        fail(3, "layer norm width must be 128 or 512");
+    IRX_HIP(hipGetLastError());
+}
+
+void column_input(const float *x, long long x_estimator_stride, int b, int rows, int h, const float *in_w,
+                  const float *in_b, const float *labels, float *state, uint8_t *missing_rows, hipStream_t stream) {
+    long long total = (long long)b * h * rows * kColumnDim;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(column_input_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, x, x_estimator_stride, b, rows, h, in_w,
+                       in_b, labels, state, missing_rows);
+    IRX_HIP(hipGetLastError());
+}
+
+void build_rows(const float *state, int b, int rows, int h, const float *cls, float *seq, hipStream_t stream) {
+    long long total = (long long)b * rows * (h + kReserved) * kColumnDim;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(build_rows_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, state, b, rows, h, cls,
+                       seq);
+    IRX_HIP(hipGetLastError());
+}
+
+void gather_cls(const float *seq, long long seqs, int len, float *cls, hipStream_t stream) {
+    long long total = seqs * kReserved * kColumnDim;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(gather_cls_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, seq, seqs, len, cls);
+    IRX_HIP(hipGetLastError());
+}
+
+void add_inplace(float *y, const float *x, long long count, hipStream_t stream) {
+    if (count <= 0) return;
+    hipLaunchKernelGGL(add_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, y, x, count);
+    IRX_HIP(hipGetLastError());
+}
+
+void repeat_rows(const float *src, long long src_floats, long long copies, float *dst, hipStream_t stream) {
+    long long total = src_floats * copies;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(repeat_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, src, src_floats, copies,
+                       dst);
+    IRX_HIP(hipGetLastError());
+}
+
+void count_nonfinite(const float *x, long long count, unsigned *counter, hipStream_t stream) {
+    if (count <= 0) return;
+    hipLaunchKernelGGL(nonfinite_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, x, count, counter);
+    IRX_HIP(hipGetLastError());
+}
+
+void fill_zero(float *x, long long count, hipStream_t stream) {
+    if (count <= 0) return;
+    hipLaunchKernelGGL(zero_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, x, count);
+    IRX_HIP(hipGetLastError());
+}
+
+}  // namespace irx

@@ -1,0 +1,1150 @@
+// Host runtime of the gfx950 TabICLv2 backend and its C ABI (include/ironicl_hip.h).
+//
+// Plays the part of src/models/tabicl_v2/cuda/{build,predictor,weights,
+// workspace}.rs for the MI355X: the static-context build and cached
+// prediction as sequences of launches on one HIP stream, with every buffer
+// of a pass carved from one device arena and the context's K/V kept resident
+// in HBM.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/ironicl_hip.h"
+#include "common.hpp"
+
+namespace irx {
+
+thread_local std::string g_last_error;
+
+[[noreturn]] void fail(int status, const std::string &message) { throw Failure{status, message}; }
+
+void check_hip(hipError_t err, const char *what) {
+    if (err == hipSuccess) return;
+    int status = err == hipErrorOutOfMemory ? IRX_OUT_OF_MEMORY : IRX_DEVICE_ERROR;
+    fail(status, std::string("ROCm: ") + what + ": " + hipGetErrorString(err));
+}
+
+namespace {
+
+// ---- device memory ----
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    explicit DevBuf(size_t b) { alloc(b); }
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf &&o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr, o.bytes = 0; }
+    DevBuf &operator=(DevBuf &&o) noexcept {
+        if (this != &o) {
+            release();
+            p = o.p, bytes = o.bytes;
+            o.p = nullptr, o.bytes = 0;
+        }
+        return *this;
+    }
+    ~DevBuf() { release(); }
+    void alloc(size_t b) {
+        release();
+        if (b) {
+            IRX_HIP(hipMalloc(&p, b));
+            bytes = b;
+        }
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr, bytes = 0;
+    }
+    float *f() const { return static_cast<float *>(p); }
+};
+
+// Bump allocator over one device allocation. With `counting`, only sums sizes.
+struct Arena {
+    DevBuf buf;
+    size_t used = 0;
+    bool counting = false;
+    static size_t round(size_t floats) { return (floats * 4 + 255) & ~size_t(255); }
+    float *take(size_t floats) {
+        size_t b = round(floats);
+        if (counting) {
+            used += b;
+            return nullptr;
+        }
+        if (used + b > buf.bytes) fail(IRX_OUT_OF_MEMORY, "ROCm: workspace exhausted");
+        float *p = reinterpret_cast<float *>(static_cast<char *>(buf.p) + used);
+        used += b;
+        return p;
+    }
+    uint8_t *take_bytes(size_t bytes) { return reinterpret_cast<uint8_t *>(take((bytes + 3) / 4)); }
+};
+
+void upload(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (bytes) IRX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+}
+void download(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (bytes) IRX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+}
+
+// RoPE tables of the row stage: cos twice and [-sin, sin] per 16-wide head
+// for `len` positions (rope_tables, src/models/tabicl_v2/cpu.rs:4089-4102).
+void rope_tables(const float *freqs, int len, std::vector<float> &cos_t, std::vector<float> &sin_t) {
+    cos_t.assign((size_t)len * 16, 0.f);
+    sin_t.assign((size_t)len * 16, 0.f);
+    for (int row = 0; row < len; ++row)
+        for (int i = 0; i < 8; ++i) {
+            float angle = (float)row * freqs[i];
+            float s = sinf(angle), c = cosf(angle);
+            cos_t[row * 16 + i] = c, cos_t[row * 16 + i + 8] = c;
+            sin_t[row * 16 + i] = -s, sin_t[row * 16 + i + 8] = s;
+        }
+}
+
+}  // namespace
+}  // namespace irx
+
+using namespace irx;
+
+// ---- opaque ABI objects ----
+
+struct irx_device {
+    int ordinal = 0;
+    int compute_units = 0;
+    std::atomic<int> refs{1};
+};
+
+struct Lin {
+    const float *w = nullptr, *b = nullptr;
+};
+
+struct BlockW {
+    int dim = 0;
+    const float *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+    const float *in_w = nullptr, *in_b = nullptr;  // [3 dim, dim], [3 dim]
+    Lin out, l1, l2;
+    bool qass = false;
+    Lin qm0, qm2;  // QASS query MLP, per head: hd -> 64 -> hd
+};
+
+struct irx_weights {
+    irx_device *device = nullptr;
+    std::atomic<int> refs{1};
+    int task = 0;
+    int width = 0;
+    size_t bytes = 0;
+    DevBuf arena;
+    const float *in_w = nullptr, *in_b = nullptr;
+    const float *ind[kColumnBlocks] = {};
+    BlockW col1[kColumnBlocks], col2[kColumnBlocks], row[kRowBlocks], icl[kIclBlocks];
+    const float *cls = nullptr, *out_ln_w = nullptr, *out_ln_b = nullptr;
+    const float *ln_w = nullptr, *ln_b = nullptr;
+    Lin dec0, dec2;
+    std::vector<float> freqs_host;
+};
+
+// The context's caches on the device: per column block K then V,
+// [2, B, H+4, 8, 128, 16]; per ICL block K then V, [2, B, 8, N, 64].
+struct irx_built_cache {
+    irx_device *device = nullptr;
+    irx_shape shape{};
+    DevBuf column[kColumnBlocks];
+    DevBuf icl[kIclBlocks];
+};
+
+struct irx_predictor {
+    irx_weights *weights = nullptr;
+    irx_shape shape{};
+    size_t pass_rows = 512;
+    DevBuf column[kColumnBlocks];
+    DevBuf icl[kIclBlocks];
+    DevBuf base_scales;   // [12, 512]
+    DevBuf rope_cos, rope_sin;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    Arena ws;
+    size_t ws_rows = 0;
+};
+
+namespace {
+
+void set_device(const irx_device *d) { IRX_HIP(hipSetDevice(d->ordinal)); }
+
+// ---- stages shared by the build and the predictor ----
+
+struct Stages {
+    const irx_weights &w;
+    hipStream_t s;
+    int cus;
+
+    void linear(const float *a, long long lda, long long m, int k, const float *wt, const float *b, int n,
+                float *c, long long ldc, int epi = kEpiNone, const float *res = nullptr, long long ldr = 0) const {
+        GemmArgs g{};
+        g.a = a, g.lda = lda, g.w = wt, g.bias = b, g.residual = res, g.ldr = ldr, g.c = c;
+        g.out = OutMap::row_major(n, ldc);
+        g.m = (int)m, g.n = n, g.k = k, g.epilogue = epi;
+        gemm(g, s);
+    }
+
+    void linear_map(const float *a, long long lda, long long m, int k, const float *wt, const float *b, int n,
+                    float *c, const OutMap &map) const {
+        GemmArgs g{};
+        g.a = a, g.lda = lda, g.w = wt, g.bias = b, g.c = c, g.out = map;
+        g.m = (int)m, g.n = n, g.k = k, g.epilogue = kEpiNone;
+        gemm(g, s);
+    }
+
+    // Post-attention half of a block: out-projection + residual into `state`,
+    // then LN2, FFN (GELU) and residual (cpu.rs:1555-1601).
+    void tail(const BlockW &bw, float *state, long long m, const float *att, float *norm, float *hid) const {
+        const int d = bw.dim;
+        linear(att, d, m, d, bw.out.w, bw.out.b, d, state, d, kEpiResidual, state, d);
+        layer_norm(state, d, bw.n2w, bw.n2b, norm, d, m, d, s);
+        linear(norm, d, m, d, bw.l1.w, bw.l1.b, 2 * d, hid, 2 * d, kEpiGelu);
+        linear(hid, 2 * d, m, 2 * d, bw.l2.w, bw.l2.b, d, state, d, kEpiResidual, state, d);
+    }
+
+    // multihead_attn2 of column block `blk` for `cols` columns of `rows`
+    // states [cols, rows, 128] against cached inducing K/V: column c reads
+    // kcache + (c / group) * group_stride + (c % group) * 16384
+    // (cached_block, cpu.rs:2587-2850; column_block_f32, kernels.rs:1342).
+    void column_attend(int blk, float *state, int cols, int rows, const float *kcache, const float *vcache,
+                       int group, long long group_stride, float *norm, float *q, float *att, float *hid) const {
+        const BlockW &bw = w.col2[blk];
+        const long long m = (long long)cols * rows;
+        layer_norm(state, kColumnDim, bw.n1w, bw.n1b, norm, kColumnDim, m, kColumnDim, s);
+        linear(norm, kColumnDim, m, kColumnDim, bw.in_w, bw.in_b, kColumnDim, q, kColumnDim);
+        SmallAttention a{};
+        a.q = q, a.q_seq = (long long)rows * kColumnDim, a.q_group = (long long)group * rows * kColumnDim;
+        a.q_row = kColumnDim, a.q_head = kColumnHead;
+        a.k = kcache, a.k_seq = kColumnCache, a.k_group = group_stride, a.k_row = kColumnHead;
+        a.k_head = kInducing * kColumnHead;
+        a.v = vcache, a.v_seq = kColumnCache, a.v_group = group_stride, a.v_row = kColumnHead;
+        a.v_head = kInducing * kColumnHead;
+        a.o = att, a.o_seq = a.q_seq, a.o_group = a.q_group, a.o_row = kColumnDim, a.o_head = kColumnHead;
+        a.group = group, a.seqs = cols, a.heads = kHeads, a.q_rows = rows, a.kv_rows = kInducing;
+        a.scale = 0.25f;
+        small_attention(a, s);
+        tail(bw, state, m, att, norm, hid);
+    }
+
+    struct RowBuffers {
+        float *seq, *norm, *qkv, *att, *hid, *cls, *cnorm, *cq, *catt, *chid;
+    };
+    static RowBuffers row_buffers(Arena &a, long long seqs, int len) {
+        long long m = seqs * len, c = seqs * kReserved;
+        RowBuffers r{};
+        r.seq = a.take(m * 128), r.norm = a.take(m * 128), r.qkv = a.take(m * 384), r.att = a.take(m * 128);
+        r.hid = a.take(m * 256), r.cls = a.take(c * 128), r.cnorm = a.take(c * 128), r.cq = a.take(c * 128);
+        r.catt = a.take(c * 128), r.chid = a.take(c * 256);
+        return r;
+    }
+
+    // The row transformer (row_embedding, cpu.rs:1226-1266) for `rows` rows of
+    // `b` estimators from column states [b*h, rows_total, 128] starting at
+    // row `start`... the caller passes states whose row dimension is `rows`.
+    void row_stage(const float *state, int b, int rows, int h, float *out, const float *rope_cos,
+                   const float *rope_sin, const RowBuffers &r) const {
+        const int len = h + kReserved;
+        const long long seqs = (long long)b * rows, m = seqs * len;
+        build_rows(state, b, rows, h, w.cls, r.seq, s);
+        for (int blk = 0; blk < 2; ++blk) {
+            const BlockW &bw = w.row[blk];
+            layer_norm(r.seq, 128, bw.n1w, bw.n1b, r.norm, 128, m, 128, s);
+            linear(r.norm, 128, m, 128, bw.in_w, bw.in_b, 384, r.qkv, 384);
+            SmallAttention a{};
+            a.q = r.qkv, a.k = r.qkv + 128, a.v = r.qkv + 256;
+            a.q_seq = a.k_seq = a.v_seq = (long long)len * 384;
+            a.q_group = a.k_group = a.v_group = 0;
+            a.q_row = a.k_row = a.v_row = 384;
+            a.q_head = a.k_head = a.v_head = kColumnHead;
+            a.o = r.att, a.o_seq = (long long)len * 128, a.o_group = 0, a.o_row = 128, a.o_head = kColumnHead;
+            a.group = (int)std::min<long long>(seqs, 1 << 30), a.seqs = (int)seqs, a.heads = kHeads;
+            a.q_rows = len, a.kv_rows = len, a.scale = 0.25f, a.rope_cos = rope_cos, a.rope_sin = rope_sin;
+            small_attention(a, s);
+            tail(bw, r.seq, m, r.att, r.norm, r.hid);
+        }
+        // Block 2: only the CLS tokens query; keys and values are every token.
+        const BlockW &bw = w.row[2];
+        const long long mc = seqs * kReserved;
+        gather_cls(r.seq, seqs, len, r.cls, s);
+        layer_norm(r.seq, 128, bw.n1w, bw.n1b, r.norm, 128, m, 128, s);
+        linear(r.norm, 128, m, 128, bw.in_w + 128 * 128, bw.in_b + 128, 256, r.qkv, 256);
+        layer_norm(r.cls, 128, bw.n1w, bw.n1b, r.cnorm, 128, mc, 128, s);
+        linear(r.cnorm, 128, mc, 128, bw.in_w, bw.in_b, 128, r.cq, 128);
+        SmallAttention a{};
+        a.q = r.cq, a.q_seq = kReserved * 128, a.q_group = 0, a.q_row = 128, a.q_head = kColumnHead;
+        a.k = r.qkv, a.v = r.qkv + 128, a.k_seq = a.v_seq = (long long)len * 256, a.k_group = a.v_group = 0;
+        a.k_row = a.v_row = 256, a.k_head = a.v_head = kColumnHead;
+        a.o = r.catt, a.o_seq = kReserved * 128, a.o_group = 0, a.o_row = 128, a.o_head = kColumnHead;
+        a.group = (int)std::min<long long>(seqs, 1 << 30), a.seqs = (int)seqs, a.heads = kHeads;
+        a.q_rows = kReserved, a.kv_rows = len, a.scale = 0.25f, a.rope_cos = rope_cos, a.rope_sin = rope_sin;
+        small_attention(a, s);
+        tail(bw, r.cls, mc, r.catt, r.cnorm, r.chid);
+        // out_ln of the 4 CLS tokens = the [512] row representation.
+        layer_norm(r.cls, 128, w.out_ln_w, w.out_ln_b, out, 128, mc, 128, s);
+    }
+
+    struct IclBuffers {
+        float *norm, *qh, *qhid, *qg, *att, *hid, *partial;
+        size_t partial_floats;
+    };
+    static IclBuffers icl_buffers(Arena &a, long long rows, int b, int q_rows, int kv_rows, int cus) {
+        IclBuffers r{};
+        r.norm = a.take(rows * 512), r.qh = a.take(rows * 512), r.qhid = a.take(rows * 512);
+        r.qg = a.take(rows * 512), r.att = a.take(rows * 512), r.hid = a.take(rows * 1024);
+        int splits = icl_attention_splits(b * kHeads, q_rows, kv_rows, cus);
+        r.partial_floats = icl_attention_partial_floats(b * kHeads, q_rows, splits);
+        r.partial = r.partial_floats ? a.take(r.partial_floats) : nullptr;
+        return r;
+    }
+
+    // Query half of ICL block `blk` (cached_block with QASS, cpu.rs:2587-2850,
+    // 3798-3853) for `b` estimators x `rows` query rows [b*rows, 512], against
+    // K/V [b, 8, kv_rows, 64].
+    void icl_queries(int blk, float *x, int b, int rows, const float *k, const float *v, int kv_rows,
+                     const float *base, const IclBuffers &r) const {
+        const BlockW &bw = w.icl[blk];
+        const long long m = (long long)b * rows;
+        layer_norm(x, 512, bw.n1w, bw.n1b, r.norm, 512, m, 512, s);
+        // Q, head-major [b, 8, rows, 64].
+        OutMap qmap{64, kHeads, 0, (long long)rows * 64, rows, (long long)kHeads * rows * 64, 64};
+        linear_map(r.norm, 512, m, 512, bw.in_w, bw.in_b, 512, r.qh, qmap);
+        // QASSMax: q * base * (1 + tanh(MLP(q))) per head (reference.rs:417-428).
+        linear(r.qh, 64, m * kHeads, 64, bw.qm0.w, bw.qm0.b, 64, r.qhid, 64, kEpiGelu);
+        GemmArgs g{};
+        g.a = r.qhid, g.lda = 64, g.w = bw.qm2.w, g.bias = bw.qm2.b, g.residual = r.qh, g.ldr = 64;
+        g.qass_base = base, g.qass_rows = rows, g.c = r.qg, g.out = OutMap::row_major(64, 64);
+        g.m = (int)(m * kHeads), g.n = 64, g.k = 64, g.epilogue = kEpiQass;
+        gemm(g, s);
+        IclAttention at{};
+        at.q = r.qg, at.q_pair_stride = (long long)rows * 64, at.k = k, at.v = v;
+        at.kv_pair_stride = (long long)kv_rows * 64, at.o = r.att, at.ldo = 512;
+        at.pairs = b * kHeads, at.q_rows = rows, at.kv_rows = kv_rows;
+        at.partial = r.partial, at.partial_floats = r.partial_floats, at.compute_units = cus;
+        icl_attention(at, s);
+        tail(bw, x, m, r.att, r.norm, r.hid);
+    }
+};
+
+// ---- weights ----
+
+struct Loader {
+    irx_tensor_lookup lookup;
+    void *user;
+    int task;
+    std::vector<float> host;
+    struct Pending {
+        const float **slot;
+        size_t offset;
+    };
+    std::vector<Pending> pending;
+
+    void take(const char *name, size_t len, const float **slot, bool zero_if_missing = false) {
+        const float *data = nullptr;
+        size_t got = 0;
+        int missing = lookup(user, name, &data, &got);
+        if (missing) {
+            if (!zero_if_missing) fail(IRX_INVALID_ARGUMENT, std::string("model tensor '") + name + "' is missing");
+            data = nullptr, got = len;
+        }
+        if (got != len)
+            fail(IRX_INVALID_ARGUMENT, std::string("model tensor '") + name + "' has " + std::to_string(got) +
+                                           " values; expected " + std::to_string(len));
+        size_t offset = (host.size() + 63) / 64 * 64;
+        host.resize(offset + len, 0.f);
+        if (data) std::memcpy(host.data() + offset, data, len * sizeof(float));
+        pending.push_back({slot, offset});
+    }
+
+    void block(BlockW &b, const std::string &prefix, int dim, bool qass) {
+        const bool zb = task == IRX_TASK_REGRESSOR;  // bias-free LayerNorms (model.rs:273-280)
+        b.dim = dim, b.qass = qass;
+        auto t = [&](const char *suffix, size_t len, const float **slot, bool z = false) {
+            take((prefix + suffix).c_str(), len, slot, z);
+        };
+        const size_t d = dim;
+        t(".attn.in_proj_weight", 3 * d * d, &b.in_w);
+        t(".attn.in_proj_bias", 3 * d, &b.in_b);
+        t(".attn.out_proj.weight", d * d, &b.out.w);
+        t(".attn.out_proj.bias", d, &b.out.b);
+        t(".linear1.weight", 2 * d * d, &b.l1.w);
+        t(".linear1.bias", 2 * d, &b.l1.b);
+        t(".linear2.weight", 2 * d * d, &b.l2.w);
+        t(".linear2.bias", d, &b.l2.b);
+        t(".norm1.weight", d, &b.n1w);
+        t(".norm1.bias", d, &b.n1b, zb);
+        t(".norm2.weight", d, &b.n2w);
+        t(".norm2.bias", d, &b.n2b, zb);
+        if (qass) {
+            const size_t hd = d / kHeads;
+            t(".attn.ssmax_layer.query_mlp.0.weight", 64 * hd, &b.qm0.w);
+            t(".attn.ssmax_layer.query_mlp.0.bias", 64, &b.qm0.b);
+            t(".attn.ssmax_layer.query_mlp.2.weight", hd * 64, &b.qm2.w);
+            t(".attn.ssmax_layer.query_mlp.2.bias", hd, &b.qm2.b);
+        }
+    }
+};
+
+void weights_load(irx_weights *W, irx_tensor_lookup lookup, void *user) {
+    Loader L{lookup, user, W->task, {}, {}};
+    const bool zb = W->task == IRX_TASK_REGRESSOR;
+    const float *freqs = nullptr;
+    L.take("col_embedder.in_linear.weight", 128 * 3, &W->in_w);
+    L.take("col_embedder.in_linear.bias", 128, &W->in_b);
+    for (int b = 0; b < kColumnBlocks; ++b) {
+        std::string p = "col_embedder.tf_col.blocks." + std::to_string(b);
+        L.take((p + ".ind_vectors").c_str(), 128 * 128, &W->ind[b]);
+        L.block(W->col1[b], p + ".multihead_attn1", 128, true);
+        L.block(W->col2[b], p + ".multihead_attn2", 128, false);
+    }
+    for (int b = 0; b < kRowBlocks; ++b)
+        L.block(W->row[b], "row_interactor.tf_row.blocks." + std::to_string(b), 128, false);
+    L.take("row_interactor.cls_tokens", 4 * 128, &W->cls);
+    L.take("row_interactor.out_ln.weight", 128, &W->out_ln_w);
+    L.take("row_interactor.out_ln.bias", 128, &W->out_ln_b, zb);
+    L.take("row_interactor.tf_row.rope.freqs", 8, &freqs);
+    for (int b = 0; b < kIclBlocks; ++b)
+        L.block(W->icl[b], "icl_predictor.tf_icl.blocks." + std::to_string(b), 512, true);
+    L.take("icl_predictor.ln.weight", 512, &W->ln_w);
+    L.take("icl_predictor.ln.bias", 512, &W->ln_b, zb);
+    L.take("icl_predictor.decoder.0.weight", 1024 * 512, &W->dec0.w);
+    L.take("icl_predictor.decoder.0.bias", 1024, &W->dec0.b);
+    const size_t width = W->width;
+    L.take("icl_predictor.decoder.2.weight", width * 1024, &W->dec2.w);
+    L.take("icl_predictor.decoder.2.bias", width, &W->dec2.b);
+    W->arena.alloc(L.host.size() * sizeof(float));
+    IRX_HIP(hipMemcpy(W->arena.p, L.host.data(), L.host.size() * sizeof(float), hipMemcpyHostToDevice));
+    W->bytes = W->arena.bytes;
+    for (auto &pend : L.pending) {
+        if (pend.slot == &freqs) continue;
+        *pend.slot = W->arena.f() + pend.offset;
+    }
+    // The RoPE frequencies stay on the host: the tables are built from them.
+    for (auto &pend : L.pending)
+        if (pend.slot == &freqs) W->freqs_host.assign(L.host.begin() + pend.offset, L.host.begin() + pend.offset + 8);
+}
+
+// ---- build ----
+
+struct BuildPlan {
+    int col_chunk;   // columns per chunk of the column stage
+    int row_run;     // rows per run of the row stage
+    size_t ws_bytes; // workspace
+    size_t keep_bytes;
+};
+
+size_t column_chunk_floats(int cols, long long n) {
+    long long cn = (long long)cols * n;
+    // state is per estimator; chunk temporaries: norm, q, att (128) + kv, hid (256)
+    return (size_t)(cn * (128 * 3 + 256 * 2) + (long long)cols * 128 * (128 * 4 + 256));
+}
+
+size_t row_run_floats(long long seqs, int len) {
+    long long m = seqs * len, c = seqs * kReserved;
+    return (size_t)(m * (128 * 3 + 384 + 256) + c * (128 * 4 + 256));
+}
+
+BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus) {
+    const long long n = sh.rows, h = sh.features, b = sh.ensembles;
+    const int len = (int)h + kReserved;
+    BuildPlan p{};
+    p.keep_bytes = (size_t)kColumnBlocks * 2 * b * (h + 4) * kColumnCache * 4 +
+                   (size_t)kIclBlocks * 2 * b * kHeads * n * 64 * 4;
+    size_t cap = std::min<size_t>(budget / 4, (size_t)24 << 30);
+    int chunk = (int)h;
+    while (chunk > 1 && column_chunk_floats(chunk, n) * 4 > cap) chunk = (chunk + 1) / 2;
+    p.col_chunk = chunk;
+    int run = (int)std::min<long long>(n, 16384);
+    while (run > 64 && row_run_floats(run, len) * 4 > cap) run /= 2;
+    p.row_run = run;
+    size_t fixed = ((size_t)n * h + n * 128 + n * 512 + 6 * 128 * 128 + 12 * 512 + 2 * len * 16) * 4;
+    size_t state = (size_t)h * n * 128 * 4;  // all features' column states of one estimator
+    size_t icl = ((size_t)n * 512 * 7 + n * 1024) * 4 +
+                 icl_attention_partial_floats(kHeads, (int)n, icl_attention_splits(kHeads, (int)n, (int)n, cus)) * 4;
+    p.ws_bytes = fixed + state + column_chunk_floats(chunk, n) * 4 + row_run_floats(run, len) * 4 + icl +
+                 (size_t)64 * 256 * 40;
+    return p;
+}
+
+bool shape_ok(const irx_shape *s) {
+    return s && s->ensembles > 0 && s->features > 0 && s->rows > 0 && s->features < (1 << 20) &&
+           s->rows < (size_t)(1u << 30) && s->ensembles < 4096;
+}
+
+int report(irx_progress_fn fn, void *user, int stage, size_t done, size_t total) {
+    if (fn && fn(user, stage, done, total) != 0) fail(IRX_INTERRUPTED, "interrupted by the progress hook");
+    return 0;
+}
+
+void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *out, irx_built_cache **keep) {
+    const irx_shape sh = in->shape;
+    if (!shape_ok(&sh)) fail(IRX_INVALID_ARGUMENT, "build shape must be nonempty");
+    if (sh.rows < 64) fail(IRX_DOES_NOT_FIT, "the device builds contexts of at least 64 training rows");
+    if (!in->x || !in->column_labels || !in->icl_labels || !in->rope_frequencies || !in->cls_tokens)
+        fail(IRX_INVALID_ARGUMENT, "build inputs are missing");
+    for (int i = 0; i < kColumnBlocks; ++i)
+        if (!in->inducing_queries[i]) fail(IRX_INVALID_ARGUMENT, "inducing queries are missing");
+    for (int i = 0; i < kIclBlocks; ++i)
+        if (!in->base_scales[i]) fail(IRX_INVALID_ARGUMENT, "base scales are missing");
+    const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
+    // A grouped all-missing triple is the CPU path's (has_missing_marker, cpu.rs:4072-4084).
+    for (long long r = 0; r < (long long)B * N; ++r) {
+        const float *row = in->x + r * H;
+        for (int f = 0; f < H; ++f)
+            if (row[(f + 1) % H] == -100.0f && row[(f + 2) % H] == -100.0f && row[(f + 4) % H] == -100.0f)
+                fail(IRX_UNSUPPORTED, "a grouped feature triple is the all-missing marker");
+    }
+    set_device(W->device);
+    const int cus = W->device->compute_units;
+    BuildPlan plan = plan_build(sh, in->budget, cus);
+    if (plan.ws_bytes + plan.keep_bytes > in->budget / 10 * 9)
+        fail(IRX_DOES_NOT_FIT, "the context does not fit the device");
+
+    hipStream_t s;
+    IRX_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    struct StreamGuard {
+        hipStream_t s;
+        ~StreamGuard() {
+            (void)hipStreamSynchronize(s);
+            (void)hipStreamDestroy(s);
+        }
+    } guard{s};
+
+    auto cache = new irx_built_cache();
+    struct CacheGuard {
+        irx_built_cache *&c;
+        ~CacheGuard() { delete c; }
+    } cache_guard{cache};
+    cache->device = W->device;
+    cache->shape = sh;
+    const long long col_plane = (long long)B * L * kColumnCache;
+    const long long icl_plane = (long long)B * kHeads * N * 64;
+    for (int i = 0; i < kColumnBlocks; ++i) {
+        cache->column[i].alloc(2 * col_plane * 4);
+        fill_zero(cache->column[i].f(), 2 * col_plane, s);  // reserved CLS streams stay zero
+    }
+    for (int i = 0; i < kIclBlocks; ++i) cache->icl[i].alloc(2 * icl_plane * 4);
+
+    Arena ws;
+    ws.buf.alloc(plan.ws_bytes);
+    Stages st{*W, s, cus};
+    // Inputs shared by every estimator.
+    float *d_ind_q = ws.take(3 * 128 * 128);
+    float *d_base = ws.take(12 * 512);
+    std::vector<float> cos_t, sin_t;
+    rope_tables(W->freqs_host.data(), L, cos_t, sin_t);
+    float *d_cos = ws.take(L * 16), *d_sin = ws.take(L * 16);
+    for (int i = 0; i < 3; ++i) upload(d_ind_q + i * 128 * 128, in->inducing_queries[i], 128 * 128 * 4, s);
+    for (int i = 0; i < 12; ++i) upload(d_base + i * 512, in->base_scales[i], 512 * 4, s);
+    upload(d_cos, cos_t.data(), cos_t.size() * 4, s);
+    upload(d_sin, sin_t.data(), sin_t.size() * 4, s);
+    float *d_x = ws.take((size_t)N * H), *d_ylab = ws.take((size_t)N * 128), *d_yicl = ws.take((size_t)N * 512);
+    float *d_state = ws.take((size_t)H * N * 128);
+    const size_t mark = ws.used;
+
+    report(in->progress, in->progress_user, IRX_STAGE_BUILD, 0, B);
+    for (int e = 0; e < B; ++e) {
+        ws.used = mark;
+        upload(d_x, in->x + (size_t)e * N * H, (size_t)N * H * 4, s);
+        upload(d_ylab, in->column_labels + (size_t)e * N * 128, (size_t)N * 128 * 4, s);
+        upload(d_yicl, in->icl_labels + (size_t)e * N * 512, (size_t)N * 512 * 4, s);
+        // Column stage, chunk by chunk of features (column_stream + isab, cpu.rs:1132-1207).
+        {
+            const size_t cmark = ws.used;
+            const int C = plan.col_chunk;
+            const long long cn = (long long)C * N;
+            float *norm = ws.take(cn * 128), *q = ws.take(cn * 128), *att = ws.take(cn * 128);
+            float *kv = ws.take(cn * 256), *hid = ws.take(cn * 256);
+            float *hidden = ws.take((size_t)C * 128 * 128), *hnorm = ws.take((size_t)C * 128 * 128);
+            float *hatt = ws.take((size_t)C * 128 * 128), *hhid = ws.take((size_t)C * 128 * 256);
+            column_input(d_x, 0, 1, N, H, W->in_w, W->in_b, d_ylab, d_state, nullptr, s);
+            for (int f0 = 0; f0 < H; f0 += C) {
+                const int cols = std::min(C, H - f0);
+                const long long m = (long long)cols * N;
+                float *state = d_state + (size_t)f0 * N * 128;
+                for (int blk = 0; blk < kColumnBlocks; ++blk) {
+                    // multihead_attn1: the inducing points attend to the column's N rows, QASS'd queries.
+                    const BlockW &b1 = W->col1[blk];
+                    layer_norm(state, 128, b1.n1w, b1.n1b, norm, 128, m, 128, s);
+                    st.linear(norm, 128, m, 128, b1.in_w + 128 * 128, b1.in_b + 128, 256, kv, 256);
+                    SmallAttention a{};
+                    a.q = d_ind_q + blk * 128 * 128, a.q_seq = 0, a.q_group = 0, a.q_row = 128, a.q_head = 16;
+                    a.k = kv, a.v = kv + 128, a.k_seq = a.v_seq = (long long)N * 256, a.k_group = a.v_group = 0;
+                    a.k_row = a.v_row = 256, a.k_head = a.v_head = 16;
+                    a.o = hatt, a.o_seq = 128 * 128, a.o_group = 0, a.o_row = 128, a.o_head = 16;
+                    a.group = cols, a.seqs = cols, a.heads = kHeads, a.q_rows = kInducing, a.kv_rows = N;
+                    a.scale = 0.25f;
+                    small_attention(a, s);
+                    repeat_rows(W->ind[blk], 128 * 128, cols, hidden, s);
+                    st.tail(b1, hidden, (long long)cols * 128, hatt, hnorm, hhid);
+                    // multihead_attn2 keys and values from the inducing state, straight into the cache.
+                    const BlockW &b2 = W->col2[blk];
+                    layer_norm(hidden, 128, b2.n1w, b2.n1b, hnorm, 128, (long long)cols * 128, 128, s);
+                    float *kc = cache->column[blk].f() + ((long long)e * L + kReserved + f0) * kColumnCache;
+                    OutMap cmap{16, kHeads, col_plane, 128 * 16, 128, kColumnCache, 16};
+                    st.linear_map(hnorm, 128, (long long)cols * 128, 128, b2.in_w + 128 * 128, b2.in_b + 128, 256,
+                                  kc, cmap);
+                    st.column_attend(blk, state, cols, N, kc, kc + col_plane, cols, 0, norm, q, att, hid);
+                }
+            }
+            ws.used = cmark;
+        }
+        // Row stage in runs, into the ICL row states.
+        float *rows = ws.take((size_t)N * 512);
+        {
+            const size_t rmark = ws.used;
+            const int R = plan.row_run;
+            Stages::RowBuffers rb = Stages::row_buffers(ws, R, L);
+            float *stage = ws.take((size_t)H * R * 128);
+            for (int r0 = 0; r0 < N; r0 += R) {
+                const int len = std::min(R, N - r0);
+                // Gather the run's column states into [H, len, 128].
+                IRX_HIP(hipMemcpy2DAsync(stage, (size_t)len * 128 * 4, d_state + (size_t)r0 * 128, (size_t)N * 128 * 4,
+                                         (size_t)len * 128 * 4, H, hipMemcpyDeviceToDevice, s));
+                st.row_stage(stage, 1, len, H, rows + (size_t)r0 * 512, d_cos, d_sin, rb);
+            }
+            ws.used = rmark;
+        }
+        add_inplace(rows, d_yicl, (long long)N * 512, s);
+        // ICL stage: each block's K/V from the training rows, then their queries.
+        {
+            Stages::IclBuffers ib = Stages::icl_buffers(ws, N, 1, N, N, cus);
+            for (int blk = 0; blk < kIclBlocks; ++blk) {
+                const BlockW &bw = W->icl[blk];
+                layer_norm(rows, 512, bw.n1w, bw.n1b, ib.norm, 512, N, 512, s);
+                float *kc = cache->icl[blk].f() + (long long)e * kHeads * N * 64;
+                OutMap kvmap = OutMap::head_major(64, kHeads, N, icl_plane);
+                st.linear_map(ib.norm, 512, N, 512, bw.in_w + 512 * 512, bw.in_b + 512, 1024, kc, kvmap);
+                // The last block's row states are never read: only its K/V are kept.
+                if (blk + 1 < kIclBlocks)
+                    st.icl_queries(blk, rows, 1, N, kc, kc + icl_plane, N, d_base + blk * 512, ib);
+            }
+        }
+        IRX_HIP(hipStreamSynchronize(s));
+        report(in->progress, in->progress_user, IRX_STAGE_BUILD, e + 1, B);
+    }
+    // Non-finite cached values are an error (cuda/build.rs:340-350, 595-622).
+    {
+        unsigned *counter = reinterpret_cast<unsigned *>(ws.take(64));
+        IRX_HIP(hipMemsetAsync(counter, 0, 4, s));
+        for (int i = 0; i < kColumnBlocks; ++i) count_nonfinite(cache->column[i].f(), 2 * col_plane, counter, s);
+        for (int i = 0; i < kIclBlocks; ++i) count_nonfinite(cache->icl[i].f(), 2 * icl_plane, counter, s);
+        unsigned bad = 0;
+        download(&bad, counter, 4, s);
+        IRX_HIP(hipStreamSynchronize(s));
+        if (bad) fail(IRX_NOT_FINITE, "a cached key or value is not finite");
+    }
+    if (out) {
+        for (int i = 0; i < kColumnBlocks; ++i) {
+            // Copy feature streams only; the caller's reserved streams stay as they are.
+            for (int e = 0; e < B; ++e)
+                for (int part = 0; part < 2; ++part) {
+                    float *dst = part ? out->column_values[i] : out->column_keys[i];
+                    if (!dst) continue;
+                    const size_t off = ((size_t)e * L + kReserved) * kColumnCache;
+                    download(dst + off, cache->column[i].f() + part * col_plane + off, (size_t)H * kColumnCache * 4, s);
+                }
+        }
+        for (int i = 0; i < kIclBlocks; ++i) {
+            if (out->icl_keys[i]) download(out->icl_keys[i], cache->icl[i].f(), icl_plane * 4, s);
+            if (out->icl_values[i]) download(out->icl_values[i], cache->icl[i].f() + icl_plane, icl_plane * 4, s);
+        }
+        IRX_HIP(hipStreamSynchronize(s));
+    }
+    if (keep) {
+        *keep = cache;
+        cache = nullptr;
+    }
+}
+
+// ---- predictor ----
+
+// Buffers of one prediction pass of up to `R` rows per estimator. The same
+// function sizes the workspace (counting arena) and carves it, so the two
+// always agree; a shorter last pass uses a prefix of each buffer.
+struct PassBuffers {
+    uint8_t *flags;
+    float *state, *norm, *q, *att, *hid, *rows;
+    Stages::RowBuffers rb;
+    Stages::IclBuffers ib;
+};
+
+PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus) {
+    const long long B = sh.ensembles, H = sh.features, cr = B * H * (long long)R;
+    PassBuffers p{};
+    p.flags = a.take_bytes(B * R);
+    p.state = a.take(cr * 128), p.norm = a.take(cr * 128), p.q = a.take(cr * 128), p.att = a.take(cr * 128);
+    p.hid = a.take(cr * 256);
+    p.rb = Stages::row_buffers(a, B * (long long)R, (int)H + kReserved);
+    p.rows = a.take(B * R * 512);
+    p.ib = Stages::icl_buffers(a, B * (long long)R, (int)B, (int)R, (int)sh.rows, cus);
+    // A shorter pass may split the keys further; size the partials for the worst pass.
+    size_t worst = 0;
+    for (size_t rows = 32; rows <= R; rows += 32) {
+        int splits = icl_attention_splits((int)B * kHeads, (int)rows, (int)sh.rows, cus);
+        worst = std::max(worst, icl_attention_partial_floats((int)B * kHeads, (int)rows, splits));
+    }
+    if (worst > p.ib.partial_floats) {
+        p.ib.partial = a.take(worst);
+        p.ib.partial_floats = worst;
+    }
+    return p;
+}
+
+size_t predict_ws_floats(const irx_shape &sh, size_t R, int cus) {
+    Arena count;
+    count.counting = true;
+    pass_layout(count, sh, R, cus);
+    return count.used / 4;
+}
+
+void predict_pass(irx_predictor *P, const float *d_x, long long x_stride, int q0, int R, float *d_logits, int Q,
+                  uint8_t *flags_host) {
+    const irx_weights &W = *P->weights;
+    const irx_shape &sh = P->shape;
+    const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
+    const int width = (int)sh.outputs;
+    hipStream_t s = P->stream;
+    Stages st{W, s, W.device->compute_units};
+    Arena &ws = P->ws;
+    ws.used = 0;
+    const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus);
+    uint8_t *flags = pb.flags;
+    float *state = pb.state, *norm = pb.norm, *q = pb.q, *att = pb.att, *hid = pb.hid, *rows = pb.rows;
+    const Stages::RowBuffers &rb = pb.rb;
+    Stages::IclBuffers ib = pb.ib;
+
+    IRX_HIP(hipMemsetAsync(flags, 0, (size_t)B * R, s));
+    column_input(d_x + (size_t)q0 * H, x_stride, B, R, H, W.in_w, W.in_b, nullptr, state, flags, s);
+    const long long col_plane = (long long)B * L * kColumnCache;
+    for (int blk = 0; blk < kColumnBlocks; ++blk) {
+        const float *kc = P->column[blk].f() + kReserved * kColumnCache;
+        st.column_attend(blk, state, B * H, R, kc, kc + col_plane, H, (long long)L * kColumnCache, norm, q, att,
+                         hid);
+    }
+    st.row_stage(state, B, R, H, rows, P->rope_cos.f(), P->rope_sin.f(), rb);
+    const long long icl_plane = (long long)B * kHeads * N * 64;
+    for (int blk = 0; blk < kIclBlocks; ++blk) {
+        const float *kc = P->icl[blk].f();
+        st.icl_queries(blk, rows, B, R, kc, kc + icl_plane, N, P->base_scales.f() + blk * 512, ib);
+    }
+    // Decoder (cached_icl_decoder, cpu.rs:2543-2580) into logits [B, Q, width].
+    layer_norm(rows, 512, W.ln_w, W.ln_b, ib.norm, 512, (long long)B * R, 512, s);
+    st.linear(ib.norm, 512, (long long)B * R, 512, W.dec0.w, W.dec0.b, 1024, ib.hid, 1024, kEpiGelu);
+    OutMap lmap{width, 1, 0, 0, R, (long long)Q * width, width};
+    st.linear_map(ib.hid, 1024, (long long)B * R, 1024, W.dec2.w, W.dec2.b, width, d_logits + (size_t)q0 * width,
+                  lmap);
+    if (flags_host) {
+        std::vector<uint8_t> f((size_t)B * R);
+        download(f.data(), flags, f.size(), s);
+        IRX_HIP(hipStreamSynchronize(s));
+        for (int b = 0; b < B; ++b)
+            for (int r = 0; r < R; ++r) flags_host[q0 + r] |= f[(size_t)b * R + r];
+    }
+}
+
+void ensure_workspace(irx_predictor *P) {
+    if (P->ws_rows == P->pass_rows && P->ws.buf.p) return;
+    size_t floats = predict_ws_floats(P->shape, P->pass_rows, P->weights->device->compute_units);
+    P->ws.buf.alloc(floats * 4);
+    P->ws_rows = P->pass_rows;
+}
+
+int guarded(const char *where, auto &&fn) {
+    try {
+        fn();
+        return IRX_OK;
+    } catch (const Failure &f) {
+        g_last_error = f.message;
+        return f.status;
+    } catch (const std::bad_alloc &) {
+        g_last_error = std::string(where) + ": host out of memory";
+        return IRX_OUT_OF_MEMORY;
+    } catch (...) {
+        g_last_error = std::string(where) + ": unexpected failure";
+        return IRX_DEVICE_ERROR;
+    }
+}
+
+void device_release(irx_device *d) {
+    if (d && d->refs.fetch_sub(1) == 1) delete d;
+}
+
+}  // namespace
+
+// ===================================================================
+// C ABI
+// ===================================================================
+
+extern "C" {
+
+const char *irx_last_error(void) { return g_last_error.c_str(); }
+int irx_abi_version(void) { return IRX_ABI_VERSION; }
+
+int irx_device_open(int ordinal, irx_device **out) {
+    return guarded("irx_device_open", [&] {
+        if (!out) fail(IRX_INVALID_ARGUMENT, "out is null");
+        *out = nullptr;
+        const char *off = std::getenv("IRONICL_NO_ROCM");
+        if (off && *off) fail(IRX_NO_DEVICE, "IRONICL_NO_ROCM is set");
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count <= ordinal || ordinal < 0)
+            fail(IRX_NO_DEVICE, "no ROCm device");
+        hipDeviceProp_t props;
+        IRX_HIP(hipGetDeviceProperties(&props, ordinal));
+        if (std::strncmp(props.gcnArchName, "gfx950", 6) != 0)
+            fail(IRX_NO_DEVICE, std::string("kernels are built for gfx950, not ") + props.gcnArchName);
+        IRX_HIP(hipSetDevice(ordinal));
+        auto d = new irx_device();
+        d->ordinal = ordinal;
+        d->compute_units = props.multiProcessorCount;
+        *out = d;
+    });
+}
+
+void irx_device_close(irx_device *device) { device_release(device); }
+
+int irx_device_free_memory(irx_device *device, size_t *bytes) {
+    return guarded("irx_device_free_memory", [&] {
+        if (!device || !bytes) fail(IRX_INVALID_ARGUMENT, "null argument");
+        set_device(device);
+        size_t free_b = 0, total = 0;
+        IRX_HIP(hipMemGetInfo(&free_b, &total));
+        *bytes = free_b;
+    });
+}
+
+int irx_device_compute_units(irx_device *device, int *units) {
+    return guarded("irx_device_compute_units", [&] {
+        if (!device || !units) fail(IRX_INVALID_ARGUMENT, "null argument");
+        *units = device->compute_units;
+    });
+}
+
+int irx_weights_upload(irx_device *device, int task, irx_tensor_lookup lookup, void *user, irx_weights **out) {
+    irx_weights *W = nullptr;
+    int st = guarded("irx_weights_upload", [&] {
+        if (!device || !lookup || !out) fail(IRX_INVALID_ARGUMENT, "null argument");
+        if (task != IRX_TASK_CLASSIFIER && task != IRX_TASK_REGRESSOR) fail(IRX_INVALID_ARGUMENT, "unknown task");
+        *out = nullptr;
+        set_device(device);
+        W = new irx_weights();
+        W->device = device;
+        device->refs.fetch_add(1);
+        W->task = task;
+        W->width = task == IRX_TASK_CLASSIFIER ? 10 : 999;
+        weights_load(W, lookup, user);
+        *out = W;
+        W = nullptr;
+    });
+    if (W) irx_weights_release(W);
+    return st;
+}
+
+void irx_weights_retain(irx_weights *weights) {
+    if (weights) weights->refs.fetch_add(1);
+}
+
+void irx_weights_release(irx_weights *weights) {
+    if (!weights || weights->refs.fetch_sub(1) != 1) return;
+    irx_device *d = weights->device;
+    if (d) (void)hipSetDevice(d->ordinal);
+    delete weights;
+    device_release(d);
+}
+
+size_t irx_weights_bytes(const irx_weights *weights) { return weights ? weights->bytes : 0; }
+
+int irx_weights_budget(const irx_weights *weights, uint64_t device_limit, size_t *budget) {
+    return guarded("irx_weights_budget", [&] {
+        if (!weights || !budget) fail(IRX_INVALID_ARGUMENT, "null argument");
+        set_device(weights->device);
+        size_t free_b = 0, total = 0;
+        IRX_HIP(hipMemGetInfo(&free_b, &total));
+        if (device_limit) {
+            size_t limit = device_limit > weights->bytes ? (size_t)(device_limit - weights->bytes) : 0;
+            free_b = std::min(free_b, limit);
+        }
+        *budget = free_b;
+    });
+}
+
+size_t irx_context_bytes(int precision) { return precision == IRX_PRECISION_FP32 ? 4 : 0; }
+
+int irx_build_fits(size_t budget, int precision, const irx_shape *shape) {
+    if (precision != IRX_PRECISION_FP32 || !shape_ok(shape) || shape->rows < 64) return 0;
+    BuildPlan p = plan_build(*shape, budget, 256);
+    return p.ws_bytes + p.keep_bytes <= budget / 10 * 9;
+}
+
+int irx_build(irx_weights *weights, int precision, const irx_build_inputs *inputs, irx_build_outputs *outputs,
+              irx_built_cache **keep) {
+    return guarded("irx_build", [&] {
+        if (!weights || !inputs) fail(IRX_INVALID_ARGUMENT, "null argument");
+        if (precision != IRX_PRECISION_FP32) fail(IRX_INVALID_ARGUMENT, "only FP32 precision is built here");
+        if (keep) *keep = nullptr;
+        if (inputs->shape.outputs == 0 || inputs->shape.outputs > (size_t)weights->width)
+            fail(IRX_INVALID_ARGUMENT, "outputs exceed the decoder width");
+        build_impl(weights, inputs, outputs, keep);
+    });
+}
+
+void irx_built_cache_free(irx_built_cache *cache) {
+    if (!cache) return;
+    if (cache->device) (void)hipSetDevice(cache->device->ordinal);
+    delete cache;
+}
+
+int irx_predictor_new(irx_weights *weights, int precision, const irx_context_tensors *ctx, irx_built_cache *adopt,
+                      irx_predictor **out) {
+    irx_predictor *P = nullptr;
+    int st = guarded("irx_predictor_new", [&] {
+        if (!weights || !ctx || !out) fail(IRX_INVALID_ARGUMENT, "null argument");
+        if (precision != IRX_PRECISION_FP32) fail(IRX_INVALID_ARGUMENT, "only FP32 precision is predicted here");
+        *out = nullptr;
+        const irx_shape sh = ctx->shape;
+        if (!shape_ok(&sh) || sh.outputs == 0 || sh.outputs > (size_t)weights->width)
+            fail(IRX_INVALID_ARGUMENT, "context shape does not match the model");
+        for (int i = 0; i < kIclBlocks; ++i)
+            if (!ctx->base_scales[i]) fail(IRX_INVALID_ARGUMENT, "base scales are missing");
+        if (!ctx->rope_frequencies || !ctx->cls_tokens) fail(IRX_INVALID_ARGUMENT, "row tokens are missing");
+        set_device(weights->device);
+        const long long B = sh.ensembles, H = sh.features, N = sh.rows, L = H + kReserved;
+        const long long col_plane = B * L * kColumnCache, icl_plane = B * kHeads * N * 64;
+        const size_t cache_bytes = (size_t)(kColumnBlocks * 2 * col_plane + kIclBlocks * 2 * icl_plane) * 4;
+        P = new irx_predictor();
+        P->weights = weights;
+        irx_weights_retain(weights);
+        P->shape = sh;
+        if (adopt) {
+            if (adopt->shape.ensembles != sh.ensembles || adopt->shape.features != sh.features ||
+                adopt->shape.rows != sh.rows)
+                fail(IRX_INVALID_ARGUMENT, "the built cache does not match the context");
+            for (int i = 0; i < kColumnBlocks; ++i) P->column[i] = std::move(adopt->column[i]);
+            for (int i = 0; i < kIclBlocks; ++i) P->icl[i] = std::move(adopt->icl[i]);
+        } else {
+            size_t ws = predict_ws_floats(sh, P->pass_rows, weights->device->compute_units) * 4;
+            if (cache_bytes + ws > ctx->budget / 10 * 9) fail(IRX_DOES_NOT_FIT, "the context does not fit the device");
+            if (!ctx->icl) fail(IRX_INVALID_ARGUMENT, "ICL source is missing");
+            for (int i = 0; i < kColumnBlocks; ++i)
+                if (!ctx->column_keys[i] || !ctx->column_values[i])
+                    fail(IRX_INVALID_ARGUMENT, "column caches are missing");
+            for (int i = 0; i < kColumnBlocks; ++i) {
+                P->column[i].alloc(2 * col_plane * 4);
+                IRX_HIP(hipMemcpy(P->column[i].p, ctx->column_keys[i], col_plane * 4, hipMemcpyHostToDevice));
+                IRX_HIP(hipMemcpy(P->column[i].f() + col_plane, ctx->column_values[i], col_plane * 4,
+                                  hipMemcpyHostToDevice));
+            }
+            for (int i = 0; i < kIclBlocks; ++i) {
+                const float *k = nullptr, *v = nullptr;
+                if (ctx->icl(ctx->icl_user, (size_t)i, &k, &v) != 0 || !k || !v)
+                    fail(IRX_INVALID_ARGUMENT, "the ICL source has no block " + std::to_string(i));
+                P->icl[i].alloc(2 * icl_plane * 4);
+                IRX_HIP(hipMemcpy(P->icl[i].p, k, icl_plane * 4, hipMemcpyHostToDevice));
+                IRX_HIP(hipMemcpy(P->icl[i].f() + icl_plane, v, icl_plane * 4, hipMemcpyHostToDevice));
+            }
+        }
+        P->base_scales.alloc(12 * 512 * 4);
+        for (int i = 0; i < kIclBlocks; ++i)
+            IRX_HIP(hipMemcpy(P->base_scales.f() + i * 512, ctx->base_scales[i], 512 * 4, hipMemcpyHostToDevice));
+        std::vector<float> cos_t, sin_t;
+        rope_tables(ctx->rope_frequencies, (int)L, cos_t, sin_t);
+        P->rope_cos.alloc(cos_t.size() * 4);
+        P->rope_sin.alloc(sin_t.size() * 4);
+        IRX_HIP(hipMemcpy(P->rope_cos.p, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(P->rope_sin.p, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
+        ensure_workspace(P);
+        *out = P;
+        P = nullptr;
+    });
+    if (adopt) irx_built_cache_free(adopt);
+    if (P) irx_predictor_free(P);
+    return st;
+}
+
+void irx_predictor_free(irx_predictor *predictor) {
+    if (!predictor) return;
+    irx_weights *w = predictor->weights;
+    if (w) (void)hipSetDevice(w->device->ordinal);
+    if (predictor->stream) {
+        (void)hipStreamSynchronize(predictor->stream);
+        (void)hipStreamDestroy(predictor->stream);
+    }
+    delete predictor;
+    irx_weights_release(w);
+}
+
+int irx_predictor_streamed(const irx_predictor *) { return 0; }
+
+size_t irx_predictor_pass_rows(const irx_predictor *predictor) { return predictor ? predictor->pass_rows : 0; }
+
+int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows) {
+    return guarded("irx_predictor_set_pass_rows", [&] {
+        if (!predictor || rows < 32 || rows % 32 || rows > (1u << 20))
+            fail(IRX_INVALID_ARGUMENT, "pass rows must be a positive multiple of 32");
+        std::lock_guard<std::mutex> lock(predictor->mu);
+        set_device(predictor->weights->device);
+        predictor->pass_rows = rows;
+        ensure_workspace(predictor);
+    });
+}
+
+static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *d_logits, uint8_t *cpu_rows,
+                           irx_progress_fn progress, void *user) {
+    const size_t R = P->pass_rows;
+    if (cpu_rows) std::memset(cpu_rows, 0, q);
+    for (size_t q0 = 0; q0 < q; q0 += R) {
+        const int len = (int)std::min(R, q - q0);
+        predict_pass(P, d_x, (long long)q * P->shape.features, (int)q0, len, d_logits, (int)q, cpu_rows);
+        if (progress) {
+            IRX_HIP(hipStreamSynchronize(P->stream));
+            report(progress, user, IRX_STAGE_PREDICT, q0 + len, q);
+        }
+    }
+}
+
+int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, float *logits, uint8_t *cpu_rows,
+                          irx_progress_fn progress, void *progress_user) {
+    return guarded("irx_predictor_predict", [&] {
+        if (!predictor || (!x && q) || (!logits && q)) fail(IRX_INVALID_ARGUMENT, "null argument");
+        if (q == 0) return;
+        std::lock_guard<std::mutex> lock(predictor->mu);
+        set_device(predictor->weights->device);
+        const irx_shape &sh = predictor->shape;
+        const size_t xn = sh.ensembles * q * sh.features, ln = sh.ensembles * q * sh.outputs;
+        DevBuf dx(xn * 4), dl(ln * 4);
+        upload(dx.p, x, xn * 4, predictor->stream);
+        predict_common(predictor, dx.f(), q, dl.f(), cpu_rows, progress, progress_user);
+        download(logits, dl.p, ln * 4, predictor->stream);
+        IRX_HIP(hipStreamSynchronize(predictor->stream));
+    });
+}
+
+int irx_predictor_predict_device(irx_predictor *predictor, const float *x_device, size_t q, float *logits_device,
+                                 uint8_t *cpu_rows) {
+    return guarded("irx_predictor_predict_device", [&] {
+        if (!predictor || (!x_device && q) || (!logits_device && q)) fail(IRX_INVALID_ARGUMENT, "null argument");
+        if (q == 0) return;
+        std::lock_guard<std::mutex> lock(predictor->mu);
+        set_device(predictor->weights->device);
+        predict_common(predictor, x_device, q, logits_device, cpu_rows, nullptr, nullptr);
+        IRX_HIP(hipStreamSynchronize(predictor->stream));
+    });
+}
+
+// ---- kernel harness ----
+
+int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v, size_t pairs,
+                           size_t query_rows, size_t rows, float *out) {
+    return guarded("irx_test_icl_attention", [&] {
+        if (!device || !q || !k || !v || !out || !pairs || !query_rows || !rows)
+            fail(IRX_INVALID_ARGUMENT, "ICL attention shapes do not match");
+        if (pairs % kHeads) fail(IRX_INVALID_ARGUMENT, "pairs must be a multiple of 8 (estimators x heads)");
+        set_device(device);
+        const size_t qn = pairs * query_rows * 64, kn = pairs * rows * 64;
+        DevBuf dq(qn * 4), dk(kn * 4), dv(kn * 4), dout(qn * 4);
+        IRX_HIP(hipMemcpy(dq.p, q, qn * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dk.p, k, kn * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dv.p, v, kn * 4, hipMemcpyHostToDevice));
+        int splits = icl_attention_splits((int)pairs, (int)query_rows, (int)rows, device->compute_units);
+        size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, splits);
+        DevBuf part(pf * 4);
+        IclAttention a{};
+        a.q = dq.f(), a.q_pair_stride = (long long)query_rows * 64, a.k = dk.f(), a.v = dv.f();
+        a.kv_pair_stride = (long long)rows * 64, a.o = dout.f(), a.ldo = 512;
+        a.pairs = (int)pairs, a.q_rows = (int)query_rows, a.kv_rows = (int)rows;
+        a.partial = part.f(), a.partial_floats = pf, a.compute_units = device->compute_units;
+        icl_attention(a, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+        // Tokens [b, q, 8, 64] back to [pairs, q, 64].
+        std::vector<float> tok(qn);
+        IRX_HIP(hipMemcpy(tok.data(), dout.p, qn * 4, hipMemcpyDeviceToHost));
+        for (size_t p = 0; p < pairs; ++p) {
+            size_t b = p / kHeads, h = p % kHeads;
+            for (size_t r = 0; r < query_rows; ++r)
+                std::memcpy(out + (p * query_rows + r) * 64, tok.data() + ((b * query_rows + r) * 512 + h * 64), 256);
+        }
+    });
+}
+
+int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1, const float *w2,
+                      const float *b2, size_t rows, size_t width, size_t depth, size_t width2, float *first,
+                      float *second) {
+    return guarded("irx_test_products", [&] {
+        if (!device || !x || !w1 || !b1 || !w2 || !b2 || !first || !second || !rows || depth % 16 || width % 16)
+            fail(IRX_INVALID_ARGUMENT, "tensor product shapes do not match");
+        set_device(device);
+        DevBuf dx(rows * depth * 4), dw1(width * depth * 4), db1(width * 4), dw2(width2 * width * 4),
+            db2(width2 * 4), d1(rows * width * 4), d2(rows * width2 * 4);
+        IRX_HIP(hipMemcpy(dx.p, x, rows * depth * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dw1.p, w1, width * depth * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(db1.p, b1, width * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dw2.p, w2, width2 * width * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(db2.p, b2, width2 * 4, hipMemcpyHostToDevice));
+        GemmArgs g{};
+        g.a = dx.f(), g.lda = (long long)depth, g.w = dw1.f(), g.bias = db1.f(), g.c = d1.f();
+        g.out = OutMap::row_major((int)width, (long long)width);
+        g.m = (int)rows, g.n = (int)width, g.k = (int)depth, g.epilogue = kEpiGelu;
+        gemm(g, nullptr);
+        GemmArgs h{};
+        h.a = d1.f(), h.lda = (long long)width, h.w = dw2.f(), h.bias = db2.f(), h.c = d2.f();
+        h.out = OutMap::row_major((int)width2, (long long)width2);
+        h.m = (int)rows, h.n = (int)width2, h.k = (int)width;
+        if (width2 == width) h.epilogue = kEpiResidual, h.residual = d1.f(), h.ldr = (long long)width;
+        gemm(h, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(first, d1.p, rows * width * 4, hipMemcpyDeviceToHost));
+        IRX_HIP(hipMemcpy(second, d2.p, rows * width2 * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+int irx_test_layer_norm(irx_device *device, const float *x, const float *weight, const float *bias, size_t rows,
+                        size_t width, float *out) {
+    return guarded("irx_test_layer_norm", [&] {
+        if (!device || !x || !weight || !out || !rows || (width != 128 && width != 512))
+            fail(IRX_INVALID_ARGUMENT, "layer norm shapes do not match");
+        set_device(device);
+        DevBuf dx(rows * width * 4), dw(width * 4), db(width * 4), dy(rows * width * 4);
+        IRX_HIP(hipMemcpy(dx.p, x, rows * width * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dw.p, weight, width * 4, hipMemcpyHostToDevice));
+        if (bias) IRX_HIP(hipMemcpy(db.p, bias, width * 4, hipMemcpyHostToDevice));
+        layer_norm(dx.f(), (long long)width, dw.f(), bias ? db.f() : nullptr, dy.f(), (long long)width,
+                   (long long)rows, (int)width, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(out, dy.p, rows * width * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v, size_t heads,
+                             size_t query_rows, size_t rows, float *out) {
+    return guarded("irx_test_small_attention", [&] {
+        if (!device || !q || !k || !v || !out || !heads || !query_rows || !rows)
+            fail(IRX_INVALID_ARGUMENT, "small attention shapes do not match");
+        set_device(device);
+        const size_t qn = heads * query_rows * 16, kn = heads * rows * 16;
+        DevBuf dq(qn * 4), dk(kn * 4), dv(kn * 4), dout(qn * 4);
+        IRX_HIP(hipMemcpy(dq.p, q, qn * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dk.p, k, kn * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dv.p, v, kn * 4, hipMemcpyHostToDevice));
+        SmallAttention a{};
+        a.q = dq.f(), a.k = dk.f(), a.v = dv.f(), a.o = dout.f();
+        a.q_seq = a.q_group = 0, a.q_row = 16, a.q_head = (long long)query_rows * 16;
+        a.k_seq = a.k_group = 0, a.k_row = 16, a.k_head = (long long)rows * 16;
+        a.v_seq = a.v_group = 0, a.v_row = 16, a.v_head = (long long)rows * 16;
+        a.o_seq = a.o_group = 0, a.o_row = 16, a.o_head = (long long)query_rows * 16;
+        a.group = 1, a.seqs = 1, a.heads = (int)heads, a.q_rows = (int)query_rows, a.kv_rows = (int)rows;
+        a.scale = 0.25f;
+        small_attention(a, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(out, dout.p, qn * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+}  // extern "C"

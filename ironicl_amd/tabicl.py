@@ -1,0 +1,412 @@
+"""Host side of the ROCm backend: the reference's Executor / StaticExecutor
+surface over the C ABI.
+
+This mirrors how src/models/tabicl_v2/cpu.rs drives its CUDA backend
+(``build_tensors_cuda`` cpu.rs:737-804, ``with_cuda`` cpu.rs:1855-1910,
+``predict_logits`` cpu.rs:2057-2108): the host embeds the labels, computes
+the QASSMax base scales and the column stage's inducing queries, hands every
+array to ``irx_build`` / ``irx_predictor_*`` and post-processes logits
+(probability aggregation, regression quantiles).
+
+Nothing here computes the model on the CPU: rows the device flags for the
+CPU path (a grouped all-missing -100 triple) come back as NaN logits and are
+listed in ``Prediction.cpu_rows`` for the caller's own CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import hip
+from . import manifest as mf
+
+_erf = np.frompyfunc(math.erf, 1, 1)
+
+
+def _gelu64(x: np.ndarray) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * x * (1.0 + _erf(x / math.sqrt(2.0)).astype(np.float64))
+
+
+def _layer_norm64(x: np.ndarray, w: np.ndarray, b: np.ndarray | None) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + 1e-5) * w
+    return y + b if b is not None else y
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def validate_labels(y: np.ndarray, b: int, n: int) -> int:
+    """Class count of [B, N] labels: contiguous 0..C-1 with C in 2..=10 and the
+    same C for every estimator (validate_labels, cpu.rs:4717-4740)."""
+    classes = None
+    for e in range(b):
+        lab = y[e]
+        if not np.all((lab >= 0) & (lab <= 9) & (lab == np.floor(lab))):
+            raise ValueError("labels must be integers in 0..=9")
+        present = np.zeros(10, bool)
+        present[lab.astype(np.int64)] = True
+        c = 0
+        while c < 10 and present[c]:
+            c += 1
+        if not 2 <= c <= 10 or present[c:].any():
+            raise ValueError("each ensemble's labels must be contiguous 0..C-1 with C in 2..=10")
+        if classes is not None and classes != c:
+            raise ValueError("all ensembles must have the same class count")
+        classes = c
+    return int(classes)
+
+
+@dataclass
+class Prediction:
+    """Decoder outputs [B, Q, outputs]; rows in ``cpu_rows`` hold NaN."""
+    logits: np.ndarray
+    cpu_rows: list[int] = field(default_factory=list)
+
+
+class Executor:
+    """An official TabICLv2 model with its weights resident on the GPU
+    (Executor, cpu.rs:290-296; ModelWeights::new, cuda/weights.rs:299)."""
+
+    def __init__(self, task: str, weights: dict[str, np.ndarray], device: hip.Device | None = None):
+        if task not in (mf.CLASSIFIER, mf.REGRESSOR):
+            raise ValueError(f"unknown task {task!r}")
+        self.task = task
+        self.weights = {k: _f32(v) for k, v in weights.items()}
+        self.width = mf.decoder_width(task)
+        self.device = device if device is not None else hip.Device(0)
+
+        @hip.LOOKUP
+        def lookup(_user, name, data, length):
+            arr = self.weights.get(name.decode())
+            if arr is None:
+                return 1
+            data[0] = arr.ctypes.data_as(hip._CF)
+            length[0] = arr.size
+            return 0
+
+        handle = ctypes.c_void_p()
+        t = hip.TASK_CLASSIFIER if task == mf.CLASSIFIER else hip.TASK_REGRESSOR
+        hip.check(hip.lib().irx_weights_upload(self.device.handle, t, lookup, None, ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h:
+            hip.lib().irx_weights_release(h)
+            self.handle = None
+
+    def tensor(self, name: str) -> np.ndarray:
+        return self.weights[name]
+
+    def budget(self, device_limit: int = 0) -> int:
+        n = ctypes.c_size_t()
+        hip.check(hip.lib().irx_weights_budget(self.handle, device_limit, ctypes.byref(n)))
+        return n.value
+
+    # ---- host preparations the build and predictor take (cpu.rs:573-599, 763-771) ----
+
+    def target_embeddings(self, prefix: str, y: np.ndarray, width: int) -> np.ndarray:
+        """[N, width] label embeddings (target_embeddings, cpu.rs:1658-1680)."""
+        w = self.tensor(f"{prefix}.y_encoder.weight")
+        b = self.tensor(f"{prefix}.y_encoder.bias")
+        if self.task == mf.CLASSIFIER:
+            return _f32(w[:, y.astype(np.int64)].T + b[None, :])
+        return _f32(y[:, None].astype(np.float32) * w[:, 0][None, :] + b[None, :])
+
+    def label_embeddings(self, y: np.ndarray):
+        """Column-stage [B, N, 128] and ICL-stage [B, N, 512] label embeddings."""
+        col = np.stack([self.target_embeddings("col_embedder", ye, 128) for ye in y])
+        icl = np.stack([self.target_embeddings("icl_predictor", ye, 512) for ye in y])
+        return _f32(col), _f32(icl)
+
+    def qass_base_scale(self, prefix: str, source: int) -> np.ndarray:
+        """base = W2 gelu(w1 ln(max(source,1)) + b1) + b2 (qass_base_scale, cpu.rs:3768-3791)."""
+        n = lambda part: self.tensor(f"{prefix}.ssmax_layer.{part}")
+        log_source = math.log(max(source, 1))
+        hidden = _gelu64(n("base_mlp.0.weight")[:, 0].astype(np.float64) * log_source + n("base_mlp.0.bias"))
+        return _f32(n("base_mlp.2.weight").astype(np.float64) @ hidden + n("base_mlp.2.bias"))
+
+    def icl_base_scales(self, n: int) -> list[np.ndarray]:
+        return [self.qass_base_scale(f"icl_predictor.tf_icl.blocks.{b}.attn", n) for b in range(12)]
+
+    def inducing_queries(self, n: int) -> list[np.ndarray]:
+        """Each column block's inducing points as multihead_attn1 queries: norm1,
+        the query projection and QASSMax for n sources, tokens [128, 128]
+        (query_heads, cpu.rs:1421-1467; qassmax_f32, reference.rs:335-430)."""
+        out = []
+        for blk in range(3):
+            p = f"col_embedder.tf_col.blocks.{blk}"
+            a = f"{p}.multihead_attn1"
+            ind = self.tensor(f"{p}.ind_vectors")
+            norm = _layer_norm64(ind, self.tensor(f"{a}.norm1.weight"), self.weights.get(f"{a}.norm1.bias"))
+            w = self.tensor(f"{a}.attn.in_proj_weight")[:128].astype(np.float64)
+            bq = self.tensor(f"{a}.attn.in_proj_bias")[:128]
+            q = norm @ w.T + bq                       # [128 rows, 128]
+            qh = q.reshape(128, 8, 16)                # row, head, d
+            s = lambda part: self.tensor(f"{a}.attn.ssmax_layer.{part}").astype(np.float64)
+            base = self.qass_base_scale(f"{a}.attn", n).astype(np.float64).reshape(8, 16)
+            hidden = _gelu64(qh @ s("query_mlp.0.weight").T + s("query_mlp.0.bias"))
+            gate = hidden @ s("query_mlp.2.weight").T + s("query_mlp.2.bias")
+            gated = qh * base[None, :, :] * (1.0 + np.tanh(gate))
+            out.append(_f32(gated.reshape(128, 128)))
+        return out
+
+    def rope_frequencies(self) -> np.ndarray:
+        return self.tensor("row_interactor.tf_row.rope.freqs")
+
+    def cls_tokens(self) -> np.ndarray:
+        return self.tensor("row_interactor.cls_tokens")
+
+    # ---- build (build_context / build_tensors_cuda, cpu.rs:627-804) ----
+
+    def build_context(self, x: np.ndarray, y_train: np.ndarray, class_permutations=None,
+                      feature_permutations=None, download: bool = False, progress=None,
+                      device_limit: int = 0) -> "StaticExecutor":
+        """Build the static context of x [B, N, H], y_train [B, N] on the GPU and
+        keep it resident. With ``download``, also copy every cache tensor to the
+        host (``StaticExecutor.context``)."""
+        x = _f32(x)
+        y_train = _f32(y_train)
+        if x.ndim != 3 or y_train.shape != x.shape[:2] or min(x.shape) == 0:
+            raise ValueError("context needs nonempty x[B, N, H] and y_train[B, N]")
+        b, n, h = x.shape
+        classes = validate_labels(y_train, b, n) if self.task == mf.CLASSIFIER else 0
+        if self.task == mf.REGRESSOR and not np.all(np.isfinite(y_train)):
+            raise ValueError("regression targets must be finite")
+        col_labels, icl_labels = self.label_embeddings(y_train)
+        ind_q = self.inducing_queries(n)
+        bases = self.icl_base_scales(n)
+        freqs, cls = self.rope_frequencies(), self.cls_tokens()
+        inp = hip.BuildInputs()
+        inp.shape = hip.Shape(b, h, n, self.width)
+        inp.x, inp.column_labels, inp.icl_labels = hip.fptr(x), hip.fptr(col_labels), hip.fptr(icl_labels)
+        for i in range(3):
+            inp.inducing_queries[i] = hip.fptr(ind_q[i])
+        for i in range(12):
+            inp.base_scales[i] = hip.fptr(bases[i])
+        inp.rope_frequencies, inp.cls_tokens = hip.fptr(freqs), hip.fptr(cls)
+        inp.budget = self.budget(device_limit)
+        cb = _progress(progress)
+        inp.progress = cb
+        out = hip.BuildOutputs()
+        context = None
+        if download:
+            ck = [np.zeros((b, h + 4, 8, 128, 16), np.float32) for _ in range(3)]
+            cv = [np.zeros_like(ck[0]) for _ in range(3)]
+            ik = [np.zeros((b, 8, n, 64), np.float32) for _ in range(12)]
+            iv = [np.zeros_like(ik[0]) for _ in range(12)]
+            for i in range(3):
+                out.column_keys[i], out.column_values[i] = hip.fptr(ck[i]), hip.fptr(cv[i])
+            for i in range(12):
+                out.icl_keys[i], out.icl_values[i] = hip.fptr(ik[i]), hip.fptr(iv[i])
+            context = (ck, cv, ik, iv)
+        keep = ctypes.c_void_p()
+        hip.check(hip.lib().irx_build(self.handle, hip.PRECISION_FP32, ctypes.byref(inp), ctypes.byref(out),
+                                      ctypes.byref(keep)))
+        return StaticExecutor(self, (b, n, h), classes, class_permutations, feature_permutations,
+                              built=keep.value, context=context, base_scales=bases)
+
+    def load_context(self, context, shape, classes: int, class_permutations=None,
+                     feature_permutations=None) -> "StaticExecutor":
+        """Upload host context tensors (column K/V [B,H+4,8,128,16] x 3 each, ICL
+        K/V [B,8,N,64] x 12 each) for prediction (Executor::load_context, cpu.rs:397-406)."""
+        b, n, h = shape
+        return StaticExecutor(self, (b, n, h), classes, class_permutations, feature_permutations,
+                              built=None, context=context, base_scales=self.icl_base_scales(n))
+
+
+def _progress(fn):
+    if fn is None:
+        return hip.PROGRESS()
+
+    @hip.PROGRESS
+    def cb(_user, stage, done, total):
+        try:
+            fn(stage, done, total)
+            return 0
+        except Exception:
+            return 1
+
+    return cb
+
+
+class StaticExecutor:
+    """A context resident on the GPU and its predictor (StaticExecutor, cpu.rs:313-326;
+    Predictor, cuda/predictor.rs:93-271)."""
+
+    def __init__(self, executor: Executor, shape, classes: int, class_permutations, feature_permutations,
+                 built, context, base_scales):
+        self.executor = executor
+        self.shape = shape
+        self.classes = classes
+        b = shape[0]
+        self.class_permutations = (np.asarray(class_permutations, dtype=np.uint64).reshape(b, -1)
+                                   if class_permutations is not None
+                                   else (np.tile(np.arange(classes, dtype=np.uint64), (b, 1)) if classes else None))
+        self.feature_permutations = feature_permutations
+        self.context = context
+        b, n, h = shape
+        ctx = hip.ContextTensors()
+        ctx.shape = hip.Shape(b, h, n, executor.width)
+        self._bases = [_f32(s) for s in base_scales]
+        for i in range(12):
+            ctx.base_scales[i] = hip.fptr(self._bases[i])
+        ctx.rope_frequencies = hip.fptr(executor.rope_frequencies())
+        ctx.cls_tokens = hip.fptr(executor.cls_tokens())
+        ctx.budget = executor.budget()
+        keep_alive = []
+        if built is None:
+            ck, cv, ik, iv = [[_f32(t) for t in part] for part in context]
+            keep_alive = [ck, cv, ik, iv]
+            for i in range(3):
+                ctx.column_keys[i], ctx.column_values[i] = hip.fptr(ck[i]), hip.fptr(cv[i])
+
+            @hip.ICL_SOURCE
+            def source(_user, block, keys, values):
+                if block >= 12:
+                    return 1
+                keys[0] = ik[block].ctypes.data_as(hip._CF)
+                values[0] = iv[block].ctypes.data_as(hip._CF)
+                return 0
+
+            ctx.icl = source
+            keep_alive.append(source)
+        handle = ctypes.c_void_p()
+        hip.check(hip.lib().irx_predictor_new(executor.handle, hip.PRECISION_FP32, ctypes.byref(ctx), built,
+                                              ctypes.byref(handle)))
+        self.handle = handle.value
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h:
+            hip.lib().irx_predictor_free(h)
+            self.handle = None
+
+    def device(self) -> str:
+        return "rocm"
+
+    def streamed(self) -> bool:
+        return bool(hip.lib().irx_predictor_streamed(self.handle))
+
+    def pass_rows(self) -> int:
+        return int(hip.lib().irx_predictor_pass_rows(self.handle))
+
+    def set_pass_rows(self, rows: int) -> None:
+        hip.check(hip.lib().irx_predictor_set_pass_rows(self.handle, rows))
+
+    def outputs(self) -> int:
+        return self.classes if self.classes else self.executor.width
+
+    def predict_raw(self, x: np.ndarray, progress=None) -> Prediction:
+        """Every decoder output [B, Q, width] (Predictor::predict, predictor.rs:224-271)."""
+        x = _f32(x)
+        b, n, h = self.shape
+        if x.ndim != 3 or x.shape[0] != b or x.shape[2] != h:
+            raise ValueError(f"query shape {x.shape} does not match static context B={b} and H={h}")
+        q = x.shape[1]
+        logits = np.zeros((b, q, self.executor.width), np.float32)
+        flags = np.zeros(q, np.uint8)
+        if q:
+            hip.check(hip.lib().irx_predictor_predict(
+                self.handle, hip.fptr(x), q, hip.fptr(logits),
+                flags.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), _progress(progress), None))
+        cpu_rows = [int(r) for r in np.nonzero(flags)[0]]
+        if cpu_rows:
+            logits[:, cpu_rows, :] = np.nan
+        return Prediction(logits, cpu_rows)
+
+    def predict_logits(self, x: np.ndarray) -> Prediction:
+        """[B, Q, C] logits, C = classes (or all 999 quantiles) (cpu.rs:2057-2108)."""
+        p = self.predict_raw(x)
+        return Prediction(np.ascontiguousarray(p.logits[:, :, : self.outputs()]), p.cpu_rows)
+
+    def predict_probabilities(self, x: np.ndarray, temperature: float = 0.9, average_logits: bool = True):
+        """Aggregated class probabilities [Q, C] (cpu.rs:2338-2348, 3873-3932)."""
+        if not self.classes:
+            raise ValueError("the context is a regression fit")
+        return aggregate_classifier_probabilities(self.predict_logits(x).logits, self.class_permutations,
+                                                  temperature, average_logits)
+
+    def predict_regression(self, x: np.ndarray, alphas=(0.05, 0.5, 0.95)):
+        """(mean [Q], quantiles [Q, len(alphas)]) in standardized target units,
+        over 1024-row chunks (cpu.rs:2305-2329; quantiles.rs:80-213)."""
+        if self.classes:
+            raise ValueError("the context is a classification fit")
+        logits = self.predict_logits(x).logits
+        return summarize_quantiles(logits, alphas)
+
+
+def aggregate_classifier_probabilities(logits: np.ndarray, perms: np.ndarray, temperature: float = 0.9,
+                                       average_logits: bool = True) -> np.ndarray:
+    """member[c] = logits[perm[e][c]]; mean over estimators; softmax(x / T);
+    renormalize (aggregate_classifier_probabilities, cpu.rs:3873-3932)."""
+    if not np.isfinite(temperature) or temperature <= 0:
+        raise ValueError("softmax temperature must be positive and finite")
+    b, q, c = logits.shape
+    scale = np.float32(1.0) / np.float32(b)
+
+    def softmax(v):
+        z = v / np.float32(temperature)
+        z = np.exp(z - z.max(axis=-1, keepdims=True))
+        return z / z.sum(axis=-1, keepdims=True)
+
+    total = np.zeros((q, c), np.float32)
+    for e in range(b):
+        member = logits[e][:, perms[e].astype(np.int64)]
+        if not average_logits:
+            member = softmax(member)
+        total += member * scale
+    if average_logits:
+        total = softmax(total)
+    return (total / total.sum(axis=-1, keepdims=True)).astype(np.float32)
+
+
+def summarize_quantiles(logits: np.ndarray, alphas) -> tuple[np.ndarray, np.ndarray]:
+    """Mean and icdf at alphas of [B, Q, K] decoded quantiles, averaged over B
+    (quantiles::summarize, quantiles.rs:80-213)."""
+    b, q, k = logits.shape
+    tol = 1e-6
+    levels = (np.arange(1, k + 1, dtype=np.float64) / (k + 1)).astype(np.float32).astype(np.float64)
+    tk = max(1, min(20, k // 4))
+    xl = np.log(np.maximum(levels[:tk], tol))
+    xr = np.log(np.maximum(1.0 - levels[k - tk:], tol))
+
+    def slope(qv, x):
+        xm, qm = x.mean(), qv.mean(axis=-1, keepdims=True)
+        cov = ((qv - qm) * (x - xm)).mean(axis=-1)
+        var = ((x - xm) ** 2).mean()
+        return cov / max(var, tol)
+
+    alphas = np.asarray(alphas, dtype=np.float32).astype(np.float64)
+    mean = np.zeros(q)
+    quant = np.zeros((q, len(alphas)))
+    for e in range(b):
+        s = np.sort(logits[e].astype(np.float32), axis=-1).astype(np.float64)
+        mean += s.mean(axis=-1)
+        bl = np.clip(np.abs(slope(s[:, :tk], xl)), 0.01, 100.0)
+        br = np.clip(np.abs(-slope(s[:, k - tk:], xr)), 0.01, 100.0)
+        al, ar = levels[0], levels[-1]
+        for j, a in enumerate(alphas):
+            if a < al:
+                v = s[:, 0] + bl * (np.log(max(a, tol)) - np.log(max(al, tol)))
+            elif a > ar:
+                omr = 1.0 - min(ar, 1.0 - tol)
+                v = s[:, -1] - br * (np.log(max(1.0 - a, tol)) - np.log(omr))
+            elif a >= ar:
+                v = s[:, -1]
+            else:
+                seg = max(int(np.searchsorted(levels[:-1], a, side="right")) - 1, 0)
+                lo, hi = levels[seg], levels[seg + 1]
+                t = min(max((a - lo) / max(hi - lo, tol), 0.0), 1.0)
+                v = s[:, seg] + t * (s[:, seg + 1] - s[:, seg])
+            quant[:, j] += v
+    return (mean / b).astype(np.float32), (quant / b).astype(np.float32)

@@ -1,0 +1,1133 @@
+/*
+ * CPU restatement of Ironicl's FP32 TabICLv2 forward pass: the oracle.
+ *
+ * TEST INFRASTRUCTURE ONLY (see tabicl_oracle.h): the checker of the HIP
+ * backend and the CPU baseline bench.py times beside it. Never part of the
+ * product path.
+ *
+ * Each function cites the reference file:line it restates.
+ */
+#include "tabicl_oracle.h"
+
+#include <math.h>
+#include <omp.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define D 128      /* column / row embedding width, cpu.rs:40 */
+#define E 512      /* ICL width, cpu.rs:41 */
+#define HEADS 8    /* cpu.rs:42 */
+#define M 128      /* inducing points, cpu.rs:43 */
+#define COLB 3     /* column blocks, cpu.rs:44 */
+#define ICLB 12    /* ICL blocks, cpu.rs:45 */
+#define RES 4      /* CLS streams, cpu.rs:47 */
+#define KEY_TILE 128 /* ATTENTION_KEY_TILE_ROWS, cpu.rs:49 */
+#define CHUNK 1024 /* QUERY_CHUNK_ROWS, cpu.rs:54 */
+#define LN_EPS 1e-5f /* reference.rs:14 */
+
+static int g_threads = 1;
+
+void ora_set_threads(int threads) { g_threads = threads > 0 ? threads : 1; }
+int ora_get_threads(void) { return g_threads; }
+
+static void set_err(char *err, size_t errlen, const char *fmt, ...) {
+    if (!err || !errlen) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+}
+
+static void *xcalloc(size_t count, size_t size) {
+    void *p = calloc(count ? count : 1, size);
+    if (!p) {
+        fprintf(stderr, "oracle: out of memory (%zu x %zu)\n", count, size);
+        abort();
+    }
+    return p;
+}
+
+/* ------------------------------------------------------------------ */
+/* Elementwise math                                                    */
+/* ------------------------------------------------------------------ */
+
+/* bounded_exp: src/kernels/cpu/ops/pointwise.rs:49-74. */
+float ora_bounded_exp(float value) {
+    float v = value < -40.0f ? -40.0f : (value > 20.0f ? 20.0f : value);
+    int exponent = (int)rintf(v * 1.44269504088896340736f);
+    float r = fmaf((float)(-exponent), 0.693147180559945309417f, v);
+    float p = fmaf(r, 1.0f / 5040.0f, 1.0f / 720.0f);
+    p = fmaf(r, p, 1.0f / 120.0f);
+    p = fmaf(r, p, 1.0f / 24.0f);
+    p = fmaf(r, p, 1.0f / 6.0f);
+    p = fmaf(r, p, 0.5f);
+    p = fmaf(r, p, 1.0f);
+    p = fmaf(r, p, 1.0f);
+    union { unsigned u; float f; } pw;
+    pw.u = (unsigned)(exponent + 127) << 23;
+    return p * pw.f;
+}
+
+/* fast_exp_negative / softmax_exp_sum_avx512: src/kernels/cpu/arch/x86_64.rs:40-51,610-660. */
+float ora_fast_exp_negative(float value) {
+    float v = value < -87.0f ? -87.0f : value;
+    int exponent = (int)rintf(v * 1.44269504088896340736f);
+    float r = v - (float)exponent * 0.693147180559945309417f;
+    float p = 1.0f / 5040.0f;
+    const float c[7] = {1.0f / 720.0f, 1.0f / 120.0f, 1.0f / 24.0f, 1.0f / 6.0f, 0.5f, 1.0f, 1.0f};
+    for (int i = 0; i < 7; ++i) p = fmaf(p, r, c[i]);
+    union { unsigned u; float f; } pw;
+    pw.u = (unsigned)(exponent + 127) << 23;
+    return p * pw.f;
+}
+
+/* fast_erf: pointwise.rs:76-91 (Abramowitz-Stegun 7.1.26). */
+static float fast_erf(float value) {
+    float mag = fabsf(value);
+    float sgn = value < 0.0f ? -1.0f : 1.0f;
+    if (mag >= 6.0f) return sgn;
+    if (mag < 1e-4f) return value * 1.12837916709551257390f;
+    float t = 1.0f / fmaf(0.3275911f, mag, 1.0f);
+    float p = fmaf(1.0614054f, t, -1.4531521f);
+    p = fmaf(p, t, 1.4214138f);
+    p = fmaf(p, t, -0.28449672f);
+    p = fmaf(p, t, 0.2548296f) * t;
+    return sgn * (1.0f - p * ora_bounded_exp(-mag * mag));
+}
+
+/* gelu (reference.rs:52-54) and fast_gelu (pointwise.rs:93-96). */
+static inline float gelu_exact(float x) { return 0.5f * x * (1.0f + erff(x / 1.41421356237309504880f)); }
+static inline float gelu_native(float x) { return 0.5f * x * (1.0f + fast_erf(x / 1.41421356237309504880f)); }
+
+void ora_gelu(int math, const float *input, size_t len, float *output) {
+    if (math == ORA_MATH_NATIVE)
+        for (size_t i = 0; i < len; ++i) output[i] = gelu_native(input[i]);
+    else
+        for (size_t i = 0; i < len; ++i) output[i] = gelu_exact(input[i]);
+}
+
+static inline float softmax_exp(int math, float x) {
+    return math == ORA_MATH_NATIVE ? ora_fast_exp_negative(x) : expf(x);
+}
+
+/* ------------------------------------------------------------------ */
+/* Dense kernels                                                       */
+/* ------------------------------------------------------------------ */
+
+/* 16-lane partial sums, the way the AVX-512 kernels reduce; any summation
+ * order is within the parity tolerance. */
+static inline float dot16(const float *a, const float *b, size_t n) {
+    float acc[16] = {0};
+    size_t k = 0;
+    for (; k + 16 <= n; k += 16)
+        for (int l = 0; l < 16; ++l) acc[l] = fmaf(a[k + l], b[k + l], acc[l]);
+    float tail = 0.0f;
+    for (; k < n; ++k) tail = fmaf(a[k], b[k], tail);
+    for (int w = 8; w >= 1; w >>= 1)
+        for (int l = 0; l < w; ++l) acc[l] += acc[l + w];
+    return acc[0] + tail;
+}
+
+/* affine_f32: reference.rs:83-120. weight [out,in] (PyTorch layout). */
+void ora_affine(const float *input, size_t rows, size_t in_dim, const float *weight,
+                const float *bias, size_t out_dim, float *output) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *x = input + r * in_dim;
+        float *y = output + r * out_dim;
+        for (size_t o = 0; o < out_dim; ++o)
+            y[o] = (bias ? bias[o] : 0.0f) + dot16(weight + o * in_dim, x, in_dim);
+    }
+}
+
+/* parallel_affine: rows split over workers (cpu.rs:3014-3048). */
+static void affine_par(int workers, const float *input, size_t rows, size_t in_dim,
+                       const float *weight, const float *bias, size_t out_dim, float *output) {
+    if (workers <= 1 || rows < 16) {
+        ora_affine(input, rows, in_dim, weight, bias, out_dim, output);
+        return;
+    }
+    size_t per = (rows + (size_t)workers - 1) / (size_t)workers;
+#pragma omp parallel for num_threads(workers) schedule(static, 1)
+    for (int w = 0; w < workers; ++w) {
+        size_t start = (size_t)w * per;
+        if (start >= rows) continue;
+        size_t len = rows - start < per ? rows - start : per;
+        ora_affine(input + start * in_dim, len, in_dim, weight, bias, out_dim, output + start * out_dim);
+    }
+}
+
+/* layer_norm_f32: reference.rs:223-252 / layer_norm_avx512 x86_64.rs:1470-1520. */
+void ora_layer_norm(const float *input, size_t rows, size_t width, const float *weight,
+                    const float *bias, float *output) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *x = input + r * width;
+        float *y = output + r * width;
+        /* Lanes of 16 as the AVX-512 kernel sums, then the tail of a width
+         * that is not a multiple of 16 (the scalar path's order). */
+        size_t body = width / 16 * 16;
+        float acc[16] = {0};
+        for (size_t c = 0; c < body; c += 16)
+            for (int l = 0; l < 16; ++l) acc[l] += x[c + l];
+        for (int w = 8; w >= 1; w >>= 1)
+            for (int l = 0; l < w; ++l) acc[l] += acc[l + w];
+        for (size_t c = body; c < width; ++c) acc[0] += x[c];
+        float mean = acc[0] / (float)width;
+        float sq[16] = {0};
+        for (size_t c = 0; c < body; c += 16)
+            for (int l = 0; l < 16; ++l) {
+                float d = x[c + l] - mean;
+                sq[l] = fmaf(d, d, sq[l]);
+            }
+        for (int w = 8; w >= 1; w >>= 1)
+            for (int l = 0; l < w; ++l) sq[l] += sq[l + w];
+        for (size_t c = body; c < width; ++c) sq[0] = fmaf(x[c] - mean, x[c] - mean, sq[0]);
+        float scale = 1.0f / sqrtf(sq[0] / (float)width + LN_EPS);
+        for (size_t c = 0; c < width; ++c)
+            y[c] = (x[c] - mean) * scale * weight[c] + (bias ? bias[c] : 0.0f);
+    }
+}
+
+/* one_hot_linear_f32: reference.rs:190-220. Labels are class indices stored as f32. */
+void ora_one_hot_linear(const float *labels, size_t rows, const float *weight, const float *bias,
+                        size_t classes, size_t out_dim, float *output) {
+    for (size_t r = 0; r < rows; ++r) {
+        size_t c = (size_t)labels[r];
+        for (size_t o = 0; o < out_dim; ++o) output[r * out_dim + o] = weight[o * classes + c] + bias[o];
+    }
+}
+
+/* rope_non_interleaved_f32: reference.rs:433-475. */
+void ora_rope(const float *input, size_t heads, size_t rows, size_t head_dim, const float *freqs,
+              size_t position_offset, float *output) {
+    size_t half = head_dim / 2;
+    for (size_t row = 0; row < rows; ++row) {
+        float position = (float)(position_offset + row);
+        for (size_t d = 0; d < half; ++d) {
+            float angle = position * freqs[d];
+            float s = sinf(angle), c = cosf(angle);
+            for (size_t h = 0; h < heads; ++h) {
+                size_t off = (h * rows + row) * head_dim;
+                float left = input[off + d], right = input[off + half + d];
+                output[off + d] = left * c - right * s;
+                output[off + half + d] = right * c + left * s;
+            }
+        }
+    }
+}
+
+/* tokens_to_heads / heads_to_tokens: cpu.rs:5007-5019, 5123-5135. */
+static void tokens_to_heads(const float *in, size_t rows, size_t dim, float *out) {
+    size_t hd = dim / HEADS;
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t h = 0; h < HEADS; ++h) memcpy(out + (h * rows + r) * hd, in + r * dim + h * hd, hd * 4);
+}
+static void heads_to_tokens(const float *in, size_t rows, size_t dim, float *out) {
+    size_t hd = dim / HEADS;
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t h = 0; h < HEADS; ++h) memcpy(out + r * dim + h * hd, in + (h * rows + r) * hd, hd * 4);
+}
+
+/* ------------------------------------------------------------------ */
+/* Attention                                                           */
+/* ------------------------------------------------------------------ */
+
+/* Source-major online attention for `heads` heads: reference.rs:792-1024.
+ * Per key tile of 128, every query row updates its running maximum and
+ * denominator, rescaling its partial output by exp(old - new). */
+static int attention_heads(int math, const float *query, size_t query_rows, const float *key,
+                           const float *value, size_t source_rows, size_t heads, size_t head_dim,
+                           float *output) {
+    float scale = 1.0f / sqrtf((float)head_dim);
+    float *scores = xcalloc(KEY_TILE, sizeof(float));
+    float *maximum = xcalloc(query_rows, sizeof(float));
+    float *denominator = xcalloc(query_rows, sizeof(float));
+    int status = 0;
+    for (size_t h = 0; h < heads && !status; ++h) {
+        const float *qh = query + h * query_rows * head_dim;
+        const float *kh = key + h * source_rows * head_dim;
+        const float *vh = value + h * source_rows * head_dim;
+        float *oh = output + h * query_rows * head_dim;
+        for (size_t r = 0; r < query_rows; ++r) maximum[r] = -INFINITY, denominator[r] = 0.0f;
+        memset(oh, 0, query_rows * head_dim * sizeof(float));
+        for (size_t s0 = 0; s0 < source_rows; s0 += KEY_TILE) {
+            size_t ns = source_rows - s0 < KEY_TILE ? source_rows - s0 : KEY_TILE;
+            for (size_t r = 0; r < query_rows; ++r) {
+                const float *q = qh + r * head_dim;
+                float tile_max = -INFINITY;
+                for (size_t s = 0; s < ns; ++s) {
+                    scores[s] = dot16(q, kh + (s0 + s) * head_dim, head_dim) * scale;
+                    if (scores[s] != scores[s]) { status = -1; break; }
+                    if (scores[s] > tile_max) tile_max = scores[s];
+                }
+                if (status) break;
+                float mx = maximum[r] > tile_max ? maximum[r] : tile_max;
+                if (isinf(mx) && mx > 0) { status = -1; break; }
+                if (mx == -INFINITY) continue;
+                float *o = oh + r * head_dim;
+                if (denominator[r] != 0.0f) {
+                    float old = expf(maximum[r] - mx);
+                    for (size_t d = 0; d < head_dim; ++d) o[d] *= old;
+                    denominator[r] *= old;
+                }
+                float sum = 0.0f;
+                for (size_t s = 0; s < ns; ++s) {
+                    scores[s] = softmax_exp(math, scores[s] - mx);
+                    sum += scores[s];
+                }
+                denominator[r] += sum;
+                maximum[r] = mx;
+                for (size_t s = 0; s < ns; ++s) {
+                    const float *v = vh + (s0 + s) * head_dim;
+                    float w = scores[s];
+                    for (size_t d = 0; d < head_dim; ++d) o[d] = fmaf(w, v[d], o[d]);
+                }
+            }
+            if (status) break;
+        }
+        for (size_t r = 0; r < query_rows && !status; ++r) {
+            float den = denominator[r];
+            if (!isfinite(den) || den == 0.0f) { status = -1; break; }
+            for (size_t d = 0; d < head_dim; ++d) oh[r * head_dim + d] /= den;
+        }
+    }
+    free(scores);
+    free(maximum);
+    free(denominator);
+    return status;
+}
+
+int ora_attention(int math, const float *query, size_t query_rows, const float *key,
+                  const float *value, size_t source_rows, size_t heads, size_t head_dim,
+                  float *output) {
+    if (!query_rows || !source_rows || !heads || !head_dim) return -1;
+    return attention_heads(math, query, query_rows, key, value, source_rows, heads, head_dim, output);
+}
+
+/* Head-parallel cached attention: parallel_cached_attention, cpu.rs:4439-4525. */
+static int attention_par(int math, int workers, const float *query, size_t query_rows,
+                         const float *key, const float *value, size_t source_rows, size_t head_dim,
+                         float *output) {
+    int w = workers < HEADS ? workers : HEADS;
+    if (w <= 1)
+        return attention_heads(math, query, query_rows, key, value, source_rows, HEADS, head_dim, output);
+    int per = (HEADS + w - 1) / w;
+    int status = 0;
+#pragma omp parallel for num_threads(w) schedule(static, 1) reduction(| : status)
+    for (int t = 0; t < w; ++t) {
+        int start = t * per;
+        if (start >= HEADS) continue;
+        int nh = HEADS - start < per ? HEADS - start : per;
+        size_t qe = query_rows * head_dim, se = source_rows * head_dim;
+        status |= attention_heads(math, query + start * qe, query_rows, key + start * se,
+                                  value + start * se, source_rows, (size_t)nh, head_dim,
+                                  output + start * qe) != 0;
+    }
+    return status ? -1 : 0;
+}
+
+/* scaled_dot_product_attention_f32: reference.rs:482-540, and softmax_f32. */
+int ora_attention_materialized(const float *query, size_t query_rows, const float *key,
+                               const float *value, size_t source_rows, size_t heads,
+                               size_t head_dim, float *output) {
+    float scale = 1.0f / sqrtf((float)head_dim);
+    float *scores = xcalloc(source_rows, sizeof(float));
+    for (size_t h = 0; h < heads; ++h)
+        for (size_t r = 0; r < query_rows; ++r) {
+            const float *q = query + (h * query_rows + r) * head_dim;
+            float mx = -INFINITY;
+            for (size_t s = 0; s < source_rows; ++s) {
+                float acc = 0.0f;
+                for (size_t d = 0; d < head_dim; ++d) acc = fmaf(q[d], key[(h * source_rows + s) * head_dim + d], acc);
+                scores[s] = acc * scale;
+                if (scores[s] > mx) mx = scores[s];
+            }
+            float sum = 0.0f;
+            for (size_t s = 0; s < source_rows; ++s) sum += (scores[s] = expf(scores[s] - mx));
+            for (size_t s = 0; s < source_rows; ++s) scores[s] /= sum;
+            float *o = output + (h * query_rows + r) * head_dim;
+            for (size_t d = 0; d < head_dim; ++d) o[d] = 0.0f;
+            for (size_t s = 0; s < source_rows; ++s)
+                for (size_t d = 0; d < head_dim; ++d)
+                    o[d] = fmaf(scores[s], value[(h * source_rows + s) * head_dim + d], o[d]);
+        }
+    free(scores);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Model weights                                                       */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    size_t dim;
+    const float *n1w, *n1b, *n2w, *n2b;
+    const float *in_w, *in_b, *out_w, *out_b;
+    const float *l1w, *l1b, *l2w, *l2b;
+    int qass;
+    const float *bm0w, *bm0b, *bm2w, *bm2b, *qm0w, *qm0b, *qm2w, *qm2b;
+} blk_t;
+
+struct ora_model {
+    int task, math;
+    size_t width, targets;
+    const float *in_w, *in_b, *col_yw, *col_yb;
+    const float *ind[COLB];
+    blk_t col1[COLB], col2[COLB], row[3], icl[ICLB];
+    const float *cls, *out_ln_w, *out_ln_b, *freqs;
+    const float *icl_yw, *icl_yb, *ln_w, *ln_b, *dec0_w, *dec0_b, *dec2_w, *dec2_b;
+    float *arena;
+    size_t arena_used, arena_cap;
+};
+
+typedef struct {
+    ora_model *m;
+    ora_lookup lookup;
+    void *user;
+    char *err;
+    size_t errlen;
+    int failed;
+} loader_t;
+
+static const float *take(loader_t *L, const char *name, size_t expected, int zero_if_missing) {
+    if (L->failed) return NULL;
+    const float *data = NULL;
+    size_t len = 0;
+    int missing = L->lookup(L->user, name, &data, &len);
+    if (missing) {
+        if (!zero_if_missing) {
+            set_err(L->err, L->errlen, "model tensor '%s' is missing", name);
+            L->failed = 1;
+            return NULL;
+        }
+        data = NULL;
+        len = expected;
+    }
+    if (len != expected) {
+        set_err(L->err, L->errlen, "model tensor '%s' has %zu values; expected %zu", name, len, expected);
+        L->failed = 1;
+        return NULL;
+    }
+    ora_model *m = L->m;
+    if (m->arena_used + expected > m->arena_cap) {
+        set_err(L->err, L->errlen, "oracle weight arena overflow at '%s'", name);
+        L->failed = 1;
+        return NULL;
+    }
+    float *dst = m->arena + m->arena_used;
+    if (data) memcpy(dst, data, expected * sizeof(float));
+    else memset(dst, 0, expected * sizeof(float));
+    m->arena_used += expected;
+    return dst;
+}
+
+static void load_block(loader_t *L, blk_t *b, const char *prefix, size_t dim, int qass) {
+    char name[256];
+    int zero_bias = L->m->task == ORA_REGRESSOR; /* model.rs:273-280 */
+    b->dim = dim;
+    b->qass = qass;
+#define T(field, suffix, len, z) (snprintf(name, sizeof name, "%s%s", prefix, suffix), b->field = take(L, name, len, z))
+    T(in_w, ".attn.in_proj_weight", 3 * dim * dim, 0);
+    T(in_b, ".attn.in_proj_bias", 3 * dim, 0);
+    T(out_w, ".attn.out_proj.weight", dim * dim, 0);
+    T(out_b, ".attn.out_proj.bias", dim, 0);
+    T(l1w, ".linear1.weight", 2 * dim * dim, 0);
+    T(l1b, ".linear1.bias", 2 * dim, 0);
+    T(l2w, ".linear2.weight", 2 * dim * dim, 0);
+    T(l2b, ".linear2.bias", dim, 0);
+    T(n1w, ".norm1.weight", dim, 0);
+    T(n1b, ".norm1.bias", dim, zero_bias);
+    T(n2w, ".norm2.weight", dim, 0);
+    T(n2b, ".norm2.bias", dim, zero_bias);
+    if (qass) {
+        size_t hd = dim / HEADS;
+        T(bm0w, ".attn.ssmax_layer.base_mlp.0.weight", 64, 0);
+        T(bm0b, ".attn.ssmax_layer.base_mlp.0.bias", 64, 0);
+        T(bm2w, ".attn.ssmax_layer.base_mlp.2.weight", dim * 64, 0);
+        T(bm2b, ".attn.ssmax_layer.base_mlp.2.bias", dim, 0);
+        T(qm0w, ".attn.ssmax_layer.query_mlp.0.weight", 64 * hd, 0);
+        T(qm0b, ".attn.ssmax_layer.query_mlp.0.bias", 64, 0);
+        T(qm2w, ".attn.ssmax_layer.query_mlp.2.weight", hd * 64, 0);
+        T(qm2b, ".attn.ssmax_layer.query_mlp.2.bias", hd, 0);
+    }
+#undef T
+}
+
+ora_model *ora_model_new(int task, ora_lookup lookup, void *user, int math, char *err, size_t errlen) {
+    ora_model *m = xcalloc(1, sizeof *m);
+    m->task = task;
+    m->math = math;
+    m->targets = task == ORA_CLASSIFIER ? 10 : 1;
+    m->width = task == ORA_CLASSIFIER ? 10 : 999;
+    m->arena_cap = 30u * 1000u * 1000u; /* > 28.6 M parameters */
+    m->arena = xcalloc(m->arena_cap, sizeof(float));
+    loader_t L = {m, lookup, user, err, errlen, 0};
+    int zb = task == ORA_REGRESSOR;
+    char name[256];
+    m->in_w = take(&L, "col_embedder.in_linear.weight", D * 3, 0);
+    m->in_b = take(&L, "col_embedder.in_linear.bias", D, 0);
+    m->col_yw = take(&L, "col_embedder.y_encoder.weight", D * m->targets, 0);
+    m->col_yb = take(&L, "col_embedder.y_encoder.bias", D, 0);
+    for (int b = 0; b < COLB; ++b) {
+        snprintf(name, sizeof name, "col_embedder.tf_col.blocks.%d.ind_vectors", b);
+        m->ind[b] = take(&L, name, M * D, 0);
+        snprintf(name, sizeof name, "col_embedder.tf_col.blocks.%d.multihead_attn1", b);
+        load_block(&L, &m->col1[b], name, D, 1);
+        snprintf(name, sizeof name, "col_embedder.tf_col.blocks.%d.multihead_attn2", b);
+        load_block(&L, &m->col2[b], name, D, 0);
+    }
+    for (int b = 0; b < 3; ++b) {
+        snprintf(name, sizeof name, "row_interactor.tf_row.blocks.%d", b);
+        load_block(&L, &m->row[b], name, D, 0);
+    }
+    m->cls = take(&L, "row_interactor.cls_tokens", RES * D, 0);
+    m->out_ln_w = take(&L, "row_interactor.out_ln.weight", D, 0);
+    m->out_ln_b = take(&L, "row_interactor.out_ln.bias", D, zb);
+    m->freqs = take(&L, "row_interactor.tf_row.rope.freqs", 8, 0);
+    for (int b = 0; b < ICLB; ++b) {
+        snprintf(name, sizeof name, "icl_predictor.tf_icl.blocks.%d", b);
+        load_block(&L, &m->icl[b], name, E, 1);
+    }
+    m->icl_yw = take(&L, "icl_predictor.y_encoder.weight", E * m->targets, 0);
+    m->icl_yb = take(&L, "icl_predictor.y_encoder.bias", E, 0);
+    m->ln_w = take(&L, "icl_predictor.ln.weight", E, 0);
+    m->ln_b = take(&L, "icl_predictor.ln.bias", E, zb);
+    m->dec0_w = take(&L, "icl_predictor.decoder.0.weight", 1024 * E, 0);
+    m->dec0_b = take(&L, "icl_predictor.decoder.0.bias", 1024, 0);
+    m->dec2_w = take(&L, "icl_predictor.decoder.2.weight", m->width * 1024, 0);
+    m->dec2_b = take(&L, "icl_predictor.decoder.2.bias", m->width, 0);
+    if (L.failed) {
+        ora_model_free(m);
+        return NULL;
+    }
+    return m;
+}
+
+void ora_model_free(ora_model *m) {
+    if (!m) return;
+    free(m->arena);
+    free(m);
+}
+
+size_t ora_model_width(const ora_model *m) { return m->width; }
+
+/* ------------------------------------------------------------------ */
+/* QASSMax                                                             */
+/* ------------------------------------------------------------------ */
+
+/* qass_base_scale: cpu.rs:3768-3791 (exact GELU, ln(max(source,1))). */
+static void qass_base(const blk_t *b, size_t source, float *scale) {
+    float log_source = logf((float)(source > 1 ? source : 1));
+    float hidden[64];
+    for (int i = 0; i < 64; ++i) hidden[i] = gelu_exact(fmaf(b->bm0w[i], log_source, b->bm0b[i]));
+    ora_affine(hidden, 1, 64, b->bm2w, b->bm2b, b->dim, scale);
+}
+
+/* The query gate q * base * (1 + tanh(MLP_q(q))), over [heads, rows, hd]:
+ * Executor path qassmax_f32 (reference.rs:396-428, exact GELU) and
+ * StaticExecutor::qass (cpu.rs:3798-3853, GELU per the math mode). */
+static void qass_gate(const blk_t *b, int gelu_math, int workers, const float *base, float *qh,
+                      size_t rows) {
+    size_t hd = b->dim / HEADS, qr = HEADS * rows;
+    float *hidden = xcalloc(qr * 64, sizeof(float));
+    float *gate = xcalloc(qr * hd, sizeof(float));
+    affine_par(workers, qh, qr, hd, b->qm0w, b->qm0b, 64, hidden);
+    ora_gelu(gelu_math, hidden, qr * 64, hidden);
+    affine_par(workers, hidden, qr, 64, b->qm2w, b->qm2b, hd, gate);
+    for (size_t h = 0; h < HEADS; ++h)
+        for (size_t r = 0; r < rows; ++r)
+            for (size_t d = 0; d < hd; ++d) {
+                size_t i = (h * rows + r) * hd + d;
+                qh[i] = qh[i] * base[h * hd + d] * (1.0f + tanhf(gate[i]));
+            }
+    free(hidden);
+    free(gate);
+}
+
+void ora_qassmax(const float *queries, size_t heads, size_t rows, size_t head_dim,
+                 size_t source_len, size_t hidden, const float *bm0_w, const float *bm0_b,
+                 const float *bm2_w, const float *bm2_b, const float *qm0_w, const float *qm0_b,
+                 const float *qm2_w, const float *qm2_b, float *output) {
+    size_t embed = heads * head_dim, qr = heads * rows;
+    float log_source = logf((float)(source_len > 1 ? source_len : 1));
+    float *bh = xcalloc(hidden, sizeof(float));
+    float *base = xcalloc(embed, sizeof(float));
+    float *qh = xcalloc(qr * hidden, sizeof(float));
+    for (size_t i = 0; i < hidden; ++i) bh[i] = gelu_exact(fmaf(bm0_w[i], log_source, bm0_b[i]));
+    ora_affine(bh, 1, hidden, bm2_w, bm2_b, embed, base);
+    ora_affine(queries, qr, head_dim, qm0_w, qm0_b, hidden, qh);
+    for (size_t i = 0; i < qr * hidden; ++i) qh[i] = gelu_exact(qh[i]);
+    ora_affine(qh, qr, hidden, qm2_w, qm2_b, head_dim, output);
+    for (size_t h = 0; h < heads; ++h)
+        for (size_t r = 0; r < rows; ++r)
+            for (size_t d = 0; d < head_dim; ++d) {
+                size_t i = (h * rows + r) * head_dim + d;
+                output[i] = queries[i] * base[h * head_dim + d] * (1.0f + tanhf(output[i]));
+            }
+    free(bh);
+    free(base);
+    free(qh);
+}
+
+/* ------------------------------------------------------------------ */
+/* Transformer block                                                   */
+/* ------------------------------------------------------------------ */
+
+/* source_heads: cpu.rs:1356-1416. LN1 then the K and V projections, head
+ * major; RoPE on the keys for the row stage. Outputs [8, rows, hd] each. */
+static void source_heads(const ora_model *m, const blk_t *b, const float *src, size_t rows, int rope,
+                         int workers, float *kh, float *vh) {
+    size_t d = b->dim;
+    float *norm = xcalloc(rows * d, sizeof(float));
+    float *proj = xcalloc(rows * d, sizeof(float));
+    ora_layer_norm(src, rows, d, b->n1w, b->n1b, norm);
+    affine_par(workers, norm, rows, d, b->in_w + d * d, b->in_b + d, d, proj);
+    tokens_to_heads(proj, rows, d, kh);
+    if (rope) {
+        memcpy(proj, kh, rows * d * 4);
+        ora_rope(proj, HEADS, rows, d / HEADS, m->freqs, 0, kh);
+    }
+    affine_par(workers, norm, rows, d, b->in_w + 2 * d * d, b->in_b + 2 * d, d, proj);
+    tokens_to_heads(proj, rows, d, vh);
+    free(norm);
+    free(proj);
+}
+
+typedef struct {
+    const float *qass_base; /* NULL without QASS; else [dim] base scale */
+    int qass_gelu;          /* GELU math of the QASS query MLP */
+    int rope;
+    int workers;            /* affine / head workers (cached path) */
+} attend_opts;
+
+/* attend (cpu.rs:1475-1602) and cached_block (cpu.rs:2587-2850): LN1 + Q
+ * projection (+QASS, +RoPE), attention, out-projection + residual, then the
+ * residual feed-forward block. out may alias nothing; q is [q_rows, dim]. */
+static int attend(const ora_model *m, const blk_t *b, const float *q, size_t q_rows, const float *kh,
+                  const float *vh, size_t source_rows, const attend_opts *o, float *out) {
+    size_t d = b->dim, hd = d / HEADS;
+    float *t0 = xcalloc(q_rows * 2 * d, sizeof(float));
+    float *t1 = xcalloc(q_rows * 2 * d, sizeof(float));
+    int st = 0;
+    ora_layer_norm(q, q_rows, d, b->n1w, b->n1b, t0);
+    affine_par(o->workers, t0, q_rows, d, b->in_w, b->in_b, d, t1);
+    tokens_to_heads(t1, q_rows, d, t0); /* t0 = query heads */
+    if (o->qass_base) qass_gate(b, o->qass_gelu, o->workers, o->qass_base, t0, q_rows);
+    if (o->rope) {
+        memcpy(t1, t0, q_rows * d * 4);
+        ora_rope(t1, HEADS, q_rows, hd, m->freqs, 0, t0);
+    }
+    st = attention_par(m->math, o->workers, t0, q_rows, kh, vh, source_rows, hd, t1);
+    if (st) goto done;
+    heads_to_tokens(t1, q_rows, d, t0);
+    affine_par(o->workers, t0, q_rows, d, b->out_w, b->out_b, d, t1);
+    for (size_t i = 0; i < q_rows * d; ++i) out[i] = q[i] + t1[i];
+    ora_layer_norm(out, q_rows, d, b->n2w, b->n2b, t0);
+    affine_par(o->workers, t0, q_rows, d, b->l1w, b->l1b, 2 * d, t1);
+    ora_gelu(m->math, t1, q_rows * 2 * d, t1);
+    affine_par(o->workers, t1, q_rows, 2 * d, b->l2w, b->l2b, d, t0);
+    for (size_t i = 0; i < q_rows * d; ++i) out[i] += t0[i];
+done:
+    free(t0);
+    free(t1);
+    return st;
+}
+
+/* ------------------------------------------------------------------ */
+/* Stages                                                              */
+/* ------------------------------------------------------------------ */
+
+/* target_embeddings: cpu.rs:1658-1680. */
+static void target_embeddings(const ora_model *m, const float *w, const float *bias, const float *y,
+                              size_t n, size_t width, float *out) {
+    if (m->task == ORA_CLASSIFIER) {
+        ora_one_hot_linear(y, n, w, bias, 10, width, out);
+    } else {
+        for (size_t r = 0; r < n; ++r)
+            for (size_t o = 0; o < width; ++o) out[r * width + o] = y[r] * w[o] + bias[o];
+    }
+}
+
+/* Grouped features (f+1, f+2, f+4) mod H and the 3->128 input affine, with the
+ * all-missing marker: cpu.rs:1144-1157 and 2461-2473. */
+static void column_input(const ora_model *m, const float *x, size_t t, size_t h, size_t f, float *emb) {
+    static const size_t offs[3] = {1, 2, 4};
+    for (size_t r = 0; r < t; ++r) {
+        float s[3];
+        for (int p = 0; p < 3; ++p) s[p] = x[r * h + (f + offs[p]) % h];
+        float *e = emb + r * D;
+        for (size_t c = 0; c < D; ++c) {
+            float v = fmaf(m->in_w[c * 3 + 0], s[0], m->in_b[c]);
+            v = fmaf(m->in_w[c * 3 + 1], s[1], v);
+            e[c] = fmaf(m->in_w[c * 3 + 2], s[2], v);
+        }
+        if (s[0] == -100.0f && s[1] == -100.0f && s[2] == -100.0f)
+            for (size_t c = 0; c < D; ++c) e[c] = -100.0f;
+    }
+}
+
+/* Executor::column_stream + isab (cpu.rs:1132-1207): one feature over t rows,
+ * the first n of them training rows. With kv != NULL, writes the three
+ * multihead_attn2 K/V [8,128,16] (kv[2*block], kv[2*block+1]). Returns
+ * non-zero for an all-missing column that a context cannot hold. */
+static int column_stream(const ora_model *m, const float *x, const float *ycol, size_t t, size_t h,
+                         size_t n, size_t f, float *emb, float **kv) {
+    column_input(m, x, t, h, f, emb);
+    for (size_t r = 0; r < n; ++r)
+        for (size_t c = 0; c < D; ++c) emb[r * D + c] += ycol[r * D + c];
+    float *kh = xcalloc((n > M ? n : M) * D, sizeof(float));
+    float *vh = xcalloc((n > M ? n : M) * D, sizeof(float));
+    float *hidden = xcalloc(M * D, sizeof(float));
+    float *next = xcalloc(t * D, sizeof(float));
+    float base[D];
+    int st = 0;
+    for (int blk = 0; blk < COLB && !st; ++blk) {
+        int all_missing = 1;
+        for (size_t i = 0; i < t * D && all_missing; ++i) all_missing = emb[i] == -100.0f;
+        if (all_missing) { /* isab shortcut, cpu.rs:1187-1189 */
+            if (kv) st = -2;
+            continue;
+        }
+        /* multihead_attn1: inducing points attend to the n training rows, with QASS. */
+        source_heads(m, &m->col1[blk], emb, n, 0, 1, kh, vh);
+        qass_base(&m->col1[blk], n, base);
+        attend_opts o1 = {base, ORA_MATH_EXACT, 0, 1};
+        st = attend(m, &m->col1[blk], m->ind[blk], M, kh, vh, n, &o1, hidden);
+        if (st) break;
+        /* multihead_attn2: all t rows attend to the inducing state. */
+        source_heads(m, &m->col2[blk], hidden, M, 0, 1, kh, vh);
+        if (kv) {
+            memcpy(kv[2 * blk], kh, M * D * 4);
+            memcpy(kv[2 * blk + 1], vh, M * D * 4);
+        }
+        attend_opts o2 = {NULL, ORA_MATH_EXACT, 0, 1};
+        st = attend(m, &m->col2[blk], emb, t, kh, vh, M, &o2, next);
+        memcpy(emb, next, t * D * 4);
+    }
+    free(kh);
+    free(vh);
+    free(hidden);
+    free(next);
+    return st;
+}
+
+/* Executor::row_embedding (cpu.rs:1226-1266) and its StaticExecutor twin
+ * (cpu.rs:3106-3144): CLS tokens replace the reserved streams, blocks 0 and 1
+ * self-attend over L tokens with RoPE, block 2 lets the CLS tokens attend,
+ * then out_ln of the four CLS tokens is the [512] row representation. */
+static int row_embedding(const ora_model *m, const float *seq_in, size_t streams, float *out512) {
+    size_t L = streams;
+    float *seq = xcalloc(L * D, sizeof(float));
+    float *nxt = xcalloc(L * D, sizeof(float));
+    float *kh = xcalloc(L * D, sizeof(float));
+    float *vh = xcalloc(L * D, sizeof(float));
+    float cls_out[RES * D];
+    int st = 0;
+    memcpy(seq, seq_in, L * D * 4);
+    memcpy(seq, m->cls, RES * D * 4);
+    attend_opts o = {NULL, ORA_MATH_EXACT, 1, 1};
+    for (int blk = 0; blk < 2 && !st; ++blk) {
+        source_heads(m, &m->row[blk], seq, L, 1, 1, kh, vh);
+        st = attend(m, &m->row[blk], seq, L, kh, vh, L, &o, nxt);
+        memcpy(seq, nxt, L * D * 4);
+    }
+    if (!st) {
+        source_heads(m, &m->row[2], seq, L, 1, 1, kh, vh);
+        st = attend(m, &m->row[2], seq, RES, kh, vh, L, &o, cls_out);
+    }
+    if (!st) ora_layer_norm(cls_out, RES, D, m->out_ln_w, m->out_ln_b, out512);
+    free(seq);
+    free(nxt);
+    free(kh);
+    free(vh);
+    return st;
+}
+
+/* row_embeddings: rows split over workers (cpu.rs:1209-1224, 3064-3104). */
+static int row_embeddings(const ora_model *m, const float *columns, size_t t, size_t streams,
+                          int workers, float *rows) {
+    int st = 0;
+#pragma omp parallel for num_threads(workers) schedule(static) reduction(| : st)
+    for (size_t r = 0; r < t; ++r)
+        st |= row_embedding(m, columns + r * streams * D, streams, rows + r * E) != 0;
+    return st ? -1 : 0;
+}
+
+/* Decoder: cpu.rs:1297-1333 and 2543-2580. */
+static void decoder(const ora_model *m, const float *rows, size_t t, int workers, float *logits) {
+    float *norm = xcalloc(t * E, sizeof(float));
+    float *hidden = xcalloc(t * 1024, sizeof(float));
+    ora_layer_norm(rows, t, E, m->ln_w, m->ln_b, norm);
+    affine_par(workers, norm, t, E, m->dec0_w, m->dec0_b, 1024, hidden);
+    ora_gelu(m->math, hidden, t * 1024, hidden);
+    affine_par(workers, hidden, t, 1024, m->dec2_w, m->dec2_b, m->width, logits);
+    free(norm);
+    free(hidden);
+}
+
+/* Executor::column_embeddings (cpu.rs:1073-1121): features on workers. */
+static int column_embeddings(const ora_model *m, const float *x, const float *y, size_t t, size_t h,
+                             size_t n, int workers, float *columns, float *const *feature_kv) {
+    size_t streams = h + RES;
+    float *ycol = xcalloc(n * D, sizeof(float));
+    target_embeddings(m, m->col_yw, m->col_yb, y, n, D, ycol);
+    for (size_t r = 0; r < t; ++r) memcpy(columns + r * streams * D, m->cls, RES * D * 4);
+    int st = 0;
+#pragma omp parallel for num_threads(workers) schedule(static) reduction(| : st)
+    for (size_t f = 0; f < h; ++f) {
+        float *emb = xcalloc(t * D, sizeof(float));
+        float *kv[6];
+        for (int i = 0; i < 6; ++i) kv[i] = feature_kv ? feature_kv[i] + f * M * D : NULL;
+        st |= column_stream(m, x, ycol, t, h, n, f, emb, feature_kv ? kv : NULL) != 0;
+        for (size_t r = 0; r < t; ++r) memcpy(columns + (r * streams + RES + f) * D, emb + r * D, D * 4);
+        free(emb);
+    }
+    free(ycol);
+    return st ? -1 : 0;
+}
+
+/* Executor::icl_rows (cpu.rs:1270-1295): labels into the training rows, then
+ * twelve blocks whose K/V come from the training rows only. Serial, as the
+ * reference builds one estimator's ICL stage on one thread. */
+static int icl_rows(const ora_model *m, float *rows, const float *y, size_t t, size_t n,
+                    float *const *keys, float *const *values) {
+    float *yicl = xcalloc(n * E, sizeof(float));
+    target_embeddings(m, m->icl_yw, m->icl_yb, y, n, E, yicl);
+    for (size_t i = 0; i < n * E; ++i) rows[i] += yicl[i];
+    free(yicl);
+    float *kh = keys ? NULL : xcalloc(n * E, sizeof(float));
+    float *vh = values ? NULL : xcalloc(n * E, sizeof(float));
+    float *next = xcalloc(t * E, sizeof(float));
+    float base[E];
+    int st = 0;
+    for (int blk = 0; blk < ICLB && !st; ++blk) {
+        float *k = keys ? keys[blk] : kh, *v = values ? values[blk] : vh;
+        source_heads(m, &m->icl[blk], rows, n, 0, 1, k, v);
+        qass_base(&m->icl[blk], n, base);
+        attend_opts o = {base, ORA_MATH_EXACT, 0, 1};
+        st = attend(m, &m->icl[blk], rows, t, k, v, n, &o, next);
+        memcpy(rows, next, t * E * 4);
+    }
+    free(kh);
+    free(vh);
+    free(next);
+    return st;
+}
+
+static int validate_shapes(const ora_model *m, size_t b, size_t n, size_t h, const float *y,
+                           char *err, size_t errlen) {
+    if (!b || !n || !h) {
+        set_err(err, errlen, "context needs nonempty x[B, N, H] and y_train[B, N]");
+        return -1;
+    }
+    if (m->task == ORA_CLASSIFIER) {
+        for (size_t i = 0; i < b * n; ++i) {
+            float v = y[i];
+            if (!(v >= 0.0f && v <= 9.0f && v == floorf(v))) {
+                set_err(err, errlen, "labels must be integers in 0..=9");
+                return -1;
+            }
+        }
+    } else {
+        for (size_t i = 0; i < b * n; ++i)
+            if (!isfinite(y[i])) {
+                set_err(err, errlen, "regression targets must be finite");
+                return -1;
+            }
+    }
+    return 0;
+}
+
+int ora_build_context(const ora_model *m, size_t b, size_t n, size_t h, const float *x, const float *y,
+                      float *const *column_keys, float *const *column_values, float *const *icl_keys,
+                      float *const *icl_values, char *err, size_t errlen) {
+    if (validate_shapes(m, b, n, h, y, err, errlen)) return -1;
+    size_t streams = h + RES, stream_el = (size_t)M * D;
+    int workers = g_threads;
+    for (size_t e = 0; e < b; ++e) {
+        const float *xe = x + e * n * h, *ye = y + e * n;
+        float *columns = xcalloc(n * streams * D, sizeof(float));
+        float *fkv[6];
+        for (int i = 0; i < 6; ++i) fkv[i] = xcalloc(h * stream_el, sizeof(float));
+        int st = column_embeddings(m, xe, ye, n, h, n, workers, columns, fkv);
+        if (st) {
+            set_err(err, errlen, st == -2 ? "a static context for an all-missing feature column"
+                                          : "softmax normalization is not finite");
+            for (int i = 0; i < 6; ++i) free(fkv[i]);
+            free(columns);
+            return -1;
+        }
+        for (int blk = 0; blk < COLB; ++blk) {
+            float *ck = column_keys[blk] + e * streams * stream_el;
+            float *cv = column_values[blk] + e * streams * stream_el;
+            memset(ck, 0, RES * stream_el * 4); /* reserved streams, cpu.rs:936-938 */
+            memset(cv, 0, RES * stream_el * 4);
+            memcpy(ck + RES * stream_el, fkv[2 * blk], h * stream_el * 4);
+            memcpy(cv + RES * stream_el, fkv[2 * blk + 1], h * stream_el * 4);
+        }
+        for (int i = 0; i < 6; ++i) free(fkv[i]);
+        float *rows = xcalloc(n * E, sizeof(float));
+        st = row_embeddings(m, columns, n, streams, workers, rows);
+        free(columns);
+        float *ik[ICLB], *iv[ICLB];
+        for (int blk = 0; blk < ICLB; ++blk) {
+            ik[blk] = icl_keys[blk] + e * HEADS * n * (E / HEADS);
+            iv[blk] = icl_values[blk] + e * HEADS * n * (E / HEADS);
+        }
+        if (!st) st = icl_rows(m, rows, ye, n, n, ik, iv);
+        free(rows);
+        if (st) {
+            set_err(err, errlen, "softmax normalization is not finite");
+            return -1;
+        }
+    }
+    return 0;
+}
+
+static int forward_uncached(const ora_model *m, size_t b, size_t t, size_t n, size_t h, const float *x,
+                            const float *y, float *logits, float *trace_columns, float *trace_rows,
+                            char *err, size_t errlen) {
+    if (validate_shapes(m, b, n, h, y, err, errlen)) return -1;
+    if (t < n) {
+        set_err(err, errlen, "total rows are fewer than training rows");
+        return -1;
+    }
+    size_t streams = h + RES, test = t - n;
+    int workers = g_threads;
+    for (size_t e = 0; e < b; ++e) {
+        const float *xe = x + e * t * h, *ye = y + e * n;
+        float *columns = xcalloc(t * streams * D, sizeof(float));
+        int st = column_embeddings(m, xe, ye, t, h, n, workers, columns, NULL);
+        float *rows = xcalloc(t * E, sizeof(float));
+        if (!st) st = row_embeddings(m, columns, t, streams, workers, rows);
+        if (trace_columns) memcpy(trace_columns + e * t * streams * D, columns, t * streams * D * 4);
+        if (trace_rows) memcpy(trace_rows + e * t * E, rows, t * E * 4);
+        free(columns);
+        if (!st) st = icl_rows(m, rows, ye, t, n, NULL, NULL);
+        if (!st && logits) {
+            float *dec = xcalloc(t * m->width, sizeof(float));
+            decoder(m, rows, t, 1, dec);
+            memcpy(logits + e * test * m->width, dec + n * m->width, test * m->width * 4);
+            free(dec);
+        }
+        free(rows);
+        if (st) {
+            set_err(err, errlen, "softmax normalization is not finite");
+            return -1;
+        }
+    }
+    return 0;
+}
+
+int ora_predict_uncached(const ora_model *m, size_t b, size_t t, size_t n, size_t h, const float *x,
+                         const float *y, float *logits, char *err, size_t errlen) {
+    return forward_uncached(m, b, t, n, h, x, y, logits, NULL, NULL, err, errlen);
+}
+
+int ora_trace_uncached(const ora_model *m, size_t b, size_t t, size_t n, size_t h, const float *x,
+                       const float *y, float *columns, float *rows, char *err, size_t errlen) {
+    return forward_uncached(m, b, t, n, h, x, y, NULL, columns, rows, err, errlen);
+}
+
+/* StaticExecutor::predict_estimator (cpu.rs:2259-2273) for one chunk of q rows. */
+static int predict_chunk(const ora_model *m, size_t n, size_t h, size_t q, const float *x,
+                         const float *const *ck, const float *const *cv, const float *const *ik,
+                         const float *const *iv, const float (*bases)[E], float *logits) {
+    size_t streams = h + RES, stream_el = (size_t)M * D;
+    int workers = g_threads;
+    float *columns = xcalloc(q * streams * D, sizeof(float));
+    for (size_t r = 0; r < q; ++r) memcpy(columns + r * streams * D, m->cls, RES * D * 4);
+    int st = 0;
+    /* cached_column_embeddings: features on workers (cpu.rs:2388-2443). */
+    int fw = workers < (int)h ? workers : (int)h;
+#pragma omp parallel for num_threads(fw) schedule(static) reduction(| : st)
+    for (size_t f = 0; f < h; ++f) {
+        float *emb = xcalloc(q * D, sizeof(float));
+        float *next = xcalloc(q * D, sizeof(float));
+        column_input(m, x, q, h, f, emb);
+        for (int blk = 0; blk < COLB; ++blk) {
+            const float *k = ck[blk] + (RES + f) * stream_el, *v = cv[blk] + (RES + f) * stream_el;
+            attend_opts o = {NULL, m->math, 0, 1};
+            st |= attend(m, &m->col2[blk], emb, q, k, v, M, &o, next) != 0;
+            memcpy(emb, next, q * D * 4);
+        }
+        for (size_t r = 0; r < q; ++r) memcpy(columns + (r * streams + RES + f) * D, emb + r * D, D * 4);
+        free(emb);
+        free(next);
+    }
+    float *rows = xcalloc(q * E, sizeof(float));
+    if (!st) st = row_embeddings(m, columns, q, streams, workers, rows);
+    free(columns);
+    float *next = xcalloc(q * E, sizeof(float));
+    for (int blk = 0; blk < ICLB && !st; ++blk) {
+        attend_opts o = {bases[blk], m->math, 0, workers};
+        st = attend(m, &m->icl[blk], rows, q, ik[blk], iv[blk], n, &o, next);
+        memcpy(rows, next, q * E * 4);
+    }
+    if (!st) decoder(m, rows, q, workers, logits);
+    free(rows);
+    free(next);
+    return st;
+}
+
+int ora_predict_cached(const ora_model *m, size_t b, size_t n, size_t h, size_t q, const float *x,
+                       const float *const *column_keys, const float *const *column_values,
+                       const float *const *icl_keys, const float *const *icl_values, float *logits,
+                       char *err, size_t errlen) {
+    if (!b || !n || !h) {
+        set_err(err, errlen, "empty context shape");
+        return -1;
+    }
+    if (!q) return 0;
+    size_t streams = h + RES, stream_el = (size_t)M * D, icl_el = (size_t)n * E;
+    float (*bases)[E] = xcalloc(ICLB, sizeof *bases);
+    for (int blk = 0; blk < ICLB; ++blk) qass_base(&m->icl[blk], n, bases[blk]); /* cpu.rs:588-599 */
+    int st = 0;
+    for (size_t e = 0; e < b && !st; ++e) {
+        const float *ck[COLB], *cv[COLB], *ik[ICLB], *iv[ICLB];
+        for (int blk = 0; blk < COLB; ++blk) {
+            ck[blk] = column_keys[blk] + e * streams * stream_el;
+            cv[blk] = column_values[blk] + e * streams * stream_el;
+        }
+        for (int blk = 0; blk < ICLB; ++blk) {
+            ik[blk] = icl_keys[blk] + e * icl_el;
+            iv[blk] = icl_values[blk] + e * icl_el;
+        }
+        for (size_t s = 0; s < q && !st; s += CHUNK) {
+            size_t len = q - s < CHUNK ? q - s : CHUNK;
+            st = predict_chunk(m, n, h, len, x + (e * q + s) * h, ck, cv, ik, iv,
+                               (const float(*)[E])bases, logits + (e * q + s) * m->width);
+        }
+    }
+    free(bases);
+    if (st) set_err(err, errlen, "softmax normalization is not finite");
+    return st ? -1 : 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Host post-processing                                                */
+/* ------------------------------------------------------------------ */
+
+static void softmax_t(float *v, size_t n, float temperature) {
+    float mx = -INFINITY;
+    for (size_t i = 0; i < n; ++i) if (v[i] / temperature > mx) mx = v[i] / temperature;
+    float den = 0.0f;
+    for (size_t i = 0; i < n; ++i) den += (v[i] = expf(v[i] / temperature - mx));
+    for (size_t i = 0; i < n; ++i) v[i] /= den;
+}
+
+/* aggregate_classifier_probabilities: cpu.rs:3873-3932. */
+int ora_aggregate(const float *logits, size_t b, size_t q, size_t classes, const uint64_t *perm,
+                  float temperature, int average_logits, float *out) {
+    if (!isfinite(temperature) || temperature <= 0.0f || classes > 10) return -1;
+    float member[10];
+    float scale = 1.0f / (float)b;
+    memset(out, 0, q * classes * 4);
+    for (size_t e = 0; e < b; ++e)
+        for (size_t r = 0; r < q; ++r) {
+            for (size_t c = 0; c < classes; ++c)
+                member[c] = logits[(e * q + r) * classes + (size_t)perm[e * classes + c]];
+            if (!average_logits) softmax_t(member, classes, temperature);
+            for (size_t c = 0; c < classes; ++c) out[r * classes + c] += member[c] * scale;
+        }
+    for (size_t r = 0; r < q; ++r) {
+        float *row = out + r * classes;
+        if (average_logits) softmax_t(row, classes, temperature);
+        float sum = 0.0f;
+        for (size_t c = 0; c < classes; ++c) sum += row[c];
+        for (size_t c = 0; c < classes; ++c) row[c] /= sum;
+    }
+    return 0;
+}
+
+static int cmp_float(const void *a, const void *b) {
+    float x = *(const float *)a, y = *(const float *)b;
+    return (x > y) - (x < y);
+}
+
+/* tail_slope: quantiles.rs:202-213. */
+static double tail_slope(const float *q, const double *x, size_t n) {
+    double xm = 0, qm = 0;
+    for (size_t i = 0; i < n; ++i) xm += x[i], qm += q[i];
+    xm /= (double)n;
+    qm /= (double)n;
+    double cov = 0, var = 0;
+    for (size_t i = 0; i < n; ++i) {
+        cov += ((double)q[i] - qm) * (x[i] - xm);
+        var += (x[i] - xm) * (x[i] - xm);
+    }
+    double v = var / (double)n;
+    return (cov / (double)n) / (v > 1e-6 ? v : 1e-6);
+}
+
+/* quantiles::summarize (quantiles.rs:80-199): per estimator and row, sort the
+ * decoded quantiles, fit exponential tails, evaluate; average over B. */
+int ora_regression_summary(const float *logits, size_t b, size_t q, size_t k, const float *alphas,
+                           size_t n_alphas, float *mean_out, float *quant_out) {
+    if (k < 2) return -1;
+    const double TOL = 1e-6;
+    double *levels = xcalloc(k, sizeof(double));
+    for (size_t i = 0; i < k; ++i) levels[i] = (double)(float)((double)(i + 1) / (double)(k + 1));
+    double *msum = xcalloc(q, sizeof(double));
+    double *qsum = xcalloc(q * (n_alphas ? n_alphas : 1), sizeof(double));
+    float *sorted = xcalloc(k, sizeof(float));
+    size_t tk = k / 4 < 20 ? k / 4 : 20;
+    if (tk < 1) tk = 1;
+    double *xl = xcalloc(tk, sizeof(double)), *xr = xcalloc(tk, sizeof(double));
+    for (size_t i = 0; i < tk; ++i) {
+        xl[i] = log(levels[i] > TOL ? levels[i] : TOL);
+        double om = 1.0 - levels[k - tk + i];
+        xr[i] = log(om > TOL ? om : TOL);
+    }
+    for (size_t e = 0; e < b; ++e)
+        for (size_t r = 0; r < q; ++r) {
+            memcpy(sorted, logits + (e * q + r) * k, k * 4);
+            qsort(sorted, k, sizeof(float), cmp_float);
+            double m = 0;
+            for (size_t i = 0; i < k; ++i) m += sorted[i];
+            msum[r] += m / (double)k;
+            double left = tail_slope(sorted, xl, tk), right = tail_slope(sorted + k - tk, xr, tk);
+            double bl = fabs(left), br = fabs(-right);
+            bl = bl < 0.01 ? 0.01 : (bl > 100.0 ? 100.0 : bl);
+            br = br < 0.01 ? 0.01 : (br > 100.0 ? 100.0 : br);
+            for (size_t a = 0; a < n_alphas; ++a) {
+                double alpha = alphas[a], al = levels[0], ar = levels[k - 1];
+                double ql = sorted[0], qr = sorted[k - 1], v;
+                if (alpha < al) {
+                    v = ql + bl * (log(alpha > TOL ? alpha : TOL) - log(al > TOL ? al : TOL));
+                } else if (alpha > ar) {
+                    double omr = 1.0 - (ar < 1.0 - TOL ? ar : 1.0 - TOL);
+                    double om = 1.0 - alpha;
+                    v = qr - br * (log(om > TOL ? om : TOL) - log(omr));
+                } else if (alpha >= ar) {
+                    v = qr;
+                } else {
+                    size_t lo = 0, hi = k - 1; /* partition_point over levels[..k-1] of level <= alpha */
+                    while (lo < hi) {
+                        size_t mid = (lo + hi) / 2;
+                        if (levels[mid] <= alpha) lo = mid + 1; else hi = mid;
+                    }
+                    size_t seg = lo ? lo - 1 : 0;
+                    double l0 = levels[seg], l1 = levels[seg + 1];
+                    double span = l1 - l0 > TOL ? l1 - l0 : TOL;
+                    double t = (alpha - l0) / span;
+                    t = t < 0 ? 0 : (t > 1 ? 1 : t);
+                    v = (double)sorted[seg] + t * ((double)sorted[seg + 1] - (double)sorted[seg]);
+                }
+                qsum[r * n_alphas + a] += v;
+            }
+        }
+    for (size_t r = 0; r < q; ++r) {
+        if (mean_out) mean_out[r] = (float)(msum[r] / (double)b);
+        for (size_t a = 0; a < n_alphas; ++a)
+            if (quant_out) quant_out[r * n_alphas + a] = (float)(qsum[r * n_alphas + a] / (double)b);
+    }
+    free(levels);
+    free(msum);
+    free(qsum);
+    free(sorted);
+    free(xl);
+    free(xr);
+    return 0;
+}

@@ -1,0 +1,135 @@
+"""Kernel families on the GPU through the C ABI harness, against float64
+references (the reference's tests/cuda_products.rs:54-103 and
+tests/cuda_attention.rs:58-118 at FP32)."""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from ironicl_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def device():
+    return hip.Device(0)
+
+
+def values(count: int, seed: int) -> np.ndarray:
+    """tests/cuda_products.rs:9-24: a 64-bit LCG, unit = (state >> 40) / 2^24,
+    value = (unit - 0.5) * 0.2."""
+    out = np.empty(count, np.float32)
+    state = seed
+    mask = (1 << 64) - 1
+    for i in range(count):
+        state = (state * 6364136223846793005 + 1442695040888963407) & mask
+        out[i] = np.float32(((state >> 40) / float(1 << 24) - 0.5) * 0.2)
+    return out
+
+
+def fast_values(count: int, seed: int, scale: float = 1.0) -> np.ndarray:
+    return (np.random.default_rng(seed).uniform(-1.0, 1.0, count) * scale).astype(np.float32)
+
+
+def gelu64(x):
+    from scipy.special import erf
+    return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))
+
+
+@pytest.mark.parametrize("m,n,k,n2", [(65, 64, 64, 64), (300, 512, 512, 10), (513, 1024, 512, 512),
+                                      (128, 512, 1024, 512), (4096, 384, 128, 128), (7, 1024, 512, 999)])
+def test_products_match_float64(device, m, n, k, n2):
+    gen = values if m * k < 300_000 else fast_values
+    x = gen(m * k, 1)
+    w1, b1 = gen(n * k, 2), gen(n, 3)
+    w2, b2 = gen(n2 * n, 4), gen(n2, 5)
+    first = np.zeros(m * n, np.float32)
+    second = np.zeros(m * n2, np.float32)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_products(device.handle, F(x), F(w1), F(b1), F(w2), F(b2), m, n, k, n2,
+                                          F(first), F(second)))
+    y = gelu64(x.reshape(m, k).astype(np.float64) @ w1.reshape(n, k).T.astype(np.float64) + b1)
+    z = y @ w2.reshape(n2, n).T.astype(np.float64) + b2
+    if n2 == n:
+        z = z + y
+
+    def rel(got, want):
+        return np.abs(got.reshape(want.shape) - want).max() / np.abs(want).max()
+
+    assert rel(first, y) < 1e-5 and rel(second, z) < 1e-5, (rel(first, y), rel(second, z))
+
+
+def attention64(q, k, v, scale):
+    s = (q.astype(np.float64) @ k.astype(np.float64).T) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return (p / p.sum(-1, keepdims=True)) @ v.astype(np.float64)
+
+
+@pytest.mark.parametrize("rows", [1, 63, 64, 65, 2000, 10007])
+def test_icl_attention_matches_float64(device, rows):
+    pairs = 64
+    k = fast_values(pairs * rows * 64, 2).reshape(pairs, rows, 64)
+    v = fast_values(pairs * rows * 64, 3).reshape(pairs, rows, 64)
+    for query_rows in (1, 5, 16, 17, 64, 100):
+        q = fast_values(pairs * query_rows * 64, 1, scale=3.0).reshape(pairs, query_rows, 64)
+        out = np.zeros_like(q)
+        F = hip.fptr
+        hip.check(hip.lib().irx_test_icl_attention(device.handle, F(q), F(k), F(v), pairs, query_rows, rows,
+                                                   F(out)))
+        worst = 0.0
+        for pair in (0, 17, 63):
+            rows_sel = sorted({0, query_rows // 2, query_rows - 1})
+            want = attention64(q[pair, rows_sel], k[pair], v[pair], 0.125)
+            worst = max(worst, np.abs(out[pair, rows_sel] - want).max())
+        assert worst < 1e-5, (rows, query_rows, worst)
+
+
+def test_icl_attention_peaked_scores(device):
+    """Large logits: one key dominates; the online max must stay exact."""
+    pairs, rows, qr = 8, 3000, 40
+    k = fast_values(pairs * rows * 64, 7).reshape(pairs, rows, 64)
+    v = fast_values(pairs * rows * 64, 8).reshape(pairs, rows, 64)
+    q = (k[:, 1234:1234 + qr] * 40.0).copy()
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_icl_attention(device.handle, F(q), F(k), F(v), pairs, qr, rows, F(out)))
+    for pair in (0, 5):
+        want = attention64(q[pair], k[pair], v[pair], 0.125)
+        assert np.abs(out[pair] - want).max() < 1e-5
+
+
+@pytest.mark.parametrize("rows,width", [(1, 128), (333, 128), (1000, 512), (4, 512)])
+def test_layer_norm_matches_float64(device, rows, width):
+    x = fast_values(rows * width, 4, 3.0) + 0.5
+    w, b = fast_values(width, 5, 0.1) + 1.0, fast_values(width, 6, 0.1)
+    out = np.zeros_like(x)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_layer_norm(device.handle, F(x), F(w), F(b), rows, width, F(out)))
+    x64 = x.reshape(rows, width).astype(np.float64)
+    want = (x64 - x64.mean(1, keepdims=True)) / np.sqrt(x64.var(1, keepdims=True) + 1e-5) * w + b
+    assert np.abs(out.reshape(rows, width) - want).max() < 1e-5
+
+
+@pytest.mark.parametrize("query_rows,rows", [(1, 1), (4, 68), (68, 68), (130, 128), (128, 1000), (504, 504)])
+def test_small_attention_matches_float64(device, query_rows, rows):
+    heads = 8
+    q = fast_values(heads * query_rows * 16, 1, 3.0).reshape(heads, query_rows, 16)
+    k = fast_values(heads * rows * 16, 2).reshape(heads, rows, 16)
+    v = fast_values(heads * rows * 16, 3).reshape(heads, rows, 16)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_small_attention(device.handle, F(q), F(k), F(v), heads, query_rows, rows,
+                                                 F(out)))
+    for h in range(heads):
+        assert np.abs(out[h] - attention64(q[h], k[h], v[h], 0.25)).max() < 1e-5
+
+
+def test_harness_rejects_bad_shapes(device):
+    z = np.zeros(64, np.float32)
+    F = hip.fptr
+    assert hip.lib().irx_test_icl_attention(device.handle, F(z), F(z), F(z), 3, 1, 1, F(z)) == hip.INVALID_ARGUMENT
+    assert hip.lib().irx_test_products(device.handle, F(z), F(z), F(z), F(z), F(z), 1, 8, 8, 8, F(z),
+                                       F(z)) == hip.INVALID_ARGUMENT

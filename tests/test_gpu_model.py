@@ -1,0 +1,175 @@
+"""Whole-model parity of the GPU path against the oracle, through the C ABI.
+
+The bar (north star): every logit / regression output within
+|gpu - cpu| <= 1e-5 + 1e-4 |cpu| of the oracle's FP32 CPU path on identical
+inputs and weights, with identical argmax."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from ironicl_amd import hip
+from ironicl_amd import synthetic as S
+from ironicl_amd import tabicl
+from test_oracle_model import reference_lcg_data
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-5, 1e-4
+
+
+def assert_parity(gpu, cpu, what=""):
+    gpu, cpu = np.asarray(gpu, np.float64), np.asarray(cpu, np.float64)
+    err = np.abs(gpu - cpu) - (ATOL + RTOL * np.abs(cpu))
+    worst = np.unravel_index(np.argmax(err), err.shape)
+    assert err.max() <= 0, f"{what}: |gpu-cpu| {abs(gpu[worst] - cpu[worst]):.3e} at {worst} (cpu {cpu[worst]:.6f})"
+
+
+@pytest.fixture(scope="module")
+def device():
+    return hip.Device(0)
+
+
+@pytest.fixture(scope="module")
+def clf(device, clf_weights):
+    return tabicl.Executor("classifier", clf_weights, device)
+
+
+@pytest.fixture(scope="module")
+def clf_oracle(clf_weights):
+    O.set_threads(16)
+    return O.OracleModel("classifier", clf_weights, O.EXACT)
+
+
+@pytest.fixture(scope="module")
+def lcg(clf, clf_oracle):
+    x, y, xt, shifts = reference_lcg_data(2, 240, 250, 5)
+    ctx_cpu = clf_oracle.build_context(x, y)
+    ctx_gpu = clf.build_context(x, y, class_permutations=shifts, download=True)
+    return x, y, xt, shifts, ctx_cpu, ctx_gpu
+
+
+def test_built_context_matches_oracle(lcg):
+    x, y, xt, shifts, ctx_cpu, ctx_gpu = lcg
+    ck, cv, ik, iv = ctx_gpu.context
+    for blk in range(3):
+        np.testing.assert_allclose(ck[blk][:, 4:], ctx_cpu[0][blk][:, 4:], atol=1e-4, rtol=1e-3)
+        np.testing.assert_allclose(cv[blk][:, 4:], ctx_cpu[1][blk][:, 4:], atol=1e-4, rtol=1e-3)
+    for blk in range(12):
+        np.testing.assert_allclose(ik[blk], ctx_cpu[2][blk], atol=2e-4, rtol=1e-3, err_msg=f"icl {blk} keys")
+        np.testing.assert_allclose(iv[blk], ctx_cpu[3][blk], atol=2e-4, rtol=1e-3, err_msg=f"icl {blk} values")
+
+
+def test_cached_prediction_on_the_oracle_context(clf, clf_oracle, lcg):
+    """The predictor alone: the oracle's context uploaded, GPU vs CPU predict."""
+    x, y, xt, shifts, ctx_cpu, _ = lcg
+    st = clf.load_context(ctx_cpu, x.shape, 3, shifts)
+    gpu = st.predict_raw(xt).logits
+    cpu = clf_oracle.predict_cached(ctx_cpu, xt)
+    assert_parity(gpu, cpu, "predict on the oracle context")
+    assert np.array_equal(gpu[..., :3].argmax(-1), cpu[..., :3].argmax(-1))
+
+
+def test_built_context_prediction_matches_uncached_oracle(clf_oracle, lcg):
+    """Build and predict on the GPU against the oracle's uncached forward."""
+    x, y, xt, shifts, _, ctx_gpu = lcg
+    gpu = ctx_gpu.predict_raw(xt).logits
+    cpu = clf_oracle.predict_uncached(x, y, xt)
+    assert_parity(gpu, cpu, "build + predict")
+    assert np.array_equal(gpu[..., :3].argmax(-1), cpu[..., :3].argmax(-1))
+    probs = ctx_gpu.predict_probabilities(xt)
+    ref = O.aggregate(np.ascontiguousarray(cpu[..., :3]), shifts)
+    np.testing.assert_allclose(probs, ref, atol=1e-5)
+
+
+def test_pass_rows_and_device_path_do_not_change_results(lcg):
+    *_, ctx_gpu = lcg
+    xt = lcg[2]
+    whole = ctx_gpu.predict_raw(xt).logits
+    ctx_gpu.set_pass_rows(32)
+    try:
+        small = ctx_gpu.predict_raw(xt).logits
+    finally:
+        ctx_gpu.set_pass_rows(512)
+    np.testing.assert_allclose(small, whole, atol=1e-6, rtol=1e-6)
+    import torch
+
+    dx = torch.from_numpy(xt).cuda()
+    dl = torch.zeros((2, xt.shape[1], 10), device="cuda")
+    torch.cuda.synchronize()
+    hip.check(hip.lib().irx_predictor_predict_device(ctx_gpu.handle, dx.data_ptr(), xt.shape[1], dl.data_ptr(),
+                                                     None))
+    np.testing.assert_array_equal(dl.cpu().numpy(), whole)
+
+
+def test_missing_marker_rows_are_flagged(lcg):
+    *_, ctx_gpu = lcg
+    xt = lcg[2][:, :40].copy()
+    xt[1, 7, :] = -100.0   # every grouped triple of row 7 in estimator 1
+    p = ctx_gpu.predict_raw(xt)
+    assert p.cpu_rows == [7]
+    assert np.all(np.isnan(p.logits[:, 7])) and np.all(np.isfinite(np.delete(p.logits, 7, axis=1)))
+
+
+def test_config_clf_1k_end_to_end(clf, clf_oracle):
+    """1024 train rows x 54 features, 7 classes, 8 test rows."""
+    w = S.WORKLOADS["clf-1k"]
+    x, y, xt, meta = S.workload_data(w)
+    st = clf.build_context(x, y)
+    gpu = st.predict_logits(xt).logits
+    cpu = clf_oracle.predict_uncached(x, y, xt)[..., :7]
+    assert_parity(gpu, cpu, "clf-1k")
+    assert np.array_equal(gpu.argmax(-1), cpu.argmax(-1))
+
+
+def test_regressor_quantiles(device, reg_weights):
+    w = S.WORKLOADS["reg-20k"]
+    x, y, xt, meta = S.workload_data(w, train_rows=300, test_rows=40, features=7)
+    ex = tabicl.Executor("regressor", reg_weights, device)
+    st = ex.build_context(x, y)
+    gpu = st.predict_logits(xt).logits
+    m = O.OracleModel("regressor", reg_weights, O.EXACT)
+    cpu = m.predict_uncached(x, y, xt)
+    assert_parity(gpu, cpu, "regressor quantiles")
+    alphas = [0.05, 0.5, 0.95]
+    gm, gq = tabicl.summarize_quantiles(gpu, alphas)
+    cm, cq = O.regression_summary(cpu, alphas)
+    assert_parity(gm, cm, "mean")
+    assert_parity(gq, cq, "quantiles")
+
+
+def test_ensemble_with_feature_permutations(clf, clf_oracle):
+    w = S.WORKLOADS["clf-200k"]
+    x, y, xt, meta = S.workload_data(w, train_rows=200, test_rows=30, features=9)
+    x, y, xt = x[:3], y[:3], xt[:3]
+    st = clf.build_context(x, y, class_permutations=meta["class_permutations"][:3])
+    gpu = st.predict_logits(xt).logits
+    cpu = clf_oracle.predict_uncached(x, y, xt)[..., :10]
+    assert_parity(gpu, cpu, "3 estimators")
+
+
+def test_progress_hook_can_interrupt(clf):
+    x, y, xt, _ = reference_lcg_data(2, 128, 8, 5)
+    calls = []
+
+    def hook(stage, done, total):
+        calls.append((stage, done, total))
+        if done == 1:
+            raise RuntimeError("stop")
+
+    with pytest.raises(hip.HipError) as e:
+        clf.build_context(x, y, progress=hook)
+    assert e.value.status == hip.INTERRUPTED
+    assert calls[0] == (hip.STAGE_BUILD, 0, 2)
+
+
+def test_build_rejects_missing_marker_and_tiny_contexts(clf):
+    x, y, _, _ = reference_lcg_data(1, 128, 1, 5)
+    x[0, 3, :] = -100.0
+    with pytest.raises(hip.HipError) as e:
+        clf.build_context(x, y)
+    assert e.value.status == hip.UNSUPPORTED
+    x, y, _, _ = reference_lcg_data(1, 32, 1, 5)
+    with pytest.raises(hip.HipError) as e:
+        clf.build_context(x, y)
+    assert e.value.status == hip.DOES_NOT_FIT

@@ -1,0 +1,147 @@
+"""Whole-model checks of the oracle (CPU only): the official manifest, an
+independent float64 restatement on tiny shapes, and the reference's model
+invariants (tests/checkpoint_fixtures.rs:202-353; cpu.rs:5368-5411)."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import ROOT  # noqa: F401
+from ironicl_amd import manifest as mf
+from ironicl_amd import synthetic as S
+from reference_np import Model
+
+
+def reference_lcg_data(b, n, q, h, classes=3):
+    """Data of built_context_matches_the_uncached_forward_pass
+    (tests/checkpoint_fixtures.rs:216-233): an LCG in [-2, 2), class shifts per estimator."""
+    state = 0x2545F491
+    x = np.empty(b * (n + q) * h, np.float32)
+    for i in range(x.size):
+        state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+        x[i] = np.float32((state >> 8) / float(1 << 24) * 4.0 - 2.0)
+    x = x.reshape(b, n + q, h)
+    shifts = np.array([[(c + e) % classes for c in range(classes)] for e in range(b)], np.uint64)
+    y = np.array([[shifts[e][row % classes] for row in range(n)] for e in range(b)], np.float32)
+    return x[:, :n].copy(), y, x[:, n:].copy(), shifts
+
+
+@pytest.mark.parametrize("task", [mf.CLASSIFIER, mf.REGRESSOR])
+def test_manifest_matches_official_profile(task):
+    names = mf.tensor_manifest(task)
+    count, params, nbytes = mf.PROFILE[task]
+    assert len(names) == count
+    total = sum(int(np.prod(s)) for s in names.values())
+    assert total == params and 4 * total == nbytes
+    w = S.random_weights(task)
+    assert sorted(w) == sorted(names)
+    assert all(w[k].shape == names[k] for k in names)
+
+
+def test_random_weights_are_seeded_and_bounded(clf_weights):
+    again = S.random_weights("classifier")
+    assert all(np.array_equal(clf_weights[k], again[k]) for k in clf_weights)
+    w = clf_weights["icl_predictor.tf_icl.blocks.3.linear1.weight"]
+    assert np.abs(w).max() <= 1 / np.sqrt(512) + 1e-7
+    assert np.allclose(clf_weights["row_interactor.tf_row.rope.freqs"], 100000.0 ** (-np.arange(8) / 8))
+
+
+@pytest.mark.parametrize("task", [mf.CLASSIFIER, mf.REGRESSOR])
+def test_oracle_matches_float64_restatement(task, clf_weights, reg_weights):
+    weights = clf_weights if task == mf.CLASSIFIER else reg_weights
+    rng = np.random.default_rng(11)
+    n, q, h = 48, 5, 4
+    x = rng.normal(size=(n + q, h)).astype(np.float32)
+    y = (np.arange(n) % 3).astype(np.float32) if task == mf.CLASSIFIER else rng.normal(size=n).astype(np.float32)
+    ref_cols, ref_rows, ref_logits = Model(task, weights).forward(x.astype(np.float64), y.astype(np.float64), n)
+    m = O.OracleModel(task, weights, O.EXACT)
+    cols, rows = m.trace_uncached(x[None], y[None], n)
+    cols[0, :, :4] = 0.0
+    np.testing.assert_allclose(cols[0], ref_cols, atol=2e-5, rtol=1e-4)
+    np.testing.assert_allclose(rows[0], ref_rows, atol=2e-5, rtol=1e-4)
+    logits = m.predict_uncached(x[None, :n], y[None], x[None, n:])
+    np.testing.assert_allclose(logits[0], ref_logits[n:], atol=1e-5, rtol=1e-4)
+    ctx = m.build_context(x[None, :n], y[None])
+    np.testing.assert_allclose(m.predict_cached(ctx, x[None, n:])[0], ref_logits[n:], atol=1e-5, rtol=1e-4)
+
+
+@pytest.fixture(scope="module")
+def lcg_case(clf_weights):
+    b, n, q, h = 2, 240, 250, 5
+    x, y, xt, shifts = reference_lcg_data(b, n, q, h)
+    m = O.OracleModel("classifier", clf_weights, O.EXACT)
+    O.set_threads(4)
+    ctx = m.build_context(x, y)
+    return m, x, y, xt, ctx
+
+
+def test_cached_matches_uncached(lcg_case):
+    m, x, y, xt, ctx = lcg_case
+    cached = m.predict_cached(ctx, xt)
+    uncached = m.predict_uncached(x, y, xt)
+    assert np.abs(cached - uncached).max() <= 1e-4
+    assert np.array_equal(cached.argmax(-1), uncached.argmax(-1))
+
+
+def test_context_layout_reserved_streams_are_zero(lcg_case):
+    _, x, _, _, (ck, cv, ik, iv) = lcg_case
+    b, n, h = x.shape
+    assert ck[0].shape == (b, h + 4, 8, 128, 16) and ik[0].shape == (b, 8, n, 64)
+    for t in ck + cv:
+        assert not t[:, :4].any() and t[:, 4:].any()
+
+
+def test_threads_do_not_change_results(lcg_case):
+    m, _, _, xt, ctx = lcg_case
+    O.set_threads(1)
+    serial = m.predict_cached(ctx, xt)
+    O.set_threads(4)
+    parallel = m.predict_cached(ctx, xt)
+    assert np.array_equal(serial, parallel)
+
+
+def test_training_row_permutation_invariance(lcg_case):
+    m, x, y, xt, ctx = lcg_case
+    perm = np.random.default_rng(2).permutation(x.shape[1])
+    ctx_p = m.build_context(np.ascontiguousarray(x[:, perm]), np.ascontiguousarray(y[:, perm]))
+    np.testing.assert_allclose(m.predict_cached(ctx_p, xt[:, :40]), m.predict_cached(ctx, xt[:, :40]), atol=2e-5)
+
+
+def test_rows_are_independent_and_chunks_join_in_place(lcg_case):
+    """large_cached_query_runs_in_chunks (tests/checkpoint_fixtures.rs:297-353)."""
+    m, _, _, xt, ctx = lcg_case
+    big = np.concatenate([xt] * 5, axis=1)[:, :1100]
+    whole = m.predict_cached(ctx, big)
+    part = m.predict_cached(ctx, big[:, 1000:1100])
+    np.testing.assert_array_equal(whole[:, 1000:1100], part)
+    np.testing.assert_array_equal(whole[:, :250], whole[:, 250:500])
+
+
+def test_native_math_within_tolerance_of_exact(clf_weights, lcg_case):
+    _, x, y, xt, ctx = lcg_case
+    native = O.OracleModel("classifier", clf_weights, O.NATIVE)
+    exact = lcg_case[0].predict_cached(ctx, xt[:, :50])
+    approx = native.predict_cached(ctx, xt[:, :50])
+    assert np.all(np.abs(approx - exact) <= 1e-5 + 1e-4 * np.abs(exact))
+
+
+def test_missing_marker_rows_run_on_the_cpu_path(clf_weights):
+    m = O.OracleModel("classifier", clf_weights, O.EXACT)
+    x, y, xt, _ = reference_lcg_data(1, 64, 4, 5)
+    xt[0, 1, :] = -100.0
+    out = m.predict_uncached(x, y, xt)
+    assert np.all(np.isfinite(out))
+
+
+def test_invalid_labels_are_rejected(clf_weights):
+    m = O.OracleModel("classifier", clf_weights, O.EXACT)
+    x, _, _, _ = reference_lcg_data(1, 64, 1, 5)
+    with pytest.raises(ValueError):
+        m.build_context(x, np.full((1, 64), 10.0, np.float32))
+
+
+def test_missing_tensor_is_reported(clf_weights):
+    w = dict(clf_weights)
+    del w["icl_predictor.ln.weight"]
+    with pytest.raises(ValueError, match="icl_predictor.ln.weight"):
+        O.OracleModel("classifier", w)
