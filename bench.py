@@ -1,0 +1,218 @@
+"""Benchmark of the MI355X TabICLv2 FP32 forward: cached-prediction test rows/s
+and static-context build ms on one GPU.
+
+Workload (N=1): the 50,000-train-row classifier: 50,000 x 64 features
+N(0,1), 10 classes from a seeded linear map, random-init FP32 weights of the
+official architecture; the static context is built once and held in HBM;
+4,096 test rows are predicted in passes of 512 against the cached ICL K/V.
+
+A step is one prediction of the 4,096 test rows, inputs already in HBM. The
+build is timed separately (host FP32 inputs to a resident context). The
+dominant kernel (ICL attention) is timed live with HIP events on its own
+stream over the timed steps; the oracle (C restatement of the reference CPU
+path) is timed on the host's cores on a bounded sample of the same rows.
+
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBPS = 8000.0
+WORKLOAD = "clf-50k"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_facts() -> dict:
+    facts = {"logical_cpus": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                facts["cpu_model"] = line.split(":", 1)[1].strip()
+        facts["avx512"] = "avx512f" in open("/proc/cpuinfo").read()
+    except Exception:
+        pass
+    return facts
+
+
+def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target_s: float) -> dict:
+    """The oracle's cached prediction on the host cores, on a bounded sample of
+    the workload's test rows (sized for about target_s seconds of CPU work)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    O.set_threads(threads)
+    m = O.OracleModel("classifier", weights, O.NATIVE)
+    rows = 8
+    t0 = time.perf_counter()
+    logits = m.predict_cached(context_host, np.ascontiguousarray(x_test[:, :rows]))
+    dt = time.perf_counter() - t0
+    more = int(min(x_test.shape[1] - rows, max(0, rows * (target_s / max(dt, 1e-3) - 1))))
+    if more > 0:
+        t1 = time.perf_counter()
+        extra = m.predict_cached(context_host, np.ascontiguousarray(x_test[:, rows:rows + more]))
+        dt += time.perf_counter() - t1
+        logits = np.concatenate([logits, extra], axis=1)
+        rows += more
+    gpu = gpu_logits[:, :rows, : logits.shape[2]]
+    cpu = logits[..., : gpu.shape[2]]
+    excess = np.abs(gpu - cpu) - (1e-5 + 1e-4 * np.abs(cpu))
+    return {
+        "value": rows / dt,
+        "unit": "rows/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"cached prediction of the first {rows} of the {x_test.shape[1]} test rows against the same "
+                  f"50k-row context, C restatement of the reference CPU path (native-approximation math, "
+                  f"{threads} threads = ceil(logical/2) as the reference defaults)",
+        "seconds": dt,
+        "parity_rows": rows,
+        "parity_max_abs_diff": float(np.abs(gpu - cpu).max()),
+        "parity_ok": bool(excess.max() <= 0 and np.array_equal(gpu.argmax(-1), cpu.argmax(-1))),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--build-repeats", type=int, default=2)
+    ap.add_argument("--pass-rows", type=int, default=512)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    from ironicl_amd import hip, hipmem, synthetic, tabicl
+
+    w = synthetic.WORKLOADS[WORKLOAD]
+    log("generating weights and data")
+    weights = synthetic.random_weights("classifier")
+    x, y, xt, meta = synthetic.workload_data(w)
+    b, n, h = x.shape
+    q = xt.shape[1]
+    device = hip.Device(0)
+    executor = tabicl.Executor("classifier", weights, device)
+
+    # Warm-up build: also downloads the context for the CPU baseline.
+    log("warm-up build (with context download)")
+    t0 = time.perf_counter()
+    context = executor.build_context(x, y, download=not args.no_cpu)
+    log(f"warm-up build {1000 * (time.perf_counter() - t0):.1f} ms")
+    context_host = context.context
+    build_ms = []
+    for i in range(args.build_repeats):
+        del context
+        hipmem.synchronize()
+        t0 = time.perf_counter()
+        context = executor.build_context(x, y)
+        hipmem.synchronize()
+        build_ms.append(1000 * (time.perf_counter() - t0))
+        log(f"build {i}: {build_ms[-1]:.1f} ms")
+    context.set_pass_rows(args.pass_rows)
+
+    dx = hipmem.DeviceArray.from_host(xt)
+    dl = hipmem.DeviceArray((b, q, executor.width))
+
+    def step():
+        hip.check(hip.lib().irx_predictor_predict_device(context.handle, dx.ptr, q, dl.ptr, None))
+
+    for _ in range(args.warmup):
+        step()
+    hipmem.synchronize()
+    log(f"timing {args.steps} steps of {q} rows")
+    hip.profile_enable(True)
+    hipmem.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    hipmem.synchronize()
+    elapsed = time.perf_counter() - t0
+    stats = {f: hip.profile_read(f) for f in hip.KERNEL_FAMILIES}
+    hip.profile_enable(False)
+    ms_per_step = 1000 * elapsed / args.steps
+    rows_per_s = q * args.steps / elapsed
+    gpu_logits = dl.to_host()
+
+    # The same prediction from host buffers (PCIe included), for reference.
+    t0 = time.perf_counter()
+    context.predict_raw(xt)
+    host_rows_per_s = q / (time.perf_counter() - t0)
+
+    icl = stats["icl_attention"]
+    icl_ms = icl["milliseconds"] / max(icl["launches"], 1)
+    icl_flops = icl["flops"] / max(icl["launches"], 1)
+    achieved = icl_flops / (icl_ms * 1e-3) / 1e12
+    roofline = {
+        "kernel": "icl_attention_kernel (cross-attention of 512 queries x 50,000 cached keys x 8 heads, FP32 MFMA)",
+        "bound": "mfma",
+        "achieved": achieved,
+        "peak": MFMA_FP32_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
+        "traffic": None,
+        "avg_launch_ms": icl_ms,
+        "flops_per_launch": icl_flops,
+    }
+    breakdown = {f: {"ms_per_step": s["milliseconds"] / args.steps, "launches_per_step": s["launches"] / args.steps,
+                     "tflops": (s["flops"] / (s["milliseconds"] * 1e-3) / 1e12) if s["milliseconds"] else 0.0,
+                     "gbps": (s["bytes"] / (s["milliseconds"] * 1e-3) / 1e9) if s["milliseconds"] else 0.0}
+                 for f, s in stats.items()}
+
+    result = {
+        "metric": "test rows/sec vs cached context; static-context build ms (1 MI355X)",
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded random-init FP32 weights of the official TabICLv2 classifier; x ~ N(0,1); "
+                "labels from a seeded linear map",
+        "config": {
+            "workload": "clf-50k: 50,000 train rows x 64 features, 10 classes, 4,096 test rows in passes of 512, "
+                        "1 estimator; context built once and resident in HBM",
+            "train_rows": n, "features": h, "test_rows": q, "pass_rows": args.pass_rows, "estimators": b,
+            "classes": w.classes,
+        },
+        "build_ms": float(np.median(build_ms)),
+        "build_ms_all": build_ms,
+        "rows_per_s_host_buffers": host_rows_per_s,
+        "roofline": roofline,
+        "kernels": breakdown,
+    }
+    if not args.no_cpu:
+        threads = max(1, (os.cpu_count() or 2) // 2)
+        log(f"CPU baseline on {threads} threads")
+        result["cpu_baseline"] = cpu_baseline(weights, context_host, xt, gpu_logits, threads, args.cpu_seconds)
+        result["cpu_baseline"].update(host_facts())
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

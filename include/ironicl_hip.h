@@ -193,6 +193,24 @@ int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, fl
 int irx_predictor_predict_device(irx_predictor *predictor, const float *x_device, size_t q,
                                  float *logits_device, uint8_t *cpu_rows);
 
+/* ---- Kernel timing (opt-in). No counterpart in the reference, whose
+ * profile.rs (src/profile.rs:5-146) times CPU phases: this records HIP events
+ * on the stream each kernel family launches on, with each launch's
+ * algorithmic FLOPs and minimal HBM bytes, for roofline measurement. ---- */
+
+typedef struct irx_kernel_stats {
+    uint64_t launches;
+    double milliseconds; /* summed kernel durations */
+    double flops;        /* algorithmic FLOPs of those launches */
+    double bytes;        /* minimal HBM bytes: operands read once, results written once */
+} irx_kernel_stats;
+
+/* Starts (enable != 0) or stops recording; starting clears the totals. */
+int irx_profile_enable(int enable);
+/* Totals of one kernel family: "gemm", "icl_attention", "icl_merge",
+ * "small_attention", "layer_norm" or "glue". Waits for recorded launches. */
+int irx_profile_read(const char *family, irx_kernel_stats *out);
+
 /* ---- Kernel harness (cuda/testing.rs:27-207): one kernel family on host data ---- */
 
 /* softmax(q k^T / 8) v for `pairs` (estimator, head) pairs: q [pairs, query_rows, 64],

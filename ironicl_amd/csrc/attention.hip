@@ -387,11 +387,17 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         size_t need = icl_attention_partial_floats(args.pairs, args.q_rows, g.splits);
         if (!args.partial || args.partial_floats < need) fail(3, "ICL attention partial buffer is too small");
     }
-    hipLaunchKernelGGL(icl_attention_kernel<kIclWaves>, dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
-                       args, g);
-    IRX_HIP(hipGetLastError());
+    {
+        const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
+        KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, 4.0 * 64.0 * pairs * (2.0 * kv + 2.0 * q));
+        hipLaunchKernelGGL(icl_attention_kernel<kIclWaves>, dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
+                           args, g);
+        IRX_HIP(hipGetLastError());
+    }
     if (g.splits > 1) {
         long long total = (long long)args.pairs * args.q_rows * 64;
+        KernelTimer timer(kFamIclMerge, stream, 0.0,
+                          4.0 * ((double)g.splits * args.pairs * args.q_rows * 65.0 + (double)total));
         hipLaunchKernelGGL(icl_merge_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, args, g.splits,
                            g.q_padded);
         IRX_HIP(hipGetLastError());
@@ -410,6 +416,9 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
     int qtiles = (int)ceil_div(args.q_rows, 64);
     long long blocks = (long long)qtiles * args.heads * args.seqs;
     if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
+    const double sh = (double)args.seqs * args.heads;
+    KernelTimer timer(kFamSmall, stream, 4.0 * sh * args.q_rows * args.kv_rows * 16.0,
+                      4.0 * sh * 32.0 * (args.q_rows + args.kv_rows));
     hipLaunchKernelGGL(small_attention_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, args, qtiles);
     IRX_HIP(hipGetLastError());
 }

@@ -58,6 +58,26 @@ __device__ __forceinline__ float gelu_erf(float x) {
 
 inline unsigned ceil_div(size_t a, size_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 
+// ---- opt-in kernel timing (irx_profile_enable / irx_profile_read) ----
+
+enum KernelFamily { kFamGemm, kFamIcl, kFamIclMerge, kFamSmall, kFamNorm, kFamGlue, kFamCount };
+
+// Records HIP events around one launch on `stream` while profiling is on,
+// with the launch's algorithmic FLOPs and minimal HBM bytes.
+class KernelTimer {
+  public:
+    KernelTimer(KernelFamily family, hipStream_t stream, double flops, double bytes);
+    ~KernelTimer();
+    KernelTimer(const KernelTimer &) = delete;
+    KernelTimer &operator=(const KernelTimer &) = delete;
+
+  private:
+    KernelFamily family_;
+    hipStream_t stream_;
+    double flops_, bytes_;
+    hipEvent_t start_ = nullptr, stop_ = nullptr;
+};
+
 // ---- launchers (defined in the kernel translation units) ----
 
 // Where a product writes element (m, n): segments of `col_seg` columns go to

@@ -175,6 +175,9 @@ void launch(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, BM), tiles_n = (int)ceil_div(args.n, BN);
     int tiles = tiles_m * tiles_n;
     int per_xcd = (tiles + 7) / 8;
+    const double m = args.m, n = args.n, k = args.k;
+    const double resid = (args.epilogue & (kEpiResidual | kEpiQass)) ? m * n : 0.0;
+    KernelTimer timer(kFamGemm, stream, 2.0 * m * n * k, 4.0 * (m * k + n * k + m * n + resid));
     hipLaunchKernelGGL((gemm_kernel<BM, BN>), dim3(per_xcd * 8), dim3(256), 0, stream, args, tiles_m, tiles_n,
                        per_xcd);
     IRX_HIP(hipGetLastError());

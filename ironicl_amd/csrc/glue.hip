@@ -149,6 +149,7 @@ void layer_norm(const float *x, long long ldx, const float *weight, const float 
     if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(y) & 15) || (ldx & 3) || (ldy & 3))
         fail(3, "layer norm operands must be 16-byte aligned");
     dim3 grid(ceil_div(rows, 4));
+    KernelTimer timer(kFamNorm, stream, 8.0 * rows * width, 8.0 * rows * width);
     if (width == 128)
         hipLaunchKernelGGL(layer_norm_kernel<128>, grid, dim3(256), 0, stream, x, ldx, weight, bias, y, ldy, rows);
     else if (width == 512)
@@ -162,6 +163,7 @@ void column_input(const float *x, long long x_estimator_stride, int b, int rows,
                   const float *in_b, const float *labels, float *state, uint8_t *missing_rows, hipStream_t stream) {
     long long total = (long long)b * h * rows * kColumnDim;
     if (total <= 0) return;
+    KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * total + 4.0 * b * rows * h);
     hipLaunchKernelGGL(column_input_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, x, x_estimator_stride, b, rows, h, in_w,
                        in_b, labels, state, missing_rows);
     IRX_HIP(hipGetLastError());
@@ -170,6 +172,7 @@ void column_input(const float *x, long long x_estimator_stride, int b, int rows,
 void build_rows(const float *state, int b, int rows, int h, const float *cls, float *seq, hipStream_t stream) {
     long long total = (long long)b * rows * (h + kReserved) * kColumnDim;
     if (total <= 0) return;
+    KernelTimer timer(kFamGlue, stream, 0.0, 8.0 * total);
     hipLaunchKernelGGL(build_rows_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, state, b, rows, h, cls,
                        seq);
     IRX_HIP(hipGetLastError());
@@ -178,12 +181,14 @@ void build_rows(const float *state, int b, int rows, int h, const float *cls, fl
 void gather_cls(const float *seq, long long seqs, int len, float *cls, hipStream_t stream) {
     long long total = seqs * kReserved * kColumnDim;
     if (total <= 0) return;
+    KernelTimer timer(kFamGlue, stream, 0.0, 8.0 * total);
     hipLaunchKernelGGL(gather_cls_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, seq, seqs, len, cls);
     IRX_HIP(hipGetLastError());
 }
 
 void add_inplace(float *y, const float *x, long long count, hipStream_t stream) {
     if (count <= 0) return;
+    KernelTimer timer(kFamGlue, stream, 0.0, 12.0 * count);
     hipLaunchKernelGGL(add_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, y, x, count);
     IRX_HIP(hipGetLastError());
 }
@@ -191,6 +196,7 @@ void add_inplace(float *y, const float *x, long long count, hipStream_t stream) 
 void repeat_rows(const float *src, long long src_floats, long long copies, float *dst, hipStream_t stream) {
     long long total = src_floats * copies;
     if (total <= 0) return;
+    KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * total + 4.0 * src_floats);
     hipLaunchKernelGGL(repeat_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, src, src_floats, copies,
                        dst);
     IRX_HIP(hipGetLastError());
@@ -198,12 +204,14 @@ void repeat_rows(const float *src, long long src_floats, long long copies, float
 
 void count_nonfinite(const float *x, long long count, unsigned *counter, hipStream_t stream) {
     if (count <= 0) return;
+    KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * count);
     hipLaunchKernelGGL(nonfinite_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, x, count, counter);
     IRX_HIP(hipGetLastError());
 }
 
 void fill_zero(float *x, long long count, hipStream_t stream) {
     if (count <= 0) return;
+    KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * count);
     hipLaunchKernelGGL(zero_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, x, count);
     IRX_HIP(hipGetLastError());
 }

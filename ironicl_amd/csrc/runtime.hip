@@ -30,6 +30,61 @@ void check_hip(hipError_t err, const char *what) {
     fail(status, std::string("ROCm: ") + what + ": " + hipGetErrorString(err));
 }
 
+// ---- kernel timing ----
+
+namespace {
+struct PendingTiming {
+    KernelFamily family;
+    hipEvent_t start, stop;
+    double flops, bytes;
+};
+struct FamilyTotals {
+    uint64_t launches = 0;
+    double ms = 0, flops = 0, bytes = 0;
+};
+std::atomic<bool> g_profiling{false};
+std::mutex g_profile_mu;
+std::vector<PendingTiming> g_pending;
+FamilyTotals g_totals[kFamCount];
+const char *const kFamilyNames[kFamCount] = {"gemm", "icl_attention", "icl_merge", "small_attention",
+                                             "layer_norm", "glue"};
+
+void drain_timings() {
+    for (auto &p : g_pending) {
+        float ms = 0.f;
+        if (hipEventSynchronize(p.stop) == hipSuccess && hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+            FamilyTotals &t = g_totals[p.family];
+            t.launches += 1, t.ms += ms, t.flops += p.flops, t.bytes += p.bytes;
+        }
+        (void)hipEventDestroy(p.start);
+        (void)hipEventDestroy(p.stop);
+    }
+    g_pending.clear();
+}
+}  // namespace
+
+KernelTimer::KernelTimer(KernelFamily family, hipStream_t stream, double flops, double bytes)
+    : family_(family), stream_(stream), flops_(flops), bytes_(bytes) {
+    if (!g_profiling.load(std::memory_order_relaxed)) return;
+    if (hipEventCreate(&start_) != hipSuccess || hipEventCreate(&stop_) != hipSuccess ||
+        hipEventRecord(start_, stream_) != hipSuccess) {
+        if (start_) (void)hipEventDestroy(start_);
+        if (stop_) (void)hipEventDestroy(stop_);
+        start_ = stop_ = nullptr;
+    }
+}
+
+KernelTimer::~KernelTimer() {
+    if (!start_) return;
+    if (hipEventRecord(stop_, stream_) != hipSuccess) {
+        (void)hipEventDestroy(start_);
+        (void)hipEventDestroy(stop_);
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_profile_mu);
+    g_pending.push_back({family_, start_, stop_, flops_, bytes_});
+}
+
 namespace {
 
 // ---- device memory ----
@@ -1036,6 +1091,32 @@ int irx_predictor_predict_device(irx_predictor *predictor, const float *x_device
         set_device(predictor->weights->device);
         predict_common(predictor, x_device, q, logits_device, cpu_rows, nullptr, nullptr);
         IRX_HIP(hipStreamSynchronize(predictor->stream));
+    });
+}
+
+// ---- kernel timing ----
+
+int irx_profile_enable(int enable) {
+    return guarded("irx_profile_enable", [&] {
+        std::lock_guard<std::mutex> lock(g_profile_mu);
+        drain_timings();
+        if (enable)
+            for (auto &t : g_totals) t = FamilyTotals{};
+        g_profiling.store(enable != 0);
+    });
+}
+
+int irx_profile_read(const char *family, irx_kernel_stats *out) {
+    return guarded("irx_profile_read", [&] {
+        if (!family || !out) fail(IRX_INVALID_ARGUMENT, "null argument");
+        int f = -1;
+        for (int i = 0; i < kFamCount; ++i)
+            if (std::strcmp(family, kFamilyNames[i]) == 0) f = i;
+        if (f < 0) fail(IRX_INVALID_ARGUMENT, std::string("unknown kernel family '") + family + "'");
+        std::lock_guard<std::mutex> lock(g_profile_mu);
+        drain_timings();
+        const FamilyTotals &t = g_totals[f];
+        out->launches = t.launches, out->milliseconds = t.ms, out->flops = t.flops, out->bytes = t.bytes;
     });
 }
 

@@ -51,6 +51,11 @@ class ContextTensors(ctypes.Structure):
                 ("cls_tokens", _CF), ("budget", _sz)]
 
 
+class KernelStats(ctypes.Structure):
+    _fields_ = [("launches", ctypes.c_uint64), ("milliseconds", ctypes.c_double), ("flops", ctypes.c_double),
+                ("bytes", ctypes.c_double)]
+
+
 # Every entry point include/ironicl_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "irx_last_error": (ctypes.c_char_p, []),
@@ -80,6 +85,8 @@ SIGNATURES = {
                                              PROGRESS, ctypes.c_void_p]),
     "irx_predictor_predict_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p,
                                                     ctypes.POINTER(ctypes.c_uint8)]),
+    "irx_profile_enable": (ctypes.c_int, [ctypes.c_int]),
+    "irx_profile_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(KernelStats)]),
     "irx_test_icl_attention": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
     "irx_test_products": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _CF, _CF, _sz, _sz, _sz, _sz, _F, _F]),
     "irx_test_layer_norm": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _F]),
@@ -122,6 +129,19 @@ def fptr(a: np.ndarray | None):
         return None
     assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
     return a.ctypes.data_as(_F)
+
+
+KERNEL_FAMILIES = ("gemm", "icl_attention", "icl_merge", "small_attention", "layer_norm", "glue")
+
+
+def profile_enable(enable: bool = True) -> None:
+    check(lib().irx_profile_enable(1 if enable else 0))
+
+
+def profile_read(family: str) -> dict:
+    s = KernelStats()
+    check(lib().irx_profile_read(family.encode(), ctypes.byref(s)))
+    return {"launches": int(s.launches), "milliseconds": s.milliseconds, "flops": s.flops, "bytes": s.bytes}
 
 
 class Device:

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from ironicl_amd import hip
+from ironicl_amd import hip, hipmem
 from ironicl_amd import synthetic as S
 from ironicl_amd import tabicl
 from test_oracle_model import reference_lcg_data
@@ -92,14 +92,26 @@ def test_pass_rows_and_device_path_do_not_change_results(lcg):
     finally:
         ctx_gpu.set_pass_rows(512)
     np.testing.assert_allclose(small, whole, atol=1e-6, rtol=1e-6)
-    import torch
+    dx = hipmem.DeviceArray.from_host(xt)
+    dl = hipmem.DeviceArray.from_host(np.zeros((2, xt.shape[1], 10), np.float32))
+    hip.check(hip.lib().irx_predictor_predict_device(ctx_gpu.handle, dx.ptr, xt.shape[1], dl.ptr, None))
+    np.testing.assert_array_equal(dl.to_host(), whole)
 
-    dx = torch.from_numpy(xt).cuda()
-    dl = torch.zeros((2, xt.shape[1], 10), device="cuda")
-    torch.cuda.synchronize()
-    hip.check(hip.lib().irx_predictor_predict_device(ctx_gpu.handle, dx.data_ptr(), xt.shape[1], dl.data_ptr(),
-                                                     None))
-    np.testing.assert_array_equal(dl.cpu().numpy(), whole)
+
+def test_kernel_timing_records_launches(lcg):
+    *_, ctx_gpu = lcg
+    hip.profile_enable(True)
+    try:
+        ctx_gpu.predict_raw(lcg[2])
+        icl = hip.profile_read("icl_attention")
+        gemm = hip.profile_read("gemm")
+    finally:
+        hip.profile_enable(False)
+    assert icl["launches"] == 12 and icl["milliseconds"] > 0
+    assert icl["flops"] == pytest.approx(12 * 4.0 * 16 * 250 * 240 * 64)
+    assert gemm["launches"] > 50 and gemm["flops"] > 0
+    with pytest.raises(hip.HipError):
+        hip.profile_read("nonsense")
 
 
 def test_missing_marker_rows_are_flagged(lcg):
