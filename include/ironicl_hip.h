@@ -205,8 +205,18 @@ typedef struct irx_kernel_stats {
     double bytes;        /* minimal HBM bytes: operands read once, results written once */
 } irx_kernel_stats;
 
-/* Starts (enable != 0) or stops recording; starting clears the totals. */
-int irx_profile_enable(int enable);
+/* Kernel families, as bits of irx_profile_enable's mask. */
+#define IRX_PROFILE_GEMM (1u << 0)
+#define IRX_PROFILE_ICL_ATTENTION (1u << 1)
+#define IRX_PROFILE_ICL_MERGE (1u << 2)
+#define IRX_PROFILE_SMALL_ATTENTION (1u << 3)
+#define IRX_PROFILE_LAYER_NORM (1u << 4)
+#define IRX_PROFILE_GLUE (1u << 5)
+#define IRX_PROFILE_ALL 0xffffffffu
+
+/* Records the families in `families` (0 stops recording); a non-zero mask
+ * clears the totals first. Recording adds two events per recorded launch. */
+int irx_profile_enable(unsigned families);
 /* Totals of one kernel family: "gemm", "icl_attention", "icl_merge",
  * "small_attention", "layer_norm" or "glue". Waits for recorded launches. */
 int irx_profile_read(const char *family, irx_kernel_stats *out);

@@ -18,6 +18,10 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libironicl_hip.so")
 SOURCES = ["gemm.hip", "attention.hip", "glue.hip", "runtime.hip"]
+# The attention kernels take maxima of MFMA results; with IEEE mode off they
+# skip the NaN-quieting copy before every v_max (no NaN reaches a softmax:
+# inputs are checked finite and masked keys are -inf, not NaN).
+EXTRA = {"attention.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
 ARCH = "gfx950"
 
 
@@ -31,12 +35,15 @@ def hipcc() -> str:
 def flags() -> list[str]:
     return [f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-result",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            # Keep MFMA accumulators in VGPRs: the softmax and epilogues read
+            # them with VALU ops, and AGPR<->VGPR copies cost issue slots.
+            "-mllvm", "-amdgpu-mfma-vgpr-form",
             "-I", os.path.join(HERE, "..", "include")]
 
 
 def _compile(src: str) -> str:
     out = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *flags(), "-c", os.path.join(CSRC, src), "-o", out]
+    cmd = [hipcc(), *flags(), *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", out]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")

@@ -15,12 +15,13 @@
 //    its 64 output dims across the two 32-row output tiles. The online softmax
 //    state (running max, sum) is therefore per lane: a tile needs one swap
 //    between the lane halves for the max, and the output rescale is a scalar
-//    multiply. Scores live in the exp2 domain (q pre-scaled by log2(e)/8).
-//    The P^T operand of the second product is the first product's
-//    accumulator register as is; each lane fetches the V element of the key
-//    that register holds. Keys stream through double-buffered LDS tiles of 64
-//    (K rows padded to 68 floats, V columns interleaved (d, d + 32) so one
-//    8-byte read serves both output tiles).
+//    multiply (skipped when no lane's maximum moved). Scores live in the exp2
+//    domain (q pre-scaled by log2(e)/8). The P^T operand of the second
+//    product is the first product's accumulator register as is; each lane
+//    fetches the V elements of the key that register holds. The two output
+//    tiles take the even and the odd dims, so one 8-byte LDS read serves both.
+//    Keys stream through double-buffered LDS tiles of 64 (K rows padded to 68
+//    floats); only a range's last tile is clamped and masked.
 //
 //    Few queries (a prediction pass) split the keys over workgroups; each
 //    split writes its normalized partial output and log2-sum-exp, and a merge
@@ -50,7 +51,8 @@ struct IclLaunch {
 template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention p, IclLaunch g) {
     constexpr int THREADS = WAVES * 64;
-    constexpr int LOADS = kKeyTile * 16 / THREADS;  // float4 (K) and float2-pair (V) loads per thread
+    constexpr int LOADS = kKeyTile * 16 / THREADS;  // float4 loads of K and of V per thread per tile
+    constexpr int KEY_STEP = THREADS / 16;
     __shared__ __attribute__((aligned(16))) float Ks[2][kKeyTile * kKStride];
     __shared__ __attribute__((aligned(16))) float Vs[2][kKeyTile * 64];
 
@@ -89,30 +91,31 @@ __global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention 
         }
     }
 
+    // Tile staging: this thread moves keys (tid / 16) + KEY_STEP i, float4 column tid % 16.
     const float *kbase = p.k + pair * p.kv_pair_stride;
     const float *vbase = p.v + pair * p.kv_pair_stride;
-    f32x4 kload[LOADS];
-    f32x4 vload[LOADS];
+    const int lkey = tid >> 4, lcol = (tid & 15) * 4;
+    f32x4 kload[LOADS], vload[LOADS];
     auto load_tile = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            int idx = tid + THREADS * i, key = idx >> 4, c = idx & 15;
-            int gk = min(k0 + key, k_end - 1);
-            kload[i] = *reinterpret_cast<const f32x4 *>(kbase + (long long)gk * 64 + 4 * c);
-            f32x2 lo = *reinterpret_cast<const f32x2 *>(vbase + (long long)gk * 64 + 2 * c);
-            f32x2 hi = *reinterpret_cast<const f32x2 *>(vbase + (long long)gk * 64 + 32 + 2 * c);
-            vload[i] = f32x4{lo[0], hi[0], lo[1], hi[1]};
+            const int key = min(k0 + lkey + KEY_STEP * i, k_end - 1);
+            const long long off = (long long)key * 64 + lcol;
+            kload[i] = *reinterpret_cast<const f32x4 *>(kbase + off);
+            vload[i] = *reinterpret_cast<const f32x4 *>(vbase + off);
         }
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            int idx = tid + THREADS * i, key = idx >> 4, c = idx & 15;
-            *reinterpret_cast<f32x4 *>(&Ks[buf][key * kKStride + 4 * c]) = kload[i];
-            *reinterpret_cast<f32x4 *>(&Vs[buf][key * 64 + 4 * c]) = vload[i];
+            const int key = lkey + KEY_STEP * i;
+            *reinterpret_cast<f32x4 *>(&Ks[buf][key * kKStride + lcol]) = kload[i];
+            *reinterpret_cast<f32x4 *>(&Vs[buf][key * 64 + lcol]) = vload[i];
         }
     };
 
+    // O^T accumulators: o0 holds even dims d = 2i, o1 odd dims d = 2i + 1, where
+    // i = half*4 + (r&3) + 8*(r>>2) is the accumulator row of register r.
     f32x16 o0, o1;
 #pragma unroll
     for (int r = 0; r < 16; ++r) o0[r] = 0.f, o1[r] = 0.f;
@@ -126,55 +129,65 @@ __global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention 
         const bool more = k0 + kKeyTile < k_end;
         if (more) load_tile(k0 + kKeyTile);
 
-        f32x16 s[2];
+        // S^T for both 32-key blocks, accumulations interleaved.
+        f32x4 ka[8], kb[8];
+        const float *krow = &Ks[buf][r32 * kKStride + 32 * half];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-            const float *krow = &Ks[buf][(kb * 32 + r32) * kKStride + 32 * half];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                f32x4 kv = *reinterpret_cast<const f32x4 *>(krow + 4 * c);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[e], qreg[4 * c + e], s[kb], 0, 0, 0);
-            }
+        for (int c = 0; c < 8; ++c) {
+            ka[c] = *reinterpret_cast<const f32x4 *>(krow + 4 * c);
+            kb[c] = *reinterpret_cast<const f32x4 *>(krow + 32 * kKStride + 4 * c);
         }
-        // Mask keys past the range; tile maximum over this lane's 32 keys and its partner's.
-        float mt = -INFINITY;
+        f32x16 s0, s1;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int r = 0; r < 16; ++r) s0[r] = 0.f, s1[r] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[c][e], qreg[4 * c + e], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[c][e], qreg[4 * c + e], s1, 0, 0, 0);
+            }
+        // Only the last tile of a range can hold keys past it.
+        if (k0 + kKeyTile > k_end) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                int key = k0 + kb * 32 + half * 4 + (r & 3) + 8 * (r >> 2);
-                if (key >= k_end) s[kb][r] = -INFINITY;
-                mt = fmaxf(mt, s[kb][r]);
+                const int key = k0 + half * 4 + (r & 3) + 8 * (r >> 2);
+                if (key >= k_end) s0[r] = -INFINITY;
+                if (key + 32 >= k_end) s1[r] = -INFINITY;
             }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
         const float m_new = fmaxf(m_run, mt);
-        const float alpha = exp2f(m_run - m_new);
+        // Rescale only when some lane's running maximum moved (rare after the first tiles).
+        if (__any(m_new > m_run)) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o0[r] *= alpha, o1[r] *= alpha;
+        }
         m_run = m_new;
         float lsum = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int r = 0; r < 16; ++r) {
+            s0[r] = __builtin_amdgcn_exp2f(s0[r] - m_new);
+            s1[r] = __builtin_amdgcn_exp2f(s1[r] - m_new);
+            lsum += s0[r] + s1[r];
+        }
+        l_run += lsum;
+        // O^T += V^T P^T: register r of s0 / s1 is key (half*4 + (r&3) + 8*(r>>2)) of block 0 / 1.
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float e = exp2f(s[kb][r] - m_new);
-                s[kb][r] = e;
-                lsum += e;
-            }
-        l_run = l_run * alpha + lsum;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o0[r] *= alpha, o1[r] *= alpha;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                int key = kb * 32 + half * 4 + (r & 3) + 8 * (r >> 2);
-                f32x2 vv = *reinterpret_cast<const f32x2 *>(&Vs[buf][key * 64 + 2 * r32]);
-                o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[0], s[kb][r], o0, 0, 0, 0);
-                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[1], s[kb][r], o1, 0, 0, 0);
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int key = half * 4 + (r & 3) + 8 * (r >> 2);
+            const f32x2 v0 = *reinterpret_cast<const f32x2 *>(&Vs[buf][key * 64 + 2 * r32]);
+            const f32x2 v1 = *reinterpret_cast<const f32x2 *>(&Vs[buf][(key + 32) * 64 + 2 * r32]);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[0], s0[r], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[1], s0[r], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[0], s1[r], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[1], s1[r], o1, 0, 0, 0);
+        }
         if (more) store_tile(buf ^ 1);
         __syncthreads();
         buf ^= 1;
@@ -183,24 +196,19 @@ __global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention 
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     if (qrow >= p.q_rows) return;
     const float inv = 1.0f / l_tot;
+    float *dst;
     if (g.splits == 1) {
         const int b = pair / kHeads, head = pair - b * kHeads;
-        float *dst = p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            int d = half * 4 + (r & 3) + 8 * (r >> 2);
-            dst[d] = o0[r] * inv;
-            dst[32 + d] = o1[r] * inv;
-        }
+        dst = p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64;
     } else {
-        float *dst = p.partial + (((long long)split * p.pairs + pair) * g.q_padded + qrow) * 65;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            int d = half * 4 + (r & 3) + 8 * (r >> 2);
-            dst[d] = o0[r] * inv;
-            dst[32 + d] = o1[r] * inv;
-        }
+        dst = p.partial + (((long long)split * p.pairs + pair) * g.q_padded + qrow) * 65;
         if (half == 0) dst[64] = m_run + log2f(l_tot);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = half * 4 + (r & 3) + 8 * (r >> 2);
+        dst[2 * i] = o0[r] * inv;
+        dst[2 * i + 1] = o1[r] * inv;
     }
 }
 
@@ -219,7 +227,7 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
     float num = 0.f, den = 0.f;
     for (int s = 0; s < splits; ++s) {
         const float *part = p.partial + (((long long)s * p.pairs + pair) * q_padded + qrow) * 65;
-        float w = exp2f(part[64] - mx);
+        float w = __builtin_amdgcn_exp2f(part[64] - mx);
         num += w * part[d];
         den += w;
     }
@@ -338,7 +346,7 @@ __global__ __launch_bounds__(64) void small_attention_kernel(SmallAttention p, i
                 mt = fmaxf(mt, s[j]);
             }
             const float m_new = fmaxf(m_run, mt);
-            const float alpha = exp2f(m_run - m_new);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             m_run = m_new;
             l_run *= alpha;
 #pragma unroll
@@ -346,7 +354,7 @@ __global__ __launch_bounds__(64) void small_attention_kernel(SmallAttention p, i
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 if (j < nj) {
-                    const float e = exp2f(s[j] - m_new);
+                    const float e = __builtin_amdgcn_exp2f(s[j] - m_new);
                     l_run += e;
                     const float *vr = &Vs[(j0 + j) * 16];
 #pragma unroll

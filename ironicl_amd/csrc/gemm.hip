@@ -5,14 +5,12 @@
 // A is [M, K] activations, W is [N, K] in PyTorch Linear layout, so both
 // operands are K-contiguous.
 //
-// Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a BM x BN tile; each
-// wave a (BM/2) x (BN/2) block of 32 x 32 v_mfma_f32_32x32x2f32 tiles. K runs
-// in 16-deep steps through double-buffered LDS, one barrier per step, with
-// the next step's global loads in flight during the current step's MFMAs.
-// Within a 16-deep step, lanes 0-31 feed k = 0..7 and lanes 32-63 feed
-// k = 8..15 (one MFMA consumes one k from each half), so every lane reads
-// its eight operands as two 16-byte LDS loads; rows are padded to 20 floats
-// so a half-wave's 16-byte reads hit distinct banks.
+// Two kernels, both on v_mfma_f32_32x32x2f32: tiled (BM x BN per workgroup,
+// 32-deep K steps through double-buffered LDS, one barrier per step, the next
+// step's global loads in flight during the MFMAs; LDS rows padded to 36
+// floats so a half-wave's 16-byte reads hit distinct banks) for products with
+// many tiles, and split-K (a 32 x 32 tile per workgroup, K split over its four
+// waves, LDS reduction) for the small ones of a prediction pass.
 //
 // Workgroups walk tiles XCD by XCD: the dispatcher sends workgroup i to XCD
 // i % 8, so tile (i % 8) * per_xcd + i / 8 gives each XCD one contiguous band
@@ -25,8 +23,8 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 16;
-constexpr int kLdsStride = 20;
+constexpr int kBK = 32;
+constexpr int kLdsStride = 36;
 
 __device__ __forceinline__ long long col_offset(const OutMap &o, int n) {
     int seg = n / o.col_seg;
@@ -36,10 +34,35 @@ __device__ __forceinline__ long long col_offset(const OutMap &o, int n) {
     return plane * o.plane_stride + head * o.head_stride + within;
 }
 
+// Epilogue of one accumulator value at (row, col): bias, then GELU, residual
+// or the QASS gate, then the output map.
+__device__ __forceinline__ void store_out(const GemmArgs &p, bool grouped, int row, int col, long long coff,
+                                          float bias, float acc) {
+    float v = acc + bias;
+    if (p.epilogue & kEpiGelu) v = gelu_erf(v);
+    if (p.epilogue & kEpiResidual) v += p.residual[(long long)row * p.ldr + col];
+    if (p.epilogue & kEpiQass) {
+        const int head = (row / p.qass_rows) % kHeads;
+        v = p.residual[(long long)row * p.ldr + col] * p.qass_base[head * p.n + col] * (1.0f + tanhf(v));
+    }
+    long long roff;
+    if (grouped) {
+        int g = row / p.out.rows_per_group;
+        roff = g * p.out.group_stride + (long long)(row - g * p.out.rows_per_group) * p.out.ldc;
+    } else {
+        roff = (long long)row * p.out.ldc;
+    }
+    p.c[roff + coff] = v;
+}
+
+// Large products: a BM x BN tile per 256-thread workgroup (2 x 2 waves of
+// (BM/2) x (BN/2)), K in 32-deep steps through double-buffered LDS. Within a
+// step lanes 0-31 feed k = 0..15 and lanes 32-63 k = 16..31, one k from each
+// half per MFMA, so a lane reads its 16 operands as four 16-byte LDS loads.
 template <int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
     constexpr int MI = BM / 64, NI = BN / 64;
-    constexpr int A_LOADS = BM / 64, B_LOADS = BN / 64;
+    constexpr int A_LOADS = BM * kBK / 4 / 256, B_LOADS = BN * kBK / 4 / 256;
     __shared__ __attribute__((aligned(16))) float As[2][BM * kLdsStride];
     __shared__ __attribute__((aligned(16))) float Bs[2][BN * kLdsStride];
 
@@ -52,38 +75,29 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, int tiles_m, int 
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, r32 = lane & 31;
 
-    // Global loads: thread t covers float4 (row = idx / 4, k4 = idx % 4), idx = t + 256 i.
+    // Global loads: thread t covers float4 (row = idx / 8, k4 = idx % 8), idx = t + 256 i.
     const float *a_src[A_LOADS];
-    bool a_ok[A_LOADS];
     int a_lds[A_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-        int idx = tid + 256 * i, row = idx >> 2, k4 = idx & 3;
-        int grow = m0 + row;
-        a_ok[i] = grow < p.m;
-        a_src[i] = p.a + (long long)(a_ok[i] ? grow : 0) * p.lda + k4 * 4;
+        int idx = tid + 256 * i, row = idx >> 3, k4 = idx & 7;
+        a_src[i] = p.a + (long long)min(m0 + row, p.m - 1) * p.lda + k4 * 4;
         a_lds[i] = row * kLdsStride + k4 * 4;
     }
     const float *b_src[B_LOADS];
-    bool b_ok[B_LOADS];
     int b_lds[B_LOADS];
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-        int idx = tid + 256 * i, row = idx >> 2, k4 = idx & 3;
-        int gcol = n0 + row;
-        b_ok[i] = gcol < p.n;
-        b_src[i] = p.w + (long long)(b_ok[i] ? gcol : 0) * p.k + k4 * 4;
+        int idx = tid + 256 * i, row = idx >> 3, k4 = idx & 7;
+        b_src[i] = p.w + (long long)min(n0 + row, p.n - 1) * p.k + k4 * 4;
         b_lds[i] = row * kLdsStride + k4 * 4;
     }
-    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
     f32x4 a_reg[A_LOADS], b_reg[B_LOADS];
     auto load_tile = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < A_LOADS; ++i)
-            a_reg[i] = a_ok[i] ? *reinterpret_cast<const f32x4 *>(a_src[i] + k0) : zero4;
+        for (int i = 0; i < A_LOADS; ++i) a_reg[i] = *reinterpret_cast<const f32x4 *>(a_src[i] + k0);
 #pragma unroll
-        for (int i = 0; i < B_LOADS; ++i)
-            b_reg[i] = b_ok[i] ? *reinterpret_cast<const f32x4 *>(b_src[i] + k0) : zero4;
+        for (int i = 0; i < B_LOADS; ++i) b_reg[i] = *reinterpret_cast<const f32x4 *>(b_src[i] + k0);
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
@@ -104,27 +118,25 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, int tiles_m, int 
     load_tile(0);
     store_tile(0);
     __syncthreads();
-    const int a_row = (wm * (BM / 2) + r32) * kLdsStride + 8 * half;
-    const int b_row = (wn * (BN / 2) + r32) * kLdsStride + 8 * half;
+    const int a_row = (wm * (BM / 2) + r32) * kLdsStride + 16 * half;
+    const int b_row = (wn * (BN / 2) + r32) * kLdsStride + 16 * half;
     for (int kt = 0; kt < ktiles; ++kt) {
         const int buf = kt & 1;
         const bool more = kt + 1 < ktiles;
         if (more) load_tile((kt + 1) * kBK);
-        f32x4 af[MI][2], bf[NI][2];
+        f32x4 af[MI][4], bf[NI][4];
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-            const float *s = &As[buf][a_row + i * 32 * kLdsStride];
-            af[i][0] = *reinterpret_cast<const f32x4 *>(s);
-            af[i][1] = *reinterpret_cast<const f32x4 *>(s + 4);
-        }
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-            const float *s = &Bs[buf][b_row + j * 32 * kLdsStride];
-            bf[j][0] = *reinterpret_cast<const f32x4 *>(s);
-            bf[j][1] = *reinterpret_cast<const f32x4 *>(s + 4);
-        }
+            for (int c = 0; c < 4; ++c)
+                af[i][c] = *reinterpret_cast<const f32x4 *>(&As[buf][a_row + i * 32 * kLdsStride + 4 * c]);
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                bf[j][c] = *reinterpret_cast<const f32x4 *>(&Bs[buf][b_row + j * 32 * kLdsStride + 4 * c]);
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -144,30 +156,78 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, int tiles_m, int 
         const long long coff = col_offset(p.out, col);
         const float bias = p.bias ? p.bias[col] : 0.f;
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * (BM / 2) + i * 32 + half * 4 + (r & 3) + 8 * (r >> 2);
-                if (row >= p.m) continue;
-                float v = acc[i][j][r] + bias;
-                if (p.epilogue & kEpiGelu) v = gelu_erf(v);
-                if (p.epilogue & kEpiResidual) v += p.residual[(long long)row * p.ldr + col];
-                if (p.epilogue & kEpiQass) {
-                    const int head = (row / p.qass_rows) % kHeads;
-                    v = p.residual[(long long)row * p.ldr + col] * p.qass_base[head * p.n + col] *
-                        (1.0f + tanhf(v));
-                }
-                long long roff;
-                if (grouped) {
-                    int g = row / p.out.rows_per_group;
-                    roff = g * p.out.group_stride + (long long)(row - g * p.out.rows_per_group) * p.out.ldc;
-                } else {
-                    roff = (long long)row * p.out.ldc;
-                }
-                p.c[roff + coff] = v;
+                if (row < p.m) store_out(p, grouped, row, col, coff, bias, acc[i][j][r]);
             }
-        }
     }
+}
+
+// Small products (few output tiles): a 32 x 32 tile per workgroup whose four
+// waves each take a quarter of K, reading their operands straight from L2 in
+// MFMA order (one 16-deep step ahead), then reduce through LDS; each wave
+// finishes four of the sixteen accumulator registers.
+__global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
+    __shared__ float red[4][16][64];
+    const int bid = blockIdx.x;
+    const int tile = (bid % 8) * per_xcd + bid / 8;
+    if (tile >= tiles_m * tiles_n) return;
+    const int tm = tile / tiles_n, tn = tile - (tile / tiles_n) * tiles_n;
+    const int m0 = tm * 32, n0 = tn * 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = lane >> 5, r32 = lane & 31;
+    const int kq = p.k / 4;
+    const float *a = p.a + (long long)min(m0 + r32, p.m - 1) * p.lda + wave * kq + 8 * half;
+    const float *b = p.w + (long long)min(n0 + r32, p.n - 1) * p.k + wave * kq + 8 * half;
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    f32x4 a0 = *reinterpret_cast<const f32x4 *>(a), a1 = *reinterpret_cast<const f32x4 *>(a + 4);
+    f32x4 b0 = *reinterpret_cast<const f32x4 *>(b), b1 = *reinterpret_cast<const f32x4 *>(b + 4);
+    const int steps = kq / 16;
+    for (int s = 0; s < steps; ++s) {
+        f32x4 na0 = a0, na1 = a1, nb0 = b0, nb1 = b1;
+        if (s + 1 < steps) {
+            const int off = 16 * (s + 1);
+            na0 = *reinterpret_cast<const f32x4 *>(a + off);
+            na1 = *reinterpret_cast<const f32x4 *>(a + off + 4);
+            nb0 = *reinterpret_cast<const f32x4 *>(b + off);
+            nb1 = *reinterpret_cast<const f32x4 *>(b + off + 4);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[t], b0[t], acc, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[t], b1[t], acc, 0, 0, 0);
+        a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    const bool grouped = p.out.rows_per_group < p.m;
+    const int col = n0 + r32;
+    if (col >= p.n) return;
+    const long long coff = col_offset(p.out, col);
+    const float bias = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const int r = wave * 4 + rr;
+        const float v = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
+        const int row = m0 + half * 4 + (r & 3) + 8 * (r >> 2);
+        if (row < p.m) store_out(p, grouped, row, col, coff, bias, v);
+    }
+}
+
+struct Flops {
+    double flops, bytes;
+};
+
+Flops work(const GemmArgs &args) {
+    const double m = args.m, n = args.n, k = args.k;
+    const double resid = (args.epilogue & (kEpiResidual | kEpiQass)) ? m * n : 0.0;
+    return {2.0 * m * n * k, 4.0 * (m * k + n * k + m * n + resid)};
 }
 
 template <int BM, int BN>
@@ -175,11 +235,20 @@ void launch(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, BM), tiles_n = (int)ceil_div(args.n, BN);
     int tiles = tiles_m * tiles_n;
     int per_xcd = (tiles + 7) / 8;
-    const double m = args.m, n = args.n, k = args.k;
-    const double resid = (args.epilogue & (kEpiResidual | kEpiQass)) ? m * n : 0.0;
-    KernelTimer timer(kFamGemm, stream, 2.0 * m * n * k, 4.0 * (m * k + n * k + m * n + resid));
+    const Flops f = work(args);
+    KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
     hipLaunchKernelGGL((gemm_kernel<BM, BN>), dim3(per_xcd * 8), dim3(256), 0, stream, args, tiles_m, tiles_n,
                        per_xcd);
+    IRX_HIP(hipGetLastError());
+}
+
+void launch_splitk(const GemmArgs &args, hipStream_t stream) {
+    int tiles_m = (int)ceil_div(args.m, 32), tiles_n = (int)ceil_div(args.n, 32);
+    int tiles = tiles_m * tiles_n;
+    int per_xcd = (tiles + 7) / 8;
+    const Flops f = work(args);
+    KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
+    hipLaunchKernelGGL(gemm_splitk_kernel, dim3(per_xcd * 8), dim3(256), 0, stream, args, tiles_m, tiles_n, per_xcd);
     IRX_HIP(hipGetLastError());
 }
 
@@ -187,15 +256,18 @@ void launch(const GemmArgs &args, hipStream_t stream) {
 
 void gemm(const GemmArgs &args, hipStream_t stream) {
     if (args.m <= 0 || args.n <= 0) return;
-    if (args.k <= 0 || args.k % kBK != 0 || args.lda % 4 != 0 ||
+    if (args.k <= 0 || args.k % 64 != 0 || args.lda % 4 != 0 ||
         (reinterpret_cast<uintptr_t>(args.a) & 15) || (reinterpret_cast<uintptr_t>(args.w) & 15))
-        fail(3, "gemm: K must be a positive multiple of 16 with 16-byte aligned rows");
+        fail(3, "gemm: K must be a positive multiple of 64 with 16-byte aligned rows");
     if ((args.epilogue & (kEpiResidual | kEpiQass)) && !args.residual)
         fail(3, "gemm: residual epilogue without a residual");
-    // Large products take 128 x 128 tiles; ones that would leave the 256 CUs
-    // idle take 64 x 64.
-    long long big_tiles = (long long)ceil_div(args.m, 128) * ceil_div(args.n, 128);
-    if (big_tiles >= 512)
+    // Products with few 64 x 64 tiles split K over a workgroup's waves; large
+    // ones take 128 x 128 tiles, the rest 64 x 64.
+    const long long small_tiles = (long long)ceil_div(args.m, 64) * ceil_div(args.n, 64);
+    const long long big_tiles = (long long)ceil_div(args.m, 128) * ceil_div(args.n, 128);
+    if (small_tiles < 256)
+        launch_splitk(args, stream);
+    else if (big_tiles >= 512)
         launch<128, 128>(args, stream);
     else
         launch<64, 64>(args, stream);

@@ -42,7 +42,7 @@ struct FamilyTotals {
     uint64_t launches = 0;
     double ms = 0, flops = 0, bytes = 0;
 };
-std::atomic<bool> g_profiling{false};
+std::atomic<unsigned> g_profiling{0};
 std::mutex g_profile_mu;
 std::vector<PendingTiming> g_pending;
 FamilyTotals g_totals[kFamCount];
@@ -65,7 +65,7 @@ void drain_timings() {
 
 KernelTimer::KernelTimer(KernelFamily family, hipStream_t stream, double flops, double bytes)
     : family_(family), stream_(stream), flops_(flops), bytes_(bytes) {
-    if (!g_profiling.load(std::memory_order_relaxed)) return;
+    if (!(g_profiling.load(std::memory_order_relaxed) & (1u << family))) return;
     if (hipEventCreate(&start_) != hipSuccess || hipEventCreate(&stop_) != hipSuccess ||
         hipEventRecord(start_, stream_) != hipSuccess) {
         if (start_) (void)hipEventDestroy(start_);
@@ -1096,13 +1096,13 @@ int irx_predictor_predict_device(irx_predictor *predictor, const float *x_device
 
 // ---- kernel timing ----
 
-int irx_profile_enable(int enable) {
+int irx_profile_enable(unsigned families) {
     return guarded("irx_profile_enable", [&] {
         std::lock_guard<std::mutex> lock(g_profile_mu);
         drain_timings();
-        if (enable)
+        if (families)
             for (auto &t : g_totals) t = FamilyTotals{};
-        g_profiling.store(enable != 0);
+        g_profiling.store(families);
     });
 }
 

@@ -85,7 +85,7 @@ SIGNATURES = {
                                              PROGRESS, ctypes.c_void_p]),
     "irx_predictor_predict_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p,
                                                     ctypes.POINTER(ctypes.c_uint8)]),
-    "irx_profile_enable": (ctypes.c_int, [ctypes.c_int]),
+    "irx_profile_enable": (ctypes.c_int, [ctypes.c_uint]),
     "irx_profile_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(KernelStats)]),
     "irx_test_icl_attention": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
     "irx_test_products": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _CF, _CF, _sz, _sz, _sz, _sz, _F, _F]),
@@ -134,8 +134,15 @@ def fptr(a: np.ndarray | None):
 KERNEL_FAMILIES = ("gemm", "icl_attention", "icl_merge", "small_attention", "layer_norm", "glue")
 
 
-def profile_enable(enable: bool = True) -> None:
-    check(lib().irx_profile_enable(1 if enable else 0))
+def profile_enable(families=True) -> None:
+    """Record the named kernel families (True: all; False or (): none)."""
+    if families is True:
+        mask = 0xFFFFFFFF
+    elif not families:
+        mask = 0
+    else:
+        mask = sum(1 << KERNEL_FAMILIES.index(f) for f in families)
+    check(lib().irx_profile_enable(mask))
 
 
 def profile_read(family: str) -> dict:
