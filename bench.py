@@ -97,6 +97,8 @@ def main() -> int:
     ap.add_argument("--pass-rows", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run the plain copy kernel over BYTES (reference for traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -105,6 +107,11 @@ def main() -> int:
 
     from ironicl_amd import hip, hipmem, synthetic, tabicl
 
+    if args.copy_calibration:
+        device = hip.Device(0)
+        hip.check(hip.lib().irx_test_copy(device.handle, args.copy_calibration // 4))
+        print(json.dumps({"copy_bytes": args.copy_calibration}), flush=True)
+        return 0
     w = synthetic.WORKLOADS[WORKLOAD]
     log("generating weights and data")
     weights = synthetic.random_weights("classifier")

@@ -235,6 +235,9 @@ int irx_test_products(irx_device *device, const float *x, const float *w1, const
 /* LayerNorm over width (128 or 512), eps 1e-5. */
 int irx_test_layer_norm(irx_device *device, const float *x, const float *weight, const float *bias,
                         size_t rows, size_t width, float *out);
+/* A plain device-to-device copy of `floats` floats by a one-float4-per-thread
+ * kernel: the known-size reference for HBM traffic counters. */
+int irx_test_copy(irx_device *device, size_t floats);
 /* 16-wide-head attention: q [heads, query_rows, 16], k and v [heads, rows, 16]. */
 int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v,
                              size_t heads, size_t query_rows, size_t rows, float *out);

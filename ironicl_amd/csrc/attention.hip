@@ -48,7 +48,10 @@ struct IclLaunch {
     int qtiles, splits, keys_per_split, per_xcd, q_padded;
 };
 
-template <int WAVES>
+// SPLIT: the keys are split over workgroups and each writes a partial output
+// and its log2-sum-exp (prediction passes); otherwise the output is final
+// (the build's self-attention over all training rows).
+template <int WAVES, bool SPLIT>
 __global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention p, IclLaunch g) {
     constexpr int THREADS = WAVES * 64;
     constexpr int LOADS = kKeyTile * 16 / THREADS;  // float4 loads of K and of V per thread per tile
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention 
     if (qrow >= p.q_rows) return;
     const float inv = 1.0f / l_tot;
     float *dst;
-    if (g.splits == 1) {
+    if constexpr (!SPLIT) {
         const int b = pair / kHeads, head = pair - b * kHeads;
         dst = p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64;
     } else {
@@ -398,8 +401,12 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
     {
         const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
         KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, 4.0 * 64.0 * pairs * (2.0 * kv + 2.0 * q));
-        hipLaunchKernelGGL(icl_attention_kernel<kIclWaves>, dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
-                           args, g);
+        if (g.splits > 1)
+            hipLaunchKernelGGL((icl_attention_kernel<kIclWaves, true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
+                               stream, args, g);
+        else
+            hipLaunchKernelGGL((icl_attention_kernel<kIclWaves, false>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
+                               stream, args, g);
         IRX_HIP(hipGetLastError());
     }
     if (g.splits > 1) {

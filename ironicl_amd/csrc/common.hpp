@@ -121,7 +121,7 @@ struct GemmArgs {
     int epilogue;
 };
 
-// C = epilogue(A W^T + bias) on FP32 MFMA. K must be a multiple of 16.
+// C = epilogue(A W^T + bias) on FP32 MFMA. K must be a multiple of 64.
 void gemm(const GemmArgs &args, hipStream_t stream);
 
 // LayerNorm over `width` (128 or 512), eps 1e-5, two passes (reference.rs:223-252).
@@ -178,5 +178,6 @@ void repeat_rows(const float *src, long long src_floats, long long copies, float
                  hipStream_t stream);
 void count_nonfinite(const float *x, long long count, unsigned *counter, hipStream_t stream);
 void fill_zero(float *x, long long count, hipStream_t stream);
+void copy_floats(const float *src, float *dst, long long count, hipStream_t stream);
 
 }  // namespace irx

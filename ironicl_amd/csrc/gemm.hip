@@ -35,18 +35,20 @@ __device__ __forceinline__ long long col_offset(const OutMap &o, int n) {
 }
 
 // Epilogue of one accumulator value at (row, col): bias, then GELU, residual
-// or the QASS gate, then the output map.
-__device__ __forceinline__ void store_out(const GemmArgs &p, bool grouped, int row, int col, long long coff,
-                                          float bias, float acc) {
+// or the QASS gate, then the output map. EPI and GROUPED are compile-time so
+// each instantiation is straight-line code.
+template <int EPI, bool GROUPED>
+__device__ __forceinline__ void store_out(const GemmArgs &p, int row, int col, long long coff, float bias,
+                                          float acc) {
     float v = acc + bias;
-    if (p.epilogue & kEpiGelu) v = gelu_erf(v);
-    if (p.epilogue & kEpiResidual) v += p.residual[(long long)row * p.ldr + col];
-    if (p.epilogue & kEpiQass) {
+    if constexpr (EPI == kEpiGelu) v = gelu_erf(v);
+    if constexpr (EPI == kEpiResidual) v += p.residual[(long long)row * p.ldr + col];
+    if constexpr (EPI == kEpiQass) {
         const int head = (row / p.qass_rows) % kHeads;
         v = p.residual[(long long)row * p.ldr + col] * p.qass_base[head * p.n + col] * (1.0f + tanhf(v));
     }
     long long roff;
-    if (grouped) {
+    if constexpr (GROUPED) {
         int g = row / p.out.rows_per_group;
         roff = g * p.out.group_stride + (long long)(row - g * p.out.rows_per_group) * p.out.ldc;
     } else {
@@ -59,7 +61,7 @@ __device__ __forceinline__ void store_out(const GemmArgs &p, bool grouped, int r
 // (BM/2) x (BN/2)), K in 32-deep steps through double-buffered LDS. Within a
 // step lanes 0-31 feed k = 0..15 and lanes 32-63 k = 16..31, one k from each
 // half per MFMA, so a lane reads its 16 operands as four 16-byte LDS loads.
-template <int BM, int BN>
+template <int BM, int BN, int EPI, bool GROUPED>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
     constexpr int MI = BM / 64, NI = BN / 64;
     constexpr int A_LOADS = BM * kBK / 4 / 256, B_LOADS = BN * kBK / 4 / 256;
@@ -148,7 +150,6 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, i
     }
 
     // Epilogue. Lane (r32, half) holds column r32 and rows half*4 + (r&3) + 8*(r>>2).
-    const bool grouped = p.out.rows_per_group < p.m;
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
         const int col = n0 + wn * (BN / 2) + j * 32 + r32;
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, i
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * (BM / 2) + i * 32 + half * 4 + (r & 3) + 8 * (r >> 2);
-                if (row < p.m) store_out(p, grouped, row, col, coff, bias, acc[i][j][r]);
+                if (row < p.m) store_out<EPI, GROUPED>(p, row, col, coff, bias, acc[i][j][r]);
             }
     }
 }
@@ -169,6 +170,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, i
 // waves each take a quarter of K, reading their operands straight from L2 in
 // MFMA order (one 16-deep step ahead), then reduce through LDS; each wave
 // finishes four of the sixteen accumulator registers.
+template <int EPI, bool GROUPED>
 __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
     __shared__ float red[4][16][64];
     const int bid = blockIdx.x;
@@ -206,7 +208,6 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
-    const bool grouped = p.out.rows_per_group < p.m;
     const int col = n0 + r32;
     if (col >= p.n) return;
     const long long coff = col_offset(p.out, col);
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
         const int r = wave * 4 + rr;
         const float v = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
         const int row = m0 + half * 4 + (r & 3) + 8 * (r >> 2);
-        if (row < p.m) store_out(p, grouped, row, col, coff, bias, v);
+        if (row < p.m) store_out<EPI, GROUPED>(p, row, col, coff, bias, v);
     }
 }
 
@@ -230,26 +231,53 @@ Flops work(const GemmArgs &args) {
     return {2.0 * m * n * k, 4.0 * (m * k + n * k + m * n + resid)};
 }
 
+// Kernel of one epilogue kind and output map.
+template <template <int, bool> class K>
+void dispatch_epilogue(const GemmArgs &args, dim3 grid, hipStream_t stream, int tiles_m, int tiles_n, int per_xcd) {
+    const bool grouped = args.out.rows_per_group < args.m;
+    const Flops f = work(args);
+    KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
+#define IRX_GEMM_CASE(E)                                                                                         \
+    if (args.epilogue == E) {                                                                                    \
+        if (grouped)                                                                                             \
+            hipLaunchKernelGGL((K<E, true>::kernel), grid, dim3(256), 0, stream, args, tiles_m, tiles_n, per_xcd); \
+        else                                                                                                     \
+            hipLaunchKernelGGL((K<E, false>::kernel), grid, dim3(256), 0, stream, args, tiles_m, tiles_n, per_xcd); \
+        IRX_HIP(hipGetLastError());                                                                              \
+        return;                                                                                                  \
+    }
+    IRX_GEMM_CASE(kEpiNone)
+    IRX_GEMM_CASE(kEpiGelu)
+    IRX_GEMM_CASE(kEpiResidual)
+    IRX_GEMM_CASE(kEpiQass)
+#undef IRX_GEMM_CASE
+    fail(3, "gemm: unknown epilogue");
+}
+
+template <int BM, int BN>
+struct Tiled {
+    template <int E, bool G>
+    struct K {
+        static constexpr auto kernel = gemm_kernel<BM, BN, E, G>;
+    };
+};
+
+template <int E, bool G>
+struct SplitK {
+    static constexpr auto kernel = gemm_splitk_kernel<E, G>;
+};
+
 template <int BM, int BN>
 void launch(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, BM), tiles_n = (int)ceil_div(args.n, BN);
-    int tiles = tiles_m * tiles_n;
-    int per_xcd = (tiles + 7) / 8;
-    const Flops f = work(args);
-    KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
-    hipLaunchKernelGGL((gemm_kernel<BM, BN>), dim3(per_xcd * 8), dim3(256), 0, stream, args, tiles_m, tiles_n,
-                       per_xcd);
-    IRX_HIP(hipGetLastError());
+    int per_xcd = (tiles_m * tiles_n + 7) / 8;
+    dispatch_epilogue<Tiled<BM, BN>::template K>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
 }
 
 void launch_splitk(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, 32), tiles_n = (int)ceil_div(args.n, 32);
-    int tiles = tiles_m * tiles_n;
-    int per_xcd = (tiles + 7) / 8;
-    const Flops f = work(args);
-    KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
-    hipLaunchKernelGGL(gemm_splitk_kernel, dim3(per_xcd * 8), dim3(256), 0, stream, args, tiles_m, tiles_n, per_xcd);
-    IRX_HIP(hipGetLastError());
+    int per_xcd = (tiles_m * tiles_n + 7) / 8;
+    dispatch_epilogue<SplitK>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
 }
 
 }  // namespace

@@ -136,6 +136,13 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(const float *x, long lon
     if (__any(bad) && (threadIdx.x & 63) == 0) atomicAdd(counter, 1u);
 }
 
+// A plain copy, one float4 per thread: the reference point that scales the
+// HBM traffic counters of the other kernels.
+__global__ __launch_bounds__(256) void copy_kernel(const float *src, float *dst, long long count4) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx < count4) reinterpret_cast<f32x4 *>(dst)[idx] = reinterpret_cast<const f32x4 *>(src)[idx];
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(float *x, long long count) {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     if (idx < count) x[idx] = 0.f;
@@ -206,6 +213,15 @@ void count_nonfinite(const float *x, long long count, unsigned *counter, hipStre
     if (count <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * count);
     hipLaunchKernelGGL(nonfinite_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, x, count, counter);
+    IRX_HIP(hipGetLastError());
+}
+
+void copy_floats(const float *src, float *dst, long long count, hipStream_t stream) {
+    if (count <= 0) return;
+    if (count % 4 || (reinterpret_cast<uintptr_t>(src) & 15) || (reinterpret_cast<uintptr_t>(dst) & 15))
+        fail(3, "copy: count must be a multiple of 4 floats with 16-byte aligned buffers");
+    KernelTimer timer(kFamGlue, stream, 0.0, 8.0 * count);
+    hipLaunchKernelGGL(copy_kernel, dim3(ceil_div(count / 4, 256)), dim3(256), 0, stream, src, dst, count / 4);
     IRX_HIP(hipGetLastError());
 }
 

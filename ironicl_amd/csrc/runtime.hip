@@ -1203,6 +1203,17 @@ int irx_test_layer_norm(irx_device *device, const float *x, const float *weight,
     });
 }
 
+int irx_test_copy(irx_device *device, size_t floats) {
+    return guarded("irx_test_copy", [&] {
+        if (!device || !floats || floats % 4) fail(IRX_INVALID_ARGUMENT, "copy size must be a multiple of 4 floats");
+        set_device(device);
+        DevBuf src(floats * 4), dst(floats * 4);
+        fill_zero(src.f(), (long long)floats, nullptr);
+        copy_floats(src.f(), dst.f(), (long long)floats, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+    });
+}
+
 int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v, size_t heads,
                              size_t query_rows, size_t rows, float *out) {
     return guarded("irx_test_small_attention", [&] {
