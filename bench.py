@@ -20,6 +20,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import subprocess
 import sys
 import time
@@ -32,6 +33,9 @@ sys.path.insert(0, ROOT)
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBPS = 8000.0
 WORKLOAD = "clf-50k"
+# rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the prediction-phase ICL attention
+# launch on this workload, calibrated against a plain copy kernel.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "icl_attention_kernel_clf-50k.md")
 
 
 def log(msg: str) -> None:
@@ -49,6 +53,17 @@ def host_facts() -> dict:
     except Exception:
         pass
     return facts
+
+
+def profiled_traffic() -> int | None:
+    """HBM bytes per launch of the dominant kernel, from the committed counter
+    summary (two rocprofv3 --pmc passes scaled by the copy-kernel factors)."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch = (\d+)$", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target_s: float) -> dict:
@@ -185,7 +200,8 @@ def main() -> int:
         "peak": MFMA_FP32_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
-        "traffic": None,
+        "traffic": profiled_traffic(),
+        "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
         "avg_launch_ms": icl_ms,
         "flops_per_launch": icl_flops,
     }
