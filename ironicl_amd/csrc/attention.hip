@@ -33,6 +33,8 @@
 //    through LDS in chunks of 64, optional RoPE on queries and keys.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace irx {
 namespace {
 
@@ -41,23 +43,49 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kKeyTile = 64;
-constexpr int kKStride = 68;
 constexpr float kLog2e = 1.44269504088896340736f;
 
 struct IclLaunch {
     int qtiles, splits, keys_per_split, per_xcd, q_padded;
 };
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kIclWaves = 4;
+constexpr int kIclQueries = kIclWaves * 64;  // queries per workgroup, 64 per wave
+
+// One 64-key tile of K and V in LDS, 16 KB each, written by direct global ->
+// LDS loads (a wave-wide 16-byte load lands as 1 KB, lane after lane). K is
+// kept in 1 KB blocks b = (chunk / 4) * 4 + key / 16, each holding 16 keys x
+// 4 chunks of 4 dims at position (chunk % 4) * 16 + key % 16, so that the 16
+// lanes of a 16-byte LDS read that fetch one chunk of 16 consecutive keys
+// touch every bank once. V is key-major: a half-wave reads one key's 64 dims.
+struct IclTile {
+    float k[kKeyTile * 64];
+    float v[kKeyTile * 64];
+};
+
+__device__ __forceinline__ void wait_loads() {
+    // vmcnt(0); expcnt and lgkmcnt left at their maxima (no wait).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// Maximum / sum of a lane's value and its partner's in the other half-wave
+// (lane l and l ^ 32 hold the same query).
+__device__ __forceinline__ float halves_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // SPLIT: the keys are split over workgroups and each writes a partial output
-// and its log2-sum-exp (prediction passes); otherwise the output is final
-// (the build's self-attention over all training rows).
-template <int WAVES, bool SPLIT>
-__global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention p, IclLaunch g) {
-    constexpr int THREADS = WAVES * 64;
-    constexpr int LOADS = kKeyTile * 16 / THREADS;  // float4 loads of K and of V per thread per tile
-    constexpr int KEY_STEP = THREADS / 16;
-    __shared__ __attribute__((aligned(16))) float Ks[2][kKeyTile * kKStride];
-    __shared__ __attribute__((aligned(16))) float Vs[2][kKeyTile * 64];
+// and its log2-sum-exp, merged afterwards; otherwise the output is final.
+template <bool SPLIT>
+__global__ __launch_bounds__(kIclWaves * 64, 2) void icl_attention_kernel(IclAttention p, IclLaunch g) {
+    __shared__ __attribute__((aligned(16))) IclTile tiles[2];
 
     const int total = g.qtiles * p.pairs * g.splits;
     const int bid = blockIdx.x;
@@ -67,193 +95,263 @@ __global__ __launch_bounds__(WAVES * 64) void icl_attention_kernel(IclAttention 
     const int rest = t_id / g.qtiles;
     const int split = rest % g.splits;
     const int pair = rest / g.splits;
-    const int k_begin = split * g.keys_per_split;
-    const int k_end = min(p.kv_rows, k_begin + g.keys_per_split);
+    // Workgroup-uniform; read into scalars so the key loop runs on scalar registers.
+    const int k_begin = __builtin_amdgcn_readfirstlane(split * g.keys_per_split);
+    const int k_end = __builtin_amdgcn_readfirstlane(min(p.kv_rows, k_begin + g.keys_per_split));
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int half = lane >> 5, r32 = lane & 31;
-    const int qrow = qt * (WAVES * 32) + wave * 32 + r32;
+    // Query block j of this wave holds rows qrow0 + 32 j.
+    const int qrow0 = qt * kIclQueries + wave * 64 + r32;
 
-    // This lane's query: dims 32*half .. 32*half + 31, scaled into the exp2 domain.
-    float qreg[32];
+    // The lane's queries: dims 32*half .. 32*half + 31, scaled into the exp2 domain.
+    float qreg[2][32];
     {
         const float scale = 0.125f * kLog2e;
-        if (qrow < p.q_rows) {
-            const float *src = p.q + pair * p.q_pair_stride + (long long)qrow * 64 + 32 * half;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                f32x4 v = *reinterpret_cast<const f32x4 *>(src + 4 * c);
-                qreg[4 * c + 0] = v[0] * scale;
-                qreg[4 * c + 1] = v[1] * scale;
-                qreg[4 * c + 2] = v[2] * scale;
-                qreg[4 * c + 3] = v[3] * scale;
+        for (int j = 0; j < 2; ++j) {
+            const int qrow = qrow0 + 32 * j;
+            if (qrow < p.q_rows) {
+                const float *src = p.q + pair * p.q_pair_stride + (long long)qrow * 64 + 32 * half;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    f32x4 v = *reinterpret_cast<const f32x4 *>(src + 4 * c);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) qreg[j][4 * c + e] = v[e] * scale;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 32; ++t) qreg[j][t] = 0.f;
             }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 32; ++t) qreg[t] = 0.f;
         }
     }
 
-    // Tile staging: this thread moves keys (tid / 16) + KEY_STEP i, float4 column tid % 16.
+    // Staging: wave w moves K blocks 4w .. 4w + 3 (chunks 4w .. 4w + 3 of key
+    // blocks 0..3) and V blocks 4w .. 4w + 3 (keys 16w .. 16w + 15).
     const float *kbase = p.k + pair * p.kv_pair_stride;
     const float *vbase = p.v + pair * p.kv_pair_stride;
-    const int lkey = tid >> 4, lcol = (tid & 15) * 4;
-    f32x4 kload[LOADS], vload[LOADS];
-    auto load_tile = [&](int k0) {
+    // Lane offsets (floats) within a full tile: K key 16 i + lane % 16, chunk
+    // 4w + lane / 16; V key 16w + 4i + lane / 16, chunk lane % 16. The wave
+    // index is read into a scalar so that tile bases and LDS destinations are
+    // scalar arithmetic.
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int k_lane = (lane & 15) * 64 + 4 * (4 * wv + (lane >> 4));
+    const int v_lane = (lane >> 4) * 64 + 4 * (lane & 15);
+    auto issue_tile = [&](int k0, int buf) {
+        const float *kt = kbase + (long long)k0 * 64, *vt = vbase + (long long)(k0 + 16 * wv) * 64;
+        if (k0 + kKeyTile <= k_end) {
 #pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int key = min(k0 + lkey + KEY_STEP * i, k_end - 1);
-            const long long off = (long long)key * 64 + lcol;
-            kload[i] = *reinterpret_cast<const f32x4 *>(kbase + off);
-            vload[i] = *reinterpret_cast<const f32x4 *>(vbase + off);
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int key = lkey + KEY_STEP * i;
-            *reinterpret_cast<f32x4 *>(&Ks[buf][key * kKStride + lcol]) = kload[i];
-            *reinterpret_cast<f32x4 *>(&Vs[buf][key * 64 + lcol]) = vload[i];
-        }
-    };
-
-    // O^T accumulators: o0 holds even dims d = 2i, o1 odd dims d = 2i + 1, where
-    // i = half*4 + (r&3) + 8*(r>>2) is the accumulator row of register r.
-    f32x16 o0, o1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o0[r] = 0.f, o1[r] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
-
-    load_tile(k_begin);
-    store_tile(0);
-    __syncthreads();
-    int buf = 0;
-    for (int k0 = k_begin; k0 < k_end; k0 += kKeyTile) {
-        const bool more = k0 + kKeyTile < k_end;
-        if (more) load_tile(k0 + kKeyTile);
-
-        // S^T for both 32-key blocks, accumulations interleaved.
-        f32x4 ka[8], kb[8];
-        const float *krow = &Ks[buf][r32 * kKStride + 32 * half];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            ka[c] = *reinterpret_cast<const f32x4 *>(krow + 4 * c);
-            kb[c] = *reinterpret_cast<const f32x4 *>(krow + 32 * kKStride + 4 * c);
-        }
-        f32x16 s0, s1;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s0[r] = 0.f, s1[r] = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[c][e], qreg[4 * c + e], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[c][e], qreg[4 * c + e], s1, 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_global_load_lds(kt + i * 1024 + k_lane, (lds_void *)&tiles[buf].k[(4 * wv + i) * 256],
+                                                 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vt + i * 256 + v_lane, (lds_void *)&tiles[buf].v[(4 * wv + i) * 256],
+                                                 16, 0, 0);
             }
+        } else {
+            // A range's last tile: keys past it repeat its last key (masked later).
+            const int last = k_end - 1 - k0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kk = min(16 * i + (lane & 15), last);
+                const int vk = min(16 * wv + 4 * i + (lane >> 4), last);
+                __builtin_amdgcn_global_load_lds(kbase + (long long)(k0 + kk) * 64 + 4 * (4 * wv + (lane >> 4)),
+                                                 (lds_void *)&tiles[buf].k[(4 * wv + i) * 256], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vbase + (long long)(k0 + vk) * 64 + 4 * (lane & 15),
+                                                 (lds_void *)&tiles[buf].v[(4 * wv + i) * 256], 16, 0, 0);
+            }
+        }
+    };
+
+    // O^T accumulators of query block j: o[j][0] even dims d = 2i, o[j][1] odd
+    // dims d = 2i + 1, where i = half*4 + (r&3) + 8*(r>>2) for register r.
+    f32x16 o[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][0][r] = 0.f, o[j][1][r] = 0.f;
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    // K fragment of chunk 8*half + cc for key r32 of block 0 is at kfrag + (cc >> 2) * 1024 + (cc & 3) * 64;
+    // block 1 (keys 32..63) is 512 floats further.
+    const int kfrag = (8 * half + (r32 >> 4)) * 256 + (r32 & 15) * 4;
+
+    issue_tile(k_begin, 0);
+    int buf = 0;
+    for (int k0 = k_begin; k0 < k_end; k0 = __builtin_amdgcn_readfirstlane(k0 + kKeyTile)) {
+        wait_loads();
+        __syncthreads();
+        if (k0 + kKeyTile < k_end) issue_tile(k0 + kKeyTile, buf ^ 1);
+        const float *kt = tiles[buf].k;
+        const float *vt = tiles[buf].v;
+
+        // S^T[key, q] for key blocks 0 / 1 and query blocks 0 / 1.
+        f32x16 s[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[j][0][r] = 0.f, s[j][1][r] = 0.f;
+        // K fragments are read one chunk ahead of their MFMAs (the scheduling
+        // groups keep the compiler from sinking the reads to their first use).
+        f32x4 ka = *reinterpret_cast<const f32x4 *>(kt + kfrag);
+        f32x4 kb = *reinterpret_cast<const f32x4 *>(kt + kfrag + 512);
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) {
+            f32x4 na = ka, nb = kb;
+            if (cc < 7) {
+                const int off = kfrag + ((cc + 1) >> 2) * 1024 + ((cc + 1) & 3) * 64;
+                na = *reinterpret_cast<const f32x4 *>(kt + off);
+                nb = *reinterpret_cast<const f32x4 *>(kt + off + 512);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    s[j][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[e], qreg[j][4 * cc + e], s[j][0], 0, 0, 0);
+                    s[j][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[e], qreg[j][4 * cc + e], s[j][1], 0, 0, 0);
+                }
+            if (cc < 7) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the two DS reads
+                __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // then this chunk's MFMAs
+            }
+            ka = na, kb = nb;
+        }
         // Only the last tile of a range can hold keys past it.
         if (k0 + kKeyTile > k_end) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + half * 4 + (r & 3) + 8 * (r >> 2);
-                if (key >= k_end) s0[r] = -INFINITY;
-                if (key + 32 >= k_end) s1[r] = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    if (key >= k_end) s[j][0][r] = -INFINITY;
+                    if (key + 32 >= k_end) s[j][1][r] = -INFINITY;
+                }
             }
         }
-        float mt = -INFINITY;
+        // Online softmax per query block (exp2 domain).
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float m_new = fmaxf(m_run, mt);
-        // Rescale only when some lane's running maximum moved (rare after the first tiles).
-        if (__any(m_new > m_run)) {
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
+        for (int j = 0; j < 2; ++j) {
+            float mt = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o0[r] *= alpha, o1[r] *= alpha;
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(s[j][0][r], s[j][1][r]));
+            const float m_new = fmaxf(m_run[j], halves_max(mt));
+            // Rescale only when some lane's running maximum moved (rare after the first tiles).
+            if (__any(m_new > m_run[j])) {
+                const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+                l_run[j] *= alpha;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[j][0][r] *= alpha, o[j][1][r] *= alpha;
+            }
+            m_run[j] = m_new;
+            float lsum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[j][0][r] = __builtin_amdgcn_exp2f(s[j][0][r] - m_new);
+                s[j][1][r] = __builtin_amdgcn_exp2f(s[j][1][r] - m_new);
+                lsum += s[j][0][r] + s[j][1][r];
+            }
+            l_run[j] += lsum;
         }
-        m_run = m_new;
-        float lsum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            s0[r] = __builtin_amdgcn_exp2f(s0[r] - m_new);
-            s1[r] = __builtin_amdgcn_exp2f(s1[r] - m_new);
-            lsum += s0[r] + s1[r];
-        }
-        l_run += lsum;
-        // O^T += V^T P^T: register r of s0 / s1 is key (half*4 + (r&3) + 8*(r>>2)) of block 0 / 1.
+        // O^T += V^T P^T: register r of s[j][b] is key b*32 + half*4 + (r&3) + 8*(r>>2);
+        // the lane fetches that key's dims 2*r32 and 2*r32 + 1.
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int key = half * 4 + (r & 3) + 8 * (r >> 2);
-            const f32x2 v0 = *reinterpret_cast<const f32x2 *>(&Vs[buf][key * 64 + 2 * r32]);
-            const f32x2 v1 = *reinterpret_cast<const f32x2 *>(&Vs[buf][(key + 32) * 64 + 2 * r32]);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[0], s0[r], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[1], s0[r], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[0], s1[r], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[1], s1[r], o1, 0, 0, 0);
+            const f32x2 v0 = *reinterpret_cast<const f32x2 *>(vt + key * 64 + 2 * r32);
+            const f32x2 v1 = *reinterpret_cast<const f32x2 *>(vt + (key + 32) * 64 + 2 * r32);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                o[j][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[0], s[j][0][r], o[j][0], 0, 0, 0);
+                o[j][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[1], s[j][0][r], o[j][1], 0, 0, 0);
+                o[j][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[0], s[j][1][r], o[j][0], 0, 0, 0);
+                o[j][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[1], s[j][1][r], o[j][1], 0, 0, 0);
+            }
         }
-        if (more) store_tile(buf ^ 1);
-        __syncthreads();
         buf ^= 1;
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    if (qrow >= p.q_rows) return;
-    const float inv = 1.0f / l_tot;
-    float *dst;
-    if constexpr (!SPLIT) {
-        const int b = pair / kHeads, head = pair - b * kHeads;
-        dst = p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64;
-    } else {
-        dst = p.partial + (((long long)split * p.pairs + pair) * g.q_padded + qrow) * 65;
-        if (half == 0) dst[64] = m_run + log2f(l_tot);
-    }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = half * 4 + (r & 3) + 8 * (r >> 2);
-        dst[2 * i] = o0[r] * inv;
-        dst[2 * i + 1] = o1[r] * inv;
+    for (int j = 0; j < 2; ++j) {
+        const int qrow = qrow0 + 32 * j;
+        const float l_tot = halves_sum(l_run[j]);
+        if (qrow >= p.q_rows) continue;
+        const float inv = 1.0f / l_tot;
+        float *dst;
+        if constexpr (!SPLIT) {
+            const int b = pair / kHeads, head = pair - b * kHeads;
+            dst = p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64;
+        } else {
+            const long long row = ((long long)split * p.pairs + pair) * g.q_padded + qrow;
+            dst = p.partial + row * 64;
+            if (half == 0) p.partial[(long long)g.splits * p.pairs * g.q_padded * 64 + row] = m_run[j] + log2f(l_tot);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = half * 4 + (r & 3) + 8 * (r >> 2);
+            f32x2 v;
+            v[0] = o[j][0][r] * inv, v[1] = o[j][1][r] * inv;
+            *reinterpret_cast<f32x2 *>(dst + 2 * i) = v;
+        }
     }
 }
 
-// Merge of split partials by their log2-sum-exp, into tokens [b * q_rows + row, head * 64 + d].
+// Merge of split partials by their log2-sum-exp, into tokens [b * q_rows +
+// row, head * 64 + d]. Partial outputs are [splits, pairs, q_padded, 64],
+// followed by the log2-sum-exps [splits, pairs, q_padded]. One wave per
+// (pair, row): lane = split group (lane / 16, every fourth split) x four dims.
 __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int splits, int q_padded) {
-    long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    long long total = (long long)p.pairs * p.q_rows * 64;
-    if (idx >= total) return;
-    int d = idx & 63;
-    long long pq = idx >> 6;
-    int qrow = (int)(pq % p.q_rows);
-    int pair = (int)(pq / p.q_rows);
+    const long long pq = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pq >= (long long)p.pairs * p.q_rows) return;
+    const int lane = threadIdx.x & 63, sg = lane >> 4, d = (lane & 15) * 4;
+    const int qrow = (int)(pq % p.q_rows);
+    const int pair = (int)(pq / p.q_rows);
+    const long long step = (long long)p.pairs * q_padded;  // rows between splits
+    const long long row0 = (long long)pair * q_padded + qrow;
+    const float *lse = p.partial + (long long)splits * step * 64 + row0;
     float mx = -INFINITY;
-    for (int s = 0; s < splits; ++s)
-        mx = fmaxf(mx, p.partial[(((long long)s * p.pairs + pair) * q_padded + qrow) * 65 + 64]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < splits; ++s) {
-        const float *part = p.partial + (((long long)s * p.pairs + pair) * q_padded + qrow) * 65;
-        float w = __builtin_amdgcn_exp2f(part[64] - mx);
-        num += w * part[d];
+    for (int s = sg; s < splits; s += 4) mx = fmaxf(mx, lse[s * step]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+#pragma unroll 4
+    for (int s = sg; s < splits; s += 4) {
+        const float w = __builtin_amdgcn_exp2f(lse[s * step] - mx);
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + s * step) * 64 + d);
+        num += w * v;
         den += w;
     }
-    int b = pair / kHeads, head = pair - b * kHeads;
-    p.o[((long long)b * p.q_rows + qrow) * p.ldo + head * 64 + d] = num / den;
+#pragma unroll
+    for (int off = 16; off <= 32; off *= 2) {
+        den += __shfl_xor(den, off, 64);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) num[e] += __shfl_xor(num[e], off, 64);
+    }
+    if (sg != 0) return;
+    const int b = pair / kHeads, head = pair - b * kHeads;
+    *reinterpret_cast<f32x4 *>(p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64 + d) = num * (1.0f / den);
 }
-
-constexpr int kIclWaves = 4;
 
 IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units) {
     IclLaunch g{};
-    g.qtiles = (int)ceil_div(q_rows, kIclWaves * 32);
-    g.q_padded = g.qtiles * kIclWaves * 32;
-    long long base = (long long)g.qtiles * pairs;
-    long long want = 2LL * compute_units;
+    g.qtiles = (int)ceil_div(q_rows, kIclQueries);
+    g.q_padded = g.qtiles * kIclQueries;
+    const long long base = (long long)g.qtiles * pairs;
+    const long long slots = 2LL * compute_units;  // two workgroups fit a CU
+    const int max_splits = std::max(1, kv_rows / 512);
     int splits = 1;
-    if (base < want) {
-        splits = (int)ceil_div(want, base);
-        int max_splits = (int)ceil_div(kv_rows, 512);
-        splits = splits < max_splits ? splits : max_splits;
-        if (splits < 1) splits = 1;
+    if (base < slots) {
+        // Few queries: split the keys until one round of workgroups fills the chip.
+        splits = std::min((int)ceil_div(slots, base), max_splits);
+    } else {
+        // Many: take the split count (up to 8) whose last round of workgroups is
+        // fullest, preferring fewer splits unless more are clearly better.
+        double best = 0.0;
+        for (int s = 1; s <= std::min(8, max_splits); ++s) {
+            const long long units = base * s, rounds = (units + slots - 1) / slots;
+            const double fill = (double)units / (double)(rounds * slots);
+            if (fill > best + 0.02) best = fill, splits = s;
+        }
     }
-    int per = (int)ceil_div(ceil_div(kv_rows, splits), kKeyTile) * kKeyTile;
+    const int per = (int)ceil_div(ceil_div(kv_rows, splits), kKeyTile) * kKeyTile;
     g.keys_per_split = per;
     g.splits = (int)ceil_div(kv_rows, per);
     g.per_xcd = (int)ceil_div((long long)g.qtiles * pairs * g.splits, 8);
@@ -383,7 +481,7 @@ int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units) 
 
 size_t icl_attention_partial_floats(int pairs, int q_rows, int splits) {
     if (splits <= 1) return 0;
-    size_t q_padded = ceil_div(q_rows, kIclWaves * 32) * (size_t)(kIclWaves * 32);
+    size_t q_padded = ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
     return (size_t)splits * pairs * q_padded * 65;
 }
 
@@ -391,7 +489,9 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
     if (args.pairs <= 0 || args.q_rows <= 0) return;
     if (args.kv_rows <= 0) fail(3, "ICL attention needs at least one key");
     if ((reinterpret_cast<uintptr_t>(args.q) & 15) || (reinterpret_cast<uintptr_t>(args.k) & 15) ||
-        (reinterpret_cast<uintptr_t>(args.v) & 15) || (args.q_pair_stride & 3) || (args.kv_pair_stride & 3))
+        (reinterpret_cast<uintptr_t>(args.v) & 15) || (reinterpret_cast<uintptr_t>(args.o) & 15) ||
+        (reinterpret_cast<uintptr_t>(args.partial) & 15) || (args.q_pair_stride & 3) || (args.kv_pair_stride & 3) ||
+        (args.ldo & 3))
         fail(3, "ICL attention operands must be 16-byte aligned");
     IclLaunch g = plan_icl(args.pairs, args.q_rows, args.kv_rows, args.compute_units);
     if (g.splits > 1) {
@@ -402,18 +502,18 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
         KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, 4.0 * 64.0 * pairs * (2.0 * kv + 2.0 * q));
         if (g.splits > 1)
-            hipLaunchKernelGGL((icl_attention_kernel<kIclWaves, true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
-                               stream, args, g);
+            hipLaunchKernelGGL((icl_attention_kernel<true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
+                               args, g);
         else
-            hipLaunchKernelGGL((icl_attention_kernel<kIclWaves, false>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
-                               stream, args, g);
+            hipLaunchKernelGGL((icl_attention_kernel<false>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
+                               args, g);
         IRX_HIP(hipGetLastError());
     }
     if (g.splits > 1) {
-        long long total = (long long)args.pairs * args.q_rows * 64;
+        long long rows = (long long)args.pairs * args.q_rows;
         KernelTimer timer(kFamIclMerge, stream, 0.0,
-                          4.0 * ((double)g.splits * args.pairs * args.q_rows * 65.0 + (double)total));
-        hipLaunchKernelGGL(icl_merge_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, args, g.splits,
+                          4.0 * ((double)g.splits * rows * 65.0 + (double)rows * 64.0));
+        hipLaunchKernelGGL(icl_merge_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, args, g.splits,
                            g.q_padded);
         IRX_HIP(hipGetLastError());
     }
