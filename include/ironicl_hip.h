@@ -181,6 +181,11 @@ int irx_predictor_streamed(const irx_predictor *predictor);
 size_t irx_predictor_pass_rows(const irx_predictor *predictor);
 /* Sets the query rows per pass (a multiple of 32, at least 32). */
 int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows);
+/* Streams the passes of a prediction alternate between: 2 (the default) lets
+ * one pass's short launches overlap the other pass's work; 1 runs every pass
+ * in order on one stream. Results are identical either way. No counterpart in
+ * the reference (its predictor runs passes in order, predictor.rs:224-271). */
+int irx_predictor_set_streams(irx_predictor *predictor, int streams);
 
 /* Predictor::predict (predictor.rs:224-271): x [B, Q, H] on the host, logits
  * [B, Q, outputs] on the host. cpu_rows, when not NULL, gets Q flags: 1 for a
@@ -203,6 +208,8 @@ typedef struct irx_kernel_stats {
     double milliseconds; /* summed kernel durations */
     double flops;        /* algorithmic FLOPs of those launches */
     double bytes;        /* minimal HBM bytes: operands read once, results written once */
+    double busy_milliseconds; /* union of the launch intervals (launches on the
+                               * predictor's two streams may overlap) */
 } irx_kernel_stats;
 
 /* Kernel families, as bits of irx_profile_enable's mask. */

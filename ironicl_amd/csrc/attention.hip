@@ -473,6 +473,174 @@ __global__ __launch_bounds__(64) void small_attention_kernel(SmallAttention p, i
             f32x4{o[4 * c] * inv, o[4 * c + 1] * inv, o[4 * c + 2] * inv, o[4 * c + 3] * inv};
 }
 
+// ---- 16-wide heads on matrix cores, up to 128 keys ----
+//
+// One wave per (sequence, head) and a chunk of 16 * QB queries (the wave
+// loops over every waves_per_seq-th chunk). The wave stages its keys (RoPE
+// applied) and the transposed values into its own LDS, then per chunk
+// computes S^T = K Q^T with v_mfma_f32_16x16x4f32 and keeps every score of
+// its queries in registers: lane l holds keys 16 b + 4 (l / 16) + r of query
+// l % 16 of each block. The softmax is exact (no running rescale); O^T = V^T
+// P^T takes the score registers as its operand, the four k slots of MFMA i
+// being keys 16 b + 4 g + i. K-step st of the first product pairs lane group
+// g with dim 4 g + st, so each lane's Q and K operands are one 16-byte load.
+constexpr int kShortKeyBlocks = 8;  // up to 128 keys
+constexpr int kShortKeys = kShortKeyBlocks * 16;
+constexpr int kShortKStride = 20;               // K rows padded to 20 floats
+constexpr int kShortVStride = kShortKeys + 4;   // V^T rows padded to 132 floats
+
+template <int QB, bool ROPE>
+__global__ __launch_bounds__(64) void small_attention_mfma_kernel(SmallAttention p, int waves_per_seq) {
+    __shared__ __attribute__((aligned(16))) float Ks[kShortKeys * kShortKStride];
+    __shared__ __attribute__((aligned(16))) float Vt[16 * kShortVStride];
+    const int item = blockIdx.x / waves_per_seq;
+    const int c_first = blockIdx.x - item * waves_per_seq;
+    const int head = item % p.heads, seq = item / p.heads;
+    const int gq = seq / p.group, sq = seq - gq * p.group;
+    const float *qb = p.q + gq * p.q_group + sq * p.q_seq + head * p.q_head;
+    const float *kb = p.k + gq * p.k_group + sq * p.k_seq + head * p.k_head;
+    const float *vb = p.v + gq * p.v_group + sq * p.v_seq + head * p.v_head;
+    float *ob = p.o + gq * p.o_group + sq * p.o_seq + head * p.o_head;
+    const int lane = threadIdx.x, g = lane >> 4, l16 = lane & 15;
+    const int kv = p.kv_rows;
+    const int kblocks = (kv + 15) / 16;
+
+    // Stage K (rotated) as [key][20] and V transposed as [dim][132]; keys past kv are zero.
+    for (int key = lane; key < kblocks * 16; key += 64) {
+        float kr[16], vr[16];
+        if (key < kv) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(kb + (long long)key * p.k_row + 4 * c);
+                const f32x4 b = *reinterpret_cast<const f32x4 *>(vb + (long long)key * p.v_row + 4 * c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kr[4 * c + e] = a[e], vr[4 * c + e] = b[e];
+            }
+            if constexpr (ROPE) {
+                const float *cs = p.rope_cos + key * 16, *sn = p.rope_sin + key * 16;
+                float r[16];
+#pragma unroll
+                for (int d = 0; d < 16; ++d) r[d] = kr[d] * cs[d] + kr[d ^ 8] * sn[d];
+#pragma unroll
+                for (int d = 0; d < 16; ++d) kr[d] = r[d];
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < 16; ++d) kr[d] = 0.f, vr[d] = 0.f;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            f32x4 a;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] = kr[4 * c + e];
+            *reinterpret_cast<f32x4 *>(&Ks[key * kShortKStride + 4 * c]) = a;
+        }
+#pragma unroll
+        for (int d = 0; d < 16; ++d) Vt[d * kShortVStride + key] = vr[d];
+    }
+    __syncthreads();
+
+    const float scale = p.scale * kLog2e;
+    const int chunks = (p.q_rows + 16 * QB - 1) / (16 * QB);
+    for (int c = c_first; c < chunks; c += waves_per_seq) {
+        const int q0 = c * 16 * QB;
+        // This lane's query operands: dims 4g .. 4g+3 of query q0 + 16 j + l16.
+        f32x4 qf[QB];
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+            const int row = q0 + 16 * j + l16;
+            f32x4 q = {0.f, 0.f, 0.f, 0.f};
+            if (row < p.q_rows) {
+                const float *src = qb + (long long)row * p.q_row;
+                q = *reinterpret_cast<const f32x4 *>(src + 4 * g);
+                if constexpr (ROPE) {
+                    // Rotate-half pairs dim d with d ^ 8, held in dims 4 (g ^ 2) .. of the same row.
+                    const f32x4 qp = *reinterpret_cast<const f32x4 *>(src + 4 * (g ^ 2));
+                    const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_cos + row * 16 + 4 * g);
+                    const f32x4 sn = *reinterpret_cast<const f32x4 *>(p.rope_sin + row * 16 + 4 * g);
+                    q = q * cs + qp * sn;
+                }
+            }
+            qf[j] = q * scale;
+        }
+        // Scores S^T for every key block.
+        f32x4 s[QB][kShortKeyBlocks];
+#pragma unroll
+        for (int b = 0; b < kShortKeyBlocks; ++b) {
+            if (b < kblocks) {
+                const f32x4 kf = *reinterpret_cast<const f32x4 *>(&Ks[(16 * b + l16) * kShortKStride + 4 * g]);
+#pragma unroll
+                for (int j = 0; j < QB; ++j) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[j][st], acc, 0, 0, 0);
+                    s[j][b] = acc;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < QB; ++j) s[j][b] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            }
+        }
+        if (kv < kblocks * 16) {
+            const int b = kblocks - 1;
+#pragma unroll
+            for (int bb = 0; bb < kShortKeyBlocks; ++bb) {
+                if (bb != b) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (16 * bb + 4 * g + r >= kv)
+#pragma unroll
+                        for (int j = 0; j < QB; ++j) s[j][bb][r] = -INFINITY;
+            }
+        }
+        // Exact softmax per query: lanes l16, l16 + 16, l16 + 32, l16 + 48 share a query.
+        float inv[QB];
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < kShortKeyBlocks; ++b)
+                if (b < kblocks) m = fmaxf(m, fmaxf(fmaxf(s[j][b][0], s[j][b][1]), fmaxf(s[j][b][2], s[j][b][3])));
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            float l = 0.f;
+#pragma unroll
+            for (int b = 0; b < kShortKeyBlocks; ++b) {
+                if (b < kblocks) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        s[j][b][r] = __builtin_amdgcn_exp2f(s[j][b][r] - m);
+                        l += s[j][b][r];
+                    }
+                }
+            }
+            l += __shfl_xor(l, 16, 64);
+            l += __shfl_xor(l, 32, 64);
+            inv[j] = 1.0f / l;
+        }
+        // O^T = V^T P^T.
+        f32x4 o[QB];
+#pragma unroll
+        for (int j = 0; j < QB; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < kShortKeyBlocks; ++b) {
+            if (b < kblocks) {
+                const f32x4 vf = *reinterpret_cast<const f32x4 *>(&Vt[l16 * kShortVStride + 16 * b + 4 * g]);
+#pragma unroll
+                for (int j = 0; j < QB; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[i], s[j][b][i], o[j], 0, 0, 0);
+            }
+        }
+        // Lane l holds O[query q0 + 16 j + l16][dims 4g .. 4g+3].
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+            const int row = q0 + 16 * j + l16;
+            if (row < p.q_rows) *reinterpret_cast<f32x4 *>(ob + (long long)row * p.o_row + 4 * g) = o[j] * inv[j];
+        }
+    }
+}
+
 }  // namespace
 
 int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units) {
@@ -528,13 +696,37 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
           args.q_group | args.k_group | args.v_group | args.o_group | args.q_head | args.k_head | args.v_head |
           args.o_head) & 3))
         fail(3, "small attention operands must be 16-byte aligned");
-    int qtiles = (int)ceil_div(args.q_rows, 64);
-    long long blocks = (long long)qtiles * args.heads * args.seqs;
-    if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
     const double sh = (double)args.seqs * args.heads;
     KernelTimer timer(kFamSmall, stream, 4.0 * sh * args.q_rows * args.kv_rows * 16.0,
                       4.0 * sh * 32.0 * (args.q_rows + args.kv_rows));
-    hipLaunchKernelGGL(small_attention_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, args, qtiles);
+    if (args.kv_rows <= kShortKeys) {
+        // Matrix cores: 16 * qb queries per wave; about 8192 waves in flight.
+        const int qb = args.q_rows <= 16 ? 1 : (args.q_rows <= 80 ? 5 : 4);
+        const long long items = (long long)args.seqs * args.heads;
+        const long long chunks = ceil_div(args.q_rows, 16 * qb);
+        const long long per = std::max<long long>(1, std::min<long long>(chunks, ceil_div(8192, items)));
+        const long long waves = items * per;
+        if (waves > 0x7fffffffLL) fail(3, "small attention grid is too large");
+        const bool rope = args.rope_cos != nullptr;
+#define IRX_SMALL_CASE(QB)                                                                                          \
+    if (qb == QB) {                                                                                                \
+        if (rope)                                                                                                  \
+            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, true>), dim3((unsigned)waves), dim3(64), 0, stream, \
+                               args, (int)per);                                                                    \
+        else                                                                                                       \
+            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, false>), dim3((unsigned)waves), dim3(64), 0,        \
+                               stream, args, (int)per);                                                            \
+    }
+        IRX_SMALL_CASE(1)
+        IRX_SMALL_CASE(4)
+        IRX_SMALL_CASE(5)
+#undef IRX_SMALL_CASE
+    } else {
+        int qtiles = (int)ceil_div(args.q_rows, 64);
+        long long blocks = (long long)qtiles * args.heads * args.seqs;
+        if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
+        hipLaunchKernelGGL(small_attention_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, args, qtiles);
+    }
     IRX_HIP(hipGetLastError());
 }
 

@@ -41,20 +41,39 @@ struct PendingTiming {
 struct FamilyTotals {
     uint64_t launches = 0;
     double ms = 0, flops = 0, bytes = 0;
+    std::vector<std::pair<double, double>> spans;  // launch intervals, ms after g_epoch
 };
 std::atomic<unsigned> g_profiling{0};
 std::mutex g_profile_mu;
 std::vector<PendingTiming> g_pending;
 FamilyTotals g_totals[kFamCount];
+hipEvent_t g_epoch = nullptr;  // recorded when profiling is enabled
+
+// Length of the union of intervals (launches on several streams may overlap).
+double union_ms(std::vector<std::pair<double, double>> v) {
+    std::sort(v.begin(), v.end());
+    double total = 0, lo = 0, hi = -1e300;
+    for (const auto &[a, b] : v) {
+        if (a > hi) {
+            if (hi > lo) total += hi - lo;
+            lo = a, hi = b;
+        } else if (b > hi) {
+            hi = b;
+        }
+    }
+    if (hi > lo) total += hi - lo;
+    return total;
+}
 const char *const kFamilyNames[kFamCount] = {"gemm", "icl_attention", "icl_merge", "small_attention",
                                              "layer_norm", "glue"};
 
 void drain_timings() {
     for (auto &p : g_pending) {
-        float ms = 0.f;
+        float ms = 0.f, at = 0.f;
         if (hipEventSynchronize(p.stop) == hipSuccess && hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
             FamilyTotals &t = g_totals[p.family];
             t.launches += 1, t.ms += ms, t.flops += p.flops, t.bytes += p.bytes;
+            if (g_epoch && hipEventElapsedTime(&at, g_epoch, p.start) == hipSuccess) t.spans.emplace_back(at, at + ms);
         }
         (void)hipEventDestroy(p.start);
         (void)hipEventDestroy(p.stop);
@@ -221,8 +240,13 @@ struct irx_predictor {
     DevBuf base_scales;   // [12, 512]
     DevBuf rope_cos, rope_sin;
     hipStream_t stream = nullptr;
+    // Passes alternate between two streams, each with its own workspace, so
+    // that one pass's short launches overlap the other's.
+    hipStream_t side_stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    int streams = 2;
     std::mutex mu;
-    Arena ws;
+    Arena ws, side_ws;
     size_t ws_rows = 0;
 };
 
@@ -759,15 +783,15 @@ size_t predict_ws_floats(const irx_shape &sh, size_t R, int cus) {
     return count.used / 4;
 }
 
-void predict_pass(irx_predictor *P, const float *d_x, long long x_stride, int q0, int R, float *d_logits, int Q,
-                  uint8_t *flags_host) {
+void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stride, int q0, int R, float *d_logits,
+                  int Q, uint8_t *flags_host) {
     const irx_weights &W = *P->weights;
     const irx_shape &sh = P->shape;
     const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
     const int width = (int)sh.outputs;
-    hipStream_t s = P->stream;
+    hipStream_t s = slot ? P->side_stream : P->stream;
     Stages st{W, s, W.device->compute_units};
-    Arena &ws = P->ws;
+    Arena &ws = slot ? P->side_ws : P->ws;
     ws.used = 0;
     const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus);
     uint8_t *flags = pb.flags;
@@ -805,9 +829,12 @@ void predict_pass(irx_predictor *P, const float *d_x, long long x_stride, int q0
 }
 
 void ensure_workspace(irx_predictor *P) {
-    if (P->ws_rows == P->pass_rows && P->ws.buf.p) return;
+    if (P->ws_rows == P->pass_rows && P->ws.buf.p && P->side_ws.buf.p) return;
+    if (P->stream) IRX_HIP(hipStreamSynchronize(P->stream));
+    if (P->side_stream) IRX_HIP(hipStreamSynchronize(P->side_stream));
     size_t floats = predict_ws_floats(P->shape, P->pass_rows, P->weights->device->compute_units);
     P->ws.buf.alloc(floats * 4);
+    P->side_ws.buf.alloc(floats * 4);
     P->ws_rows = P->pass_rows;
 }
 
@@ -1015,6 +1042,9 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         IRX_HIP(hipMemcpy(P->rope_cos.p, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(P->rope_sin.p, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
+        IRX_HIP(hipStreamCreateWithFlags(&P->side_stream, hipStreamNonBlocking));
+        IRX_HIP(hipEventCreateWithFlags(&P->fork, hipEventDisableTiming));
+        IRX_HIP(hipEventCreateWithFlags(&P->join, hipEventDisableTiming));
         ensure_workspace(P);
         *out = P;
         P = nullptr;
@@ -1032,6 +1062,12 @@ void irx_predictor_free(irx_predictor *predictor) {
         (void)hipStreamSynchronize(predictor->stream);
         (void)hipStreamDestroy(predictor->stream);
     }
+    if (predictor->side_stream) {
+        (void)hipStreamSynchronize(predictor->side_stream);
+        (void)hipStreamDestroy(predictor->side_stream);
+    }
+    if (predictor->fork) (void)hipEventDestroy(predictor->fork);
+    if (predictor->join) (void)hipEventDestroy(predictor->join);
     delete predictor;
     irx_weights_release(w);
 }
@@ -1039,6 +1075,14 @@ void irx_predictor_free(irx_predictor *predictor) {
 int irx_predictor_streamed(const irx_predictor *) { return 0; }
 
 size_t irx_predictor_pass_rows(const irx_predictor *predictor) { return predictor ? predictor->pass_rows : 0; }
+
+int irx_predictor_set_streams(irx_predictor *predictor, int streams) {
+    return guarded("irx_predictor_set_streams", [&] {
+        if (!predictor || streams < 1 || streams > 2) fail(IRX_INVALID_ARGUMENT, "streams must be 1 or 2");
+        std::lock_guard<std::mutex> lock(predictor->mu);
+        predictor->streams = streams;
+    });
+}
 
 int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows) {
     return guarded("irx_predictor_set_pass_rows", [&] {
@@ -1055,14 +1099,21 @@ static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *
                            irx_progress_fn progress, void *user) {
     const size_t R = P->pass_rows;
     if (cpu_rows) std::memset(cpu_rows, 0, q);
-    for (size_t q0 = 0; q0 < q; q0 += R) {
+    // The side stream starts after everything already queued on the main one
+    // (the inputs' upload), and the main stream ends after the side's passes.
+    IRX_HIP(hipEventRecord(P->fork, P->stream));
+    IRX_HIP(hipStreamWaitEvent(P->side_stream, P->fork, 0));
+    int slot = 0;
+    for (size_t q0 = 0; q0 < q; q0 += R, slot = P->streams > 1 ? slot ^ 1 : 0) {
         const int len = (int)std::min(R, q - q0);
-        predict_pass(P, d_x, (long long)q * P->shape.features, (int)q0, len, d_logits, (int)q, cpu_rows);
+        predict_pass(P, slot, d_x, (long long)q * P->shape.features, (int)q0, len, d_logits, (int)q, cpu_rows);
         if (progress) {
-            IRX_HIP(hipStreamSynchronize(P->stream));
+            IRX_HIP(hipStreamSynchronize(slot ? P->side_stream : P->stream));
             report(progress, user, IRX_STAGE_PREDICT, q0 + len, q);
         }
     }
+    IRX_HIP(hipEventRecord(P->join, P->side_stream));
+    IRX_HIP(hipStreamWaitEvent(P->stream, P->join, 0));
 }
 
 int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, float *logits, uint8_t *cpu_rows,
@@ -1100,8 +1151,12 @@ int irx_profile_enable(unsigned families) {
     return guarded("irx_profile_enable", [&] {
         std::lock_guard<std::mutex> lock(g_profile_mu);
         drain_timings();
-        if (families)
+        if (families) {
             for (auto &t : g_totals) t = FamilyTotals{};
+            if (!g_epoch) IRX_HIP(hipEventCreate(&g_epoch));
+            IRX_HIP(hipEventRecord(g_epoch, nullptr));
+            IRX_HIP(hipEventSynchronize(g_epoch));
+        }
         g_profiling.store(families);
     });
 }
@@ -1117,6 +1172,7 @@ int irx_profile_read(const char *family, irx_kernel_stats *out) {
         drain_timings();
         const FamilyTotals &t = g_totals[f];
         out->launches = t.launches, out->milliseconds = t.ms, out->flops = t.flops, out->bytes = t.bytes;
+        out->busy_milliseconds = union_ms(t.spans);
     });
 }
 

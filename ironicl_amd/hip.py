@@ -53,7 +53,7 @@ class ContextTensors(ctypes.Structure):
 
 class KernelStats(ctypes.Structure):
     _fields_ = [("launches", ctypes.c_uint64), ("milliseconds", ctypes.c_double), ("flops", ctypes.c_double),
-                ("bytes", ctypes.c_double)]
+                ("bytes", ctypes.c_double), ("busy_milliseconds", ctypes.c_double)]
 
 
 # Every entry point include/ironicl_hip.h declares, with its ctypes signature.
@@ -81,6 +81,7 @@ SIGNATURES = {
     "irx_predictor_streamed": (ctypes.c_int, [ctypes.c_void_p]),
     "irx_predictor_pass_rows": (_sz, [ctypes.c_void_p]),
     "irx_predictor_set_pass_rows": (ctypes.c_int, [ctypes.c_void_p, _sz]),
+    "irx_predictor_set_streams": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "irx_predictor_predict": (ctypes.c_int, [ctypes.c_void_p, _CF, _sz, _F, ctypes.POINTER(ctypes.c_uint8),
                                              PROGRESS, ctypes.c_void_p]),
     "irx_predictor_predict_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p,
@@ -149,7 +150,8 @@ def profile_enable(families=True) -> None:
 def profile_read(family: str) -> dict:
     s = KernelStats()
     check(lib().irx_profile_read(family.encode(), ctypes.byref(s)))
-    return {"launches": int(s.launches), "milliseconds": s.milliseconds, "flops": s.flops, "bytes": s.bytes}
+    return {"launches": int(s.launches), "milliseconds": s.milliseconds, "flops": s.flops, "bytes": s.bytes,
+            "busy_milliseconds": s.busy_milliseconds}
 
 
 class Device:

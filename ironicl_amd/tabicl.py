@@ -303,6 +303,10 @@ class StaticExecutor:
     def set_pass_rows(self, rows: int) -> None:
         hip.check(hip.lib().irx_predictor_set_pass_rows(self.handle, rows))
 
+    def set_streams(self, streams: int) -> None:
+        """Passes alternate between `streams` (1 or 2) HIP streams; results are identical."""
+        hip.check(hip.lib().irx_predictor_set_streams(self.handle, streams))
+
     def outputs(self) -> int:
         return self.classes if self.classes else self.executor.width
 

@@ -98,6 +98,22 @@ def test_pass_rows_and_device_path_do_not_change_results(lcg):
     np.testing.assert_array_equal(dl.to_host(), whole)
 
 
+def test_one_and_two_streams_give_identical_results(lcg):
+    *_, ctx_gpu = lcg
+    xt = lcg[2]
+    ctx_gpu.set_pass_rows(32)  # 250 rows: 8 passes alternating between the streams
+    try:
+        two = ctx_gpu.predict_raw(xt).logits
+        ctx_gpu.set_streams(1)
+        one = ctx_gpu.predict_raw(xt).logits
+    finally:
+        ctx_gpu.set_streams(2)
+        ctx_gpu.set_pass_rows(512)
+    np.testing.assert_array_equal(two, one)
+    with pytest.raises(hip.HipError):
+        ctx_gpu.set_streams(3)
+
+
 def test_kernel_timing_records_launches(lcg):
     *_, ctx_gpu = lcg
     hip.profile_enable(True)
@@ -108,6 +124,7 @@ def test_kernel_timing_records_launches(lcg):
     finally:
         hip.profile_enable(False)
     assert icl["launches"] == 12 and icl["milliseconds"] > 0
+    assert 0 < icl["busy_milliseconds"] <= icl["milliseconds"] * (1 + 1e-6)
     assert icl["flops"] == pytest.approx(12 * 4.0 * 16 * 250 * 240 * 64)
     assert gemm["launches"] > 50 and gemm["flops"] > 0
     with pytest.raises(hip.HipError):
