@@ -484,29 +484,32 @@ __global__ __launch_bounds__(64) void small_attention_kernel(SmallAttention p, i
 // P^T takes the score registers as its operand, the four k slots of MFMA i
 // being keys 16 b + 4 g + i. K-step st of the first product pairs lane group
 // g with dim 4 g + st, so each lane's Q and K operands are one 16-byte load.
-constexpr int kShortKeyBlocks = 8;  // up to 128 keys
-constexpr int kShortKeys = kShortKeyBlocks * 16;
-constexpr int kShortKStride = 20;               // K rows padded to 20 floats
-constexpr int kShortVStride = kShortKeys + 4;   // V^T rows padded to 132 floats
+constexpr int kShortKeys = 128;     // keys the matrix-core path takes
+constexpr int kShortKStride = 20;   // K rows padded to 20 floats
 
-template <int QB, bool ROPE>
-__global__ __launch_bounds__(64) void small_attention_mfma_kernel(SmallAttention p, int waves_per_seq) {
-    __shared__ __attribute__((aligned(16))) float Ks[kShortKeys * kShortKStride];
-    __shared__ __attribute__((aligned(16))) float Vt[16 * kShortVStride];
-    const int item = blockIdx.x / waves_per_seq;
-    const int c_first = blockIdx.x - item * waves_per_seq;
+template <int QB, int KB, bool ROPE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallAttention p, int groups_per_seq) {
+    constexpr int KEYS = KB * 16, VSTRIDE = KEYS + 4;
+    __shared__ __attribute__((aligned(16))) float Ks[KEYS * kShortKStride];
+    __shared__ __attribute__((aligned(16))) float Vt[16 * VSTRIDE];
+    // Workgroup j of a (sequence, head) item: its WAVES waves take query chunks
+    // (j * WAVES + wave) + k * groups_per_seq * WAVES and share the staged keys.
+    const int item = blockIdx.x / groups_per_seq;
+    const int wave = threadIdx.x >> 6;
+    const int c_first = (blockIdx.x - item * groups_per_seq) * WAVES + wave;
+    const int c_step = groups_per_seq * WAVES;
     const int head = item % p.heads, seq = item / p.heads;
     const int gq = seq / p.group, sq = seq - gq * p.group;
     const float *qb = p.q + gq * p.q_group + sq * p.q_seq + head * p.q_head;
     const float *kb = p.k + gq * p.k_group + sq * p.k_seq + head * p.k_head;
     const float *vb = p.v + gq * p.v_group + sq * p.v_seq + head * p.v_head;
     float *ob = p.o + gq * p.o_group + sq * p.o_seq + head * p.o_head;
-    const int lane = threadIdx.x, g = lane >> 4, l16 = lane & 15;
+    const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
     const int kv = p.kv_rows;
     const int kblocks = (kv + 15) / 16;
 
-    // Stage K (rotated) as [key][20] and V transposed as [dim][132]; keys past kv are zero.
-    for (int key = lane; key < kblocks * 16; key += 64) {
+    // Stage K (rotated) as [key][20] and V transposed as [dim][KEYS + 4]; keys past kv are zero.
+    for (int key = threadIdx.x; key < kblocks * 16; key += 64 * WAVES) {
         float kr[16], vr[16];
         if (key < kv) {
 #pragma unroll
@@ -536,13 +539,13 @@ __global__ __launch_bounds__(64) void small_attention_mfma_kernel(SmallAttention
             *reinterpret_cast<f32x4 *>(&Ks[key * kShortKStride + 4 * c]) = a;
         }
 #pragma unroll
-        for (int d = 0; d < 16; ++d) Vt[d * kShortVStride + key] = vr[d];
+        for (int d = 0; d < 16; ++d) Vt[d * VSTRIDE + key] = vr[d];
     }
     __syncthreads();
 
     const float scale = p.scale * kLog2e;
     const int chunks = (p.q_rows + 16 * QB - 1) / (16 * QB);
-    for (int c = c_first; c < chunks; c += waves_per_seq) {
+    for (int c = c_first; c < chunks; c += c_step) {
         const int q0 = c * 16 * QB;
         // This lane's query operands: dims 4g .. 4g+3 of query q0 + 16 j + l16.
         f32x4 qf[QB];
@@ -564,9 +567,9 @@ __global__ __launch_bounds__(64) void small_attention_mfma_kernel(SmallAttention
             qf[j] = q * scale;
         }
         // Scores S^T for every key block.
-        f32x4 s[QB][kShortKeyBlocks];
+        f32x4 s[QB][KB];
 #pragma unroll
-        for (int b = 0; b < kShortKeyBlocks; ++b) {
+        for (int b = 0; b < KB; ++b) {
             if (b < kblocks) {
                 const f32x4 kf = *reinterpret_cast<const f32x4 *>(&Ks[(16 * b + l16) * kShortKStride + 4 * g]);
 #pragma unroll
@@ -584,7 +587,7 @@ __global__ __launch_bounds__(64) void small_attention_mfma_kernel(SmallAttention
         if (kv < kblocks * 16) {
             const int b = kblocks - 1;
 #pragma unroll
-            for (int bb = 0; bb < kShortKeyBlocks; ++bb) {
+            for (int bb = 0; bb < KB; ++bb) {
                 if (bb != b) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -599,13 +602,13 @@ __global__ __launch_bounds__(64) void small_attention_mfma_kernel(SmallAttention
         for (int j = 0; j < QB; ++j) {
             float m = -INFINITY;
 #pragma unroll
-            for (int b = 0; b < kShortKeyBlocks; ++b)
+            for (int b = 0; b < KB; ++b)
                 if (b < kblocks) m = fmaxf(m, fmaxf(fmaxf(s[j][b][0], s[j][b][1]), fmaxf(s[j][b][2], s[j][b][3])));
             m = fmaxf(m, __shfl_xor(m, 16, 64));
             m = fmaxf(m, __shfl_xor(m, 32, 64));
             float l = 0.f;
 #pragma unroll
-            for (int b = 0; b < kShortKeyBlocks; ++b) {
+            for (int b = 0; b < KB; ++b) {
                 if (b < kblocks) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -623,9 +626,9 @@ __global__ __launch_bounds__(64) void small_attention_mfma_kernel(SmallAttention
 #pragma unroll
         for (int j = 0; j < QB; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int b = 0; b < kShortKeyBlocks; ++b) {
+        for (int b = 0; b < KB; ++b) {
             if (b < kblocks) {
-                const f32x4 vf = *reinterpret_cast<const f32x4 *>(&Vt[l16 * kShortVStride + 16 * b + 4 * g]);
+                const f32x4 vf = *reinterpret_cast<const f32x4 *>(&Vt[l16 * VSTRIDE + 16 * b + 4 * g]);
 #pragma unroll
                 for (int j = 0; j < QB; ++j)
 #pragma unroll
@@ -701,25 +704,34 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
                       4.0 * sh * 32.0 * (args.q_rows + args.kv_rows));
     if (args.kv_rows <= kShortKeys) {
         // Matrix cores: 16 * qb queries per wave; about 8192 waves in flight.
+        // Long query sets share each item's staged keys among four waves.
         const int qb = args.q_rows <= 16 ? 1 : (args.q_rows <= 80 ? 5 : 4);
+        const int kb = args.kv_rows <= 80 ? 5 : 8;
         const long long items = (long long)args.seqs * args.heads;
         const long long chunks = ceil_div(args.q_rows, 16 * qb);
-        const long long per = std::max<long long>(1, std::min<long long>(chunks, ceil_div(8192, items)));
-        const long long waves = items * per;
-        if (waves > 0x7fffffffLL) fail(3, "small attention grid is too large");
+        const int waves = (qb == 4 && chunks >= 4) ? 4 : 1;
+        const long long groups = std::max<long long>(
+            1, std::min<long long>(ceil_div(chunks, waves), ceil_div(8192, items * waves)));
+        const long long blocks = items * groups;
+        if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
         const bool rope = args.rope_cos != nullptr;
-#define IRX_SMALL_CASE(QB)                                                                                          \
-    if (qb == QB) {                                                                                                \
-        if (rope)                                                                                                  \
-            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, true>), dim3((unsigned)waves), dim3(64), 0, stream, \
-                               args, (int)per);                                                                    \
-        else                                                                                                       \
-            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, false>), dim3((unsigned)waves), dim3(64), 0,        \
-                               stream, args, (int)per);                                                            \
+#define IRX_SMALL_CASE(QB, KB, W)                                                                                 \
+    if (qb == QB && kb == KB && waves == W) {                                                                    \
+        if (rope)                                                                                                \
+            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, KB, true, W>), dim3((unsigned)blocks), dim3(64 * W), \
+                               0, stream, args, (int)groups);                                                    \
+        else                                                                                                     \
+            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, KB, false, W>), dim3((unsigned)blocks),           \
+                               dim3(64 * W), 0, stream, args, (int)groups);                                      \
     }
-        IRX_SMALL_CASE(1)
-        IRX_SMALL_CASE(4)
-        IRX_SMALL_CASE(5)
+        IRX_SMALL_CASE(1, 5, 1)
+        IRX_SMALL_CASE(1, 8, 1)
+        IRX_SMALL_CASE(5, 5, 1)
+        IRX_SMALL_CASE(5, 8, 1)
+        IRX_SMALL_CASE(4, 5, 1)
+        IRX_SMALL_CASE(4, 8, 1)
+        IRX_SMALL_CASE(4, 5, 4)
+        IRX_SMALL_CASE(4, 8, 4)
 #undef IRX_SMALL_CASE
     } else {
         int qtiles = (int)ceil_div(args.q_rows, 64);

@@ -57,6 +57,34 @@ __device__ __forceinline__ void store_out(const GemmArgs &p, int row, int col, l
     p.c[roff + coff] = v;
 }
 
+// The 16 accumulator rows row0 + (r&3) + 8*(r>>2) of one column of a plain
+// row-major output: one lane pointer per block, per-row offsets that are the
+// same for every lane (scalar), and no row bounds checks when the tile's rows
+// all exist.
+template <int EPI>
+__device__ __forceinline__ void store_rows(const GemmArgs &p, int row0, int col, long long coff, float bias,
+                                           const f32x16 &acc, bool full_rows) {
+    const long long ldc = p.out.ldc;
+    float *dst = p.c + (long long)row0 * ldc + coff;
+    const float *res = nullptr;
+    if constexpr (EPI == kEpiResidual) res = p.residual + (long long)row0 * p.ldr + col;
+    auto one = [&](int r) {
+        const int dr = (r & 3) + 8 * (r >> 2);
+        float v = acc[r] + bias;
+        if constexpr (EPI == kEpiGelu) v = gelu_erf(v);
+        if constexpr (EPI == kEpiResidual) v += res[dr * p.ldr];
+        dst[dr * ldc] = v;
+    };
+    if (full_rows) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) one(r);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (row0 + (r & 3) + 8 * (r >> 2) < p.m) one(r);
+    }
+}
+
 // Large products: a BM x BN tile per 256-thread workgroup (2 x 2 waves of
 // (BM/2) x (BN/2)), K in 32-deep steps through double-buffered LDS. Within a
 // step lanes 0-31 feed k = 0..15 and lanes 32-63 k = 16..31, one k from each
@@ -157,12 +185,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, i
         const long long coff = col_offset(p.out, col);
         const float bias = p.bias ? p.bias[col] : 0.f;
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < MI; ++i) {
+            const int row0 = m0 + wm * (BM / 2) + i * 32 + half * 4;
+            if constexpr (!GROUPED && EPI != kEpiQass) {
+                store_rows<EPI>(p, row0, col, coff, bias, acc[i][j], m0 + BM <= p.m);
+            } else {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * (BM / 2) + i * 32 + half * 4 + (r & 3) + 8 * (r >> 2);
-                if (row < p.m) store_out<EPI, GROUPED>(p, row, col, coff, bias, acc[i][j][r]);
+                for (int r = 0; r < 16; ++r) {
+                    const int row = row0 + (r & 3) + 8 * (r >> 2);
+                    if (row < p.m) store_out<EPI, GROUPED>(p, row, col, coff, bias, acc[i][j][r]);
+                }
             }
+        }
     }
 }
 
@@ -212,12 +246,39 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
     if (col >= p.n) return;
     const long long coff = col_offset(p.out, col);
     const float bias = p.bias ? p.bias[col] : 0.f;
+    // This wave finishes registers 4 wave .. 4 wave + 3: rows half*4 + rr + 8 wave.
+    const int row0 = m0 + half * 4 + 8 * wave;
+    f32x16 v16;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
         const int r = wave * 4 + rr;
-        const float v = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
-        const int row = m0 + half * 4 + (r & 3) + 8 * (r >> 2);
-        if (row < p.m) store_out<EPI, GROUPED>(p, row, col, coff, bias, v);
+        v16[rr] = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
+    }
+    if constexpr (!GROUPED && EPI != kEpiQass) {
+        const long long ldc = p.out.ldc;
+        float *dst = p.c + (long long)row0 * ldc + coff;
+        const float *res = nullptr;
+        if constexpr (EPI == kEpiResidual) res = p.residual + (long long)row0 * p.ldr + col;
+        auto one = [&](int rr) {
+            float v = v16[rr] + bias;
+            if constexpr (EPI == kEpiGelu) v = gelu_erf(v);
+            if constexpr (EPI == kEpiResidual) v += res[rr * p.ldr];
+            dst[rr * ldc] = v;
+        };
+        if (m0 + 32 <= p.m) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) one(rr);
+        } else {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                if (row0 + rr < p.m) one(rr);
+        }
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int row = row0 + rr;
+            if (row < p.m) store_out<EPI, GROUPED>(p, row, col, coff, bias, v16[rr]);
+        }
     }
 }
 
@@ -289,13 +350,15 @@ void gemm(const GemmArgs &args, hipStream_t stream) {
         fail(3, "gemm: K must be a positive multiple of 64 with 16-byte aligned rows");
     if ((args.epilogue & (kEpiResidual | kEpiQass)) && !args.residual)
         fail(3, "gemm: residual epilogue without a residual");
-    // Products with few 64 x 64 tiles split K over a workgroup's waves; large
-    // ones take 128 x 128 tiles, the rest 64 x 64.
+    // Products with few 64 x 64 tiles split K over a workgroup's waves; those
+    // with four or more 128 x 128 tiles per CU take them (GELU ones, whose
+    // epilogue is long, from two per CU), the rest 64 x 64 (measured on the
+    // prediction pass's products).
     const long long small_tiles = (long long)ceil_div(args.m, 64) * ceil_div(args.n, 64);
     const long long big_tiles = (long long)ceil_div(args.m, 128) * ceil_div(args.n, 128);
     if (small_tiles < 256)
         launch_splitk(args, stream);
-    else if (big_tiles >= 512)
+    else if (big_tiles >= 1024 || (args.epilogue == kEpiGelu && big_tiles >= 512))
         launch<128, 128>(args, stream);
     else
         launch<64, 64>(args, stream);

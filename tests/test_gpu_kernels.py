@@ -114,7 +114,8 @@ def test_layer_norm_matches_float64(device, rows, width):
 
 
 @pytest.mark.parametrize("query_rows,rows", [(1, 1), (4, 68), (16, 16), (17, 33), (68, 68), (80, 127), (81, 100),
-                                             (130, 128), (512, 128), (128, 129), (128, 1000), (504, 504)])
+                                             (130, 128), (512, 128), (600, 50), (1000, 100), (128, 129),
+                                             (128, 1000), (504, 504)])
 def test_small_attention_matches_float64(device, query_rows, rows):
     heads = 8
     q = fast_values(heads * query_rows * 16, 1, 3.0).reshape(heads, query_rows, 16)
