@@ -7,26 +7,30 @@
 //    backend (src/kernels/cuda/kernels.rs:183-213, 1523-1702), with the
 //    semantics of softmax(q k^T / 8) v in FP32 (src/kernels/reference.rs:792-1024).
 //
-//    A wave owns 32 queries. It computes the transposed products
+//    A wave owns 64 queries (two blocks of 32). It computes the transposed
+//    products
 //      S^T[key, q] = K Q^T       (v_mfma_f32_32x32x2f32, k = head dim)
 //      O^T[d, q]  += V^T P^T     (k = keys)
 //    so that in the accumulator layout lane (q = lane % 32, half = lane / 32)
 //    holds all of one query's scores for half of each 32-key block, and all of
-//    its 64 output dims across the two 32-row output tiles. The online softmax
-//    state (running max, sum) is therefore per lane: a tile needs one swap
-//    between the lane halves for the max, and the output rescale is a scalar
-//    multiply (skipped when no lane's maximum moved). Scores live in the exp2
-//    domain (q pre-scaled by log2(e)/8). The P^T operand of the second
-//    product is the first product's accumulator register as is; each lane
-//    fetches the V elements of the key that register holds. The two output
-//    tiles take the even and the odd dims, so one 8-byte LDS read serves both.
-//    Keys stream through double-buffered LDS tiles of 64 (K rows padded to 68
-//    floats); only a range's last tile is clamped and masked.
+//    its 64 output dims across the two 32-row output tiles; each K or V
+//    fragment read from LDS feeds both query blocks. The softmax state is per
+//    lane. Scores live in the exp2 domain (q pre-scaled by log2(e)/8) and are
+//    exponentiated against a lazy reference (see the kernel): the subtraction
+//    rides in the first MFMA's accumulator and the maximum is only taken when
+//    the reference must move. The P^T operand of the second product is the
+//    first product's accumulator register as is; each lane fetches the V
+//    elements of the key that register holds. The two output tiles take the
+//    even and the odd dims, so one 8-byte LDS read serves both. Keys stream
+//    through double-buffered 64-key LDS tiles filled by direct global -> LDS
+//    loads; only a range's last tile is clamped and masked. One workgroup of
+//    four waves per CU: each wave may use 512 registers.
 //
-//    Few queries (a prediction pass) split the keys over workgroups; each
-//    split writes its normalized partial output and log2-sum-exp, and a merge
-//    kernel combines them. Workgroups sharing a (pair, split) K/V range are
-//    placed on the same XCD so the range is read into one L2.
+//    Key ranges are split over workgroups to fill the chip (prediction passes)
+//    or to even out its last round (the build); each split writes its
+//    normalized partial output and log2-sum-exp, and a merge kernel combines
+//    them. Workgroups sharing a (pair, split) K/V range are placed on the same
+//    XCD so the range is read into one L2.
 //
 // 2. Attention of 16-wide heads on the vector ALUs (column ISAB and row
 //    transformer), one thread per (sequence, head, query row), keys staged
@@ -84,7 +88,7 @@ __device__ __forceinline__ float halves_sum(float x) {
 // SPLIT: the keys are split over workgroups and each writes a partial output
 // and its log2-sum-exp, merged afterwards; otherwise the output is final.
 template <bool SPLIT>
-__global__ __launch_bounds__(kIclWaves * 64, 2) void icl_attention_kernel(IclAttention p, IclLaunch g) {
+__global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAttention p, IclLaunch g) {
     __shared__ __attribute__((aligned(16))) IclTile tiles[2];
 
     const int total = g.qtiles * p.pairs * g.splits;
@@ -169,7 +173,21 @@ __global__ __launch_bounds__(kIclWaves * 64, 2) void icl_attention_kernel(IclAtt
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][0][r] = 0.f, o[j][1][r] = 0.f;
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    // Softmax reference m_ref[j] per query (shared by the lane pair l, l ^ 32):
+    // probabilities are exp2(s - m_ref). It is raised, and the tile redone,
+    // only when a tile's probabilities could exceed 2^64 or when it is still
+    // unset (-inf, the first tile), so most tiles skip the maximum reduction;
+    // -m_ref is the products' initial accumulator, which folds the subtraction
+    // into the MFMA. Relative to the true running maximum a probability is at
+    // most 2^64 and anything below 2^-126 of the maximum is lost, as in the
+    // exact online softmax.
+    float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    f32x16 neg_ref[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) neg_ref[j][r] = INFINITY;
+    constexpr float kLazyLimit = 18446744073709551616.0f;  // 2^64
     // K fragment of chunk 8*half + cc for key r32 of block 0 is at kfrag + (cc >> 2) * 1024 + (cc & 3) * 64;
     // block 1 (keys 32..63) is 512 floats further.
     const int kfrag = (8 * half + (r32 >> 4)) * 256 + (r32 & 15) * 4;
@@ -183,12 +201,8 @@ __global__ __launch_bounds__(kIclWaves * 64, 2) void icl_attention_kernel(IclAtt
         const float *kt = tiles[buf].k;
         const float *vt = tiles[buf].v;
 
-        // S^T[key, q] for key blocks 0 / 1 and query blocks 0 / 1.
+        // S^T[key, q] - m_ref for key blocks 0 / 1 and query blocks 0 / 1.
         f32x16 s[2][2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[j][0][r] = 0.f, s[j][1][r] = 0.f;
         // K fragments are read one chunk ahead of their MFMAs (the scheduling
         // groups keep the compiler from sinking the reads to their first use).
         f32x4 ka = *reinterpret_cast<const f32x4 *>(kt + kfrag);
@@ -205,8 +219,10 @@ __global__ __launch_bounds__(kIclWaves * 64, 2) void icl_attention_kernel(IclAtt
             for (int e = 0; e < 4; ++e)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    s[j][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[e], qreg[j][4 * cc + e], s[j][0], 0, 0, 0);
-                    s[j][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[e], qreg[j][4 * cc + e], s[j][1], 0, 0, 0);
+                    const f32x16 &c0 = (cc == 0 && e == 0) ? neg_ref[j] : s[j][0];
+                    const f32x16 &c1 = (cc == 0 && e == 0) ? neg_ref[j] : s[j][1];
+                    s[j][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[e], qreg[j][4 * cc + e], c0, 0, 0, 0);
+                    s[j][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[e], qreg[j][4 * cc + e], c1, 0, 0, 0);
                 }
             if (cc < 7) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the two DS reads
@@ -226,27 +242,57 @@ __global__ __launch_bounds__(kIclWaves * 64, 2) void icl_attention_kernel(IclAtt
                 }
             }
         }
-        // Online softmax per query block (exp2 domain).
+        // Softmax per query block (exp2 domain) against the lazy reference.
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            float mt = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(s[j][0][r], s[j][1][r]));
-            const float m_new = fmaxf(m_run[j], halves_max(mt));
-            // Rescale only when some lane's running maximum moved (rare after the first tiles).
-            if (__any(m_new > m_run[j])) {
-                const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
-                l_run[j] *= alpha;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[j][0][r] *= alpha, o[j][1][r] *= alpha;
-            }
-            m_run[j] = m_new;
             float lsum = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                s[j][0][r] = __builtin_amdgcn_exp2f(s[j][0][r] - m_new);
-                s[j][1][r] = __builtin_amdgcn_exp2f(s[j][1][r] - m_new);
+                s[j][0][r] = __builtin_amdgcn_exp2f(s[j][0][r]);
+                s[j][1][r] = __builtin_amdgcn_exp2f(s[j][1][r]);
                 lsum += s[j][0][r] + s[j][1][r];
+            }
+            if (__any(!(lsum <= kLazyLimit))) {
+                // The reference is unset or too low for this tile: recompute the
+                // block's scores from zero and raise it to the running maximum.
+                f32x16 t0, t1;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) t0[r] = 0.f, t1[r] = 0.f;
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) {
+                    const int off = kfrag + (cc >> 2) * 1024 + (cc & 3) * 64;
+                    const f32x4 a = *reinterpret_cast<const f32x4 *>(kt + off);
+                    const f32x4 b = *reinterpret_cast<const f32x4 *>(kt + off + 512);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        t0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qreg[j][4 * cc + e], t0, 0, 0, 0);
+                        t1 = __builtin_amdgcn_mfma_f32_32x32x2f32(b[e], qreg[j][4 * cc + e], t1, 0, 0, 0);
+                    }
+                }
+                if (k0 + kKeyTile > k_end) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = k0 + half * 4 + (r & 3) + 8 * (r >> 2);
+                        if (key >= k_end) t0[r] = -INFINITY;
+                        if (key + 32 >= k_end) t1[r] = -INFINITY;
+                    }
+                }
+                float mt = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(t0[r], t1[r]));
+                const float m_new = fmaxf(m_ref[j], halves_max(mt));
+                const float alpha = __builtin_amdgcn_exp2f(m_ref[j] - m_new);
+                l_run[j] *= alpha;
+                lsum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    o[j][0][r] *= alpha, o[j][1][r] *= alpha;
+                    neg_ref[j][r] = -m_new;
+                    s[j][0][r] = __builtin_amdgcn_exp2f(t0[r] - m_new);
+                    s[j][1][r] = __builtin_amdgcn_exp2f(t1[r] - m_new);
+                    lsum += s[j][0][r] + s[j][1][r];
+                }
+                m_ref[j] = m_new;
             }
             l_run[j] += lsum;
         }
@@ -281,7 +327,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 2) void icl_attention_kernel(IclAtt
         } else {
             const long long row = ((long long)split * p.pairs + pair) * g.q_padded + qrow;
             dst = p.partial + row * 64;
-            if (half == 0) p.partial[(long long)g.splits * p.pairs * g.q_padded * 64 + row] = m_run[j] + log2f(l_tot);
+            if (half == 0) p.partial[(long long)g.splits * p.pairs * g.q_padded * 64 + row] = m_ref[j] + log2f(l_tot);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -335,7 +381,7 @@ IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units) {
     g.qtiles = (int)ceil_div(q_rows, kIclQueries);
     g.q_padded = g.qtiles * kIclQueries;
     const long long base = (long long)g.qtiles * pairs;
-    const long long slots = 2LL * compute_units;  // two workgroups fit a CU
+    const long long slots = compute_units;  // one workgroup per CU (its waves use up to 512 registers)
     const int max_splits = std::max(1, kv_rows / 512);
     int splits = 1;
     if (base < slots) {
