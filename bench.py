@@ -14,6 +14,9 @@ the GPU to themselves (its rate in the two-stream steps, over the union of its
 launch intervals, is reported beside it). The build is timed separately (host
 FP32 inputs to a resident context). The oracle (C restatement of the reference
 CPU path) is timed on the host's cores on a bounded sample of the same rows.
+Passes of 1, 8, 16 and 32 rows, where streaming the cached K/V from HBM bounds
+the cross-attention, are timed after the steps and reported with their HBM
+fraction.
 
 Prints one JSON line.
 """
@@ -36,6 +39,9 @@ sys.path.insert(0, ROOT)
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBPS = 8000.0
 WORKLOAD = "clf-50k"
+# Pass sizes of the HBM-bound sweep of the cross-attention, and passes timed each.
+SMALL_PASSES = (1, 8, 16, 32)
+SMALL_PASS_REPEATS = 10
 # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the prediction-phase ICL attention
 # launch on this workload, calibrated against a plain copy kernel.
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "icl_attention_kernel_clf-50k.md")
@@ -199,6 +205,48 @@ def main() -> int:
     hipmem.synchronize()
     stats = {f: hip.profile_read(f) for f in hip.KERNEL_FAMILIES}
     hip.profile_enable(False)
+
+    # Passes of few rows: the cross-attention streams every layer's cached
+    # K/V (12 x 204.8 MB at 50,000 keys, far beyond the 256 MB MALL) for a
+    # handful of queries, so HBM bounds it. Algorithmic bytes per launch:
+    # K + V of one layer plus Q in and the attended rows out.
+    small = {}
+    if b != 1:
+        raise SystemExit("the small-pass sweep expects one estimator")
+    kv_bytes = 2.0 * b * 8 * n * 64 * 4
+    context.set_pass_rows(max(SMALL_PASSES))  # each prediction below is one pass
+    for qb in SMALL_PASSES:
+
+        def small_step():
+            hip.check(hip.lib().irx_predictor_predict_device(context.handle, dx.ptr, qb, dl.ptr, None))
+
+        small_step()
+        hipmem.synchronize()
+        hip.profile_enable(["icl_attention", "icl_merge"])
+        t0 = time.perf_counter()
+        for _ in range(SMALL_PASS_REPEATS):
+            small_step()
+        hipmem.synchronize()
+        pass_ms = 1000 * (time.perf_counter() - t0) / SMALL_PASS_REPEATS
+        att = hip.profile_read("icl_attention")
+        mrg = hip.profile_read("icl_merge")
+        hip.profile_enable(False)
+        launch_ms = att["milliseconds"] / max(att["launches"], 1)
+        merge_ms = mrg["milliseconds"] / max(att["launches"], 1)
+        algo = kv_bytes + 2.0 * b * 8 * qb * 64 * 4
+        small[str(qb)] = {
+            "avg_launch_ms": launch_ms,
+            "merge_ms_per_launch": merge_ms,
+            "bytes_per_launch": algo,
+            "achieved_gbps": algo / (launch_ms * 1e-3) / 1e9,
+            "frac": algo / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "frac_with_merge": algo / ((launch_ms + merge_ms) * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "ms_per_pass": pass_ms,
+            "launches": att["launches"],
+        }
+        log(f"pass of {qb:2d} rows: {pass_ms:.2f} ms, attention {1e3 * launch_ms:.1f} us/launch, "
+            f"{small[str(qb)]['achieved_gbps']:.0f} GB/s")
+    context.set_pass_rows(args.pass_rows)
     context.set_streams(2)
 
     # The same prediction from host buffers (PCIe included), for reference.
@@ -265,6 +313,10 @@ def main() -> int:
         "rows_per_s_host_buffers": host_rows_per_s,
         "one_stream": {"ms_per_step": one_stream_ms, "rows_per_s": q / (one_stream_ms * 1e-3)},
         "roofline": roofline,
+        "small_pass_hbm": {
+            "kernel": "icl_decode_kernel (passes of <= 32 rows against the 2.46 GB cached K/V, one stream)",
+            "bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s", "by_pass_rows": small,
+        },
         "kernel_ms_per_step": kernel_ms,
         "kernels": breakdown,
     }

@@ -339,10 +339,197 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
     }
 }
 
+// Few queries (a pass of at most 32 rows): the attention is bound by reading
+// K and V from HBM. A workgroup of kDecodeWaves waves takes one (pair, key
+// range); its waves take the range's 16-key blocks in turn, so together they
+// stream it front to back. Products run on the 16x16x4 FP32 MFMA over QG
+// groups of 16 queries, which pads a pass to 16 or 32 queries rather than 64.
+// Operands go straight from global memory into registers in MFMA order:
+//   scores S^T (key x query): A = K[key = lane % 16][dim 16 (lane / 16) + m],
+//     B = Q[query = lane % 16][same dim], for m = 0..15; lane l's result
+//     register r is key 4 (l / 16) + r, query l % 16;
+//   output O^T (dim x query), tile t: A = V[key 4 (l / 16) + r][dim 4 (l % 16)
+//     + t], B = that lane's own probability r: no data moves between lanes.
+// Every K load is a lane's 64 contiguous bytes of one key and every V load
+// four whole 256-byte rows per instruction. The next block's loads are issued
+// before the current block's products. The softmax is the lazy-reference form
+// above; the waves' partial results are merged through LDS at the end.
+constexpr int kDecodeQueries = 32;
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeOStride = 68;  // floats per query row of the LDS merge area
+
+template <int QG, bool SPLIT>
+__global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAttention p, IclLaunch g) {
+    __shared__ float red_o[kDecodeWaves][QG * 16 * kDecodeOStride];
+    __shared__ float red_m[kDecodeWaves][QG * 16], red_l[kDecodeWaves][QG * 16];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 4, i16 = lane & 15;
+    const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
+    const int k_begin = split * g.keys_per_split;
+    const int k_end = min(p.kv_rows, k_begin + g.keys_per_split);
+
+    float q[QG][16];
+    {
+        const float scale = 0.125f * kLog2e;
+#pragma unroll
+        for (int gq = 0; gq < QG; ++gq) {
+            const int row = 16 * gq + i16;
+            if (row < p.q_rows) {
+                const float *src = p.q + pair * p.q_pair_stride + (long long)row * 64 + 16 * grp;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const f32x4 v = *reinterpret_cast<const f32x4 *>(src + 4 * c);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) q[gq][4 * c + e] = v[e] * scale;
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < 16; ++m) q[gq][m] = 0.f;
+            }
+        }
+    }
+    const float *kbase = p.k + pair * p.kv_pair_stride;
+    const float *vbase = p.v + pair * p.kv_pair_stride;
+    // Block at k0: K dims 16 grp .. +15 of key k0 + i16, and V dims 4 i16 ..
+    // +3 of keys k0 + 4 grp + r. Keys past the range repeat its last key
+    // (masked below).
+    auto load = [&](int k0, f32x4 *kd, f32x4 *vd) {
+        const int key = min(k0 + i16, k_end - 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kd[c] = *reinterpret_cast<const f32x4 *>(kbase + (long long)key * 64 + 16 * grp + 4 * c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int vk = min(k0 + 4 * grp + r, k_end - 1);
+            vd[r] = *reinterpret_cast<const f32x4 *>(vbase + (long long)vk * 64 + 4 * i16);
+        }
+    };
+
+    f32x4 o[QG][4];
+    float neg_ref[QG], m_ref[QG], l_run[QG];
+#pragma unroll
+    for (int gq = 0; gq < QG; ++gq) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[gq][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        neg_ref[gq] = INFINITY, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
+    }
+    constexpr float kLazyLimit = 18446744073709551616.0f;  // 2^64
+    constexpr int kStride = 16 * kDecodeWaves;
+
+    f32x4 kf[4], vf[4];
+    int k0 = k_begin + 16 * wave;
+    if (k0 < k_end) load(k0, kf, vf);
+    for (; k0 < k_end; k0 += kStride) {
+        f32x4 nk[4], nv[4];
+        const bool more = k0 + kStride < k_end;
+        if (more) load(k0 + kStride, nk, nv);
+        const bool tail = k0 + 16 > k_end;
+#pragma unroll
+        for (int gq = 0; gq < QG; ++gq) {
+            f32x4 s = {neg_ref[gq], neg_ref[gq], neg_ref[gq], neg_ref[gq]};
+#pragma unroll
+            for (int m = 0; m < 16; ++m) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[m >> 2][m & 3], q[gq][m], s, 0, 0, 0);
+            if (tail) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (k0 + 4 * grp + r >= k_end) s[r] = -INFINITY;
+            }
+            float lsum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[r] = __builtin_amdgcn_exp2f(s[r]);
+                lsum += s[r];
+            }
+            if (__any(!(lsum <= kLazyLimit))) {
+                // Unset or too low a reference: redo this block's scores from zero.
+                s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int m = 0; m < 16; ++m)
+                    s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[m >> 2][m & 3], q[gq][m], s, 0, 0, 0);
+                if (tail) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (k0 + 4 * grp + r >= k_end) s[r] = -INFINITY;
+                }
+                float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+                mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+                mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                const float m_new = fmaxf(m_ref[gq], mt);
+                const float alpha = __builtin_amdgcn_exp2f(m_ref[gq] - m_new);
+                l_run[gq] *= alpha;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) o[gq][t] *= alpha;
+                neg_ref[gq] = -m_new;
+                m_ref[gq] = m_new;
+                lsum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    s[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
+                    lsum += s[r];
+                }
+            }
+            l_run[gq] += lsum;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    o[gq][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r][t], s[r], o[gq][t], 0, 0, 0);
+        }
+        if (more) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kf[c] = nk[c], vf[c] = nv[c];
+        }
+    }
+
+    // Each wave's (reference, sum, unnormalised output) per query to LDS:
+    // lane (grp, i16) holds dims 16 grp + 4 r + t of query 16 gq + i16.
+#pragma unroll
+    for (int gq = 0; gq < QG; ++gq) {
+        float l = l_run[gq];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const int qi = 16 * gq + i16;
+        if (grp == 0) red_m[wave][qi] = m_ref[gq], red_l[wave][qi] = l;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const f32x4 v = {o[gq][0][r], o[gq][1][r], o[gq][2][r], o[gq][3][r]};
+            *reinterpret_cast<f32x4 *>(&red_o[wave][qi * kDecodeOStride + 16 * grp + 4 * r]) = v;
+        }
+    }
+    __syncthreads();
+    // Merge: thread t takes query (t / 16) + 16 j and dims 4 (t % 16) .. +3.
+    // A wave that got no block has reference -inf and sum 0.
+#pragma unroll
+    for (int j = 0; j < QG; ++j) {
+        const int qi = (threadIdx.x >> 4) + 16 * j, d = 4 * (threadIdx.x & 15);
+        if (qi >= p.q_rows) continue;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, red_m[w][qi]);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        float den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            const float wgt = __builtin_amdgcn_exp2f(red_m[w][qi] - mx);
+            acc += wgt * *reinterpret_cast<const f32x4 *>(&red_o[w][qi * kDecodeOStride + d]);
+            den += wgt * red_l[w][qi];
+        }
+        const f32x4 out = acc * (1.0f / den);
+        if constexpr (!SPLIT) {
+            const int b = pair / kHeads, head = pair - b * kHeads;
+            *reinterpret_cast<f32x4 *>(p.o + ((long long)b * p.q_rows + qi) * p.ldo + head * 64 + d) = out;
+        } else {
+            const long long row = ((long long)split * p.pairs + pair) * g.q_padded + qi;
+            *reinterpret_cast<f32x4 *>(p.partial + row * 64 + d) = out;
+            if (d == 0) p.partial[(long long)g.splits * p.pairs * g.q_padded * 64 + row] = mx + log2f(den);
+        }
+    }
+}
+
 // Merge of split partials by their log2-sum-exp, into tokens [b * q_rows +
 // row, head * 64 + d]. Partial outputs are [splits, pairs, q_padded, 64],
 // followed by the log2-sum-exps [splits, pairs, q_padded]. One wave per
 // (pair, row): lane = split group (lane / 16, every fourth split) x four dims.
+// Each round loads eight splits per group at once and folds them into the
+// lane's running reference; the four groups are combined at the end.
 __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int splits, int q_padded) {
     const long long pq = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (pq >= (long long)p.pairs * p.q_rows) return;
@@ -352,24 +539,48 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
     const long long step = (long long)p.pairs * q_padded;  // rows between splits
     const long long row0 = (long long)pair * q_padded + qrow;
     const float *lse = p.partial + (long long)splits * step * 64 + row0;
-    float mx = -INFINITY;
-    for (int s = sg; s < splits; s += 4) mx = fmaxf(mx, lse[s * step]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float m_run = -INFINITY, den = 0.f;
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.f;
-#pragma unroll 4
-    for (int s = sg; s < splits; s += 4) {
-        const float w = __builtin_amdgcn_exp2f(lse[s * step] - mx);
-        const f32x4 v = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + s * step) * 64 + d);
-        num += w * v;
-        den += w;
+    for (int s0 = sg; s0 < splits; s0 += 32) {
+        float l8[8];
+        f32x4 v8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int s = s0 + 4 * j;
+            if (s < splits) {
+                l8[j] = lse[s * step];
+                v8[j] = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + s * step) * 64 + d);
+            } else {
+                l8[j] = -INFINITY;
+                v8[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        float m_new = m_run;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m_new = fmaxf(m_new, l8[j]);
+        const float a = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while m_run is -inf
+        num *= a, den *= a;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float w = __builtin_amdgcn_exp2f(l8[j] - m_new);
+            num += w * v8[j];
+            den += w;
+        }
+        m_run = m_new;
     }
 #pragma unroll
     for (int off = 16; off <= 32; off *= 2) {
-        den += __shfl_xor(den, off, 64);
+        const float m_o = __shfl_xor(m_run, off, 64), den_o = __shfl_xor(den, off, 64);
+        f32x4 num_o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) num[e] += __shfl_xor(num[e], off, 64);
+        for (int e = 0; e < 4; ++e) num_o[e] = __shfl_xor(num[e], off, 64);
+        const float m_new = fmaxf(m_run, m_o);
+        if (m_new != -INFINITY) {  // both groups empty: nothing to combine
+            const float a = __builtin_amdgcn_exp2f(m_run - m_new), b = __builtin_amdgcn_exp2f(m_o - m_new);
+            num = a * num + b * num_o;
+            den = a * den + b * den_o;
+            m_run = m_new;
+        }
     }
     if (sg != 0) return;
     const int b = pair / kHeads, head = pair - b * kHeads;
@@ -378,6 +589,19 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
 
 IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units) {
     IclLaunch g{};
+    if (q_rows <= kDecodeQueries) {
+        // One workgroup per (pair, key range), about two per CU, at least 256
+        // keys each; ranges in whole rounds of the waves' 16-key blocks.
+        g.qtiles = 1;
+        g.q_padded = kDecodeQueries;
+        const int want = std::max(1, (int)ceil_div(2LL * compute_units, pairs));
+        const int splits = std::max(1, std::min(want, kv_rows / 256));
+        const int per = (int)ceil_div(ceil_div(kv_rows, splits), 16 * kDecodeWaves) * 16 * kDecodeWaves;
+        g.keys_per_split = per;
+        g.splits = (int)ceil_div(kv_rows, per);
+        g.per_xcd = 0;
+        return g;
+    }
     g.qtiles = (int)ceil_div(q_rows, kIclQueries);
     g.q_padded = g.qtiles * kIclQueries;
     const long long base = (long long)g.qtiles * pairs;
@@ -698,7 +922,8 @@ int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units) 
 
 size_t icl_attention_partial_floats(int pairs, int q_rows, int splits) {
     if (splits <= 1) return 0;
-    size_t q_padded = ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
+    size_t q_padded = q_rows <= kDecodeQueries ? (size_t)kDecodeQueries
+                                                : ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
     return (size_t)splits * pairs * q_padded * 65;
 }
 
@@ -718,12 +943,26 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
     {
         const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
         KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, 4.0 * 64.0 * pairs * (2.0 * kv + 2.0 * q));
-        if (g.splits > 1)
+        if (args.q_rows <= kDecodeQueries) {
+            const dim3 blocks((unsigned)((long long)args.pairs * g.splits)), threads(kDecodeWaves * 64);
+            if (args.q_rows <= 16) {
+                if (g.splits > 1)
+                    hipLaunchKernelGGL((icl_decode_kernel<1, true>), blocks, threads, 0, stream, args, g);
+                else
+                    hipLaunchKernelGGL((icl_decode_kernel<1, false>), blocks, threads, 0, stream, args, g);
+            } else {
+                if (g.splits > 1)
+                    hipLaunchKernelGGL((icl_decode_kernel<2, true>), blocks, threads, 0, stream, args, g);
+                else
+                    hipLaunchKernelGGL((icl_decode_kernel<2, false>), blocks, threads, 0, stream, args, g);
+            }
+        } else if (g.splits > 1) {
             hipLaunchKernelGGL((icl_attention_kernel<true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
                                args, g);
-        else
+        } else {
             hipLaunchKernelGGL((icl_attention_kernel<false>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
                                args, g);
+        }
         IRX_HIP(hipGetLastError());
     }
     if (g.splits > 1) {
