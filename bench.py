@@ -121,6 +121,8 @@ def main() -> int:
     ap.add_argument("--pass-rows", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--context-io", metavar="DIR", default=None,
+                    help="also time exporting the resident context to an IRCNTXT file in DIR and reloading it")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel over BYTES (reference for traffic counters)")
     args = ap.parse_args()
@@ -249,6 +251,31 @@ def main() -> int:
     context.set_pass_rows(args.pass_rows)
     context.set_streams(2)
 
+    context_io = None
+    if args.context_io:
+        # Export streams the 30 cache tensors out of HBM into a temporary file
+        # (hashing as it goes) and renames it into place; the reload maps the
+        # file, verifies its digest and every value, and uploads it to HBM.
+        import tempfile
+        path = os.path.join(tempfile.mkdtemp(dir=args.context_io), "context.irctx")
+        resident = executor.build_context(x, y)
+        t0 = time.perf_counter()
+        resident.save_context(path)
+        export_s = time.perf_counter() - t0
+        size = os.path.getsize(path)
+        t0 = time.perf_counter()
+        loaded = executor.load_context(path)
+        hipmem.synchronize()
+        import_s = time.perf_counter() - t0
+        loaded.set_pass_rows(args.pass_rows)
+        check = loaded.predict_raw(xt[:, :512]).logits
+        context_io = {"bytes": size, "export_s": export_s, "export_gbps": size / export_s / 1e9,
+                      "import_s": import_s, "import_gbps": size / import_s / 1e9,
+                      "reload_identical": bool(np.array_equal(check, gpu_logits[:, :512]))}
+        del loaded, resident
+        os.remove(path)
+        log(f"context export {export_s:.2f} s, verified reload {import_s:.2f} s ({size / 1e9:.2f} GB)")
+
     # The same prediction from host buffers (PCIe included), for reference.
     t0 = time.perf_counter()
     context.predict_raw(xt)
@@ -317,6 +344,7 @@ def main() -> int:
             "kernel": "icl_decode_kernel (passes of <= 32 rows against the 2.46 GB cached K/V, one stream)",
             "bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s", "by_pass_rows": small,
         },
+        "context_io": context_io,
         "kernel_ms_per_step": kernel_ms,
         "kernels": breakdown,
     }

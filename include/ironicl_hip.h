@@ -186,6 +186,16 @@ int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows);
  * in order on one stream. Results are identical either way. No counterpart in
  * the reference (its predictor runs passes in order, predictor.rs:224-271). */
 int irx_predictor_set_streams(irx_predictor *predictor, int streams);
+/* Copies floats [offset, offset + floats) of one resident context tensor to
+ * host memory, after every pass issued before the call. `tensor` indexes the
+ * reference's context tensor order (context_tensors, cpu.rs:4106-4123):
+ * 0..5 = column.{0..2}.{key,value} [B, H+4, 8, 128, 16], 6..29 =
+ * icl.{0..11}.{key,value} [B, 8, N, 64]. It is what exporting a GPU-built
+ * context to IRCNTXT needs (StaticExecutor::save_context, cpu.rs:1716-1742;
+ * the reference's CUDA build always writes the tensors to host pages,
+ * cpu.rs:744-805, where this backend keeps them in HBM until asked). */
+int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t offset, size_t floats,
+                               float *dst);
 
 /* Predictor::predict (predictor.rs:224-271): x [B, Q, H] on the host, logits
  * [B, Q, outputs] on the host. cpu_rows, when not NULL, gets Q flags: 1 for a

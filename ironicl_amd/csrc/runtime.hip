@@ -1084,6 +1084,29 @@ int irx_predictor_set_streams(irx_predictor *predictor, int streams) {
     });
 }
 
+int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t offset, size_t floats, float *dst) {
+    return guarded("irx_predictor_read_context", [&] {
+        if (!predictor || (floats && !dst)) fail(IRX_INVALID_ARGUMENT, "context read needs a predictor and a buffer");
+        const irx_shape &s = predictor->shape;
+        const size_t col_plane = s.ensembles * (s.features + kReserved) * (size_t)kColumnCache;
+        const size_t icl_plane = s.ensembles * (size_t)kHeads * s.rows * kIclHead;
+        const size_t column_tensors = 2 * kColumnBlocks;
+        if (tensor >= column_tensors + 2 * kIclBlocks) fail(IRX_INVALID_ARGUMENT, "context tensor index out of range");
+        const bool column = tensor < column_tensors;
+        const size_t index = column ? tensor : tensor - column_tensors;
+        const size_t plane = column ? col_plane : icl_plane;
+        if (offset > plane || floats > plane - offset) fail(IRX_INVALID_ARGUMENT, "context read past the tensor's end");
+        if (!floats) return;
+        const DevBuf &buf = column ? predictor->column[index / 2] : predictor->icl[index / 2];
+        const float *src = buf.f() + (index % 2) * plane + offset;
+        std::lock_guard<std::mutex> lock(predictor->mu);
+        set_device(predictor->weights->device);
+        // On the predictor's stream: after every pass issued before the call.
+        IRX_HIP(hipMemcpyAsync(dst, src, floats * 4, hipMemcpyDeviceToHost, predictor->stream));
+        IRX_HIP(hipStreamSynchronize(predictor->stream));
+    });
+}
+
 int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows) {
     return guarded("irx_predictor_set_pass_rows", [&] {
         if (!predictor || rows < 32 || rows % 32 || rows > (1u << 20))

@@ -16,11 +16,14 @@ listed in ``Prediction.cpu_rows`` for the caller's own CPU path.
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import math
+import os
 from dataclasses import dataclass, field
 
 import numpy as np
 
+from . import context_file as cf
 from . import hip
 from . import manifest as mf
 
@@ -76,12 +79,22 @@ class Executor:
     """An official TabICLv2 model with its weights resident on the GPU
     (Executor, cpu.rs:290-296; ModelWeights::new, cuda/weights.rs:299)."""
 
-    def __init__(self, task: str, weights: dict[str, np.ndarray], device: hip.Device | None = None):
+    def __init__(self, task: str, weights: dict[str, np.ndarray], device: hip.Device | None = None,
+                 source_sha256: str | None = None):
+        """`source_sha256` (64 hex digits) is the source checkpoint's SHA-256
+        the model artifact records (ModelSummary::source_sha256), which
+        context identities and IRCNTXT files carry. Without one, the SHA-256
+        of the weights themselves stands in (`weights_sha256`)."""
         if task not in (mf.CLASSIFIER, mf.REGRESSOR):
             raise ValueError(f"unknown task {task!r}")
         self.task = task
         self.weights = {k: _f32(v) for k, v in weights.items()}
         self.width = mf.decoder_width(task)
+        if source_sha256 is None:
+            source_sha256 = weights_sha256(task, self.weights)
+        if len(source_sha256) != 64 or any(c not in "0123456789abcdef" for c in source_sha256):
+            raise ValueError("source_sha256 must be 64 lowercase hex digits")
+        self.source_sha256 = source_sha256
         self.device = device if device is not None else hip.Device(0)
 
         @hip.LOOKUP
@@ -168,12 +181,11 @@ class Executor:
 
     # ---- build (build_context / build_tensors_cuda, cpu.rs:627-804) ----
 
-    def build_context(self, x: np.ndarray, y_train: np.ndarray, class_permutations=None,
-                      feature_permutations=None, download: bool = False, progress=None,
-                      device_limit: int = 0) -> "StaticExecutor":
-        """Build the static context of x [B, N, H], y_train [B, N] on the GPU and
-        keep it resident. With ``download``, also copy every cache tensor to the
-        host (``StaticExecutor.context``)."""
+    def context_metadata(self, x: np.ndarray, y_train: np.ndarray, class_permutations=None,
+                         feature_permutations=None, optimize: str = "safe") -> cf.Metadata:
+        """Validate a context's inputs and describe it, with its cache identity
+        (context_metadata, cpu.rs:809-869). Permutations default to the
+        identity: class [B, C] (classifier) and feature [B, H]."""
         x = _f32(x)
         y_train = _f32(y_train)
         if x.ndim != 3 or y_train.shape != x.shape[:2] or min(x.shape) == 0:
@@ -182,6 +194,63 @@ class Executor:
         classes = validate_labels(y_train, b, n) if self.task == mf.CLASSIFIER else 0
         if self.task == mf.REGRESSOR and not np.all(np.isfinite(y_train)):
             raise ValueError("regression targets must be finite")
+        cperm = (np.asarray(class_permutations, dtype=np.uint64).reshape(-1) if class_permutations is not None
+                 else np.tile(np.arange(classes, dtype=np.uint64), b))
+        fperm = (np.asarray(feature_permutations, dtype=np.uint64).reshape(-1) if feature_permutations is not None
+                 else np.tile(np.arange(h, dtype=np.uint64), b))
+        meta = cf.Metadata(bytes.fromhex(self.source_sha256),
+                           cf.context_identity(self.source_sha256, optimize, x, y_train, cperm, fperm),
+                           b, n, h, classes, cperm, fperm)
+        try:
+            cf.validate_metadata(meta)
+        except cf.ContextError as e:
+            raise ValueError(str(e)) from None
+        return meta
+
+    def build_context(self, x: np.ndarray, y_train: np.ndarray, class_permutations=None,
+                      feature_permutations=None, download: bool = False, progress=None,
+                      device_limit: int = 0, cache_dir=False, optimize: str = "safe") -> "StaticExecutor":
+        """Build the static context of x [B, N, H], y_train [B, N] on the GPU and
+        keep it resident (Executor::build_context, cpu.rs:600-673). With
+        ``download``, also copy every cache tensor to the host
+        (``StaticExecutor.context``).
+
+        ``cache_dir`` (None/True: the default cache directory, False: none, or
+        a path): load the context from ``<identity>.irctx`` there when that
+        file holds exactly this context, else build it and write it there.
+        A missing, invalid or mismatched entry is rebuilt; a failed write
+        leaves the context in HBM only (cpu.rs:645-672). Only ``optimize="safe"``
+        (FP32) builds on this backend."""
+        if optimize != "safe":
+            raise ValueError("this backend builds FP32 contexts only (optimize='safe')")
+        meta = self.context_metadata(x, y_train, class_permutations, feature_permutations, optimize)
+        directory = cf.resolve_cache_dir(cache_dir)
+        if directory is not None:
+            path = cf.cache_path(directory, meta)
+            cached = cf.read_cached(path, meta)
+            if cached is not None:
+                try:
+                    cf.validate_for_model(cached, self.source_sha256, self.task)
+                except cf.ContextError:
+                    cached = None
+            if cached is not None:
+                try:
+                    os.utime(path)  # the entry's last use, for clear_cache
+                except OSError:
+                    pass
+                return self._attach(cached)
+        executor = self._build(_f32(x), _f32(y_train), meta, download, progress, device_limit)
+        if directory is not None:
+            # Caching is best effort: a context that cannot be written is still returned.
+            try:
+                directory.mkdir(parents=True, exist_ok=True)
+                executor.save_context(path)
+            except (OSError, ValueError):
+                pass
+        return executor
+
+    def _build(self, x, y_train, meta: cf.Metadata, download: bool, progress, device_limit: int) -> "StaticExecutor":
+        b, n, h = x.shape
         col_labels, icl_labels = self.label_embeddings(y_train)
         ind_q = self.inducing_queries(n)
         bases = self.icl_base_scales(n)
@@ -212,16 +281,55 @@ class Executor:
         keep = ctypes.c_void_p()
         hip.check(hip.lib().irx_build(self.handle, hip.PRECISION_FP32, ctypes.byref(inp), ctypes.byref(out),
                                       ctypes.byref(keep)))
-        return StaticExecutor(self, (b, n, h), classes, class_permutations, feature_permutations,
-                              built=keep.value, context=context, base_scales=bases)
+        return StaticExecutor(self, (b, n, h), meta.class_count, meta.class_permutations,
+                              meta.feature_permutations, built=keep.value, context=context, base_scales=bases,
+                              metadata=meta)
 
-    def load_context(self, context, shape, classes: int, class_permutations=None,
-                     feature_permutations=None) -> "StaticExecutor":
+    def _attach(self, context: cf.ContextFile) -> "StaticExecutor":
+        """Upload a verified context for prediction (with_executor / with_cuda, cpu.rs:1745-1910)."""
+        meta = context.metadata
+        b, n, _ = meta.shape
+        return StaticExecutor(self, meta.shape, meta.class_count, meta.class_permutations,
+                              meta.feature_permutations, built=None, context=context.host_tensors(),
+                              base_scales=self.icl_base_scales(n), metadata=meta, keep_alive=context)
+
+    def load_context(self, path) -> "StaticExecutor":
+        """Load a persisted IRCNTXT context, verify it against this model and
+        upload it to HBM (Executor::load_context, cpu.rs:397-406)."""
+        context = cf.read(path)
+        cf.validate_for_model(context, self.source_sha256, self.task)
+        return self._attach(context)
+
+    def load_context_bytes(self, data: bytes) -> "StaticExecutor":
+        """The same from the bytes ``StaticExecutor.encode_context`` wrote
+        (Executor::load_context_bytes, cpu.rs:415-424)."""
+        context = cf.from_bytes(data)
+        cf.validate_for_model(context, self.source_sha256, self.task)
+        return self._attach(context)
+
+    def load_context_tensors(self, context, shape, classes: int, class_permutations=None,
+                             feature_permutations=None) -> "StaticExecutor":
         """Upload host context tensors (column K/V [B,H+4,8,128,16] x 3 each, ICL
-        K/V [B,8,N,64] x 12 each) for prediction (Executor::load_context, cpu.rs:397-406)."""
+        K/V [B,8,N,64] x 12 each) for prediction, without a file."""
         b, n, h = shape
         return StaticExecutor(self, (b, n, h), classes, class_permutations, feature_permutations,
                               built=None, context=context, base_scales=self.icl_base_scales(n))
+
+
+def weights_sha256(task: str, weights: dict[str, np.ndarray]) -> str:
+    """A model identity from the weights themselves: SHA-256 over the task and,
+    in the official manifest's order, each tensor's name, shape and FP32
+    bytes. It stands in for a source checkpoint's SHA-256 when there is none
+    (random-init weights)."""
+    digest = hashlib.sha256(f"ironicl-weights\0{task}\0".encode())
+    for name, shape in mf.tensor_manifest(task).items():
+        arr = weights.get(name)
+        if arr is None:
+            continue
+        arr = np.ascontiguousarray(arr, dtype="<f4")
+        digest.update(name.encode() + b"\0" + np.asarray(arr.shape, dtype="<u8").tobytes())
+        digest.update(memoryview(arr).cast("B"))
+    return digest.hexdigest()
 
 
 def _progress(fn):
@@ -244,10 +352,12 @@ class StaticExecutor:
     Predictor, cuda/predictor.rs:93-271)."""
 
     def __init__(self, executor: Executor, shape, classes: int, class_permutations, feature_permutations,
-                 built, context, base_scales):
+                 built, context, base_scales, metadata: cf.Metadata | None = None, keep_alive=None):
         self.executor = executor
         self.shape = shape
         self.classes = classes
+        self.metadata = metadata
+        self._keep_alive = keep_alive
         b = shape[0]
         self.class_permutations = (np.asarray(class_permutations, dtype=np.uint64).reshape(b, -1)
                                    if class_permutations is not None
@@ -309,6 +419,53 @@ class StaticExecutor:
 
     def outputs(self) -> int:
         return self.classes if self.classes else self.executor.width
+
+    # ---- persistence (StaticExecutor::save_context / encode_context, cpu.rs:1716-1742) ----
+
+    def _tensor_source(self):
+        """Values of each context tensor, from the host copy when there is one,
+        otherwise streamed out of HBM (irx_predictor_read_context)."""
+        if self.context is not None:
+            ck, cv, ik, iv = self.context
+            named = {}
+            for i in range(mf.COLUMN_BLOCKS):
+                named[f"column.{i}.key"], named[f"column.{i}.value"] = ck[i], cv[i]
+            for i in range(mf.ICL_BLOCKS):
+                named[f"icl.{i}.key"], named[f"icl.{i}.value"] = ik[i], iv[i]
+            flat = {k: np.ascontiguousarray(v, dtype=np.float32).reshape(-1) for k, v in named.items()}
+            return lambda name, start, count: flat[name][start:start + count]
+        index = {name: i for i, (name, _) in enumerate(cf.context_tensor_specs(*self.shape))}
+        buffers = {}
+
+        def read(name, start, count):
+            buf = buffers.get(count)
+            if buf is None:
+                buffers.clear()
+                buf = buffers[count] = np.empty(count, np.float32)
+            hip.check(hip.lib().irx_predictor_read_context(self.handle, index[name], start, count,
+                                                           buf.ctypes.data_as(ctypes.c_void_p)))
+            return buf
+
+        return read
+
+    def _persistable(self) -> cf.Metadata:
+        if self.metadata is None:
+            raise ValueError("this context has no identity metadata (built from bare tensors); "
+                             "build it with Executor.build_context to save it")
+        return self.metadata
+
+    def save_context(self, path) -> None:
+        """Write the context as an IRCNTXT file, atomically, streaming its
+        tensors from HBM when no host copy exists."""
+        meta = self._persistable()
+        cf.write(path, meta, cf.context_tensor_specs(*self.shape), self._tensor_source())
+
+    def context_encoded_len(self) -> int:
+        return cf.encoded_len(self._persistable(), cf.context_tensor_specs(*self.shape))
+
+    def encode_context(self, sink) -> None:
+        """Encode the context into the binary file-like `sink` as save_context writes it."""
+        cf.encode(self._persistable(), cf.context_tensor_specs(*self.shape), self._tensor_source(), sink)
 
     def predict_raw(self, x: np.ndarray, progress=None) -> Prediction:
         """Every decoder output [B, Q, width] (Predictor::predict, predictor.rs:224-271)."""

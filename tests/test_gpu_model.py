@@ -63,7 +63,7 @@ def test_built_context_matches_oracle(lcg):
 def test_cached_prediction_on_the_oracle_context(clf, clf_oracle, lcg):
     """The predictor alone: the oracle's context uploaded, GPU vs CPU predict."""
     x, y, xt, shifts, ctx_cpu, _ = lcg
-    st = clf.load_context(ctx_cpu, x.shape, 3, shifts)
+    st = clf.load_context_tensors(ctx_cpu, x.shape, 3, shifts)
     gpu = st.predict_raw(xt).logits
     cpu = clf_oracle.predict_cached(ctx_cpu, xt)
     assert_parity(gpu, cpu, "predict on the oracle context")
