@@ -352,8 +352,9 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
 //     + t], B = that lane's own probability r: no data moves between lanes.
 // Every K load is a lane's 64 contiguous bytes of one key and every V load
 // four whole 256-byte rows per instruction. The next block's loads are issued
-// before the current block's products. The softmax is the lazy-reference form
-// above; the waves' partial results are merged through LDS at the end.
+// before the current block's products, into the other of two register sets.
+// The softmax is the lazy-reference form above; the waves' partial results
+// are merged through LDS at the end.
 constexpr int kDecodeQueries = 32;
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeOStride = 68;  // floats per query row of the LDS merge area
@@ -414,14 +415,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
     constexpr float kLazyLimit = 18446744073709551616.0f;  // 2^64
     constexpr int kStride = 16 * kDecodeWaves;
 
-    f32x4 kf[4], vf[4];
-    int k0 = k_begin + 16 * wave;
-    if (k0 < k_end) load(k0, kf, vf);
-    for (; k0 < k_end; k0 += kStride) {
-        f32x4 nk[4], nv[4];
-        const bool more = k0 + kStride < k_end;
-        if (more) load(k0 + kStride, nk, nv);
-        const bool tail = k0 + 16 > k_end;
+    // One 16-key block at kk (kk < k_end): scores, lazy softmax, output.
+    auto process = [&](int kk, const f32x4 *kf, const f32x4 *vf) {
+        const bool tail = kk + 16 > k_end;
 #pragma unroll
         for (int gq = 0; gq < QG; ++gq) {
             f32x4 s = {neg_ref[gq], neg_ref[gq], neg_ref[gq], neg_ref[gq]};
@@ -430,7 +426,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
             if (tail) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (k0 + 4 * grp + r >= k_end) s[r] = -INFINITY;
+                    if (kk + 4 * grp + r >= k_end) s[r] = -INFINITY;
             }
             float lsum = 0.f;
 #pragma unroll
@@ -447,7 +443,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
                 if (tail) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (k0 + 4 * grp + r >= k_end) s[r] = -INFINITY;
+                        if (kk + 4 * grp + r >= k_end) s[r] = -INFINITY;
                 }
                 float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
                 mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
@@ -473,10 +469,23 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
                 for (int t = 0; t < 4; ++t)
                     o[gq][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r][t], s[r], o[gq][t], 0, 0, 0);
         }
-        if (more) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) kf[c] = nk[c], vf[c] = nv[c];
-        }
+    };
+
+    // Two register sets in turn: the next block's loads are always issued
+    // (past the range they re-read its last key, a cached row) before the
+    // current block's products, and no registers are copied between sets, so
+    // each block waits only for its own loads.
+    f32x4 k_a[4], v_a[4], k_b[4], v_b[4];
+    int k0 = k_begin + 16 * wave;
+    load(k0, k_a, v_a);
+    while (k0 < k_end) {
+        load(k0 + kStride, k_b, v_b);
+        process(k0, k_a, v_a);
+        k0 += kStride;
+        if (k0 >= k_end) break;
+        load(k0 + kStride, k_a, v_a);
+        process(k0, k_b, v_b);
+        k0 += kStride;
     }
 
     // Each wave's (reference, sum, unnormalised output) per query to LDS:
