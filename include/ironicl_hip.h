@@ -213,6 +213,42 @@ int irx_predictor_predict_device(irx_predictor *predictor, const float *x_device
  * on the stream each kernel family launches on, with each launch's
  * algorithmic FLOPs and minimal HBM bytes, for roofline measurement. ---- */
 
+/* ---- TabICL preprocessing on the GPU (f64) ----
+ * Fitting every kept feature at once replaces fit_feature
+ * (src/models/tabicl_v2/preprocess.rs:259-296, run per feature on CPU
+ * threads there); transforming replaces Normalization::transform and
+ * Preprocessor::ensemble_rows (:223-254, :588-613), writing each member's
+ * FP32 rows where the predictor reads them. The ensemble draws, labels and
+ * the IRPREP bytes stay host code. */
+
+/* x [rows, columns] on the host, f32 (x_f64 = 0) or f64; kept: increasing
+ * indices of the kept columns; methods[groups]: 0 none, 1 power, unique.
+ * statistics [groups, 9, kept_count] f64 receives, per group and kept feature,
+ * mean, scale, minimum, maximum, lower, upper, then (power groups) lambda,
+ * mean, scale (Normalization::statistics order; none groups leave the last
+ * three 0). Errors as fit_feature's. */
+int irx_preprocess_fit(irx_device *device, const void *x, int x_f64, size_t rows, size_t columns,
+                       const uint32_t *kept, size_t kept_count, const int *methods, size_t groups,
+                       double outlier_threshold, double *statistics);
+
+typedef struct irx_preprocessor irx_preprocessor;
+/* A fitted preprocessor resident on the device: statistics as
+ * irx_preprocess_fit returns them, member_groups[members] and
+ * feature_orders[members, kept_count] (each a permutation of 0..kept_count). */
+int irx_preprocessor_new(irx_device *device, size_t columns, const uint32_t *kept, size_t kept_count,
+                         const int *methods, size_t groups, const double *statistics, size_t members,
+                         const uint32_t *member_groups, const uint32_t *feature_orders, irx_preprocessor **out);
+void irx_preprocessor_free(irx_preprocessor *preprocessor);
+/* x [rows, columns] on the host. With members_out, out receives each member's
+ * rows [members, rows, kept_count] (the predictor's x); otherwise each
+ * group's rows [groups, rows, kept_count]. out is device memory when
+ * out_on_device. A group whose power transform overflows within a chunk of
+ * chunk_rows rows is recomputed for that chunk clipped to the training range
+ * (the reference predicts in chunks of 8,192 rows, fitted.rs:13; training
+ * rows are one chunk). */
+int irx_preprocessor_transform(irx_preprocessor *preprocessor, const void *x, int x_f64, size_t rows,
+                               size_t chunk_rows, int members_out, float *out, int out_on_device);
+
 typedef struct irx_kernel_stats {
     uint64_t launches;
     double milliseconds; /* summed kernel durations */
@@ -256,6 +292,11 @@ int irx_test_layer_norm(irx_device *device, const float *x, const float *weight,
  * kernel: the known-size reference for HBM traffic counters. */
 int irx_test_copy(irx_device *device, size_t floats);
 /* 16-wide-head attention: q [heads, query_rows, 16], k and v [heads, rows, 16]. */
+/* The Yeo-Johnson PowerTransformer fit alone (yeo_johnson.rs fit_power) on
+ * each column of x [rows, columns] f64 as given: lambda_mean_scale [3, columns]
+ * and, when not NULL, the fitted standardized values [rows, columns]. */
+int irx_test_power_fit(irx_device *device, const double *x, size_t rows, size_t columns, double *lambda_mean_scale,
+                       double *fitted);
 int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v,
                              size_t heads, size_t query_rows, size_t rows, float *out);
 

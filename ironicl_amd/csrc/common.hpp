@@ -167,6 +167,54 @@ int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units);
 size_t icl_attention_partial_floats(int pairs, int q_rows, int splits);
 void icl_attention(const IclAttention &args, hipStream_t stream);
 
+// TabICL preprocessing (preprocess.hip), in f64. Fit: statistics of every
+// kept feature, [groups, 9, kept_count] (mean, scale, minimum, maximum,
+// lower, upper, then lambda, mean, scale of the power transform), and a
+// status per feature (0 ok, 1 non-finite statistics, 2 Yeo-Johnson bounds
+// not finite, 3 power transform not finite). Features go `batch` at a time
+// through `scratch` (batch x 3 x rows doubles).
+struct PreprocessFit {
+    const void *x;  // [rows, columns], f32 or f64 (x_f64)
+    int x_f64;
+    long long rows, columns;
+    const unsigned *kept;
+    int kept_count;
+    int groups;
+    int methods[2];  // 0 none, 1 power
+    double threshold;
+    double *scratch;
+    int batch;
+    double *stats;
+    int *status;
+    int raw;         // power fit on the values as given (a test of the Yeo-Johnson fit alone)
+    double *fitted;  // raw mode: fitted values [kept_count, rows], or null
+};
+void preprocess_fit(const PreprocessFit &args, hipStream_t stream);
+
+// Transform: every group's FP32 rows [groups, rows, kept_count]. `redo`
+// (null on the first pass) marks the (chunk, group) pairs to recompute with
+// clipping after `overflow` flagged them.
+struct PreprocessTransform {
+    const void *x;
+    int x_f64;
+    long long rows, columns;
+    const unsigned *kept;
+    int kept_count;
+    int groups;
+    int methods[2];
+    const double *stats;
+    long long chunk_rows;
+    const int *redo;
+    int *overflow;
+    int *nonfinite;
+    float *out;
+};
+void preprocess_transform(const PreprocessTransform &args, hipStream_t stream);
+// Members' rows [members, rows, features] from the group rows and each
+// member's group and feature order.
+void preprocess_gather(const float *group_rows, long long rows, int features, int members,
+                       const unsigned *member_groups, const unsigned *orders, float *out, hipStream_t stream);
+
 // Glue kernels (glue.hip).
 void column_input(const float *x, long long x_estimator_stride, int b, int rows, int h, const float *in_w, const float *in_b,
                   const float *labels, float *state, uint8_t *missing_rows, hipStream_t stream);

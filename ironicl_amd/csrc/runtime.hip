@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <string>
@@ -1319,3 +1320,228 @@ int irx_test_small_attention(irx_device *device, const float *q, const float *k,
 }
 
 }  // extern "C"
+
+// ---- TabICL preprocessing (preprocess.rs fit_feature / transform / ensemble_rows) ----
+
+namespace {
+
+constexpr size_t kFitScratchBytes = size_t(4) << 30;  // features fitted per launch: their f64 scratch
+
+const char *fit_error(int status) {
+    switch (status) {
+        case 2: return "Yeo-Johnson bounds are not finite";
+        case 3: return "the power transform of the training data is not finite";
+        default: return "Training data produced non-finite preprocessing statistics";
+    }
+}
+
+void check_methods(const int *methods, size_t groups) {
+    if (!methods || groups < 1 || groups > 2) fail(IRX_INVALID_ARGUMENT, "one or two normalization groups are needed");
+    for (size_t g = 0; g < groups; ++g)
+        if (methods[g] != 0 && methods[g] != 1) fail(IRX_INVALID_ARGUMENT, "normalization method must be 0 (none) or 1 (power)");
+    if (groups == 2 && methods[0] == methods[1]) fail(IRX_INVALID_ARGUMENT, "normalization groups must be unique");
+}
+
+void check_kept(const uint32_t *kept, size_t kept_count, size_t columns) {
+    if (!kept || !kept_count || kept_count > columns) fail(IRX_INVALID_ARGUMENT, "kept features are invalid");
+    for (size_t k = 0; k < kept_count; ++k)
+        if (kept[k] >= columns || (k && kept[k] <= kept[k - 1]))
+            fail(IRX_INVALID_ARGUMENT, "kept features must be increasing column indices");
+}
+
+}  // namespace
+
+struct irx_preprocessor {
+    irx_device *device = nullptr;
+    size_t columns = 0;
+    int kept_count = 0, groups = 0, members = 0;
+    int methods[2] = {0, 0};
+    DevBuf kept, stats, member_groups, orders;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    DevBuf x, group_rows, flags, members_out;  // grow-only workspaces
+};
+
+int irx_preprocess_fit(irx_device *device, const void *x, int x_f64, size_t rows, size_t columns,
+                       const uint32_t *kept, size_t kept_count, const int *methods, size_t groups,
+                       double outlier_threshold, double *statistics) {
+    return guarded("irx_preprocess_fit", [&] {
+        if (!device || !x || !statistics || rows < 2 || !columns)
+            fail(IRX_INVALID_ARGUMENT, "preprocessing needs at least two training rows");
+        check_kept(kept, kept_count, columns);
+        check_methods(methods, groups);
+        if (!(outlier_threshold > 0.0 && std::isfinite(outlier_threshold)))
+            fail(IRX_INVALID_ARGUMENT, "outlier_threshold must be positive and finite");
+        set_device(device);
+        const size_t elem = x_f64 ? 8 : 4;
+        DevBuf dx(rows * columns * elem), dkept(kept_count * 4), dstats(groups * 9 * kept_count * 8),
+            dstatus(kept_count * 4);
+        IRX_HIP(hipMemcpy(dx.p, x, rows * columns * elem, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dkept.p, kept, kept_count * 4, hipMemcpyHostToDevice));
+        const size_t per_feature = 3 * rows * 8;
+        const int batch = (int)std::max<size_t>(1, std::min<size_t>(kept_count, kFitScratchBytes / per_feature));
+        DevBuf scratch(batch * per_feature);
+        PreprocessFit p{};
+        p.x = dx.p, p.x_f64 = x_f64 ? 1 : 0, p.rows = (long long)rows, p.columns = (long long)columns;
+        p.kept = static_cast<const unsigned *>(dkept.p), p.kept_count = (int)kept_count, p.groups = (int)groups;
+        p.methods[0] = methods[0], p.methods[1] = groups > 1 ? methods[1] : 0;
+        p.threshold = outlier_threshold, p.scratch = static_cast<double *>(scratch.p), p.batch = batch;
+        p.stats = static_cast<double *>(dstats.p), p.status = static_cast<int *>(dstatus.p);
+        preprocess_fit(p, nullptr);
+        std::vector<int> status(kept_count);
+        IRX_HIP(hipMemcpy(status.data(), dstatus.p, kept_count * 4, hipMemcpyDeviceToHost));
+        for (int s : status)
+            if (s) fail(IRX_INVALID_ARGUMENT, fit_error(s));
+        IRX_HIP(hipMemcpy(statistics, dstats.p, groups * 9 * kept_count * 8, hipMemcpyDeviceToHost));
+    });
+}
+
+int irx_preprocessor_new(irx_device *device, size_t columns, const uint32_t *kept, size_t kept_count,
+                         const int *methods, size_t groups, const double *statistics, size_t members,
+                         const uint32_t *member_groups, const uint32_t *feature_orders, irx_preprocessor **out) {
+    if (out) *out = nullptr;
+    return guarded("irx_preprocessor_new", [&] {
+        if (!device || !out || !statistics || !member_groups || !feature_orders || !members || members > 4096)
+            fail(IRX_INVALID_ARGUMENT, "preprocessor needs statistics and 1..=4096 members");
+        check_kept(kept, kept_count, columns);
+        check_methods(methods, groups);
+        for (size_t i = 0; i < groups * 9 * kept_count; ++i)
+            if (!std::isfinite(statistics[i])) fail(IRX_INVALID_ARGUMENT, "preprocessing statistics must be finite");
+        std::vector<char> seen(kept_count);
+        for (size_t b = 0; b < members; ++b) {
+            if (member_groups[b] >= groups) fail(IRX_INVALID_ARGUMENT, "a member's group is out of range");
+            std::fill(seen.begin(), seen.end(), 0);
+            for (size_t j = 0; j < kept_count; ++j) {
+                const uint32_t f = feature_orders[b * kept_count + j];
+                if (f >= kept_count || seen[f]) fail(IRX_INVALID_ARGUMENT, "a member's feature order is not a permutation");
+                seen[f] = 1;
+            }
+        }
+        set_device(device);
+        auto P = std::make_unique<irx_preprocessor>();
+        P->columns = columns, P->kept_count = (int)kept_count, P->groups = (int)groups, P->members = (int)members;
+        P->methods[0] = methods[0], P->methods[1] = groups > 1 ? methods[1] : 0;
+        P->kept.alloc(kept_count * 4);
+        P->stats.alloc(groups * 9 * kept_count * 8);
+        P->member_groups.alloc(members * 4);
+        P->orders.alloc(members * kept_count * 4);
+        IRX_HIP(hipMemcpy(P->kept.p, kept, kept_count * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(P->stats.p, statistics, groups * 9 * kept_count * 8, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(P->member_groups.p, member_groups, members * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(P->orders.p, feature_orders, members * kept_count * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
+        device->refs.fetch_add(1);
+        P->device = device;
+        *out = P.release();
+    });
+}
+
+void irx_preprocessor_free(irx_preprocessor *p) {
+    if (!p) return;
+    (void)hipSetDevice(p->device->ordinal);
+    if (p->stream) {
+        (void)hipStreamSynchronize(p->stream);
+        (void)hipStreamDestroy(p->stream);
+    }
+    irx_device *d = p->device;
+    delete p;
+    device_release(d);
+}
+
+int irx_preprocessor_transform(irx_preprocessor *p, const void *x, int x_f64, size_t rows, size_t chunk_rows,
+                               int members_out, float *out, int out_on_device) {
+    return guarded("irx_preprocessor_transform", [&] {
+        if (!p || !x || !out || !rows || !chunk_rows) fail(IRX_INVALID_ARGUMENT, "transform needs rows and a chunk size");
+        std::lock_guard<std::mutex> lock(p->mu);
+        set_device(p->device);
+        const size_t elem = x_f64 ? 8 : 4, kept = p->kept_count;
+        const size_t xbytes = rows * p->columns * elem, gbytes = p->groups * rows * kept * 4;
+        const size_t chunks = (rows + chunk_rows - 1) / chunk_rows, nflags = chunks * p->groups;
+        auto grow = [](DevBuf &b, size_t bytes) {
+            if (b.bytes < bytes) b.alloc(bytes);
+        };
+        grow(p->x, xbytes);
+        grow(p->group_rows, gbytes);
+        grow(p->flags, (2 * nflags + 1) * 4);
+        IRX_HIP(hipMemcpyAsync(p->x.p, x, xbytes, hipMemcpyHostToDevice, p->stream));
+        int *overflow = static_cast<int *>(p->flags.p), *again = overflow + nflags, *nonfinite = again + nflags;
+        IRX_HIP(hipMemsetAsync(p->flags.p, 0, (2 * nflags + 1) * 4, p->stream));
+        PreprocessTransform t{};
+        t.x = p->x.p, t.x_f64 = x_f64 ? 1 : 0, t.rows = (long long)rows, t.columns = (long long)p->columns;
+        t.kept = static_cast<const unsigned *>(p->kept.p), t.kept_count = p->kept_count, t.groups = p->groups;
+        t.methods[0] = p->methods[0], t.methods[1] = p->methods[1];
+        t.stats = static_cast<const double *>(p->stats.p), t.chunk_rows = (long long)chunk_rows;
+        t.redo = nullptr, t.overflow = overflow, t.nonfinite = nonfinite, t.out = p->group_rows.f();
+        preprocess_transform(t, p->stream);
+        std::vector<int> flags(nflags);
+        IRX_HIP(hipMemcpyAsync(flags.data(), overflow, nflags * 4, hipMemcpyDeviceToHost, p->stream));
+        IRX_HIP(hipStreamSynchronize(p->stream));
+        if (std::any_of(flags.begin(), flags.end(), [](int f) { return f != 0; })) {
+            // TabICL's fallback: clip the overflowing chunk's rows to the
+            // training range and transform that group's chunk again.
+            t.redo = overflow, t.overflow = again;
+            preprocess_transform(t, p->stream);
+            IRX_HIP(hipMemcpyAsync(flags.data(), again, nflags * 4, hipMemcpyDeviceToHost, p->stream));
+            IRX_HIP(hipStreamSynchronize(p->stream));
+            if (std::any_of(flags.begin(), flags.end(), [](int f) { return f != 0; }))
+                fail(IRX_INVALID_ARGUMENT, "the power transform overflows even within the training range");
+        }
+        int bad = 0;
+        IRX_HIP(hipMemcpyAsync(&bad, nonfinite, 4, hipMemcpyDeviceToHost, p->stream));
+        IRX_HIP(hipStreamSynchronize(p->stream));
+        if (bad) fail(IRX_INVALID_ARGUMENT, "Preprocessing produced non-finite FP32 values");
+        if (!members_out) {
+            IRX_HIP(hipMemcpyAsync(out, p->group_rows.p, gbytes, out_on_device ? hipMemcpyDeviceToDevice
+                                                                                 : hipMemcpyDeviceToHost, p->stream));
+        } else {
+            const size_t mbytes = (size_t)p->members * rows * kept * 4;
+            float *dst = out;
+            if (!out_on_device) {
+                grow(p->members_out, mbytes);
+                dst = p->members_out.f();
+            }
+            preprocess_gather(p->group_rows.f(), (long long)rows, p->kept_count, p->members,
+                              static_cast<const unsigned *>(p->member_groups.p),
+                              static_cast<const unsigned *>(p->orders.p), dst, p->stream);
+            if (!out_on_device) IRX_HIP(hipMemcpyAsync(out, dst, mbytes, hipMemcpyDeviceToHost, p->stream));
+        }
+        IRX_HIP(hipStreamSynchronize(p->stream));
+    });
+}
+
+int irx_test_power_fit(irx_device *device, const double *x, size_t rows, size_t columns, double *lambda_mean_scale,
+                       double *fitted) {
+    return guarded("irx_test_power_fit", [&] {
+        if (!device || !x || !lambda_mean_scale || rows < 2 || !columns)
+            fail(IRX_INVALID_ARGUMENT, "power fit needs at least two rows");
+        set_device(device);
+        std::vector<uint32_t> kept(columns);
+        for (size_t c = 0; c < columns; ++c) kept[c] = (uint32_t)c;
+        DevBuf dx(rows * columns * 8), dkept(columns * 4), dstats(9 * columns * 8), dstatus(columns * 4),
+            scratch(columns * 3 * rows * 8), dfit(columns * rows * 8);
+        IRX_HIP(hipMemcpy(dx.p, x, rows * columns * 8, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dkept.p, kept.data(), columns * 4, hipMemcpyHostToDevice));
+        PreprocessFit p{};
+        p.x = dx.p, p.x_f64 = 1, p.rows = (long long)rows, p.columns = (long long)columns;
+        p.kept = static_cast<const unsigned *>(dkept.p), p.kept_count = (int)columns, p.groups = 1;
+        p.methods[0] = 1, p.threshold = 4.0, p.scratch = static_cast<double *>(scratch.p), p.batch = (int)columns;
+        p.stats = static_cast<double *>(dstats.p), p.status = static_cast<int *>(dstatus.p);
+        p.raw = 1, p.fitted = static_cast<double *>(dfit.p);
+        preprocess_fit(p, nullptr);
+        std::vector<int> status(columns);
+        std::vector<double> stats(9 * columns);
+        IRX_HIP(hipMemcpy(status.data(), dstatus.p, columns * 4, hipMemcpyDeviceToHost));
+        IRX_HIP(hipMemcpy(stats.data(), dstats.p, 9 * columns * 8, hipMemcpyDeviceToHost));
+        for (int s : status)
+            if (s == 2 || s == 3) fail(IRX_INVALID_ARGUMENT, fit_error(s));
+        for (size_t c = 0; c < columns; ++c)
+            for (int i = 0; i < 3; ++i) lambda_mean_scale[i * columns + c] = stats[(6 + i) * columns + c];
+        if (fitted) {
+            // [columns, rows] on the device -> [rows, columns]
+            std::vector<double> byc(columns * rows);
+            IRX_HIP(hipMemcpy(byc.data(), dfit.p, columns * rows * 8, hipMemcpyDeviceToHost));
+            for (size_t c = 0; c < columns; ++c)
+                for (size_t r = 0; r < rows; ++r) fitted[r * columns + c] = byc[c * rows + r];
+        }
+    });
+}

@@ -83,6 +83,17 @@ SIGNATURES = {
     "irx_predictor_set_pass_rows": (ctypes.c_int, [ctypes.c_void_p, _sz]),
     "irx_predictor_set_streams": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "irx_predictor_read_context": (ctypes.c_int, [ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p]),
+    "irx_preprocess_fit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _sz, _sz,
+                                          ctypes.c_void_p, _sz, ctypes.c_void_p, _sz, ctypes.c_double,
+                                          ctypes.c_void_p]),
+    "irx_preprocessor_new": (ctypes.c_int, [ctypes.c_void_p, _sz, ctypes.c_void_p, _sz, ctypes.c_void_p, _sz,
+                                            ctypes.c_void_p, _sz, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.POINTER(ctypes.c_void_p)]),
+    "irx_preprocessor_free": (None, [ctypes.c_void_p]),
+    "irx_test_power_fit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _sz, _sz, ctypes.c_void_p,
+                                          ctypes.c_void_p]),
+    "irx_preprocessor_transform": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _sz, _sz,
+                                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_int]),
     "irx_predictor_predict": (ctypes.c_int, [ctypes.c_void_p, _CF, _sz, _F, ctypes.POINTER(ctypes.c_uint8),
                                              PROGRESS, ctypes.c_void_p]),
     "irx_predictor_predict_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p,
