@@ -112,6 +112,61 @@ def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target
     }
 
 
+def bench_fitted(executor, x, y, xt, args) -> dict:
+    """TabICL preprocessing on the GPU and a fitted model predicting from raw
+    features: the workload's rows as raw features with every fifth column
+    log-normal, 8 ensemble members, none and power groups."""
+    from ironicl_amd import hip, hipmem
+    from ironicl_amd import preprocess as pp
+    from ironicl_amd.fitted import FittedModel
+
+    raw = np.array(x[0], dtype=np.float32)
+    raw[:, ::5] = np.exp(raw[:, ::5])
+    labels = y[0].astype(np.int64)
+    query = np.array(xt[0], dtype=np.float32)
+    query[:, ::5] = np.exp(query[:, ::5])
+    opts = pp.PreprocessOptions()
+    pp.Preprocessor.fit(opts, raw[:1000], labels[:1000], executor.device)  # warm-up
+    t0 = time.perf_counter()
+    p = pp.Preprocessor.fit(opts, raw, labels, executor.device)
+    fit_ms = 1000 * (time.perf_counter() - t0)
+    dev = hipmem.DeviceArray((p.member_count, query.shape[0], p.n_features_out))
+    p.member_rows_device(query, dev.ptr)
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        p.member_rows_device(query, dev.ptr)
+    transform_s = (time.perf_counter() - t0) / reps
+    log(f"preprocessing fit {fit_ms:.1f} ms, transform of {query.shape[0]} rows {1e3 * transform_s:.2f} ms")
+    report = {
+        "workload": f"{raw.shape[0]} x {raw.shape[1]} raw features (every fifth column log-normal), "
+                    f"{p.member_count} members, groups {'+'.join(p.group_methods)}",
+        "preprocess_fit_ms": fit_ms,
+        "transform_rows_per_s": query.shape[0] / transform_s,
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import preprocess_oracle as PO
+        sample = 8  # features
+        t0 = time.perf_counter()
+        PO.fit(raw.astype(np.float64), p.kept[:sample], p.group_methods, opts.outlier_threshold)
+        cpu_s = (time.perf_counter() - t0) * len(p.kept) / sample
+        report["cpu_baseline_fit"] = {"seconds": cpu_s, "cores": 1, "kind": "port",
+                                      "sample": f"oracle (NumPy f64) fit of {sample} of {len(p.kept)} features, "
+                                                f"scaled to all"}
+    t0 = time.perf_counter()
+    fm = FittedModel.fit(executor, raw, labels, opts)
+    hipmem.synchronize()
+    report["fit_s"] = time.perf_counter() - t0
+    fm.predict_proba(query[:512])
+    t0 = time.perf_counter()
+    fm.predict_proba(query)
+    report["predict_proba_rows_per_s"] = query.shape[0] / (time.perf_counter() - t0)
+    log(f"fitted model: fit {report['fit_s']:.2f} s, predict_proba {report['predict_proba_rows_per_s']:.0f} rows/s")
+    del fm
+    return report
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -123,6 +178,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--context-io", metavar="DIR", default=None,
                     help="also time exporting the resident context to an IRCNTXT file in DIR and reloading it")
+    ap.add_argument("--fitted", action="store_true",
+                    help="also time TabICL preprocessing on the GPU and a fitted 8-member model from raw features")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel over BYTES (reference for traffic counters)")
     args = ap.parse_args()
@@ -276,6 +333,8 @@ def main() -> int:
         os.remove(path)
         log(f"context export {export_s:.2f} s, verified reload {import_s:.2f} s ({size / 1e9:.2f} GB)")
 
+    fitted_report = bench_fitted(executor, x, y, xt, args) if args.fitted else None
+
     # The same prediction from host buffers (PCIe included), for reference.
     t0 = time.perf_counter()
     context.predict_raw(xt)
@@ -345,6 +404,7 @@ def main() -> int:
             "bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s", "by_pass_rows": small,
         },
         "context_io": context_io,
+        "fitted": fitted_report,
         "kernel_ms_per_step": kernel_ms,
         "kernels": breakdown,
     }
