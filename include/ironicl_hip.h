@@ -46,9 +46,12 @@ typedef enum irx_status {
     IRX_UNSUPPORTED = 8       /* e.g. a grouped all-missing (-100) triple in build inputs */
 } irx_status;
 
-/* Precision of the products. Only FP32 (optimize="safe",
- * Precision::Fp32 in src/models/tabicl_v2/cuda/mod.rs:71-92) exists here. */
-typedef enum irx_precision { IRX_PRECISION_FP32 = 0 } irx_precision;
+/* Precision of the products (Precision in src/models/tabicl_v2/cuda/mod.rs:71-105).
+ * FP32: optimize="safe", FP32 everywhere, the ICL cache in FP32.
+ * SPLIT: optimize="auto": the ICL cache in FP16 (cpu.rs:4038-4044) and the ICL
+ * attention's products on FP16 MFMA with queries and probabilities split into
+ * high and scaled low FP16 parts; other products in FP32. */
+typedef enum irx_precision { IRX_PRECISION_FP32 = 0, IRX_PRECISION_SPLIT = 1 } irx_precision;
 
 typedef enum irx_task { IRX_TASK_CLASSIFIER = 0, IRX_TASK_REGRESSOR = 1 } irx_task;
 
@@ -140,7 +143,7 @@ typedef struct irx_build_inputs {
 typedef struct irx_build_outputs {
     float *column_keys[3];   /* [B, H+4, 8, 128, 16] */
     float *column_values[3];
-    float *icl_keys[12];     /* [B, 8, N, 64] */
+    float *icl_keys[12];     /* [B, 8, N, 64]; FP16 bits (2 bytes each) at IRX_PRECISION_SPLIT */
     float *icl_values[12];
 } irx_build_outputs;
 
@@ -160,7 +163,8 @@ typedef struct irx_context_tensors {
     irx_shape shape;
     const float *column_keys[3];    /* [B, H+4, 8, 128, 16]; may be NULL when adopting a built cache */
     const float *column_values[3];
-    irx_icl_source icl;             /* may be NULL when adopting a built cache */
+    irx_icl_source icl;             /* may be NULL when adopting a built cache; at IRX_PRECISION_SPLIT
+                                     * its blocks are FP16 bits [B, 8, N, 64] */
     void *icl_user;
     const float *base_scales[12];   /* [512] each */
     const float *rope_frequencies;  /* [8] */
@@ -193,9 +197,11 @@ int irx_predictor_set_streams(irx_predictor *predictor, int streams);
  * icl.{0..11}.{key,value} [B, 8, N, 64]. It is what exporting a GPU-built
  * context to IRCNTXT needs (StaticExecutor::save_context, cpu.rs:1716-1742;
  * the reference's CUDA build always writes the tensors to host pages,
- * cpu.rs:744-805, where this backend keeps them in HBM until asked). */
+ * cpu.rs:744-805, where this backend keeps them in HBM until asked). Values
+ * are FP32 (4 bytes), except the ICL tensors of an IRX_PRECISION_SPLIT
+ * predictor, which are FP16 bits (2 bytes), as its context stores them. */
 int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t offset, size_t floats,
-                               float *dst);
+                               void *dst);
 
 /* Predictor::predict (predictor.rs:224-271): x [B, Q, H] on the host, logits
  * [B, Q, outputs] on the host. cpu_rows, when not NULL, gets Q flags: 1 for a
@@ -280,6 +286,9 @@ int irx_profile_read(const char *family, irx_kernel_stats *out);
  * k and v [pairs, rows, 64]; out [pairs, query_rows, 64]. */
 int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v,
                            size_t pairs, size_t query_rows, size_t rows, float *out);
+/* The same at `precision`: SPLIT packs k and v into the FP16 cache first. */
+int irx_test_icl_attention_precision(irx_device *device, int precision, const float *q, const float *k,
+                                     const float *v, size_t pairs, size_t query_rows, size_t rows, float *out);
 /* first = gelu(x w1^T + b1); second = first w2^T + b2 (+ first when width2 == width).
  * x [rows, depth], w1 [width, depth], w2 [width2, width]. */
 int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1,

@@ -1,9 +1,10 @@
 """IRCNTXT static-context artifacts and the context cache, for contexts built
 on (or uploaded to) the GPU.
 
-The byte layout is the reference's version-1 (all-FP32) IRCNTXT container
-(src/format/static_context.rs:820-987), so a file written here loads in the
-reference and a file the reference writes loads here:
+The byte layout is the reference's IRCNTXT container, version 1 (all FP32)
+or version 2 (tagged FP32 / FP16 tensors, as the reference writes GPU-built
+optimize="auto" contexts) (src/format/static_context.rs:820-987), so a file
+written here loads in the reference and a file the reference writes loads here:
 
     header (164 bytes, little-endian)
         magic b"IRCNTXT\\0" | version u32 | kind u32 = 1
@@ -47,7 +48,7 @@ from . import manifest as mf
 
 MAGIC = b"IRCNTXT\0"
 VERSION_FP32 = 1           # every tensor FP32, zero dtype tags
-VERSION_TAGGED = 2         # explicit dtype per tensor (FP32 / BF16 / FP16)
+VERSION_TAGGED = 2         # explicit dtype per tensor (FP32 / BF16 / FP16); written for FP16 ICL caches
 VERSION_PACKED_KEYS = 3    # source-tile, dimension-major ICL K
 KIND = 1
 HEADER_BYTES = 164
@@ -124,18 +125,20 @@ class Metadata:
         return self.ensemble_count, self.training_rows, self.feature_count
 
 
-def context_tensor_specs(b: int, n: int, h: int) -> list[tuple[str, tuple[int, ...]]]:
+def context_tensor_specs(b: int, n: int, h: int, icl_dtype=np.float32) -> list[tuple[str, tuple[int, ...], np.dtype]]:
     """The 30 cache tensors of a context in the reference's order
     (context_tensors, cpu.rs:4106-4123): column blocks then ICL blocks, each
-    key then value. This is also the tensor index `irx_predictor_read_context`
-    takes."""
+    key then value, with their storage (the column tensors are always FP32;
+    the ICL ones FP32, or FP16 for an optimize="auto" context, cpu.rs:4038-4044).
+    This is also the tensor index `irx_predictor_read_context` takes."""
     specs = []
     for block in range(mf.COLUMN_BLOCKS):
         shape = (b, h + mf.RESERVED, mf.HEADS, mf.INDUCING, mf.COLUMN_DIM // mf.HEADS)
-        specs += [(f"column.{block}.key", shape), (f"column.{block}.value", shape)]
+        specs += [(f"column.{block}.key", shape, np.dtype(np.float32)),
+                  (f"column.{block}.value", shape, np.dtype(np.float32))]
     for block in range(mf.ICL_BLOCKS):
         shape = (b, mf.HEADS, n, mf.ICL_DIM // mf.HEADS)
-        specs += [(f"icl.{block}.key", shape), (f"icl.{block}.value", shape)]
+        specs += [(f"icl.{block}.key", shape, np.dtype(icl_dtype)), (f"icl.{block}.value", shape, np.dtype(icl_dtype))]
     return specs
 
 
@@ -194,6 +197,20 @@ class _Entry:
     shape: tuple[int, ...]
     offset: int        # within the payload
     nbytes: int
+    dtype: np.dtype = np.dtype(np.float32)
+
+
+# StorageDType's on-disk tags in tagged versions (src/config.rs:79-86).
+_TAGS = {np.dtype(np.float32): 1, np.dtype(np.float16): 3}
+
+
+def _spec(s):
+    """(name, shape) or (name, shape, dtype), FP32 by default."""
+    name, shape = str(s[0]), tuple(int(d) for d in s[1])
+    dtype = np.dtype(s[2]) if len(s) > 2 else np.dtype(np.float32)
+    if dtype not in _TAGS:
+        raise ContextError(f"tensor '{name}' storage {dtype} is not supported (FP32 or FP16)")
+    return name, shape, dtype
 
 
 def _layout(meta: Metadata, specs: Iterable[tuple[str, tuple[int, ...]]]) -> tuple[bytes, list[_Entry], int]:
@@ -201,14 +218,16 @@ def _layout(meta: Metadata, specs: Iterable[tuple[str, tuple[int, ...]]]) -> tup
     padding), the tensors in file order with their payload offsets, and the
     whole encoded length (static_context.rs:876-987)."""
     validate_metadata(meta)
-    specs = sorted(((str(n), tuple(int(d) for d in s)) for n, s in specs), key=lambda t: t[0].encode())
+    specs = sorted((_spec(s) for s in specs), key=lambda t: t[0].encode())
     if not specs or len(specs) > MAX_TENSOR_COUNT:
         raise ContextError("static context section exceeds the resource limit")
+    # Version 1 when every tensor is FP32; version 2 tags each tensor's storage.
+    version = VERSION_FP32 if all(d == np.float32 for _, _, d in specs) else VERSION_TAGGED
     directory = bytearray()
     entries = []
     payload = 0
     previous = None
-    for name, shape in specs:
+    for name, shape, dtype in specs:
         raw = name.encode()
         if previous is not None and raw <= previous:
             raise ContextError("static context tensor names are not unique and sorted")
@@ -217,18 +236,19 @@ def _layout(meta: Metadata, specs: Iterable[tuple[str, tuple[int, ...]]]) -> tup
             raise ContextError("static context tensor name or rank is invalid")
         if min(shape) <= 0:
             raise ContextError("static context tensor dimension is zero")
-        nbytes = 4 * int(np.prod(shape, dtype=np.uint64))
+        nbytes = dtype.itemsize * int(np.prod(shape, dtype=np.uint64))
         if nbytes > MAX_TENSOR_BYTES:
             raise ContextError(f"static context tensor '{name}' exceeds the resource limit")
         offset = _align(payload)
         payload = offset + nbytes
-        directory += _ENTRY.pack(len(raw), len(shape), 0, offset, nbytes)
+        tag = 0 if version == VERSION_FP32 else _TAGS[dtype]
+        directory += _ENTRY.pack(len(raw), len(shape), tag, offset, nbytes)
         directory += struct.pack(f"<{len(shape)}Q", *shape) + raw
-        entries.append(_Entry(name, shape, offset, nbytes))
+        entries.append(_Entry(name, shape, offset, nbytes, dtype))
     if len(directory) > MAX_DIRECTORY_BYTES or payload > MAX_TOTAL_TENSOR_BYTES:
         raise ContextError("static context section exceeds the resource limit")
     head = bytearray(_HEAD.pack(
-        MAGIC, VERSION_FP32, KIND, meta.model_sha256, meta.context_sha256,
+        MAGIC, version, KIND, meta.model_sha256, meta.context_sha256,
         meta.ensemble_count, meta.training_rows, meta.feature_count, meta.class_count, *ARCHITECTURE,
         len(entries), meta.class_permutations.size, meta.feature_permutations.size,
         len(directory), payload, 0))
@@ -248,8 +268,8 @@ def encoded_len(meta: Metadata, specs) -> int:
 def encode(meta: Metadata, specs, source: TensorSource, sink, chunk_floats: int = 1 << 24) -> None:
     """Write the artifact to the binary file-like `sink` in one pass, hashing
     as it goes (StaticContextArtifact::encode, static_context.rs:842-874).
-    Values must be finite, as a stored context's are (validate_tensor,
-    static_context.rs:1167-1176)."""
+    `source` returns each tensor's values in its storage type. Values must be
+    finite, as a stored context's are (validate_tensor, static_context.rs:1167-1176)."""
     head, entries, _ = _layout(meta, specs)
     digest = hashlib.sha256()
 
@@ -262,10 +282,10 @@ def encode(meta: Metadata, specs, source: TensorSource, sink, chunk_floats: int 
     for e in entries:
         if e.offset > written:
             put(bytes(e.offset - written))
-        count = e.nbytes // 4
+        count = e.nbytes // e.dtype.itemsize
         for start in range(0, count, chunk_floats):
             n = min(chunk_floats, count - start)
-            chunk = np.ascontiguousarray(source(e.name, start, n), dtype="<f4").reshape(-1)
+            chunk = np.ascontiguousarray(source(e.name, start, n), dtype=e.dtype.newbyteorder("<")).reshape(-1)
             if chunk.size != n:
                 raise ContextError(f"tensor '{e.name}' source returned {chunk.size} values, expected {n}")
             if not np.isfinite(chunk).all():
@@ -279,8 +299,9 @@ def to_bytes(meta: Metadata, tensors: dict[str, np.ndarray]) -> bytes:
     """The whole artifact in memory (StaticContextArtifact::to_bytes)."""
     import io
 
-    specs = [(name, np.shape(arr)) for name, arr in tensors.items()]
-    flat = {name: np.ascontiguousarray(arr, dtype=np.float32).reshape(-1) for name, arr in tensors.items()}
+    specs = [(name, np.shape(arr), np.float16 if np.asarray(arr).dtype == np.float16 else np.float32)
+             for name, arr in tensors.items()]
+    flat = {name: np.ascontiguousarray(arr).reshape(-1) for name, arr in tensors.items()}
     out = io.BytesIO()
     encode(meta, specs, lambda name, start, n: flat[name][start:start + n], out)
     return out.getvalue()
@@ -337,9 +358,10 @@ class ContextFile:
 def _parse(buf) -> ContextFile:
     """Verify and index an artifact held in `buf` (bytes or a read-only
     mapping): StaticContextArtifact::from_mapping (static_context.rs:551-818).
-    Only all-FP32 contexts load: this backend predicts in FP32, and a BF16,
-    FP16 or packed-key context is one its predictor cannot read (the
-    reference's CUDA path leaves those on the CPU, cpu.rs:1862-1870)."""
+    FP32 and FP16 tensors load (an FP16 ICL cache is what optimize="auto"
+    predicts from); BF16 tensors and packed keys (version 3) are refused: no
+    predictor here reads them (the reference's CUDA path leaves such contexts
+    on its CPU, cpu.rs:1862-1870)."""
     view = memoryview(buf)
     length = len(view)
     if not HEADER_BYTES + CHECKSUM_BYTES <= length <= MAX_ARTIFACT_BYTES:
@@ -412,18 +434,25 @@ def _parse(buf) -> ContextFile:
         elements = 1
         for d in dims:
             elements *= d
-        # Version 2 tags: the reference's on-disk StorageDType numbering; only
-        # FP32 can feed this backend.
-        if version == VERSION_TAGGED and tag != _FP32_TAG:
-            raise ContextError(f"tensor '{name}' is not FP32; reduced-precision contexts are not supported "
-                               "by the FP32 GPU backend")
-        if nbytes != 4 * elements:
+        # Version 2 tags: the reference's on-disk StorageDType numbering. FP32
+        # and FP16 feed this backend; BF16 does not.
+        if version == VERSION_FP32:
+            dtype = np.dtype("<f4")
+        elif tag == _FP32_TAG:
+            dtype = np.dtype("<f4")
+        elif tag == _F16_TAG:
+            dtype = np.dtype("<f2")
+        elif tag == 2:
+            raise ContextError(f"tensor '{name}' is BF16, which this backend does not read")
+        else:
+            raise ContextError("static context tensor directory entry is invalid")
+        if nbytes != dtype.itemsize * elements:
             raise ContextError(f"static context tensor '{name}' byte length does not match its shape")
         if offset + nbytes > payload_len:
             raise ContextError(f"static context tensor '{name}' exceeds the payload section")
         total += nbytes
         ranges.append((offset, offset + nbytes))
-        values = np.frombuffer(view, dtype="<f4", count=elements, offset=payload_start + offset)
+        values = np.frombuffer(view, dtype=dtype, count=elements, offset=payload_start + offset)
         if not np.isfinite(values).all():
             raise ContextError("static context tensor contains a non-finite value")
         tensors[name] = values.reshape(dims)
@@ -435,8 +464,9 @@ def _parse(buf) -> ContextFile:
     return ContextFile(buf, version, meta, tensors)
 
 
-# StorageDType's on-disk tag for FP32 in tagged versions (src/config.rs:79-86).
+# StorageDType's on-disk tags for FP32 and FP16 in tagged versions (src/config.rs:79-86).
 _FP32_TAG = 1
+_F16_TAG = 3
 
 
 def from_bytes(data: bytes) -> ContextFile:
@@ -476,7 +506,7 @@ def validate_for_model(context: ContextFile, source_sha256: str, task: str) -> N
         raise ContextError(f"static context class count {meta.class_count} is unsupported; expected 2..=10")
     if task == mf.REGRESSOR and meta.class_count != 0:
         raise ContextError(f"static context class count {meta.class_count} is unsupported; expected 0")
-    for name, shape in context_tensor_specs(*meta.shape):
+    for name, shape, _ in context_tensor_specs(*meta.shape):
         t = context.tensor(name)
         if t is None:
             raise ContextError(f"static context cache tensor '{name}' is missing")

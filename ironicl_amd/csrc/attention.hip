@@ -339,6 +339,315 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
     }
 }
 
+// ---- Split-FP16 products over an FP16 cache (IRX_PRECISION_SPLIT, the
+// reference's optimize="auto": cuda/mod.rs:71-105) ----
+//
+// The cache holds K as FP16 [pairs, Np, 64] (Np = keys rounded up to 64,
+// zero past the keys) and V tile-transposed as FP16 [pairs, Np / 64, 64
+// dims, 64 keys], the keys of each 16-key group stored in the order 0..3,
+// 8..11, 4..7, 12..15. Queries and probabilities, FP32, are split into a high
+// FP16 part and a low part scaled by 2^11 (x = hi + lo / 2048, about 22
+// significant bits); each product is hi.K + lo.K / 2048 on the 32x32x16 FP16
+// MFMA with separate accumulators, so only the cache's own FP16 rounding
+// remains. Layouts per tile (64 keys, 4 waves x 64 queries as above):
+//   S^T (key x query): A = K[key = lane % 32 (+32)][dims 16 m + 8 (lane / 32)
+//     .. +7], B = the lane's query, same dims; result register r is key
+//     8 (r / 4) + 4 (lane / 32) + r % 4 (+32), query lane % 32 (+32 j);
+//   O^T (dim x query), 16-key step t of the tile: A = V^T[dim][the 8 keys the
+//     lane's result registers 8 (t % 2) .. +7 of key block t / 2 hold], which
+//     the stored key order makes one 16-byte read; B = those probabilities.
+// LDS rows are 128 bytes (one key of K, one dim of V^T); the 16-byte chunk c
+// of row r is stored at chunk c ^ (r % 8) so that the 8 rows a half-wave
+// group reads hit distinct banks. Probabilities stay below 2^15 (the lazy
+// reference's limit here), so their high parts fit FP16.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr float kLoScale = 2048.0f;
+
+struct IclTile16 {
+    u32x4 k[kKeyTile * 8];  // 64 rows x 8 chunks of 16 bytes
+    u32x4 v[kKeyTile * 8];
+};
+
+__device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+
+// Eight FP32 values split into high and scaled low FP16 parts.
+__device__ __forceinline__ void split8(const float *x, half8 &hi, half8 &lo) {
+    u32x4 h, l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto hp = __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]);
+        const float r0 = (x[2 * i] - (float)hp[0]) * kLoScale;
+        const float r1 = (x[2 * i + 1] - (float)hp[1]) * kLoScale;
+        const auto lp = __builtin_amdgcn_cvt_pkrtz(r0, r1);
+        h[i] = __builtin_bit_cast(unsigned, hp);
+        l[i] = __builtin_bit_cast(unsigned, lp);
+    }
+    hi = __builtin_bit_cast(half8, h);
+    lo = __builtin_bit_cast(half8, l);
+}
+
+template <bool SPLIT>
+__global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(IclAttention p, IclLaunch g) {
+    __shared__ __attribute__((aligned(16))) IclTile16 tiles[2];
+
+    const int total = g.qtiles * p.pairs * g.splits;
+    const int bid = blockIdx.x;
+    const int t_id = (bid % 8) * g.per_xcd + bid / 8;
+    if (t_id >= total) return;
+    const int qt = t_id % g.qtiles;
+    const int rest = t_id / g.qtiles;
+    const int split = rest % g.splits;
+    const int pair = rest / g.splits;
+    const int k_begin = __builtin_amdgcn_readfirstlane(split * g.keys_per_split);
+    const int k_end = __builtin_amdgcn_readfirstlane(min(p.kv_rows, k_begin + g.keys_per_split));
+    const int n_pad = (p.kv_rows + kKeyTile - 1) / kKeyTile * kKeyTile;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = lane >> 5, r32 = lane & 31;
+    const int qrow0 = qt * kIclQueries + wave * 64 + r32;
+
+    // The lane's queries, dims 16 m + 8 half .. +7 for m = 0..3, in the exp2
+    // domain, split into high and low FP16 parts.
+    half8 qh[2][4], ql[2][4];
+    {
+        const float scale = 0.125f * kLog2e;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int qrow = qrow0 + 32 * j;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                float x[8];
+                if (qrow < p.q_rows) {
+                    const float *src = p.q + pair * p.q_pair_stride + (long long)qrow * 64 + 16 * m + 8 * half;
+                    const f32x4 a = *reinterpret_cast<const f32x4 *>(src);
+                    const f32x4 b = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = a[e] * scale, x[4 + e] = b[e] * scale;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = 0.f;
+                }
+                split8(x, qh[j][m], ql[j][m]);
+            }
+        }
+    }
+
+    // Staging: a tile of K (or V^T) is 8 KB contiguous in HBM; instruction t
+    // of 8 fills LDS chunks 64 t .. 64 t + 63. Wave w issues K and V
+    // instructions 2 w and 2 w + 1. Lane i of instruction t fills LDS row
+    // 8 t + i / 8, stored chunk i % 8, i.e. source chunk (i % 8) ^ (row % 8).
+    const unsigned short *kbase = static_cast<const unsigned short *>(p.k16) + (long long)pair * n_pad * 64;
+    const unsigned short *vbase = static_cast<const unsigned short *>(p.v16) + (long long)pair * n_pad * 64;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    int src_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int t = 2 * wv + i, row = 8 * t + (lane >> 3);
+        src_off[i] = row * 64 + 8 * ((lane & 7) ^ (row & 7));  // halves
+    }
+    auto issue_tile = [&](int k0, int buf) {
+        const unsigned short *kt = kbase + (long long)k0 * 64, *vt = vbase + (long long)k0 * 64;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int t = 2 * wv + i;
+            __builtin_amdgcn_global_load_lds(kt + src_off[i], (lds_void *)&tiles[buf].k[64 * t], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vt + src_off[i], (lds_void *)&tiles[buf].v[64 * t], 16, 0, 0);
+        }
+    };
+    // LDS chunk index of row `row`, chunk c.
+    auto at = [](int row, int c) { return row * 8 + (c ^ (row & 7)); };
+
+    f32x16 oh[2][2], ol[2][2];  // [dim block][query block]
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oh[d][j][r] = 0.f, ol[d][j][r] = 0.f;
+    float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    f32x16 neg_ref[2], zero;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) neg_ref[0][r] = INFINITY, neg_ref[1][r] = INFINITY, zero[r] = 0.f;
+    constexpr float kLazyLimit16 = 32768.0f;  // 2^15: probabilities stay FP16-representable
+    const float kLoInv = 1.0f / kLoScale;
+
+    issue_tile(k_begin, 0);
+    int buf = 0;
+    for (int k0 = k_begin; k0 < k_end; k0 = __builtin_amdgcn_readfirstlane(k0 + kKeyTile)) {
+        wait_loads();
+        __syncthreads();
+        if (k0 + kKeyTile < k_end) issue_tile(k0 + kKeyTile, buf ^ 1);
+        const u32x4 *kt = tiles[buf].k;
+        const u32x4 *vt = tiles[buf].v;
+
+        // Scores of this tile against both query blocks, from the FP16 keys.
+        auto scores = [&](int j, const f32x16 &init, f32x16 &s0, f32x16 &s1) {
+            f32x16 h0 = init, h1 = init, l0 = zero, l1 = zero;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const half8 a0 = as_half8(kt[at(r32, 2 * m + half)]);
+                const half8 a1 = as_half8(kt[at(r32 + 32, 2 * m + half)]);
+                h0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qh[j][m], h0, 0, 0, 0);
+                h1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qh[j][m], h1, 0, 0, 0);
+                l0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, ql[j][m], l0, 0, 0, 0);
+                l1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ql[j][m], l1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s0[r] = h0[r] + l0[r] * kLoInv, s1[r] = h1[r] + l1[r] * kLoInv;
+            if (k0 + kKeyTile > k_end) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (key >= k_end) s0[r] = -INFINITY;
+                    if (key + 32 >= k_end) s1[r] = -INFINITY;
+                }
+            }
+        };
+
+        f32x16 s[2][2];  // [query block][key block]
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            scores(j, neg_ref[j], s[j][0], s[j][1]);
+            float lsum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[j][0][r] = __builtin_amdgcn_exp2f(s[j][0][r]);
+                s[j][1][r] = __builtin_amdgcn_exp2f(s[j][1][r]);
+                lsum += s[j][0][r] + s[j][1][r];
+            }
+            if (__any(!(lsum <= kLazyLimit16))) {
+                f32x16 t0, t1;
+                scores(j, zero, t0, t1);
+                float mt = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(t0[r], t1[r]));
+                const float m_new = fmaxf(m_ref[j], halves_max(mt));
+                const float alpha = __builtin_amdgcn_exp2f(m_ref[j] - m_new);
+                l_run[j] *= alpha;
+                lsum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    oh[0][j][r] *= alpha, oh[1][j][r] *= alpha;
+                    ol[0][j][r] *= alpha, ol[1][j][r] *= alpha;
+                    neg_ref[j][r] = -m_new;
+                    s[j][0][r] = __builtin_amdgcn_exp2f(t0[r] - m_new);
+                    s[j][1][r] = __builtin_amdgcn_exp2f(t1[r] - m_new);
+                    lsum += s[j][0][r] + s[j][1][r];
+                }
+                m_ref[j] = m_new;
+            }
+            l_run[j] += lsum;
+        }
+        // O^T += V^T P^T over the tile's four 16-key steps.
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int kb = t >> 1, g = t & 1;
+            half8 ph[2], pl[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = s[j][kb][8 * g + e];
+                split8(x, ph[j], pl[j]);
+            }
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const half8 a = as_half8(vt[at(32 * d + r32, 2 * t + half)]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    oh[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph[j], oh[d][j], 0, 0, 0);
+                    ol[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[j], ol[d][j], 0, 0, 0);
+                }
+            }
+        }
+        buf ^= 1;
+    }
+
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int qrow = qrow0 + 32 * j;
+        const float l_tot = halves_sum(l_run[j]);
+        if (qrow >= p.q_rows) continue;
+        const float inv = 1.0f / l_tot;
+        float *dst;
+        if constexpr (!SPLIT) {
+            const int b = pair / kHeads, head = pair - b * kHeads;
+            dst = p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64;
+        } else {
+            const long long row = ((long long)split * p.pairs + pair) * g.q_padded + qrow;
+            dst = p.partial + row * 64;
+            if (half == 0) p.partial[(long long)g.splits * p.pairs * g.q_padded * 64 + row] = m_ref[j] + log2f(l_tot);
+        }
+        // Register r of block d: dims 32 d + 8 (r / 4) + 4 half + r % 4.
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                f32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = (oh[d][j][4 * a + e] + ol[d][j][4 * a + e] * kLoInv) * inv;
+                *reinterpret_cast<f32x4 *>(dst + 32 * d + 8 * a + 4 * half) = v;
+            }
+    }
+}
+
+// FP32 or FP16 K/V [pairs, rows, 64] into the FP16 cache layout above (K
+// padded with zero rows, V tile-transposed with the stored key order). One
+// workgroup per (pair, 64-key tile); counts values that are not finite in
+// FP16 (beyond +-65504 or NaN) into `bad`.
+template <typename T>
+__global__ __launch_bounds__(256) void pack_icl16_kernel(const T *k, const T *v, long long rows, int pairs,
+                                                         unsigned short *k16, unsigned short *v16, unsigned *bad) {
+    __shared__ float tile[64][65];
+    const int tiles = (int)((rows + kKeyTile - 1) / kKeyTile);
+    const int pair = blockIdx.x / tiles, tix = blockIdx.x % tiles;
+    const long long n_pad = (long long)tiles * kKeyTile;
+    const long long k0 = (long long)tix * kKeyTile;
+    const T *ks = k + (long long)pair * rows * 64, *vs = v + (long long)pair * rows * 64;
+    unsigned short *kd = k16 + ((long long)pair * n_pad + k0) * 64, *vd = v16 + ((long long)pair * n_pad + k0) * 64;
+    unsigned local_bad = 0;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int key = i / 64, d = i % 64;
+        const bool in = k0 + key < rows;
+        const float kv = in ? (float)ks[(k0 + key) * 64 + d] : 0.f;
+        const float vv = in ? (float)vs[(k0 + key) * 64 + d] : 0.f;
+        const _Float16 kh = (_Float16)kv;
+        local_bad += !(fabsf(kv) <= 65504.f) + !(fabsf(vv) <= 65504.f);
+        kd[i] = __builtin_bit_cast(unsigned short, kh);
+        tile[key][d] = vv;
+    }
+    __syncthreads();
+    // V^T: row d holds the tile's keys in the stored order (positions 4..7 and
+    // 8..11 of each 16-key group swapped).
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int d = i / 64, pos = i % 64;
+        const int q16 = pos & 15, swap = (q16 >= 4 && q16 < 8) ? 4 : (q16 >= 8 && q16 < 12 ? -4 : 0);
+        const int key = (pos & ~15) + q16 + swap;
+        vd[i] = __builtin_bit_cast(unsigned short, (_Float16)tile[key][d]);
+    }
+    if (local_bad) atomicAdd(bad, local_bad);
+}
+
+// The FP16 cache back to logical FP16 K and V [pairs, rows, 64].
+__global__ __launch_bounds__(256) void unpack_icl16_kernel(const unsigned short *k16, const unsigned short *v16,
+                                                           long long rows, int pairs, unsigned short *k,
+                                                           unsigned short *v) {
+    const int tiles = (int)((rows + kKeyTile - 1) / kKeyTile);
+    const int pair = blockIdx.x / tiles, tix = blockIdx.x % tiles;
+    const long long n_pad = (long long)tiles * kKeyTile, k0 = (long long)tix * kKeyTile;
+    const unsigned short *ks = k16 + ((long long)pair * n_pad + k0) * 64;
+    const unsigned short *vs = v16 + ((long long)pair * n_pad + k0) * 64;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int key = i / 64, d = i % 64;
+        if (k0 + key >= rows) continue;
+        const int q16 = key & 15, swap = (q16 >= 4 && q16 < 8) ? 4 : (q16 >= 8 && q16 < 12 ? -4 : 0);
+        const int pos = (key & ~15) + q16 + swap;
+        k[((long long)pair * rows + k0 + key) * 64 + d] = ks[i];
+        v[((long long)pair * rows + k0 + key) * 64 + d] = vs[d * 64 + pos];
+    }
+}
+
 // Few queries (a pass of at most 32 rows): the attention is bound by reading
 // K and V from HBM. A workgroup of kDecodeWaves waves takes one (pair, key
 // range); its waves take the range's 16-key blocks in turn, so together they
@@ -596,9 +905,9 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
     *reinterpret_cast<f32x4 *>(p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64 + d) = num * (1.0f / den);
 }
 
-IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units) {
+IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units, bool f16 = false) {
     IclLaunch g{};
-    if (q_rows <= kDecodeQueries) {
+    if (q_rows <= kDecodeQueries && !f16) {
         // One workgroup per (pair, key range), about two per CU, at least 256
         // keys each; ranges in whole rounds of the waves' 16-key blocks.
         g.qtiles = 1;
@@ -925,14 +1234,14 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
 
 }  // namespace
 
-int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units) {
-    return plan_icl(pairs, q_rows, kv_rows, compute_units).splits;
+int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units, bool f16) {
+    return plan_icl(pairs, q_rows, kv_rows, compute_units, f16).splits;
 }
 
-size_t icl_attention_partial_floats(int pairs, int q_rows, int splits) {
+size_t icl_attention_partial_floats(int pairs, int q_rows, int splits, bool f16) {
     if (splits <= 1) return 0;
-    size_t q_padded = q_rows <= kDecodeQueries ? (size_t)kDecodeQueries
-                                                : ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
+    size_t q_padded = q_rows <= kDecodeQueries && !f16 ? (size_t)kDecodeQueries
+                                                       : ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
     return (size_t)splits * pairs * q_padded * 65;
 }
 
@@ -944,15 +1253,26 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         (reinterpret_cast<uintptr_t>(args.partial) & 15) || (args.q_pair_stride & 3) || (args.kv_pair_stride & 3) ||
         (args.ldo & 3))
         fail(3, "ICL attention operands must be 16-byte aligned");
-    IclLaunch g = plan_icl(args.pairs, args.q_rows, args.kv_rows, args.compute_units);
+    const bool f16 = args.k16 != nullptr;
+    if (f16 && (!args.v16 || (reinterpret_cast<uintptr_t>(args.k16) & 15) || (reinterpret_cast<uintptr_t>(args.v16) & 15)))
+        fail(3, "ICL attention FP16 cache must be 16-byte aligned");
+    IclLaunch g = plan_icl(args.pairs, args.q_rows, args.kv_rows, args.compute_units, f16);
     if (g.splits > 1) {
-        size_t need = icl_attention_partial_floats(args.pairs, args.q_rows, g.splits);
+        size_t need = icl_attention_partial_floats(args.pairs, args.q_rows, g.splits, f16);
         if (!args.partial || args.partial_floats < need) fail(3, "ICL attention partial buffer is too small");
     }
     {
         const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
-        KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, 4.0 * 64.0 * pairs * (2.0 * kv + 2.0 * q));
-        if (args.q_rows <= kDecodeQueries) {
+        const double kv_bytes = f16 ? 2.0 * 64.0 * pairs * 2.0 * kv : 4.0 * 64.0 * pairs * 2.0 * kv;
+        KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, kv_bytes + 4.0 * 64.0 * pairs * 2.0 * q);
+        if (f16) {
+            if (g.splits > 1)
+                hipLaunchKernelGGL((icl_attention_split_kernel<true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
+                                   stream, args, g);
+            else
+                hipLaunchKernelGGL((icl_attention_split_kernel<false>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
+                                   stream, args, g);
+        } else if (args.q_rows <= kDecodeQueries) {
             const dim3 blocks((unsigned)((long long)args.pairs * g.splits)), threads(kDecodeWaves * 64);
             if (args.q_rows <= 16) {
                 if (g.splits > 1)
@@ -1033,6 +1353,28 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
         if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
         hipLaunchKernelGGL(small_attention_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, args, qtiles);
     }
+    IRX_HIP(hipGetLastError());
+}
+
+void pack_icl16(const void *k, const void *v, bool src_f16, long long rows, int pairs, unsigned short *k16,
+                unsigned short *v16, unsigned *bad, hipStream_t stream) {
+    if (rows <= 0 || pairs <= 0) return;
+    const unsigned blocks = (unsigned)(pairs * ((rows + kKeyTile - 1) / kKeyTile));
+    if (src_f16)
+        hipLaunchKernelGGL(pack_icl16_kernel<_Float16>, dim3(blocks), dim3(256), 0, stream,
+                           static_cast<const _Float16 *>(k), static_cast<const _Float16 *>(v), rows, pairs, k16, v16,
+                           bad);
+    else
+        hipLaunchKernelGGL(pack_icl16_kernel<float>, dim3(blocks), dim3(256), 0, stream, static_cast<const float *>(k),
+                           static_cast<const float *>(v), rows, pairs, k16, v16, bad);
+    IRX_HIP(hipGetLastError());
+}
+
+void unpack_icl16(const unsigned short *k16, const unsigned short *v16, long long rows, int pairs, unsigned short *k,
+                  unsigned short *v, hipStream_t stream) {
+    if (rows <= 0 || pairs <= 0) return;
+    const unsigned blocks = (unsigned)(pairs * ((rows + kKeyTile - 1) / kKeyTile));
+    hipLaunchKernelGGL(unpack_icl16_kernel, dim3(blocks), dim3(256), 0, stream, k16, v16, rows, pairs, k, v);
     IRX_HIP(hipGetLastError());
 }
 

@@ -161,11 +161,23 @@ struct IclAttention {
     float *partial;       // [splits, pairs, q_rows_padded, 65] or null
     size_t partial_floats;
     int compute_units;
+    // The FP16 cache (split-FP16 products) instead of k / v: K [pairs, Np, 64]
+    // and tile-transposed V [pairs, Np / 64, 64, 64], Np = kv_rows rounded up to 64.
+    const unsigned short *k16, *v16;
 };
 // Splits the ICL attention would use, and the partial floats it needs.
-int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units);
-size_t icl_attention_partial_floats(int pairs, int q_rows, int splits);
+int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units, bool f16 = false);
+size_t icl_attention_partial_floats(int pairs, int q_rows, int splits, bool f16 = false);
 void icl_attention(const IclAttention &args, hipStream_t stream);
+// Halves of one FP16 cache plane (K or V) for `pairs` x `rows` keys.
+inline size_t icl16_plane(long long pairs, long long rows) { return (size_t)pairs * ((rows + 63) / 64 * 64) * 64; }
+// K and V [pairs, rows, 64] (FP32, or FP16 bits when src_f16) into the FP16
+// cache layout; adds the count of values not finite in FP16 to *bad.
+void pack_icl16(const void *k, const void *v, bool src_f16, long long rows, int pairs, unsigned short *k16,
+                unsigned short *v16, unsigned *bad, hipStream_t stream);
+// The FP16 cache back to logical FP16 K and V [pairs, rows, 64].
+void unpack_icl16(const unsigned short *k16, const unsigned short *v16, long long rows, int pairs,
+                  unsigned short *k, unsigned short *v, hipStream_t stream);
 
 // TabICL preprocessing (preprocess.hip), in f64. Fit: statistics of every
 // kept feature, [groups, 9, kept_count] (mean, scale, minimum, maximum,

@@ -228,6 +228,7 @@ struct irx_weights {
 struct irx_built_cache {
     irx_device *device = nullptr;
     irx_shape shape{};
+    int precision = IRX_PRECISION_FP32;  // SPLIT: the ICL buffers hold the FP16 cache layout
     DevBuf column[kColumnBlocks];
     DevBuf icl[kIclBlocks];
 };
@@ -235,6 +236,7 @@ struct irx_built_cache {
 struct irx_predictor {
     irx_weights *weights = nullptr;
     irx_shape shape{};
+    int precision = IRX_PRECISION_FP32;
     size_t pass_rows = 512;
     DevBuf column[kColumnBlocks];
     DevBuf icl[kIclBlocks];
@@ -374,21 +376,22 @@ struct Stages {
         float *norm, *qh, *qhid, *qg, *att, *hid, *partial;
         size_t partial_floats;
     };
-    static IclBuffers icl_buffers(Arena &a, long long rows, int b, int q_rows, int kv_rows, int cus) {
+    static IclBuffers icl_buffers(Arena &a, long long rows, int b, int q_rows, int kv_rows, int cus, bool f16 = false) {
         IclBuffers r{};
         r.norm = a.take(rows * 512), r.qh = a.take(rows * 512), r.qhid = a.take(rows * 512);
         r.qg = a.take(rows * 512), r.att = a.take(rows * 512), r.hid = a.take(rows * 1024);
-        int splits = icl_attention_splits(b * kHeads, q_rows, kv_rows, cus);
-        r.partial_floats = icl_attention_partial_floats(b * kHeads, q_rows, splits);
+        int splits = icl_attention_splits(b * kHeads, q_rows, kv_rows, cus, f16);
+        r.partial_floats = icl_attention_partial_floats(b * kHeads, q_rows, splits, f16);
         r.partial = r.partial_floats ? a.take(r.partial_floats) : nullptr;
         return r;
     }
 
     // Query half of ICL block `blk` (cached_block with QASS, cpu.rs:2587-2850,
     // 3798-3853) for `b` estimators x `rows` query rows [b*rows, 512], against
-    // K/V [b, 8, kv_rows, 64].
+    // K/V [b, 8, kv_rows, 64] (or the FP16 cache k16 / v16).
     void icl_queries(int blk, float *x, int b, int rows, const float *k, const float *v, int kv_rows,
-                     const float *base, const IclBuffers &r) const {
+                     const float *base, const IclBuffers &r, const unsigned short *k16 = nullptr,
+                     const unsigned short *v16 = nullptr) const {
         const BlockW &bw = w.icl[blk];
         const long long m = (long long)b * rows;
         layer_norm(x, 512, bw.n1w, bw.n1b, r.norm, 512, m, 512, s);
@@ -407,6 +410,7 @@ struct Stages {
         at.kv_pair_stride = (long long)kv_rows * 64, at.o = r.att, at.ldo = 512;
         at.pairs = b * kHeads, at.q_rows = rows, at.kv_rows = kv_rows;
         at.partial = r.partial, at.partial_floats = r.partial_floats, at.compute_units = cus;
+        at.k16 = k16, at.v16 = v16;
         icl_attention(at, s);
         tail(bw, x, m, r.att, r.norm, r.hid);
     }
@@ -530,12 +534,14 @@ size_t row_run_floats(long long seqs, int len) {
     return (size_t)(m * (128 * 3 + 384 + 256) + c * (128 * 4 + 256));
 }
 
-BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus) {
+BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus, int precision = IRX_PRECISION_FP32) {
     const long long n = sh.rows, h = sh.features, b = sh.ensembles;
     const int len = (int)h + kReserved;
+    const bool f16 = precision == IRX_PRECISION_SPLIT;
     BuildPlan p{};
     p.keep_bytes = (size_t)kColumnBlocks * 2 * b * (h + 4) * kColumnCache * 4 +
-                   (size_t)kIclBlocks * 2 * b * kHeads * n * 64 * 4;
+                   (f16 ? (size_t)kIclBlocks * 2 * icl16_plane(b * kHeads, n) * 2
+                        : (size_t)kIclBlocks * 2 * b * kHeads * n * 64 * 4);
     size_t cap = std::min<size_t>(budget / 4, (size_t)24 << 30);
     int chunk = (int)h;
     while (chunk > 1 && column_chunk_floats(chunk, n) * 4 > cap) chunk = (chunk + 1) / 2;
@@ -546,7 +552,9 @@ BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus) {
     size_t fixed = ((size_t)n * h + n * 128 + n * 512 + 6 * 128 * 128 + 12 * 512 + 2 * len * 16) * 4;
     size_t state = (size_t)h * n * 128 * 4;  // all features' column states of one estimator
     size_t icl = ((size_t)n * 512 * 7 + n * 1024) * 4 +
-                 icl_attention_partial_floats(kHeads, (int)n, icl_attention_splits(kHeads, (int)n, (int)n, cus)) * 4;
+                 icl_attention_partial_floats(kHeads, (int)n, icl_attention_splits(kHeads, (int)n, (int)n, cus, f16),
+                                              f16) * 4 +
+                 (f16 ? (size_t)2 * kHeads * n * 64 * 4 : 0);  // FP32 K/V of a block before packing
     p.ws_bytes = fixed + state + column_chunk_floats(chunk, n) * 4 + row_run_floats(run, len) * 4 + icl +
                  (size_t)64 * 256 * 40;
     return p;
@@ -562,7 +570,9 @@ int report(irx_progress_fn fn, void *user, int stage, size_t done, size_t total)
     return 0;
 }
 
-void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *out, irx_built_cache **keep) {
+void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *out, irx_built_cache **keep,
+                int precision) {
+    const bool f16 = precision == IRX_PRECISION_SPLIT;
     const irx_shape sh = in->shape;
     if (!shape_ok(&sh)) fail(IRX_INVALID_ARGUMENT, "build shape must be nonempty");
     if (sh.rows < 64) fail(IRX_DOES_NOT_FIT, "the device builds contexts of at least 64 training rows");
@@ -582,7 +592,7 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     }
     set_device(W->device);
     const int cus = W->device->compute_units;
-    BuildPlan plan = plan_build(sh, in->budget, cus);
+    BuildPlan plan = plan_build(sh, in->budget, cus, precision);
     if (plan.ws_bytes + plan.keep_bytes > in->budget / 10 * 9)
         fail(IRX_DOES_NOT_FIT, "the context does not fit the device");
 
@@ -603,13 +613,15 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     } cache_guard{cache};
     cache->device = W->device;
     cache->shape = sh;
+    cache->precision = precision;
     const long long col_plane = (long long)B * L * kColumnCache;
     const long long icl_plane = (long long)B * kHeads * N * 64;
+    const size_t plane16 = icl16_plane((long long)B * kHeads, N), est16 = icl16_plane(kHeads, N);
     for (int i = 0; i < kColumnBlocks; ++i) {
         cache->column[i].alloc(2 * col_plane * 4);
         fill_zero(cache->column[i].f(), 2 * col_plane, s);  // reserved CLS streams stay zero
     }
-    for (int i = 0; i < kIclBlocks; ++i) cache->icl[i].alloc(2 * icl_plane * 4);
+    for (int i = 0; i < kIclBlocks; ++i) cache->icl[i].alloc(f16 ? 2 * plane16 * 2 : 2 * icl_plane * 4);
 
     Arena ws;
     ws.buf.alloc(plan.ws_bytes);
@@ -626,6 +638,9 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     upload(d_sin, sin_t.data(), sin_t.size() * 4, s);
     float *d_x = ws.take((size_t)N * H), *d_ylab = ws.take((size_t)N * 128), *d_yicl = ws.take((size_t)N * 512);
     float *d_state = ws.take((size_t)H * N * 128);
+    // Cached values that are not finite (in FP16 for the FP16 cache) are counted here.
+    unsigned *counter = reinterpret_cast<unsigned *>(ws.take(64));
+    IRX_HIP(hipMemsetAsync(counter, 0, 4, s));
     const size_t mark = ws.used;
 
     report(in->progress, in->progress_user, IRX_STAGE_BUILD, 0, B);
@@ -694,16 +709,29 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
         add_inplace(rows, d_yicl, (long long)N * 512, s);
         // ICL stage: each block's K/V from the training rows, then their queries.
         {
-            Stages::IclBuffers ib = Stages::icl_buffers(ws, N, 1, N, N, cus);
+            Stages::IclBuffers ib = Stages::icl_buffers(ws, N, 1, N, N, cus, f16);
+            float *kv32 = f16 ? ws.take((size_t)2 * kHeads * N * 64) : nullptr;
             for (int blk = 0; blk < kIclBlocks; ++blk) {
                 const BlockW &bw = W->icl[blk];
                 layer_norm(rows, 512, bw.n1w, bw.n1b, ib.norm, 512, N, 512, s);
-                float *kc = cache->icl[blk].f() + (long long)e * kHeads * N * 64;
-                OutMap kvmap = OutMap::head_major(64, kHeads, N, icl_plane);
-                st.linear_map(ib.norm, 512, N, 512, bw.in_w + 512 * 512, bw.in_b + 512, 1024, kc, kvmap);
-                // The last block's row states are never read: only its K/V are kept.
-                if (blk + 1 < kIclBlocks)
-                    st.icl_queries(blk, rows, 1, N, kc, kc + icl_plane, N, d_base + blk * 512, ib);
+                if (!f16) {
+                    float *kc = cache->icl[blk].f() + (long long)e * kHeads * N * 64;
+                    OutMap kvmap = OutMap::head_major(64, kHeads, N, icl_plane);
+                    st.linear_map(ib.norm, 512, N, 512, bw.in_w + 512 * 512, bw.in_b + 512, 1024, kc, kvmap);
+                    // The last block's row states are never read: only its K/V are kept.
+                    if (blk + 1 < kIclBlocks)
+                        st.icl_queries(blk, rows, 1, N, kc, kc + icl_plane, N, d_base + blk * 512, ib);
+                } else {
+                    // FP32 K/V of this estimator, then packed into its part of the FP16 cache.
+                    const long long p32 = (long long)kHeads * N * 64;
+                    OutMap kvmap = OutMap::head_major(64, kHeads, N, p32);
+                    st.linear_map(ib.norm, 512, N, 512, bw.in_w + 512 * 512, bw.in_b + 512, 1024, kv32, kvmap);
+                    unsigned short *k16 = static_cast<unsigned short *>(cache->icl[blk].p) + e * est16;
+                    unsigned short *v16 = k16 + plane16;
+                    pack_icl16(kv32, kv32 + p32, false, N, kHeads, k16, v16, counter, s);
+                    if (blk + 1 < kIclBlocks)
+                        st.icl_queries(blk, rows, 1, N, nullptr, nullptr, N, d_base + blk * 512, ib, k16, v16);
+                }
             }
         }
         IRX_HIP(hipStreamSynchronize(s));
@@ -711,10 +739,9 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     }
     // Non-finite cached values are an error (cuda/build.rs:340-350, 595-622).
     {
-        unsigned *counter = reinterpret_cast<unsigned *>(ws.take(64));
-        IRX_HIP(hipMemsetAsync(counter, 0, 4, s));
         for (int i = 0; i < kColumnBlocks; ++i) count_nonfinite(cache->column[i].f(), 2 * col_plane, counter, s);
-        for (int i = 0; i < kIclBlocks; ++i) count_nonfinite(cache->icl[i].f(), 2 * icl_plane, counter, s);
+        if (!f16)
+            for (int i = 0; i < kIclBlocks; ++i) count_nonfinite(cache->icl[i].f(), 2 * icl_plane, counter, s);
         unsigned bad = 0;
         download(&bad, counter, 4, s);
         IRX_HIP(hipStreamSynchronize(s));
@@ -731,9 +758,20 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
                     download(dst + off, cache->column[i].f() + part * col_plane + off, (size_t)H * kColumnCache * 4, s);
                 }
         }
+        DevBuf logical(f16 ? (size_t)2 * icl_plane * 2 : 0);
         for (int i = 0; i < kIclBlocks; ++i) {
-            if (out->icl_keys[i]) download(out->icl_keys[i], cache->icl[i].f(), icl_plane * 4, s);
-            if (out->icl_values[i]) download(out->icl_values[i], cache->icl[i].f() + icl_plane, icl_plane * 4, s);
+            if (!f16) {
+                if (out->icl_keys[i]) download(out->icl_keys[i], cache->icl[i].f(), icl_plane * 4, s);
+                if (out->icl_values[i]) download(out->icl_values[i], cache->icl[i].f() + icl_plane, icl_plane * 4, s);
+            } else if (out->icl_keys[i] || out->icl_values[i]) {
+                // FP16 bits in the logical layout [B, 8, N, 64].
+                const unsigned short *k16 = static_cast<const unsigned short *>(cache->icl[i].p);
+                unsigned short *lk = static_cast<unsigned short *>(logical.p), *lv = lk + icl_plane;
+                unpack_icl16(k16, k16 + plane16, N, B * kHeads, lk, lv, s);
+                if (out->icl_keys[i]) download(out->icl_keys[i], lk, icl_plane * 2, s);
+                if (out->icl_values[i]) download(out->icl_values[i], lv, icl_plane * 2, s);
+                IRX_HIP(hipStreamSynchronize(s));
+            }
         }
         IRX_HIP(hipStreamSynchronize(s));
     }
@@ -755,7 +793,7 @@ struct PassBuffers {
     Stages::IclBuffers ib;
 };
 
-PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus) {
+PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus, bool f16) {
     const long long B = sh.ensembles, H = sh.features, cr = B * H * (long long)R;
     PassBuffers p{};
     p.flags = a.take_bytes(B * R);
@@ -763,12 +801,12 @@ PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus) {
     p.hid = a.take(cr * 256);
     p.rb = Stages::row_buffers(a, B * (long long)R, (int)H + kReserved);
     p.rows = a.take(B * R * 512);
-    p.ib = Stages::icl_buffers(a, B * (long long)R, (int)B, (int)R, (int)sh.rows, cus);
+    p.ib = Stages::icl_buffers(a, B * (long long)R, (int)B, (int)R, (int)sh.rows, cus, f16);
     // A shorter pass may split the keys further; size the partials for the worst pass.
     size_t worst = 0;
     for (size_t rows = 32; rows <= R; rows += 32) {
-        int splits = icl_attention_splits((int)B * kHeads, (int)rows, (int)sh.rows, cus);
-        worst = std::max(worst, icl_attention_partial_floats((int)B * kHeads, (int)rows, splits));
+        int splits = icl_attention_splits((int)B * kHeads, (int)rows, (int)sh.rows, cus, f16);
+        worst = std::max(worst, icl_attention_partial_floats((int)B * kHeads, (int)rows, splits, f16));
     }
     if (worst > p.ib.partial_floats) {
         p.ib.partial = a.take(worst);
@@ -777,10 +815,10 @@ PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus) {
     return p;
 }
 
-size_t predict_ws_floats(const irx_shape &sh, size_t R, int cus) {
+size_t predict_ws_floats(const irx_shape &sh, size_t R, int cus, bool f16) {
     Arena count;
     count.counting = true;
-    pass_layout(count, sh, R, cus);
+    pass_layout(count, sh, R, cus, f16);
     return count.used / 4;
 }
 
@@ -794,7 +832,8 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     Stages st{W, s, W.device->compute_units};
     Arena &ws = slot ? P->side_ws : P->ws;
     ws.used = 0;
-    const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus);
+    const bool f16 = P->precision == IRX_PRECISION_SPLIT;
+    const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus, f16);
     uint8_t *flags = pb.flags;
     float *state = pb.state, *norm = pb.norm, *q = pb.q, *att = pb.att, *hid = pb.hid, *rows = pb.rows;
     const Stages::RowBuffers &rb = pb.rb;
@@ -810,9 +849,16 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     }
     st.row_stage(state, B, R, H, rows, P->rope_cos.f(), P->rope_sin.f(), rb);
     const long long icl_plane = (long long)B * kHeads * N * 64;
+    const size_t plane16 = icl16_plane((long long)B * kHeads, N);
     for (int blk = 0; blk < kIclBlocks; ++blk) {
-        const float *kc = P->icl[blk].f();
-        st.icl_queries(blk, rows, B, R, kc, kc + icl_plane, N, P->base_scales.f() + blk * 512, ib);
+        if (!f16) {
+            const float *kc = P->icl[blk].f();
+            st.icl_queries(blk, rows, B, R, kc, kc + icl_plane, N, P->base_scales.f() + blk * 512, ib);
+        } else {
+            const unsigned short *k16 = static_cast<const unsigned short *>(P->icl[blk].p);
+            st.icl_queries(blk, rows, B, R, nullptr, nullptr, N, P->base_scales.f() + blk * 512, ib, k16,
+                           k16 + plane16);
+        }
     }
     // Decoder (cached_icl_decoder, cpu.rs:2543-2580) into logits [B, Q, width].
     layer_norm(rows, 512, W.ln_w, W.ln_b, ib.norm, 512, (long long)B * R, 512, s);
@@ -833,7 +879,8 @@ void ensure_workspace(irx_predictor *P) {
     if (P->ws_rows == P->pass_rows && P->ws.buf.p && P->side_ws.buf.p) return;
     if (P->stream) IRX_HIP(hipStreamSynchronize(P->stream));
     if (P->side_stream) IRX_HIP(hipStreamSynchronize(P->side_stream));
-    size_t floats = predict_ws_floats(P->shape, P->pass_rows, P->weights->device->compute_units);
+    size_t floats = predict_ws_floats(P->shape, P->pass_rows, P->weights->device->compute_units,
+                                      P->precision == IRX_PRECISION_SPLIT);
     P->ws.buf.alloc(floats * 4);
     P->side_ws.buf.alloc(floats * 4);
     P->ws_rows = P->pass_rows;
@@ -958,11 +1005,15 @@ int irx_weights_budget(const irx_weights *weights, uint64_t device_limit, size_t
     });
 }
 
-size_t irx_context_bytes(int precision) { return precision == IRX_PRECISION_FP32 ? 4 : 0; }
+size_t irx_context_bytes(int precision) {
+    return precision == IRX_PRECISION_FP32 ? 4 : precision == IRX_PRECISION_SPLIT ? 2 : 0;
+}
 
 int irx_build_fits(size_t budget, int precision, const irx_shape *shape) {
-    if (precision != IRX_PRECISION_FP32 || !shape_ok(shape) || shape->rows < 64) return 0;
-    BuildPlan p = plan_build(*shape, budget, 256);
+    if ((precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT) || !shape_ok(shape) ||
+        shape->rows < 64)
+        return 0;
+    BuildPlan p = plan_build(*shape, budget, 256, precision);
     return p.ws_bytes + p.keep_bytes <= budget / 10 * 9;
 }
 
@@ -970,11 +1021,12 @@ int irx_build(irx_weights *weights, int precision, const irx_build_inputs *input
               irx_built_cache **keep) {
     return guarded("irx_build", [&] {
         if (!weights || !inputs) fail(IRX_INVALID_ARGUMENT, "null argument");
-        if (precision != IRX_PRECISION_FP32) fail(IRX_INVALID_ARGUMENT, "only FP32 precision is built here");
+        if (precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT)
+            fail(IRX_INVALID_ARGUMENT, "precision must be FP32 or SPLIT");
         if (keep) *keep = nullptr;
         if (inputs->shape.outputs == 0 || inputs->shape.outputs > (size_t)weights->width)
             fail(IRX_INVALID_ARGUMENT, "outputs exceed the decoder width");
-        build_impl(weights, inputs, outputs, keep);
+        build_impl(weights, inputs, outputs, keep, precision);
     });
 }
 
@@ -989,7 +1041,9 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
     irx_predictor *P = nullptr;
     int st = guarded("irx_predictor_new", [&] {
         if (!weights || !ctx || !out) fail(IRX_INVALID_ARGUMENT, "null argument");
-        if (precision != IRX_PRECISION_FP32) fail(IRX_INVALID_ARGUMENT, "only FP32 precision is predicted here");
+        if (precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT)
+            fail(IRX_INVALID_ARGUMENT, "precision must be FP32 or SPLIT");
+        const bool f16 = precision == IRX_PRECISION_SPLIT;
         *out = nullptr;
         const irx_shape sh = ctx->shape;
         if (!shape_ok(&sh) || sh.outputs == 0 || sh.outputs > (size_t)weights->width)
@@ -1000,19 +1054,23 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         set_device(weights->device);
         const long long B = sh.ensembles, H = sh.features, N = sh.rows, L = H + kReserved;
         const long long col_plane = B * L * kColumnCache, icl_plane = B * kHeads * N * 64;
-        const size_t cache_bytes = (size_t)(kColumnBlocks * 2 * col_plane + kIclBlocks * 2 * icl_plane) * 4;
+        const size_t plane16 = icl16_plane(B * kHeads, N);
+        const size_t icl_bytes = f16 ? (size_t)kIclBlocks * 2 * plane16 * 2 : (size_t)kIclBlocks * 2 * icl_plane * 4;
+        const size_t cache_bytes = (size_t)kColumnBlocks * 2 * col_plane * 4 + icl_bytes;
         P = new irx_predictor();
         P->weights = weights;
         irx_weights_retain(weights);
         P->shape = sh;
+        P->precision = precision;
         if (adopt) {
             if (adopt->shape.ensembles != sh.ensembles || adopt->shape.features != sh.features ||
                 adopt->shape.rows != sh.rows)
                 fail(IRX_INVALID_ARGUMENT, "the built cache does not match the context");
+            if (adopt->precision != precision) fail(IRX_INVALID_ARGUMENT, "the built cache has another precision");
             for (int i = 0; i < kColumnBlocks; ++i) P->column[i] = std::move(adopt->column[i]);
             for (int i = 0; i < kIclBlocks; ++i) P->icl[i] = std::move(adopt->icl[i]);
         } else {
-            size_t ws = predict_ws_floats(sh, P->pass_rows, weights->device->compute_units) * 4;
+            size_t ws = predict_ws_floats(sh, P->pass_rows, weights->device->compute_units, f16) * 4;
             if (cache_bytes + ws > ctx->budget / 10 * 9) fail(IRX_DOES_NOT_FIT, "the context does not fit the device");
             if (!ctx->icl) fail(IRX_INVALID_ARGUMENT, "ICL source is missing");
             for (int i = 0; i < kColumnBlocks; ++i)
@@ -1024,13 +1082,32 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
                 IRX_HIP(hipMemcpy(P->column[i].f() + col_plane, ctx->column_values[i], col_plane * 4,
                                   hipMemcpyHostToDevice));
             }
+            // FP16 contexts: the source gives FP16 bits [B, 8, N, 64], packed here.
+            DevBuf staging(f16 ? (size_t)2 * icl_plane * 2 : 0), bad(f16 ? 4 : 0);
+            if (f16) IRX_HIP(hipMemset(bad.p, 0, 4));
             for (int i = 0; i < kIclBlocks; ++i) {
                 const float *k = nullptr, *v = nullptr;
                 if (ctx->icl(ctx->icl_user, (size_t)i, &k, &v) != 0 || !k || !v)
                     fail(IRX_INVALID_ARGUMENT, "the ICL source has no block " + std::to_string(i));
-                P->icl[i].alloc(2 * icl_plane * 4);
-                IRX_HIP(hipMemcpy(P->icl[i].p, k, icl_plane * 4, hipMemcpyHostToDevice));
-                IRX_HIP(hipMemcpy(P->icl[i].f() + icl_plane, v, icl_plane * 4, hipMemcpyHostToDevice));
+                if (!f16) {
+                    P->icl[i].alloc(2 * icl_plane * 4);
+                    IRX_HIP(hipMemcpy(P->icl[i].p, k, icl_plane * 4, hipMemcpyHostToDevice));
+                    IRX_HIP(hipMemcpy(P->icl[i].f() + icl_plane, v, icl_plane * 4, hipMemcpyHostToDevice));
+                } else {
+                    unsigned short *sk = static_cast<unsigned short *>(staging.p), *sv = sk + icl_plane;
+                    IRX_HIP(hipMemcpy(sk, k, icl_plane * 2, hipMemcpyHostToDevice));
+                    IRX_HIP(hipMemcpy(sv, v, icl_plane * 2, hipMemcpyHostToDevice));
+                    P->icl[i].alloc(2 * plane16 * 2);
+                    unsigned short *k16 = static_cast<unsigned short *>(P->icl[i].p);
+                    pack_icl16(sk, sv, true, N, (int)(B * kHeads), k16, k16 + plane16, static_cast<unsigned *>(bad.p),
+                               nullptr);
+                    IRX_HIP(hipDeviceSynchronize());
+                }
+            }
+            if (f16) {
+                unsigned nbad = 0;
+                IRX_HIP(hipMemcpy(&nbad, bad.p, 4, hipMemcpyDeviceToHost));
+                if (nbad) fail(IRX_NOT_FINITE, "a cached key or value is not finite");
             }
         }
         P->base_scales.alloc(12 * 512 * 4);
@@ -1085,7 +1162,7 @@ int irx_predictor_set_streams(irx_predictor *predictor, int streams) {
     });
 }
 
-int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t offset, size_t floats, float *dst) {
+int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t offset, size_t floats, void *dst) {
     return guarded("irx_predictor_read_context", [&] {
         if (!predictor || (floats && !dst)) fail(IRX_INVALID_ARGUMENT, "context read needs a predictor and a buffer");
         const irx_shape &s = predictor->shape;
@@ -1099,9 +1176,22 @@ int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t o
         if (offset > plane || floats > plane - offset) fail(IRX_INVALID_ARGUMENT, "context read past the tensor's end");
         if (!floats) return;
         const DevBuf &buf = column ? predictor->column[index / 2] : predictor->icl[index / 2];
-        const float *src = buf.f() + (index % 2) * plane + offset;
         std::lock_guard<std::mutex> lock(predictor->mu);
         set_device(predictor->weights->device);
+        if (!column && predictor->precision == IRX_PRECISION_SPLIT) {
+            // FP16 bits in the logical layout, unpacked from the cache layout.
+            const long long pairs = (long long)s.ensembles * kHeads;
+            const size_t plane16 = icl16_plane(pairs, (long long)s.rows);
+            DevBuf logical(2 * plane * 2);
+            const unsigned short *k16 = static_cast<const unsigned short *>(buf.p);
+            unsigned short *lk = static_cast<unsigned short *>(logical.p);
+            unpack_icl16(k16, k16 + plane16, (long long)s.rows, (int)pairs, lk, lk + plane, predictor->stream);
+            IRX_HIP(hipMemcpyAsync(dst, lk + (index % 2) * plane + offset, floats * 2, hipMemcpyDeviceToHost,
+                                   predictor->stream));
+            IRX_HIP(hipStreamSynchronize(predictor->stream));
+            return;
+        }
+        const float *src = buf.f() + (index % 2) * plane + offset;
         // On the predictor's stream: after every pass issued before the call.
         IRX_HIP(hipMemcpyAsync(dst, src, floats * 4, hipMemcpyDeviceToHost, predictor->stream));
         IRX_HIP(hipStreamSynchronize(predictor->stream));
@@ -1202,9 +1292,12 @@ int irx_profile_read(const char *family, irx_kernel_stats *out) {
 
 // ---- kernel harness ----
 
-int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v, size_t pairs,
-                           size_t query_rows, size_t rows, float *out) {
+int irx_test_icl_attention_precision(irx_device *device, int precision, const float *q, const float *k,
+                                     const float *v, size_t pairs, size_t query_rows, size_t rows, float *out) {
     return guarded("irx_test_icl_attention", [&] {
+        if (precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT)
+            fail(IRX_INVALID_ARGUMENT, "unsupported precision");
+        const bool f16 = precision == IRX_PRECISION_SPLIT;
         if (!device || !q || !k || !v || !out || !pairs || !query_rows || !rows)
             fail(IRX_INVALID_ARGUMENT, "ICL attention shapes do not match");
         if (pairs % kHeads) fail(IRX_INVALID_ARGUMENT, "pairs must be a multiple of 8 (estimators x heads)");
@@ -1214,10 +1307,18 @@ int irx_test_icl_attention(irx_device *device, const float *q, const float *k, c
         IRX_HIP(hipMemcpy(dq.p, q, qn * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(dk.p, k, kn * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(dv.p, v, kn * 4, hipMemcpyHostToDevice));
-        int splits = icl_attention_splits((int)pairs, (int)query_rows, (int)rows, device->compute_units);
-        size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, splits);
+        int splits = icl_attention_splits((int)pairs, (int)query_rows, (int)rows, device->compute_units, f16);
+        size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, splits, f16);
         DevBuf part(pf * 4);
+        DevBuf cache16(f16 ? 2 * icl16_plane((long long)pairs, (long long)rows) * 2 : 0), bad(f16 ? 4 : 0);
         IclAttention a{};
+        if (f16) {
+            unsigned short *k16 = static_cast<unsigned short *>(cache16.p);
+            unsigned short *v16 = k16 + icl16_plane((long long)pairs, (long long)rows);
+            IRX_HIP(hipMemset(bad.p, 0, 4));
+            pack_icl16(dk.p, dv.p, false, (long long)rows, (int)pairs, k16, v16, static_cast<unsigned *>(bad.p), nullptr);
+            a.k16 = k16, a.v16 = v16;
+        }
         a.q = dq.f(), a.q_pair_stride = (long long)query_rows * 64, a.k = dk.f(), a.v = dv.f();
         a.kv_pair_stride = (long long)rows * 64, a.o = dout.f(), a.ldo = 512;
         a.pairs = (int)pairs, a.q_rows = (int)query_rows, a.kv_rows = (int)rows;
@@ -1233,6 +1334,11 @@ int irx_test_icl_attention(irx_device *device, const float *q, const float *k, c
                 std::memcpy(out + (p * query_rows + r) * 64, tok.data() + ((b * query_rows + r) * 512 + h * 64), 256);
         }
     });
+}
+
+int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v, size_t pairs,
+                           size_t query_rows, size_t rows, float *out) {
+    return irx_test_icl_attention_precision(device, IRX_PRECISION_FP32, q, k, v, pairs, query_rows, rows, out);
 }
 
 int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1, const float *w2,

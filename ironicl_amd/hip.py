@@ -19,6 +19,7 @@ OK, NO_DEVICE, OUT_OF_MEMORY, INVALID_ARGUMENT, DEVICE_ERROR, INTERRUPTED, DOES_
 STATUS_NAMES = ["OK", "NO_DEVICE", "OUT_OF_MEMORY", "INVALID_ARGUMENT", "DEVICE_ERROR", "INTERRUPTED",
                 "DOES_NOT_FIT", "NOT_FINITE", "UNSUPPORTED"]
 PRECISION_FP32 = 0
+PRECISION_SPLIT = 1
 TASK_CLASSIFIER, TASK_REGRESSOR = 0, 1
 STAGE_BUILD, STAGE_PREDICT = 0, 1
 
@@ -101,6 +102,8 @@ SIGNATURES = {
     "irx_profile_enable": (ctypes.c_int, [ctypes.c_uint]),
     "irx_profile_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(KernelStats)]),
     "irx_test_icl_attention": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
+    "irx_test_icl_attention_precision": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _CF, _CF, _sz, _sz,
+                                                        _sz, _F]),
     "irx_test_products": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _CF, _CF, _sz, _sz, _sz, _sz, _F, _F]),
     "irx_test_layer_norm": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _F]),
     "irx_test_copy": (ctypes.c_int, [ctypes.c_void_p, _sz]),
@@ -142,6 +145,14 @@ def fptr(a: np.ndarray | None):
     if a is None:
         return None
     assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_F)
+
+
+def cache_ptr(a: np.ndarray | None):
+    """A float* ABI field holding an FP32 or (FP16 cache tensors) FP16 array."""
+    if a is None:
+        return None
+    assert a.dtype in (np.float32, np.float16) and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
     return a.ctypes.data_as(_F)
 
 

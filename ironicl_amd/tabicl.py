@@ -29,6 +29,17 @@ from . import manifest as mf
 
 _erf = np.frompyfunc(math.erf, 1, 1)
 
+# The optimize levels this backend builds and predicts at (Precision::for_optimize,
+# cuda/mod.rs:82-92): "safe" all FP32; "auto" an FP16 ICL cache with split-FP16
+# attention products.
+PRECISION = {"safe": hip.PRECISION_FP32, "auto": hip.PRECISION_SPLIT}
+
+
+def _precision(optimize: str) -> int:
+    if optimize not in PRECISION:
+        raise ValueError(f"optimize must be one of {sorted(PRECISION)} on this backend, not {optimize!r}")
+    return PRECISION[optimize]
+
 
 def _gelu64(x: np.ndarray) -> np.ndarray:
     x = np.asarray(x, dtype=np.float64)
@@ -219,10 +230,9 @@ class Executor:
         a path): load the context from ``<identity>.irctx`` there when that
         file holds exactly this context, else build it and write it there.
         A missing, invalid or mismatched entry is rebuilt; a failed write
-        leaves the context in HBM only (cpu.rs:645-672). Only ``optimize="safe"``
-        (FP32) builds on this backend."""
-        if optimize != "safe":
-            raise ValueError("this backend builds FP32 contexts only (optimize='safe')")
+        leaves the context in HBM only (cpu.rs:645-672). ``optimize`` is "safe"
+        (all FP32) or "auto" (an FP16 ICL cache read by split-FP16 attention)."""
+        precision = _precision(optimize)
         meta = self.context_metadata(x, y_train, class_permutations, feature_permutations, optimize)
         directory = cf.resolve_cache_dir(cache_dir)
         if directory is not None:
@@ -238,8 +248,11 @@ class Executor:
                     os.utime(path)  # the entry's last use, for clear_cache
                 except OSError:
                     pass
-                return self._attach(cached)
-        executor = self._build(_f32(x), _f32(y_train), meta, download, progress, device_limit)
+                try:
+                    return self._attach(cached, optimize)
+                except cf.ContextError:
+                    pass  # stored at another precision: rebuilt below
+        executor = self._build(_f32(x), _f32(y_train), meta, download, progress, device_limit, precision)
         if directory is not None:
             # Caching is best effort: a context that cannot be written is still returned.
             try:
@@ -249,7 +262,8 @@ class Executor:
                 pass
         return executor
 
-    def _build(self, x, y_train, meta: cf.Metadata, download: bool, progress, device_limit: int) -> "StaticExecutor":
+    def _build(self, x, y_train, meta: cf.Metadata, download: bool, progress, device_limit: int,
+               precision: int = hip.PRECISION_FP32) -> "StaticExecutor":
         b, n, h = x.shape
         col_labels, icl_labels = self.label_embeddings(y_train)
         ind_q = self.inducing_queries(n)
@@ -271,41 +285,54 @@ class Executor:
         if download:
             ck = [np.zeros((b, h + 4, 8, 128, 16), np.float32) for _ in range(3)]
             cv = [np.zeros_like(ck[0]) for _ in range(3)]
-            ik = [np.zeros((b, 8, n, 64), np.float32) for _ in range(12)]
+            icl_dtype = np.float16 if precision == hip.PRECISION_SPLIT else np.float32
+            ik = [np.zeros((b, 8, n, 64), icl_dtype) for _ in range(12)]
             iv = [np.zeros_like(ik[0]) for _ in range(12)]
             for i in range(3):
                 out.column_keys[i], out.column_values[i] = hip.fptr(ck[i]), hip.fptr(cv[i])
             for i in range(12):
-                out.icl_keys[i], out.icl_values[i] = hip.fptr(ik[i]), hip.fptr(iv[i])
+                out.icl_keys[i], out.icl_values[i] = hip.cache_ptr(ik[i]), hip.cache_ptr(iv[i])
             context = (ck, cv, ik, iv)
         keep = ctypes.c_void_p()
-        hip.check(hip.lib().irx_build(self.handle, hip.PRECISION_FP32, ctypes.byref(inp), ctypes.byref(out),
+        hip.check(hip.lib().irx_build(self.handle, precision, ctypes.byref(inp), ctypes.byref(out),
                                       ctypes.byref(keep)))
         return StaticExecutor(self, (b, n, h), meta.class_count, meta.class_permutations,
                               meta.feature_permutations, built=keep.value, context=context, base_scales=bases,
-                              metadata=meta)
+                              metadata=meta, precision=precision)
 
-    def _attach(self, context: cf.ContextFile) -> "StaticExecutor":
-        """Upload a verified context for prediction (with_executor / with_cuda, cpu.rs:1745-1910)."""
+    def _attach(self, context: cf.ContextFile, optimize: str | None = None) -> "StaticExecutor":
+        """Upload a verified context for prediction (with_executor / with_cuda,
+        cpu.rs:1745-1910). Its ICL storage decides the precision: FP32 caches
+        predict at "safe", FP16 caches at "auto"; an `optimize` that asks for
+        the other is an error (the reference's CUDA path would leave such a
+        context on its CPU, which this backend does not have)."""
         meta = context.metadata
         b, n, _ = meta.shape
+        icl = {context.tensor(f"icl.{i}.{kind}").dtype for i in range(12) for kind in ("key", "value")}
+        cols = {context.tensor(f"column.{i}.{kind}").dtype for i in range(3) for kind in ("key", "value")}
+        if cols != {np.dtype("<f4")} or len(icl) != 1:
+            raise cf.ContextError("the context's column caches must be FP32 and its ICL caches of one type")
+        stored = "auto" if icl == {np.dtype("<f2")} else "safe"
+        if optimize is not None and optimize != stored:
+            raise cf.ContextError(f"the context stores its ICL cache for optimize={stored!r}, not {optimize!r}")
         return StaticExecutor(self, meta.shape, meta.class_count, meta.class_permutations,
                               meta.feature_permutations, built=None, context=context.host_tensors(),
-                              base_scales=self.icl_base_scales(n), metadata=meta, keep_alive=context)
+                              base_scales=self.icl_base_scales(n), metadata=meta, keep_alive=context,
+                              precision=_precision(stored))
 
-    def load_context(self, path) -> "StaticExecutor":
+    def load_context(self, path, optimize: str | None = None) -> "StaticExecutor":
         """Load a persisted IRCNTXT context, verify it against this model and
         upload it to HBM (Executor::load_context, cpu.rs:397-406)."""
         context = cf.read(path)
         cf.validate_for_model(context, self.source_sha256, self.task)
-        return self._attach(context)
+        return self._attach(context, optimize)
 
-    def load_context_bytes(self, data: bytes) -> "StaticExecutor":
+    def load_context_bytes(self, data: bytes, optimize: str | None = None) -> "StaticExecutor":
         """The same from the bytes ``StaticExecutor.encode_context`` wrote
         (Executor::load_context_bytes, cpu.rs:415-424)."""
         context = cf.from_bytes(data)
         cf.validate_for_model(context, self.source_sha256, self.task)
-        return self._attach(context)
+        return self._attach(context, optimize)
 
     def load_context_tensors(self, context, shape, classes: int, class_permutations=None,
                              feature_permutations=None) -> "StaticExecutor":
@@ -352,11 +379,13 @@ class StaticExecutor:
     Predictor, cuda/predictor.rs:93-271)."""
 
     def __init__(self, executor: Executor, shape, classes: int, class_permutations, feature_permutations,
-                 built, context, base_scales, metadata: cf.Metadata | None = None, keep_alive=None):
+                 built, context, base_scales, metadata: cf.Metadata | None = None, keep_alive=None,
+                 precision: int = hip.PRECISION_FP32):
         self.executor = executor
         self.shape = shape
         self.classes = classes
         self.metadata = metadata
+        self.precision = precision
         self._keep_alive = keep_alive
         b = shape[0]
         self.class_permutations = (np.asarray(class_permutations, dtype=np.uint64).reshape(b, -1)
@@ -375,7 +404,9 @@ class StaticExecutor:
         ctx.budget = executor.budget()
         keep_alive = []
         if built is None:
-            ck, cv, ik, iv = [[_f32(t) for t in part] for part in context]
+            icl_dtype = np.float16 if precision == hip.PRECISION_SPLIT else np.float32
+            ck, cv = [[_f32(t) for t in part] for part in context[:2]]
+            ik, iv = [[np.ascontiguousarray(t, dtype=icl_dtype) for t in part] for part in context[2:]]
             keep_alive = [ck, cv, ik, iv]
             for i in range(3):
                 ctx.column_keys[i], ctx.column_values[i] = hip.fptr(ck[i]), hip.fptr(cv[i])
@@ -391,7 +422,7 @@ class StaticExecutor:
             ctx.icl = source
             keep_alive.append(source)
         handle = ctypes.c_void_p()
-        hip.check(hip.lib().irx_predictor_new(executor.handle, hip.PRECISION_FP32, ctypes.byref(ctx), built,
+        hip.check(hip.lib().irx_predictor_new(executor.handle, precision, ctypes.byref(ctx), built,
                                               ctypes.byref(handle)))
         self.handle = handle.value
 
@@ -432,16 +463,19 @@ class StaticExecutor:
                 named[f"column.{i}.key"], named[f"column.{i}.value"] = ck[i], cv[i]
             for i in range(mf.ICL_BLOCKS):
                 named[f"icl.{i}.key"], named[f"icl.{i}.value"] = ik[i], iv[i]
-            flat = {k: np.ascontiguousarray(v, dtype=np.float32).reshape(-1) for k, v in named.items()}
+            flat = {k: np.ascontiguousarray(v).reshape(-1) for k, v in named.items()}
             return lambda name, start, count: flat[name][start:start + count]
-        index = {name: i for i, (name, _) in enumerate(cf.context_tensor_specs(*self.shape))}
+        specs = self._specs()
+        index = {name: i for i, (name, _, _) in enumerate(specs)}
+        dtypes = {name: dtype for name, _, dtype in specs}
         buffers = {}
 
         def read(name, start, count):
-            buf = buffers.get(count)
+            key = (count, dtypes[name])
+            buf = buffers.get(key)
             if buf is None:
                 buffers.clear()
-                buf = buffers[count] = np.empty(count, np.float32)
+                buf = buffers[key] = np.empty(count, dtypes[name])
             hip.check(hip.lib().irx_predictor_read_context(self.handle, index[name], start, count,
                                                            buf.ctypes.data_as(ctypes.c_void_p)))
             return buf
@@ -454,18 +488,23 @@ class StaticExecutor:
                              "build it with Executor.build_context to save it")
         return self.metadata
 
+    def _specs(self):
+        icl_dtype = np.float16 if self.precision == hip.PRECISION_SPLIT else np.float32
+        return cf.context_tensor_specs(*self.shape, icl_dtype)
+
     def save_context(self, path) -> None:
         """Write the context as an IRCNTXT file, atomically, streaming its
-        tensors from HBM when no host copy exists."""
+        tensors from HBM when no host copy exists (FP16 ICL tensors, version
+        2, for an optimize="auto" context)."""
         meta = self._persistable()
-        cf.write(path, meta, cf.context_tensor_specs(*self.shape), self._tensor_source())
+        cf.write(path, meta, self._specs(), self._tensor_source())
 
     def context_encoded_len(self) -> int:
-        return cf.encoded_len(self._persistable(), cf.context_tensor_specs(*self.shape))
+        return cf.encoded_len(self._persistable(), self._specs())
 
     def encode_context(self, sink) -> None:
         """Encode the context into the binary file-like `sink` as save_context writes it."""
-        cf.encode(self._persistable(), cf.context_tensor_specs(*self.shape), self._tensor_source(), sink)
+        cf.encode(self._persistable(), self._specs(), self._tensor_source(), sink)
 
     def predict_raw(self, x: np.ndarray, progress=None) -> Prediction:
         """Every decoder output [B, Q, width] (Predictor::predict, predictor.rs:224-271)."""

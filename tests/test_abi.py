@@ -39,7 +39,8 @@ def test_host_queries():
     lib = hip.lib()
     assert lib.irx_abi_version() == 1
     assert lib.irx_context_bytes(hip.PRECISION_FP32) == 4
-    assert lib.irx_context_bytes(1) == 0
+    assert lib.irx_context_bytes(hip.PRECISION_SPLIT) == 2  # the FP16 ICL cache of optimize="auto"
+    assert lib.irx_context_bytes(7) == 0
     small = hip.Shape(1, 5, 240, 10)
     assert lib.irx_build_fits(1 << 40, hip.PRECISION_FP32, ctypes.byref(small)) == 1
     assert lib.irx_build_fits(1 << 20, hip.PRECISION_FP32, ctypes.byref(small)) == 0
@@ -47,6 +48,8 @@ def test_host_queries():
     assert lib.irx_build_fits(1 << 40, hip.PRECISION_FP32, ctypes.byref(tiny)) == 0
     huge = hip.Shape(8, 500, 200_000, 10)  # the 200k x 500 x 8 context fits 288 GB
     assert lib.irx_build_fits(280 << 30, hip.PRECISION_FP32, ctypes.byref(huge)) == 1
+    assert lib.irx_build_fits(1 << 40, hip.PRECISION_SPLIT, ctypes.byref(small)) == 1
+    assert lib.irx_build_fits(1 << 40, 7, ctypes.byref(small)) == 0
 
 
 def test_disable_variable_means_no_device(monkeypatch):

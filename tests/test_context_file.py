@@ -204,8 +204,32 @@ def test_rejects_reduced_precision_and_packed_versions():
     struct.pack_into("<H", data, second + 6, 1)
     assert cf.from_bytes(resign(data)).version == 2
     struct.pack_into("<H", data, second + 6, 2)
-    with pytest.raises(cf.ContextError, match="not FP32"):
+    with pytest.raises(cf.ContextError, match="BF16"):
         cf.from_bytes(resign(data))
+
+
+def test_fp16_tensors_round_trip_as_version_2():
+    """An optimize="auto" context: FP16 ICL tensors, FP32 column tensors,
+    written as version 2 with per-tensor tags (FP32 1, FP16 3; src/config.rs:79-86)."""
+    rng = np.random.default_rng(0)
+    tensors = {"column.k.0": rng.standard_normal((2, 8, 3, 16)).astype(np.float32),
+               "icl.v.0": rng.standard_normal((2, 8, 3, 64)).astype(np.float16)}
+    data = cf.to_bytes(fixture_metadata(), tensors)
+    assert struct.unpack_from("<I", data, 8)[0] == 2
+    first = 164 + 80
+    second = first + 24 + 4 * 8 + len("column.k.0")
+    assert struct.unpack_from("<H", data, first + 6)[0] == 1 and struct.unpack_from("<H", data, second + 6)[0] == 3
+    assert struct.unpack_from("<Q", data, second + 16)[0] == 2 * 3072
+    ctx = cf.from_bytes(data)
+    assert ctx.version == 2 and ctx.tensor("icl.v.0").dtype == np.float16
+    np.testing.assert_array_equal(ctx.tensor("icl.v.0"), tensors["icl.v.0"])
+    np.testing.assert_array_equal(ctx.tensor("column.k.0"), tensors["column.k.0"])
+    assert cf.to_bytes(ctx.metadata, {n: ctx.tensor(n) for n in ctx.names}) == data
+    bad = dict(tensors)
+    bad["icl.v.0"] = bad["icl.v.0"].copy()
+    bad["icl.v.0"][0, 0, 0, 0] = np.float16(np.inf)
+    with pytest.raises(cf.ContextError, match="non-finite"):
+        cf.to_bytes(fixture_metadata(), bad)
 
 
 def test_cached_read_accepts_only_the_expected_context(tmp_path):
@@ -268,10 +292,12 @@ def test_failed_write_removes_its_temporary_file(tmp_path):
 
 
 def test_context_tensor_specs_follow_the_reference_order():
-    specs = cf.context_tensor_specs(2, 100, 7)
+    specs = [s[:2] for s in cf.context_tensor_specs(2, 100, 7)]
     assert len(specs) == 30
     assert specs[0] == ("column.0.key", (2, 11, 8, 128, 16)) and specs[5] == ("column.2.value", (2, 11, 8, 128, 16))
     assert specs[6] == ("icl.0.key", (2, 8, 100, 64)) and specs[29] == ("icl.11.value", (2, 8, 100, 64))
+    f16 = cf.context_tensor_specs(1, 5, 2, np.float16)
+    assert {s[2] for s in f16[:6]} == {np.dtype(np.float32)} and {s[2] for s in f16[6:]} == {np.dtype(np.float16)}
     # File order is bytewise: icl.1.* < icl.10.* < icl.11.* < icl.2.*
     meta = fixture_metadata(training_rows=1, feature_count=1, ensemble_count=1, class_permutations=[0, 1, 2],
                             feature_permutations=[0])

@@ -87,6 +87,50 @@ def test_icl_attention_matches_float64(device, rows):
         assert worst < 1e-5, (rows, query_rows, worst)
 
 
+@pytest.mark.parametrize("rows", [1, 63, 64, 65, 2000, 10007])
+def test_icl_attention_split_fp16_matches_float64(device, rows):
+    """Split-FP16 products over the FP16 cache (optimize="auto"): against
+    float64 attention of the FP16-rounded keys and values, and against the
+    unrounded ones within the cache's own rounding."""
+    pairs = 16
+    k = fast_values(pairs * rows * 64, 2).reshape(pairs, rows, 64)
+    v = fast_values(pairs * rows * 64, 3).reshape(pairs, rows, 64)
+    k16, v16 = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+    for query_rows in (1, 5, 40, 64, 100, 300):
+        q = fast_values(pairs * query_rows * 64, 1, scale=3.0).reshape(pairs, query_rows, 64)
+        out = np.zeros_like(q)
+        F = hip.fptr
+        hip.check(hip.lib().irx_test_icl_attention_precision(device.handle, hip.PRECISION_SPLIT, F(q), F(k), F(v),
+                                                             pairs, query_rows, rows, F(out)))
+        worst16 = worst = 0.0
+        for pair in (0, 7, 15):
+            rows_sel = sorted({0, query_rows // 2, query_rows - 1})
+            want16 = attention64(q[pair, rows_sel], k16[pair], v16[pair], 0.125)
+            want = attention64(q[pair, rows_sel], k[pair], v[pair], 0.125)
+            worst16 = max(worst16, np.abs(out[pair, rows_sel] - want16).max())
+            worst = max(worst, np.abs(out[pair, rows_sel] - want).max())
+        assert worst16 < 2e-5, (rows, query_rows, worst16)
+        assert worst < 5e-3, (rows, query_rows, worst)
+
+
+@pytest.mark.parametrize("qr", [12, 40])
+def test_icl_attention_split_fp16_peaked_scores(device, qr):
+    """Large logits with the FP16 path's lower lazy limit: the reference is
+    raised more often and the output stays exact to the cache's rounding."""
+    pairs, rows = 8, 3000
+    k = fast_values(pairs * rows * 64, 7).reshape(pairs, rows, 64)
+    v = fast_values(pairs * rows * 64, 8).reshape(pairs, rows, 64)
+    q = (k[:, 1234:1234 + qr] * 40.0).copy()
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_icl_attention_precision(device.handle, hip.PRECISION_SPLIT, F(q), F(k), F(v), pairs,
+                                                         qr, rows, F(out)))
+    k16, v16 = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
+    for pair in (0, 5):
+        want = attention64(q[pair], k16[pair], v16[pair], 0.125)
+        assert np.abs(out[pair] - want).max() < 2e-5
+
+
 @pytest.mark.parametrize("qr", [12, 30, 40])
 def test_icl_attention_peaked_scores(device, qr):
     """Large logits: one key dominates; the online max must stay exact."""
