@@ -16,7 +16,8 @@ FP32 inputs to a resident context). The oracle (C restatement of the reference
 CPU path) is timed on the host's cores on a bounded sample of the same rows.
 Passes of 1, 8, 16 and 32 rows, where streaming the cached K/V from HBM bounds
 the cross-attention, are timed after the steps and reported with their HBM
-fraction.
+fraction. The same workload at optimize="auto" (FP16 ICL cache, split-FP16
+attention) is reported beside the FP32 line, with its accuracy gate.
 
 Prints one JSON line.
 """
@@ -37,6 +38,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # dense
+CLASSES = 10
 HBM_PEAK_GBPS = 8000.0
 WORKLOAD = "clf-50k"
 # Pass sizes of the HBM-bound sweep of the cross-attention, and passes timed each.
@@ -164,6 +167,76 @@ def bench_fitted(executor, x, y, xt, args) -> dict:
     report["predict_proba_rows_per_s"] = query.shape[0] / (time.perf_counter() - t0)
     log(f"fitted model: fit {report['fit_s']:.2f} s, predict_proba {report['predict_proba_rows_per_s']:.0f} rows/s")
     del fm
+    return report
+
+
+def bench_auto(executor, x, y, q, dx, gpu_logits, args) -> dict:
+    """optimize="auto" on the same workload: FP16 ICL cache, split-FP16
+    attention products. Build ms, rows/s over timed steps (two streams), the
+    attention launch's rate (single-stream steps), and the accuracy gate
+    against the "safe" logits of the main run (max |logit| difference, labels
+    that differ where safe's top-2 margin exceeds 2e-2)."""
+    from ironicl_amd import hip, hipmem
+
+    ms = []
+    ctx = executor.build_context(x, y, optimize="auto")
+    for _ in range(max(1, args.build_repeats)):
+        del ctx
+        hipmem.synchronize()
+        t0 = time.perf_counter()
+        ctx = executor.build_context(x, y, optimize="auto")
+        hipmem.synchronize()
+        ms.append(1000 * (time.perf_counter() - t0))
+    ctx.set_pass_rows(args.pass_rows)
+    b = x.shape[0]
+    dl = hipmem.DeviceArray((b, q, executor.width))
+
+    def step():
+        hip.check(hip.lib().irx_predictor_predict_device(ctx.handle, dx.ptr, q, dl.ptr, None))
+
+    for _ in range(args.warmup):
+        step()
+    hipmem.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    hipmem.synchronize()
+    elapsed = time.perf_counter() - t0
+    logits = dl.to_host()
+    ctx.set_streams(1)
+    step()
+    hip.profile_enable(["icl_attention"])
+    for _ in range(args.steps):
+        step()
+    hipmem.synchronize()
+    att = hip.profile_read("icl_attention")
+    hip.profile_enable(False)
+    ctx.set_streams(2)
+    launch_ms = att["milliseconds"] / max(att["launches"], 1)
+    flops = att["flops"] / max(att["launches"], 1)
+    safe = gpu_logits[..., :CLASSES]
+    auto = logits[..., :CLASSES]
+    top2 = np.sort(safe, axis=-1)[..., -2:]
+    decided = (top2[..., 1] - top2[..., 0]) > 2e-2
+    report = {
+        "rows_per_s": q * args.steps / elapsed,
+        "ms_per_step": 1000 * elapsed / args.steps,
+        "build_ms": float(np.median(ms)),
+        "attention": {
+            "kernel": "icl_attention_split_kernel (FP16 cache, queries and probabilities split hi + lo/2^11, "
+                      "32x32x16 FP16 MFMA)",
+            "avg_launch_ms": launch_ms,
+            "algorithmic_tflops": flops / (launch_ms * 1e-3) / 1e12,
+            # Four FP16 products per FP32-equivalent product pair (hi and lo of Q, of P).
+            "fp16_mfma_frac": 2 * flops / (launch_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
+        },
+        "gate_vs_safe": {"max_abs_logit_diff": float(np.abs(auto - safe).max()),
+                         "tolerance": 1e-2,
+                         "labels_differing_beyond_near_ties": int((auto.argmax(-1) != safe.argmax(-1))[decided].sum())},
+    }
+    log(f"auto: build {report['build_ms']:.1f} ms, {report['rows_per_s']:.0f} rows/s, attention "
+        f"{1e3 * launch_ms:.1f} us, max |logit - safe| {report['gate_vs_safe']['max_abs_logit_diff']:.2e}")
+    del ctx
     return report
 
 
@@ -333,6 +406,7 @@ def main() -> int:
         os.remove(path)
         log(f"context export {export_s:.2f} s, verified reload {import_s:.2f} s ({size / 1e9:.2f} GB)")
 
+    auto_report = bench_auto(executor, x, y, q, dx, gpu_logits, args)
     fitted_report = bench_fitted(executor, x, y, xt, args) if args.fitted else None
 
     # The same prediction from host buffers (PCIe included), for reference.
@@ -403,6 +477,7 @@ def main() -> int:
             "kernel": "icl_decode_kernel (passes of <= 32 rows against the 2.46 GB cached K/V, one stream)",
             "bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s", "by_pass_rows": small,
         },
+        "optimize_auto": auto_report,
         "context_io": context_io,
         "fitted": fitted_report,
         "kernel_ms_per_step": kernel_ms,
