@@ -211,6 +211,29 @@ def bench_auto(executor, x, y, q, dx, gpu_logits, args) -> dict:
     hipmem.synchronize()
     att = hip.profile_read("icl_attention")
     hip.profile_enable(False)
+    # Small passes over the FP16 cache (half the bytes of the FP32 one).
+    small = {}
+    n = x.shape[1]
+    kv_bytes = 2.0 * b * 8 * n * 64 * 2
+    ctx.set_pass_rows(max(SMALL_PASSES))
+    for qb in SMALL_PASSES:
+        def small_step():
+            hip.check(hip.lib().irx_predictor_predict_device(ctx.handle, dx.ptr, qb, dl.ptr, None))
+
+        small_step()
+        hipmem.synchronize()
+        hip.profile_enable(["icl_attention"])
+        for _ in range(SMALL_PASS_REPEATS):
+            small_step()
+        hipmem.synchronize()
+        st = hip.profile_read("icl_attention")
+        hip.profile_enable(False)
+        lm = st["milliseconds"] / max(st["launches"], 1)
+        algo = kv_bytes + 2.0 * b * 8 * qb * 64 * 4
+        small[str(qb)] = {"avg_launch_ms": lm, "bytes_per_launch": algo,
+                          "achieved_gbps": algo / (lm * 1e-3) / 1e9,
+                          "frac": algo / (lm * 1e-3) / 1e9 / HBM_PEAK_GBPS}
+    ctx.set_pass_rows(args.pass_rows)
     ctx.set_streams(2)
     launch_ms = att["milliseconds"] / max(att["launches"], 1)
     flops = att["flops"] / max(att["launches"], 1)
@@ -230,6 +253,7 @@ def bench_auto(executor, x, y, q, dx, gpu_logits, args) -> dict:
             # Four FP16 products per FP32-equivalent product pair (hi and lo of Q, of P).
             "fp16_mfma_frac": 2 * flops / (launch_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
         },
+        "small_pass_hbm": {"kernel": "icl_decode16_kernel (FP16 cache, 16x16x32 FP16 MFMA)", "by_pass_rows": small},
         "gate_vs_safe": {"max_abs_logit_diff": float(np.abs(auto - safe).max()),
                          "tolerance": 1e-2,
                          "labels_differing_beyond_near_ties": int((auto.argmax(-1) != safe.argmax(-1))[decided].sum())},

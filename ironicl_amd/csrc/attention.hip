@@ -842,6 +842,214 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
     }
 }
 
+// Few queries over the FP16 cache (optimize="auto"): as icl_decode_kernel,
+// HBM-bound, now on half the bytes. Blocks of 32 keys on the 16x16x32 FP16
+// MFMA, queries and probabilities split hi + lo / 2^11 as in the split kernel:
+//   S^T block b (16 rows x 16 queries, 32 dims per product): row i is key
+//     16 (i / 8) + 8 b + i % 8 of the block, A = K[that key][dims 32 m +
+//     8 (lane / 16) .. +7], B = the lane's query; result register r of lane
+//     l is row 4 (l / 16) + r, query l % 16;
+//   O^T (16 dims x 16 queries per product, 32 keys): the lane's 8
+//     probabilities (blocks 0 and 1, registers 0..3) are keys stored at
+//     positions 8 (lane / 16) .. +7 of the block in V^T, so A is one 16-byte
+//     load of V^T row dim.
+// Every K load is 64 contiguous bytes per four lanes, every V^T load 64
+// contiguous bytes of one dim row per four lanes.
+template <int QG, bool SPLIT>
+__global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclAttention p, IclLaunch g) {
+    __shared__ float red_o[kDecodeWaves][QG * 16 * kDecodeOStride];
+    __shared__ float red_m[kDecodeWaves][QG * 16], red_l[kDecodeWaves][QG * 16];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 4, i16 = lane & 15;
+    const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
+    const int k_begin = split * g.keys_per_split;
+    const int k_end = min(p.kv_rows, k_begin + g.keys_per_split);
+    const int n_pad = (p.kv_rows + kKeyTile - 1) / kKeyTile * kKeyTile;
+
+    half8 qh[QG][2], ql[QG][2];
+    {
+        const float scale = 0.125f * kLog2e;
+#pragma unroll
+        for (int gq = 0; gq < QG; ++gq) {
+            const int row = 16 * gq + i16;
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                float x[8];
+                if (row < p.q_rows) {
+                    const float *src = p.q + pair * p.q_pair_stride + (long long)row * 64 + 32 * m + 8 * grp;
+                    const f32x4 a = *reinterpret_cast<const f32x4 *>(src);
+                    const f32x4 b = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = a[e] * scale, x[4 + e] = b[e] * scale;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = 0.f;
+                }
+                split8(x, qh[gq][m], ql[gq][m]);
+            }
+        }
+    }
+    const unsigned short *kbase = p.k16 + (long long)pair * n_pad * 64;
+    const unsigned short *vbase = p.v16 + (long long)pair * n_pad * 64;
+    // Block at k0 (a multiple of 32, at most n_pad - 32): K rows of S blocks
+    // 0 and 1 (dims 32 m + 8 grp ..) and V^T rows 16 d + i16 at the block's
+    // stored positions 8 grp ..
+    auto load = [&](int k0, u32x4 *kd, u32x4 *vd) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int key = k0 + 16 * (i16 >> 3) + 8 * b + (i16 & 7);
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                kd[2 * b + m] = *reinterpret_cast<const u32x4 *>(kbase + (long long)key * 64 + 32 * m + 8 * grp);
+        }
+        const long long vt = (long long)(k0 >> 6) * 4096 + 32 * ((k0 >> 5) & 1) + 8 * grp;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            vd[d] = *reinterpret_cast<const u32x4 *>(vbase + vt + (long long)(16 * d + i16) * 64);
+    };
+
+    f32x4 oh[QG][4], ol[QG][4];
+    float neg_ref[QG], m_ref[QG], l_run[QG];
+#pragma unroll
+    for (int gq = 0; gq < QG; ++gq) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) oh[gq][d] = f32x4{0.f, 0.f, 0.f, 0.f}, ol[gq][d] = oh[gq][d];
+        neg_ref[gq] = INFINITY, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
+    }
+    constexpr float kLazyLimit16 = 32768.0f;
+    const float kLoInv = 1.0f / kLoScale;
+    constexpr int kStride = 32 * kDecodeWaves;
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+    auto process = [&](int kk, const u32x4 *kf, const u32x4 *vf) {
+        const bool tail = kk + 32 > k_end;
+#pragma unroll
+        for (int gq = 0; gq < QG; ++gq) {
+            auto scores = [&](const f32x4 &init, f32x4 &s0, f32x4 &s1) {
+                f32x4 h0 = init, h1 = init, l0 = zero4, l1 = zero4;
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    h0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), qh[gq][m], h0, 0, 0, 0);
+                    l0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), ql[gq][m], l0, 0, 0, 0);
+                    h1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), qh[gq][m], h1, 0, 0, 0);
+                    l1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), ql[gq][m], l1, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s0[r] = h0[r] + l0[r] * kLoInv, s1[r] = h1[r] + l1[r] * kLoInv;
+                if (tail) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * grp + r;
+                        if (kk + 16 * (i >> 3) + (i & 7) >= k_end) s0[r] = -INFINITY;
+                        if (kk + 16 * (i >> 3) + 8 + (i & 7) >= k_end) s1[r] = -INFINITY;
+                    }
+                }
+            };
+            const f32x4 nr = {neg_ref[gq], neg_ref[gq], neg_ref[gq], neg_ref[gq]};
+            f32x4 s0, s1;
+            scores(nr, s0, s1);
+            float lsum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s0[r] = __builtin_amdgcn_exp2f(s0[r]);
+                s1[r] = __builtin_amdgcn_exp2f(s1[r]);
+                lsum += s0[r] + s1[r];
+            }
+            if (__any(!(lsum <= kLazyLimit16))) {
+                f32x4 t0, t1;
+                scores(zero4, t0, t1);
+                float mt = fmaxf(fmaxf(fmaxf(t0[0], t0[1]), fmaxf(t0[2], t0[3])),
+                                 fmaxf(fmaxf(t1[0], t1[1]), fmaxf(t1[2], t1[3])));
+                mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+                mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                const float m_new = fmaxf(m_ref[gq], mt);
+                const float alpha = __builtin_amdgcn_exp2f(m_ref[gq] - m_new);
+                l_run[gq] *= alpha;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) oh[gq][d] *= alpha, ol[gq][d] *= alpha;
+                neg_ref[gq] = -m_new;
+                m_ref[gq] = m_new;
+                lsum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    s0[r] = __builtin_amdgcn_exp2f(t0[r] - m_new);
+                    s1[r] = __builtin_amdgcn_exp2f(t1[r] - m_new);
+                    lsum += s0[r] + s1[r];
+                }
+            }
+            l_run[gq] += lsum;
+            float x[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[r] = s0[r], x[4 + r] = s1[r];
+            half8 ph, pl;
+            split8(x, ph, pl);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                oh[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), ph, oh[gq][d], 0, 0, 0);
+                ol[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), pl, ol[gq][d], 0, 0, 0);
+            }
+        }
+    };
+
+    // Two register sets in turn; loads past the range re-read the last
+    // block of the padded cache (cached rows, results unused).
+    u32x4 k_a[4], v_a[4], k_b[4], v_b[4];
+    const int last = n_pad - 32;
+    int k0 = k_begin + 32 * wave;
+    load(min(k0, last), k_a, v_a);
+    while (k0 < k_end) {
+        load(min(k0 + kStride, last), k_b, v_b);
+        process(k0, k_a, v_a);
+        k0 += kStride;
+        if (k0 >= k_end) break;
+        load(min(k0 + kStride, last), k_a, v_a);
+        process(k0, k_b, v_b);
+        k0 += kStride;
+    }
+
+    // Per-wave partials to LDS: lane (grp, i16) holds dims 16 d + 4 grp + r of query 16 gq + i16.
+#pragma unroll
+    for (int gq = 0; gq < QG; ++gq) {
+        float l = l_run[gq];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const int qi = 16 * gq + i16;
+        if (grp == 0) red_m[wave][qi] = m_ref[gq], red_l[wave][qi] = l;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            f32x4 v;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = oh[gq][d][r] + ol[gq][d][r] * kLoInv;
+            *reinterpret_cast<f32x4 *>(&red_o[wave][qi * kDecodeOStride + 16 * d + 4 * grp]) = v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < QG; ++j) {
+        const int qi = (threadIdx.x >> 4) + 16 * j, d = 4 * (threadIdx.x & 15);
+        if (qi >= p.q_rows) continue;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, red_m[w][qi]);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        float den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            const float wgt = __builtin_amdgcn_exp2f(red_m[w][qi] - mx);
+            acc += wgt * *reinterpret_cast<const f32x4 *>(&red_o[w][qi * kDecodeOStride + d]);
+            den += wgt * red_l[w][qi];
+        }
+        const f32x4 out = acc * (1.0f / den);
+        if constexpr (!SPLIT) {
+            const int b = pair / kHeads, head = pair - b * kHeads;
+            *reinterpret_cast<f32x4 *>(p.o + ((long long)b * p.q_rows + qi) * p.ldo + head * 64 + d) = out;
+        } else {
+            const long long row = ((long long)split * p.pairs + pair) * g.q_padded + qi;
+            *reinterpret_cast<f32x4 *>(p.partial + row * 64 + d) = out;
+            if (d == 0) p.partial[(long long)g.splits * p.pairs * g.q_padded * 64 + row] = mx + log2f(den);
+        }
+    }
+}
+
 // Merge of split partials by their log2-sum-exp, into tokens [b * q_rows +
 // row, head * 64 + d]. Partial outputs are [splits, pairs, q_padded, 64],
 // followed by the log2-sum-exps [splits, pairs, q_padded]. One wave per
@@ -907,14 +1115,15 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
 
 IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units, bool f16 = false) {
     IclLaunch g{};
-    if (q_rows <= kDecodeQueries && !f16) {
+    if (q_rows <= kDecodeQueries) {
         // One workgroup per (pair, key range), about two per CU, at least 256
-        // keys each; ranges in whole rounds of the waves' 16-key blocks.
+        // keys each; ranges in whole rounds of the waves' 16-key (FP16: 32-key) blocks.
         g.qtiles = 1;
         g.q_padded = kDecodeQueries;
         const int want = std::max(1, (int)ceil_div(2LL * compute_units, pairs));
         const int splits = std::max(1, std::min(want, kv_rows / 256));
-        const int per = (int)ceil_div(ceil_div(kv_rows, splits), 16 * kDecodeWaves) * 16 * kDecodeWaves;
+        const int round = (f16 ? 32 : 16) * kDecodeWaves;
+        const int per = (int)ceil_div(ceil_div(kv_rows, splits), round) * round;
         g.keys_per_split = per;
         g.splits = (int)ceil_div(kv_rows, per);
         g.per_xcd = 0;
@@ -1240,8 +1449,8 @@ int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units, 
 
 size_t icl_attention_partial_floats(int pairs, int q_rows, int splits, bool f16) {
     if (splits <= 1) return 0;
-    size_t q_padded = q_rows <= kDecodeQueries && !f16 ? (size_t)kDecodeQueries
-                                                       : ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
+    size_t q_padded = q_rows <= kDecodeQueries ? (size_t)kDecodeQueries
+                                                : ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
     return (size_t)splits * pairs * q_padded * 65;
 }
 
@@ -1265,7 +1474,20 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
         const double kv_bytes = f16 ? 2.0 * 64.0 * pairs * 2.0 * kv : 4.0 * 64.0 * pairs * 2.0 * kv;
         KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, kv_bytes + 4.0 * 64.0 * pairs * 2.0 * q);
-        if (f16) {
+        if (f16 && args.q_rows <= kDecodeQueries) {
+            const dim3 blocks((unsigned)((long long)args.pairs * g.splits)), threads(kDecodeWaves * 64);
+            if (args.q_rows <= 16) {
+                if (g.splits > 1)
+                    hipLaunchKernelGGL((icl_decode16_kernel<1, true>), blocks, threads, 0, stream, args, g);
+                else
+                    hipLaunchKernelGGL((icl_decode16_kernel<1, false>), blocks, threads, 0, stream, args, g);
+            } else {
+                if (g.splits > 1)
+                    hipLaunchKernelGGL((icl_decode16_kernel<2, true>), blocks, threads, 0, stream, args, g);
+                else
+                    hipLaunchKernelGGL((icl_decode16_kernel<2, false>), blocks, threads, 0, stream, args, g);
+            }
+        } else if (f16) {
             if (g.splits > 1)
                 hipLaunchKernelGGL((icl_attention_split_kernel<true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
                                    stream, args, g);

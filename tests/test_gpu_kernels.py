@@ -96,7 +96,7 @@ def test_icl_attention_split_fp16_matches_float64(device, rows):
     k = fast_values(pairs * rows * 64, 2).reshape(pairs, rows, 64)
     v = fast_values(pairs * rows * 64, 3).reshape(pairs, rows, 64)
     k16, v16 = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
-    for query_rows in (1, 5, 40, 64, 100, 300):
+    for query_rows in (1, 5, 16, 17, 32, 40, 64, 100, 300):
         q = fast_values(pairs * query_rows * 64, 1, scale=3.0).reshape(pairs, query_rows, 64)
         out = np.zeros_like(q)
         F = hip.fptr
