@@ -246,11 +246,11 @@ def bench_auto(executor, x, y, q, dx, gpu_logits, args) -> dict:
         "ms_per_step": 1000 * elapsed / args.steps,
         "build_ms": float(np.median(ms)),
         "attention": {
-            "kernel": "icl_attention_split_kernel (FP16 cache, queries and probabilities split hi + lo/2^11, "
-                      "32x32x16 FP16 MFMA)",
+            "kernel": "icl_attention_split_kernel (FP16 cache, queries and probabilities split hi + lo into one "
+                      "accumulator, 32x32x16 FP16 MFMA)",
             "avg_launch_ms": launch_ms,
             "algorithmic_tflops": flops / (launch_ms * 1e-3) / 1e12,
-            # Four FP16 products per FP32-equivalent product pair (hi and lo of Q, of P).
+            # Two FP16 products (hi and lo of Q, of P) per FP32-equivalent product.
             "fp16_mfma_frac": 2 * flops / (launch_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
         },
         "small_pass_hbm": {"kernel": "icl_decode16_kernel (FP16 cache, 16x16x32 FP16 MFMA)", "by_pass_rows": small},

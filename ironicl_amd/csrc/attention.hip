@@ -346,10 +346,10 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
 // zero past the keys) and V tile-transposed as FP16 [pairs, Np / 64, 64
 // dims, 64 keys], the keys of each 16-key group stored in the order 0..3,
 // 8..11, 4..7, 12..15. Queries and probabilities, FP32, are split into a high
-// FP16 part and a low part scaled by 2^11 (x = hi + lo / 2048, about 22
-// significant bits); each product is hi.K + lo.K / 2048 on the 32x32x16 FP16
-// MFMA with separate accumulators, so only the cache's own FP16 rounding
-// remains. Layouts per tile (64 keys, 4 waves x 64 queries as above):
+// FP16 part and the FP16 remainder (x = hi + lo, about 22 significant bits);
+// each product is hi.K + lo.K on the 32x32x16 FP16 MFMA, both into one FP32
+// accumulator, so only the cache's own FP16 rounding remains. Layouts per
+// tile (64 keys, 4 waves x 64 queries as above):
 //   S^T (key x query): A = K[key = lane % 32 (+32)][dims 16 m + 8 (lane / 32)
 //     .. +7], B = the lane's query, same dims; result register r is key
 //     8 (r / 4) + 4 (lane / 32) + r % 4 (+32), query lane % 32 (+32 j);
@@ -362,7 +362,6 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
 // reference's limit here), so their high parts fit FP16.
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-constexpr float kLoScale = 2048.0f;
 
 struct IclTile16 {
     u32x4 k[kKeyTile * 8];  // 64 rows x 8 chunks of 16 bytes
@@ -371,14 +370,17 @@ struct IclTile16 {
 
 __device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
-// Eight FP32 values split into high and scaled low FP16 parts.
+// Eight FP32 values split into high and low FP16 parts, x = hi + lo. The low
+// part is not rescaled: both products accumulate into one FP32 accumulator,
+// and a low part below FP16's normal range (only for |x| < 2^-3) loses bits
+// worth less than 2^-24 |x|.
 __device__ __forceinline__ void split8(const float *x, half8 &hi, half8 &lo) {
     u32x4 h, l;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const auto hp = __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]);
-        const float r0 = (x[2 * i] - (float)hp[0]) * kLoScale;
-        const float r1 = (x[2 * i + 1] - (float)hp[1]) * kLoScale;
+        const float r0 = x[2 * i] - (float)hp[0];
+        const float r1 = x[2 * i + 1] - (float)hp[1];
         const auto lp = __builtin_amdgcn_cvt_pkrtz(r0, r1);
         h[i] = __builtin_bit_cast(unsigned, hp);
         l[i] = __builtin_bit_cast(unsigned, lp);
@@ -458,19 +460,18 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
     // LDS chunk index of row `row`, chunk c.
     auto at = [](int row, int c) { return row * 8 + (c ^ (row & 7)); };
 
-    f32x16 oh[2][2], ol[2][2];  // [dim block][query block]
+    f32x16 o[2][2];  // [dim block][query block]
 #pragma unroll
     for (int d = 0; d < 2; ++d)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) oh[d][j][r] = 0.f, ol[d][j][r] = 0.f;
+            for (int r = 0; r < 16; ++r) o[d][j][r] = 0.f;
     float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     f32x16 neg_ref[2], zero;
 #pragma unroll
     for (int r = 0; r < 16; ++r) neg_ref[0][r] = INFINITY, neg_ref[1][r] = INFINITY, zero[r] = 0.f;
     constexpr float kLazyLimit16 = 32768.0f;  // 2^15: probabilities stay FP16-representable
-    const float kLoInv = 1.0f / kLoScale;
 
     issue_tile(k_begin, 0);
     int buf = 0;
@@ -483,18 +484,16 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
 
         // Scores of this tile against both query blocks, from the FP16 keys.
         auto scores = [&](int j, const f32x16 &init, f32x16 &s0, f32x16 &s1) {
-            f32x16 h0 = init, h1 = init, l0 = zero, l1 = zero;
+            s0 = init, s1 = init;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const half8 a0 = as_half8(kt[at(r32, 2 * m + half)]);
                 const half8 a1 = as_half8(kt[at(r32 + 32, 2 * m + half)]);
-                h0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qh[j][m], h0, 0, 0, 0);
-                h1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qh[j][m], h1, 0, 0, 0);
-                l0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, ql[j][m], l0, 0, 0, 0);
-                l1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ql[j][m], l1, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qh[j][m], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qh[j][m], s1, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, ql[j][m], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ql[j][m], s1, 0, 0, 0);
             }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s0[r] = h0[r] + l0[r] * kLoInv, s1[r] = h1[r] + l1[r] * kLoInv;
             if (k0 + kKeyTile > k_end) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -528,8 +527,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
                 lsum = 0.f;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    oh[0][j][r] *= alpha, oh[1][j][r] *= alpha;
-                    ol[0][j][r] *= alpha, ol[1][j][r] *= alpha;
+                    o[0][j][r] *= alpha, o[1][j][r] *= alpha;
                     neg_ref[j][r] = -m_new;
                     s[j][0][r] = __builtin_amdgcn_exp2f(t0[r] - m_new);
                     s[j][1][r] = __builtin_amdgcn_exp2f(t1[r] - m_new);
@@ -556,8 +554,8 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
                 const half8 a = as_half8(vt[at(32 * d + r32, 2 * t + half)]);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    oh[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph[j], oh[d][j], 0, 0, 0);
-                    ol[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[j], ol[d][j], 0, 0, 0);
+                    o[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph[j], o[d][j], 0, 0, 0);
+                    o[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[j], o[d][j], 0, 0, 0);
                 }
             }
         }
@@ -586,7 +584,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
             for (int a = 0; a < 4; ++a) {
                 f32x4 v;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = (oh[d][j][4 * a + e] + ol[d][j][4 * a + e] * kLoInv) * inv;
+                for (int e = 0; e < 4; ++e) v[e] = o[d][j][4 * a + e] * inv;
                 *reinterpret_cast<f32x4 *>(dst + 32 * d + 8 * a + 4 * half) = v;
             }
     }
@@ -844,7 +842,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
 
 // Few queries over the FP16 cache (optimize="auto"): as icl_decode_kernel,
 // HBM-bound, now on half the bytes. Blocks of 32 keys on the 16x16x32 FP16
-// MFMA, queries and probabilities split hi + lo / 2^11 as in the split kernel:
+// MFMA, queries and probabilities split hi + lo as in the split kernel:
 //   S^T block b (16 rows x 16 queries, 32 dims per product): row i is key
 //     16 (i / 8) + 8 b + i % 8 of the block, A = K[that key][dims 32 m +
 //     8 (lane / 16) .. +7], B = the lane's query; result register r of lane
@@ -907,16 +905,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
             vd[d] = *reinterpret_cast<const u32x4 *>(vbase + vt + (long long)(16 * d + i16) * 64);
     };
 
-    f32x4 oh[QG][4], ol[QG][4];
+    f32x4 o[QG][4];
     float neg_ref[QG], m_ref[QG], l_run[QG];
 #pragma unroll
     for (int gq = 0; gq < QG; ++gq) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) oh[gq][d] = f32x4{0.f, 0.f, 0.f, 0.f}, ol[gq][d] = oh[gq][d];
+        for (int d = 0; d < 4; ++d) o[gq][d] = f32x4{0.f, 0.f, 0.f, 0.f};
         neg_ref[gq] = INFINITY, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
     }
     constexpr float kLazyLimit16 = 32768.0f;
-    const float kLoInv = 1.0f / kLoScale;
     constexpr int kStride = 32 * kDecodeWaves;
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
@@ -925,16 +922,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
 #pragma unroll
         for (int gq = 0; gq < QG; ++gq) {
             auto scores = [&](const f32x4 &init, f32x4 &s0, f32x4 &s1) {
-                f32x4 h0 = init, h1 = init, l0 = zero4, l1 = zero4;
+                s0 = init, s1 = init;
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
-                    h0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), qh[gq][m], h0, 0, 0, 0);
-                    l0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), ql[gq][m], l0, 0, 0, 0);
-                    h1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), qh[gq][m], h1, 0, 0, 0);
-                    l1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), ql[gq][m], l1, 0, 0, 0);
+                    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), qh[gq][m], s0, 0, 0, 0);
+                    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), ql[gq][m], s0, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), qh[gq][m], s1, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), ql[gq][m], s1, 0, 0, 0);
                 }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) s0[r] = h0[r] + l0[r] * kLoInv, s1[r] = h1[r] + l1[r] * kLoInv;
                 if (tail) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -965,7 +960,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
                 const float alpha = __builtin_amdgcn_exp2f(m_ref[gq] - m_new);
                 l_run[gq] *= alpha;
 #pragma unroll
-                for (int d = 0; d < 4; ++d) oh[gq][d] *= alpha, ol[gq][d] *= alpha;
+                for (int d = 0; d < 4; ++d) o[gq][d] *= alpha;
                 neg_ref[gq] = -m_new;
                 m_ref[gq] = m_new;
                 lsum = 0.f;
@@ -984,8 +979,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
             split8(x, ph, pl);
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                oh[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), ph, oh[gq][d], 0, 0, 0);
-                ol[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), pl, ol[gq][d], 0, 0, 0);
+                o[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), ph, o[gq][d], 0, 0, 0);
+                o[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), pl, o[gq][d], 0, 0, 0);
             }
         }
     };
@@ -1018,7 +1013,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
         for (int d = 0; d < 4; ++d) {
             f32x4 v;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = oh[gq][d][r] + ol[gq][d][r] * kLoInv;
+            for (int r = 0; r < 4; ++r) v[r] = o[gq][d][r];
             *reinterpret_cast<f32x4 *>(&red_o[wave][qi * kDecodeOStride + 16 * d + 4 * grp]) = v;
         }
     }
