@@ -294,6 +294,16 @@ int irx_test_icl_attention_precision(irx_device *device, int precision, const fl
 int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1,
                       const float *w2, const float *b2, size_t rows, size_t width, size_t depth,
                       size_t width2, float *first, float *second);
+/* The post-attention half of a 128-wide block (cpu.rs:1555-1601) on `rows`
+ * rows: s1 = state + (att wo^T + bo); out = s1 + (gelu(LN2(s1) w1^T + b1) w2^T + b2),
+ * LN2 with n2w / n2b. fused = 1 runs the one-kernel tail, 0 the separate
+ * products and LayerNorm. wo [128,128], w1 [256,128], w2 [128,256]. With
+ * repeats > 1 the tail is applied again repeats - 1 times after `out` is
+ * read (for timing with irx_profile_read). */
+int irx_test_block_tail(irx_device *device, int fused, const float *att, const float *state, size_t rows,
+                        const float *wo, const float *bo, const float *n2w, const float *n2b,
+                        const float *w1, const float *b1, const float *w2, const float *b2,
+                        size_t repeats, float *out);
 /* LayerNorm over width (128 or 512), eps 1e-5. */
 int irx_test_layer_norm(irx_device *device, const float *x, const float *weight, const float *bias,
                         size_t rows, size_t width, float *out);

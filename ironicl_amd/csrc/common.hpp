@@ -124,6 +124,23 @@ struct GemmArgs {
 // C = epilogue(A W^T + bias) on FP32 MFMA. K must be a multiple of 64.
 void gemm(const GemmArgs &args, hipStream_t stream);
 
+// Post-attention half of a 128-wide block in one kernel (cpu.rs:1555-1601):
+// s1 = state + (att Wo^T + bo); state = s1 + (gelu(LN2(s1) W1^T + b1) W2^T + b2).
+// `pack` holds Wo [128,128], W1 [256,128] and W2 [128,256] as packed by
+// tail128_pack (host code, kTail128PackFloats floats).
+constexpr size_t kTail128PackFloats = 10 * 8192;
+struct Tail128 {
+    const float *att;  // [m, 128], row stride lda
+    long long lda;
+    float *state;      // [m, 128], row stride ldx, updated in place
+    long long ldx;
+    const float *pack;
+    const float *bo, *n2w, *n2b, *b1, *b2;  // all [128] or [256]; bias-free LayerNorms pass zeros
+    long long m;
+};
+void tail128_pack(const float *wo, const float *w1, const float *w2, float *out);
+void tail128(const Tail128 &t, hipStream_t stream);
+
 // LayerNorm over `width` (128 or 512), eps 1e-5, two passes (reference.rs:223-252).
 void layer_norm(const float *x, long long ldx, const float *weight, const float *bias, float *y,
                 long long ldy, long long rows, int width, hipStream_t stream);

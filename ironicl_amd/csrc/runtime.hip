@@ -205,6 +205,7 @@ struct BlockW {
     Lin out, l1, l2;
     bool qass = false;
     Lin qm0, qm2;  // QASS query MLP, per head: hd -> 64 -> hd
+    const float *tail_pack = nullptr;  // 128-wide blocks: out, linear1, linear2 packed for tail128
 };
 
 struct irx_weights {
@@ -283,8 +284,23 @@ struct Stages {
 
     // Post-attention half of a block: out-projection + residual into `state`,
     // then LN2, FFN (GELU) and residual (cpu.rs:1555-1601).
-    void tail(const BlockW &bw, float *state, long long m, const float *att, float *norm, float *hid) const {
+    // A 128-wide block's tail runs fused (tail128) once its rows fill the
+    // chip: one wave carries 16 rows through the whole chain, so with fewer
+    // than 16384 rows (256 workgroups) the four separate launches, which
+    // spread each product over every CU, finish first. fused: -1 chooses,
+    // 0 / 1 force.
+    void tail(const BlockW &bw, float *state, long long m, const float *att, float *norm, float *hid,
+              int fused = -1) const {
         const int d = bw.dim;
+        const bool use_fused = fused < 0 ? (d == 128 && bw.tail_pack && m >= 16384) : fused == 1;
+        if (use_fused) {
+            if (d != 128 || !bw.tail_pack) fail(IRX_INVALID_ARGUMENT, "the fused tail needs a packed 128-wide block");
+            Tail128 t{};
+            t.att = att, t.lda = d, t.state = state, t.ldx = d, t.pack = bw.tail_pack, t.m = m;
+            t.bo = bw.out.b, t.n2w = bw.n2w, t.n2b = bw.n2b, t.b1 = bw.l1.b, t.b2 = bw.l2.b;
+            tail128(t, s);
+            return;
+        }
         linear(att, d, m, d, bw.out.w, bw.out.b, d, state, d, kEpiResidual, state, d);
         layer_norm(state, d, bw.n2w, bw.n2b, norm, d, m, d, s);
         linear(norm, d, m, d, bw.l1.w, bw.l1.b, 2 * d, hid, 2 * d, kEpiGelu);
@@ -446,6 +462,21 @@ struct Loader {
         pending.push_back({slot, offset});
     }
 
+    size_t offset_of(const float **slot) const {
+        for (const Pending &p : pending)
+            if (p.slot == slot) return p.offset;
+        fail(IRX_INVALID_ARGUMENT, "model tensor not loaded");
+    }
+
+    // Out-projection and FFN weights of a 128-wide block in tail128's fragment order.
+    void pack_tail(BlockW &b) {
+        const size_t wo = offset_of(&b.out.w), w1 = offset_of(&b.l1.w), w2 = offset_of(&b.l2.w);
+        const size_t offset = (host.size() + 63) / 64 * 64;
+        host.resize(offset + kTail128PackFloats, 0.f);
+        tail128_pack(host.data() + wo, host.data() + w1, host.data() + w2, host.data() + offset);
+        pending.push_back({&b.tail_pack, offset});
+    }
+
     void block(BlockW &b, const std::string &prefix, int dim, bool qass) {
         const bool zb = task == IRX_TASK_REGRESSOR;  // bias-free LayerNorms (model.rs:273-280)
         b.dim = dim, b.qass = qass;
@@ -465,6 +496,7 @@ struct Loader {
         t(".norm1.bias", d, &b.n1b, zb);
         t(".norm2.weight", d, &b.n2w);
         t(".norm2.bias", d, &b.n2b, zb);
+        if (dim == 128) pack_tail(b);
         if (qass) {
             const size_t hd = d / kHeads;
             t(".attn.ssmax_layer.query_mlp.0.weight", 64 * hd, &b.qm0.w);
@@ -1369,6 +1401,42 @@ int irx_test_products(irx_device *device, const float *x, const float *w1, const
         IRX_HIP(hipDeviceSynchronize());
         IRX_HIP(hipMemcpy(first, d1.p, rows * width * 4, hipMemcpyDeviceToHost));
         IRX_HIP(hipMemcpy(second, d2.p, rows * width2 * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+int irx_test_block_tail(irx_device *device, int fused, const float *att, const float *state, size_t rows,
+                        const float *wo, const float *bo, const float *n2w, const float *n2b, const float *w1,
+                        const float *b1, const float *w2, const float *b2, size_t repeats, float *out) {
+    return guarded("irx_test_block_tail", [&] {
+        if (!device || !att || !state || !wo || !bo || !n2w || !n2b || !w1 || !b1 || !w2 || !b2 || !out || !rows ||
+            (fused != 0 && fused != 1) || !repeats)
+            fail(IRX_INVALID_ARGUMENT, "block tail arguments do not match");
+        set_device(device);
+        const size_t n = rows * 128;
+        std::vector<float> host;
+        const size_t sizes[] = {128 * 128, 128, 128, 128, 256 * 128, 256, 128 * 256, 128, kTail128PackFloats};
+        const float *srcs[] = {wo, bo, n2w, n2b, w1, b1, w2, b2, nullptr};
+        size_t offs[9], total = 0;
+        for (int i = 0; i < 9; ++i) offs[i] = total, total += (sizes[i] + 63) / 64 * 64;
+        host.assign(total, 0.f);
+        for (int i = 0; i < 8; ++i) std::memcpy(host.data() + offs[i], srcs[i], sizes[i] * 4);
+        tail128_pack(wo, w1, w2, host.data() + offs[8]);
+        DevBuf dw(total * 4), datt(n * 4), dstate(n * 4), dnorm(n * 4), dhid(2 * n * 4);
+        IRX_HIP(hipMemcpy(dw.p, host.data(), total * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(datt.p, att, n * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dstate.p, state, n * 4, hipMemcpyHostToDevice));
+        BlockW bw{};
+        const float *f = dw.f();
+        bw.dim = 128, bw.out = {f + offs[0], f + offs[1]}, bw.n2w = f + offs[2], bw.n2b = f + offs[3];
+        bw.l1 = {f + offs[4], f + offs[5]}, bw.l2 = {f + offs[6], f + offs[7]}, bw.tail_pack = f + offs[8];
+        irx_weights none;
+        Stages st{none, nullptr, device->compute_units};
+        st.tail(bw, dstate.f(), (long long)rows, datt.f(), dnorm.f(), dhid.f(), fused);
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(out, dstate.p, n * 4, hipMemcpyDeviceToHost));
+        // Further applications (timing only) update the same state.
+        for (size_t i = 1; i < repeats; ++i) st.tail(bw, dstate.f(), (long long)rows, datt.f(), dnorm.f(), dhid.f(), fused);
+        IRX_HIP(hipDeviceSynchronize());
     });
 }
 

@@ -1,0 +1,231 @@
+// Fused tail of a 128-wide transformer block on gfx950 matrix cores.
+//
+// The post-attention half of every column and row block (cpu.rs:1555-1601):
+//   s1    = state + (att Wo^T + bo)
+//   state = s1 + (gelu(LN2(s1) W1^T + b1) W2^T + b2)
+// as one kernel instead of four launches (out-projection, LayerNorm, FFN up,
+// FFN down), so s1, LN2(s1) and the 256-wide hidden layer never leave
+// registers.
+//
+// Each wave owns 16 rows for the whole chain. Products are computed
+// transposed, D = W X^T, on v_mfma_f32_16x16x4f32: the weights are the A
+// operand and the rows the B operand. In D, lane (m, g) = (lane % 16,
+// lane / 16) holds row m's features 16 b + 4 g + r in register r of block b,
+// which is exactly what the next product's B operand needs at step r of
+// k-block b, so the chain runs without moving data between lanes. The same
+// per-lane layout is used to load att and state and to store the result.
+//
+// The weights are packed once (tail128_pack) into A-operand fragments, 1 KB
+// per 16 x 16 block, lane after lane, in the order the kernel consumes them:
+// ten 32 KB chunks (Wo in two, then per 32-unit slice of the hidden layer the
+// W1 rows and W2 columns it touches). A workgroup streams the chunks through
+// two LDS buffers with direct global -> LDS loads; every LDS read is one
+// 16-byte read per lane of consecutive addresses (no bank conflicts).
+#include "common.hpp"
+
+namespace irx {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kChunkFloats = 8192;  // 32 KB
+constexpr int kChunks = 10;
+constexpr int kTailWaves = 4;
+constexpr int kTailRows = 16 * kTailWaves;  // rows per workgroup
+
+__device__ __forceinline__ void wait_vm() {
+    // vmcnt(0); expcnt and lgkmcnt left at their maxima (no wait).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+__device__ __forceinline__ f32x4 mfma(float a, float b, const f32x4 &acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 lds4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+
+__global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
+    __shared__ __attribute__((aligned(16))) float buf[2][kChunkFloats];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
+    const long long row = (long long)blockIdx.x * kTailRows + wv * 16 + m16;
+    const bool live = row < p.m;
+    const long long r = live ? row : p.m - 1;
+
+    // Wave w moves 1 KB blocks 8 w .. 8 w + 7 of each chunk.
+    auto issue = [&](int chunk, int b) {
+        const float *src = p.pack + (long long)chunk * kChunkFloats + (8 * wv) * 256 + lane * 4;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_global_load_lds(src + i * 256, (lds_void *)&buf[b][(8 * wv + i) * 256], 16, 0, 0);
+    };
+    issue(0, 0);
+
+    // x: row m's features 16 kb + 4 g + e (att now, LN2(s1) later).
+    f32x4 x[8], s1[8], acc[8];
+    const float *att = p.att + r * p.lda + 4 * g;
+    const float *st = p.state + r * p.ldx + 4 * g;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(att + 16 * b);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) s1[b] = *reinterpret_cast<const f32x4 *>(st + 16 * b);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Out-projection: chunks 0 and 1 hold k-blocks 4c .. 4c + 3, each with
+    // the eight output blocks' fragments. The fragments of the next k-block
+    // are read while the current one's 32 products (8 independent
+    // accumulators) run.
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        wait_vm();
+        __syncthreads();
+        issue(c + 1, (c + 1) & 1);
+        const float *frag = &buf[c & 1][lane * 4];
+        f32x4 fa[2][8];
+#pragma unroll
+        for (int ob = 0; ob < 8; ++ob) fa[0][ob] = lds4(frag + ob * 256);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            if (kb < 3) {
+#pragma unroll
+                for (int ob = 0; ob < 8; ++ob) fa[(kb + 1) & 1][ob] = lds4(frag + ((kb + 1) * 8 + ob) * 256);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(fa[kb & 1][ob][e], x[4 * c + kb][e], acc[ob]);
+        }
+    }
+
+    // s1 = state + (acc + bo), then LN2 over the row's 128 features, held by
+    // lanes m, m + 16, m + 32, m + 48.
+    float sum = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 bo = *reinterpret_cast<const f32x4 *>(p.bo + 16 * b + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            s1[b][e] = s1[b][e] + (acc[b][e] + bo[e]);
+            sum += s1[b][e];
+        }
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float mean = sum / 128.f;
+    float sq = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float d = s1[b][e] - mean;
+            sq = fmaf(d, d, sq);
+        }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 w = *reinterpret_cast<const f32x4 *>(p.n2w + 16 * b + 4 * g);
+        const f32x4 bb = *reinterpret_cast<const f32x4 *>(p.n2b + 16 * b + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[b][e] = (s1[b][e] - mean) * rstd * w[e] + bb[e];
+        acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // FFN, 32 hidden units per chunk: h = gelu(W1 x + b1) for units 32 c + 16 hb
+    // + 4 g + e (even and odd k-blocks in separate accumulators, four
+    // independent chains), then acc += W2 h.
+#pragma unroll 1
+    for (int c = 0; c < 8; ++c) {
+        wait_vm();
+        __syncthreads();
+        if (c + 3 < kChunks) issue(c + 3, (c + 3) & 1);
+        const float *frag = &buf[c & 1][lane * 4];
+        f32x4 h[2][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i >> 1][i & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 fw[2][2];
+        fw[0][0] = lds4(frag), fw[0][1] = lds4(frag + 256);
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            if (kb < 7) {
+                fw[(kb + 1) & 1][0] = lds4(frag + ((kb + 1) * 2) * 256);
+                fw[(kb + 1) & 1][1] = lds4(frag + ((kb + 1) * 2 + 1) * 256);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) h[hb][kb & 1] = mfma(fw[kb & 1][hb][e], x[kb][e], h[hb][kb & 1]);
+        }
+        f32x4 f2[2][8];
+#pragma unroll
+        for (int ob = 0; ob < 8; ++ob) f2[0][ob] = lds4(frag + 4096 + ob * 256);
+        f32x4 hg[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const f32x4 b1 = *reinterpret_cast<const f32x4 *>(p.b1 + 32 * c + 16 * hb + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hg[hb][e] = gelu_erf((h[hb][0][e] + h[hb][1][e]) + b1[e]);
+        }
+#pragma unroll
+        for (int ob = 0; ob < 8; ++ob) f2[1][ob] = lds4(frag + 4096 + (8 + ob) * 256);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(f2[j][ob][e], hg[j][e], acc[ob]);
+    }
+
+    if (!live) return;
+    float *out = p.state + row * p.ldx + 4 * g;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 b2 = *reinterpret_cast<const f32x4 *>(p.b2 + 16 * b + 4 * g);
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (acc[b][e] + b2[e]) + s1[b][e];
+        *reinterpret_cast<f32x4 *>(out + 16 * b) = v;
+    }
+}
+
+}  // namespace
+
+void tail128_pack(const float *wo, const float *w1, const float *w2, float *out) {
+    // Fragment (rows r0.., columns c0..) of a row-major [.., ld] matrix:
+    // lane (n, g) = (l % 16, l / 16) holds W[r0 + n][c0 + 4 g .. c0 + 4 g + 3].
+    auto fragment = [](const float *w, int ld, int r0, int c0, float *dst) {
+        for (int l = 0; l < 64; ++l)
+            for (int e = 0; e < 4; ++e) dst[l * 4 + e] = w[(long long)(r0 + (l & 15)) * ld + c0 + 4 * (l >> 4) + e];
+    };
+    for (int c = 0; c < 2; ++c)
+        for (int kb = 0; kb < 4; ++kb)
+            for (int ob = 0; ob < 8; ++ob)
+                fragment(wo, 128, 16 * ob, 16 * (4 * c + kb), out + c * kChunkFloats + (kb * 8 + ob) * 256);
+    for (int c = 0; c < 8; ++c) {
+        float *chunk = out + (2 + c) * kChunkFloats;
+        for (int kb = 0; kb < 8; ++kb)
+            for (int hb = 0; hb < 2; ++hb) fragment(w1, 128, 32 * c + 16 * hb, 16 * kb, chunk + (kb * 2 + hb) * 256);
+        for (int j = 0; j < 2; ++j)
+            for (int ob = 0; ob < 8; ++ob) fragment(w2, 256, 16 * ob, 32 * c + 16 * j, chunk + 4096 + (j * 8 + ob) * 256);
+    }
+}
+
+void tail128(const Tail128 &t, hipStream_t stream) {
+    if (t.m <= 0) return;
+    if (!t.att || !t.state || !t.pack || !t.bo || !t.n2w || !t.n2b || !t.b1 || !t.b2)
+        fail(3, "tail128: missing tensor");
+    if ((t.lda & 3) || (t.ldx & 3) || (reinterpret_cast<uintptr_t>(t.att) & 15) ||
+        (reinterpret_cast<uintptr_t>(t.state) & 15) || (reinterpret_cast<uintptr_t>(t.pack) & 15))
+        fail(3, "tail128: rows must be 16-byte aligned");
+    const double m = (double)t.m;
+    // Products 2 m (128*128 + 2 * 128*256); bytes: att and state in, state out, weights.
+    KernelTimer timer(kFamGemm, stream, m * 2.0 * (128.0 * 128 + 2 * 128.0 * 256), m * 128 * 4 * 3.0 + kTail128PackFloats * 4.0);
+    hipLaunchKernelGGL(tail128_kernel, dim3((unsigned)ceil_div(t.m, (long long)kTailRows)), dim3(256), 0, stream, t);
+    IRX_HIP(hipGetLastError());
+}
+
+}  // namespace irx

@@ -146,6 +146,33 @@ def test_icl_attention_peaked_scores(device, qr):
         assert np.abs(out[pair] - want).max() < 1e-5
 
 
+def block_tail64(att, state, wo, bo, n2w, n2b, w1, b1, w2, b2):
+    """cpu.rs:1555-1601 in float64: out-projection + residual, LN2, FFN + residual."""
+    s1 = state.astype(np.float64) + (att.astype(np.float64) @ wo.astype(np.float64).T + bo)
+    x = (s1 - s1.mean(1, keepdims=True)) / np.sqrt(s1.var(1, keepdims=True) + 1e-5) * n2w + n2b
+    h = gelu64(x @ w1.astype(np.float64).T + b1)
+    return s1 + (h @ w2.astype(np.float64).T + b2)
+
+
+@pytest.mark.parametrize("rows", [1, 17, 64, 65, 1000, 16411])
+@pytest.mark.parametrize("fused", [0, 1])
+def test_block_tail_matches_float64(device, rows, fused):
+    att = fast_values(rows * 128, 1, 2.0)
+    state = fast_values(rows * 128, 2, 3.0)
+    wo, bo = fast_values(128 * 128, 3, 0.09), fast_values(128, 4, 0.1)
+    n2w, n2b = fast_values(128, 5, 0.2) + 1.0, fast_values(128, 6, 0.1)
+    w1, b1 = fast_values(256 * 128, 7, 0.09), fast_values(256, 8, 0.1)
+    w2, b2 = fast_values(128 * 256, 9, 0.06), fast_values(128, 10, 0.1)
+    out = np.zeros_like(state)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_block_tail(device.handle, fused, F(att), F(state), rows, F(wo), F(bo), F(n2w),
+                                            F(n2b), F(w1), F(b1), F(w2), F(b2), 1, F(out)))
+    want = block_tail64(att.reshape(rows, 128), state.reshape(rows, 128), wo.reshape(128, 128), bo, n2w, n2b,
+                        w1.reshape(256, 128), b1, w2.reshape(128, 256), b2)
+    np.testing.assert_allclose(out.reshape(rows, 128), want, rtol=1e-4, atol=1e-5)
+    assert np.abs(out.reshape(rows, 128) - want).max() < 2e-5
+
+
 @pytest.mark.parametrize("rows,width", [(1, 128), (333, 128), (1000, 512), (4, 512)])
 def test_layer_norm_matches_float64(device, rows, width):
     x = fast_values(rows * width, 4, 3.0) + 0.5
