@@ -185,10 +185,11 @@ int irx_predictor_streamed(const irx_predictor *predictor);
 size_t irx_predictor_pass_rows(const irx_predictor *predictor);
 /* Sets the query rows per pass (a multiple of 32, at least 32). */
 int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows);
-/* Streams the passes of a prediction alternate between: 2 (the default) lets
- * one pass's short launches overlap the other pass's work; 1 runs every pass
- * in order on one stream. Results are identical either way. No counterpart in
- * the reference (its predictor runs passes in order, predictor.rs:224-271). */
+/* Streams (1 to 4) the passes of a prediction rotate over: more than one lets
+ * one pass's short launches overlap another pass's work (2 is the default); 1
+ * runs every pass in order on one stream. Each stream has its own workspace.
+ * Results are identical either way. No counterpart in the reference (its
+ * predictor runs passes in order, predictor.rs:224-271). */
 int irx_predictor_set_streams(irx_predictor *predictor, int streams);
 /* Copies floats [offset, offset + floats) of one resident context tensor to
  * host memory, after every pass issued before the call. `tensor` indexes the

@@ -234,6 +234,9 @@ struct irx_built_cache {
     DevBuf icl[kIclBlocks];
 };
 
+// Most HIP streams a predictor's passes rotate over (GPU_MAX_HW_QUEUES is 4).
+constexpr int kMaxPassStreams = 4;
+
 struct irx_predictor {
     irx_weights *weights = nullptr;
     irx_shape shape{};
@@ -244,13 +247,15 @@ struct irx_predictor {
     DevBuf base_scales;   // [12, 512]
     DevBuf rope_cos, rope_sin;
     hipStream_t stream = nullptr;
-    // Passes alternate between two streams, each with its own workspace, so
-    // that one pass's short launches overlap the other's.
-    hipStream_t side_stream = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
+    // Passes rotate over `streams` HIP streams (the main one, then side[0..]),
+    // each with its own workspace, so that one pass's short launches overlap
+    // another's long ones.
+    hipStream_t side[kMaxPassStreams - 1] = {};
+    hipEvent_t fork = nullptr, join[kMaxPassStreams - 1] = {};
     int streams = 2;
     std::mutex mu;
-    Arena ws, side_ws;
+    Arena ws[kMaxPassStreams];
+    hipStream_t lane(int slot) const { return slot ? side[slot - 1] : stream; }
     size_t ws_rows = 0;
 };
 
@@ -860,9 +865,9 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     const irx_shape &sh = P->shape;
     const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
     const int width = (int)sh.outputs;
-    hipStream_t s = slot ? P->side_stream : P->stream;
+    hipStream_t s = P->lane(slot);
     Stages st{W, s, W.device->compute_units};
-    Arena &ws = slot ? P->side_ws : P->ws;
+    Arena &ws = P->ws[slot];
     ws.used = 0;
     const bool f16 = P->precision == IRX_PRECISION_SPLIT;
     const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus, f16);
@@ -908,13 +913,21 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
 }
 
 void ensure_workspace(irx_predictor *P) {
-    if (P->ws_rows == P->pass_rows && P->ws.buf.p && P->side_ws.buf.p) return;
-    if (P->stream) IRX_HIP(hipStreamSynchronize(P->stream));
-    if (P->side_stream) IRX_HIP(hipStreamSynchronize(P->side_stream));
+    bool ready = P->ws_rows == P->pass_rows;
+    for (int i = 0; i < P->streams; ++i) ready = ready && P->ws[i].buf.p;
+    if (ready) return;
+    for (int i = 0; i < kMaxPassStreams; ++i)
+        if (P->lane(i)) IRX_HIP(hipStreamSynchronize(P->lane(i)));
     size_t floats = predict_ws_floats(P->shape, P->pass_rows, P->weights->device->compute_units,
                                       P->precision == IRX_PRECISION_SPLIT);
-    P->ws.buf.alloc(floats * 4);
-    P->side_ws.buf.alloc(floats * 4);
+    // Workspaces of streams in use, at the current pass size; the others are released.
+    for (int i = 0; i < kMaxPassStreams; ++i) {
+        if (i < P->streams) {
+            if (!P->ws[i].buf.p || P->ws_rows != P->pass_rows) P->ws[i].buf.alloc(floats * 4);
+        } else {
+            P->ws[i].buf = DevBuf();
+        }
+    }
     P->ws_rows = P->pass_rows;
 }
 
@@ -1152,9 +1165,11 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         IRX_HIP(hipMemcpy(P->rope_cos.p, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(P->rope_sin.p, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
-        IRX_HIP(hipStreamCreateWithFlags(&P->side_stream, hipStreamNonBlocking));
+        for (int i = 0; i < kMaxPassStreams - 1; ++i) {
+            IRX_HIP(hipStreamCreateWithFlags(&P->side[i], hipStreamNonBlocking));
+            IRX_HIP(hipEventCreateWithFlags(&P->join[i], hipEventDisableTiming));
+        }
         IRX_HIP(hipEventCreateWithFlags(&P->fork, hipEventDisableTiming));
-        IRX_HIP(hipEventCreateWithFlags(&P->join, hipEventDisableTiming));
         ensure_workspace(P);
         *out = P;
         P = nullptr;
@@ -1172,12 +1187,14 @@ void irx_predictor_free(irx_predictor *predictor) {
         (void)hipStreamSynchronize(predictor->stream);
         (void)hipStreamDestroy(predictor->stream);
     }
-    if (predictor->side_stream) {
-        (void)hipStreamSynchronize(predictor->side_stream);
-        (void)hipStreamDestroy(predictor->side_stream);
+    for (int i = 0; i < kMaxPassStreams - 1; ++i) {
+        if (predictor->side[i]) {
+            (void)hipStreamSynchronize(predictor->side[i]);
+            (void)hipStreamDestroy(predictor->side[i]);
+        }
+        if (predictor->join[i]) (void)hipEventDestroy(predictor->join[i]);
     }
     if (predictor->fork) (void)hipEventDestroy(predictor->fork);
-    if (predictor->join) (void)hipEventDestroy(predictor->join);
     delete predictor;
     irx_weights_release(w);
 }
@@ -1188,9 +1205,12 @@ size_t irx_predictor_pass_rows(const irx_predictor *predictor) { return predicto
 
 int irx_predictor_set_streams(irx_predictor *predictor, int streams) {
     return guarded("irx_predictor_set_streams", [&] {
-        if (!predictor || streams < 1 || streams > 2) fail(IRX_INVALID_ARGUMENT, "streams must be 1 or 2");
+        if (!predictor || streams < 1 || streams > kMaxPassStreams)
+            fail(IRX_INVALID_ARGUMENT, "streams must be 1 to " + std::to_string(kMaxPassStreams));
         std::lock_guard<std::mutex> lock(predictor->mu);
+        set_device(predictor->weights->device);
         predictor->streams = streams;
+        ensure_workspace(predictor);
     });
 }
 
@@ -1245,21 +1265,24 @@ static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *
                            irx_progress_fn progress, void *user) {
     const size_t R = P->pass_rows;
     if (cpu_rows) std::memset(cpu_rows, 0, q);
-    // The side stream starts after everything already queued on the main one
-    // (the inputs' upload), and the main stream ends after the side's passes.
+    // Side streams start after everything already queued on the main one (the
+    // inputs' upload), and the main stream ends after the side streams' passes.
+    const int lanes = P->streams;
     IRX_HIP(hipEventRecord(P->fork, P->stream));
-    IRX_HIP(hipStreamWaitEvent(P->side_stream, P->fork, 0));
+    for (int i = 1; i < lanes; ++i) IRX_HIP(hipStreamWaitEvent(P->lane(i), P->fork, 0));
     int slot = 0;
-    for (size_t q0 = 0; q0 < q; q0 += R, slot = P->streams > 1 ? slot ^ 1 : 0) {
+    for (size_t q0 = 0; q0 < q; q0 += R, slot = (slot + 1) % lanes) {
         const int len = (int)std::min(R, q - q0);
         predict_pass(P, slot, d_x, (long long)q * P->shape.features, (int)q0, len, d_logits, (int)q, cpu_rows);
         if (progress) {
-            IRX_HIP(hipStreamSynchronize(slot ? P->side_stream : P->stream));
+            IRX_HIP(hipStreamSynchronize(P->lane(slot)));
             report(progress, user, IRX_STAGE_PREDICT, q0 + len, q);
         }
     }
-    IRX_HIP(hipEventRecord(P->join, P->side_stream));
-    IRX_HIP(hipStreamWaitEvent(P->stream, P->join, 0));
+    for (int i = 1; i < lanes; ++i) {
+        IRX_HIP(hipEventRecord(P->join[i - 1], P->lane(i)));
+        IRX_HIP(hipStreamWaitEvent(P->stream, P->join[i - 1], 0));
+    }
 }
 
 int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, float *logits, uint8_t *cpu_rows,

@@ -445,7 +445,7 @@ class StaticExecutor:
         hip.check(hip.lib().irx_predictor_set_pass_rows(self.handle, rows))
 
     def set_streams(self, streams: int) -> None:
-        """Passes alternate between `streams` (1 or 2) HIP streams; results are identical."""
+        """Passes rotate over `streams` (1 to 4) HIP streams; results are identical."""
         hip.check(hip.lib().irx_predictor_set_streams(self.handle, streams))
 
     def outputs(self) -> int:

@@ -98,20 +98,23 @@ def test_pass_rows_and_device_path_do_not_change_results(lcg):
     np.testing.assert_array_equal(dl.to_host(), whole)
 
 
-def test_one_and_two_streams_give_identical_results(lcg):
+def test_stream_counts_give_identical_results(lcg):
     *_, ctx_gpu = lcg
     xt = lcg[2]
-    ctx_gpu.set_pass_rows(32)  # 250 rows: 8 passes alternating between the streams
+    ctx_gpu.set_pass_rows(32)  # 250 rows: 8 passes rotating over the streams
     try:
-        two = ctx_gpu.predict_raw(xt).logits
-        ctx_gpu.set_streams(1)
-        one = ctx_gpu.predict_raw(xt).logits
+        by_streams = {}
+        for streams in (2, 1, 3, 4):
+            ctx_gpu.set_streams(streams)
+            by_streams[streams] = ctx_gpu.predict_raw(xt).logits
     finally:
         ctx_gpu.set_streams(2)
         ctx_gpu.set_pass_rows(512)
-    np.testing.assert_array_equal(two, one)
-    with pytest.raises(hip.HipError):
-        ctx_gpu.set_streams(3)
+    for streams in (2, 3, 4):
+        np.testing.assert_array_equal(by_streams[streams], by_streams[1])
+    for bad in (0, 5):
+        with pytest.raises(hip.HipError):
+            ctx_gpu.set_streams(bad)
 
 
 def test_kernel_timing_records_launches(lcg):
