@@ -281,6 +281,22 @@ int irx_profile_enable(unsigned families);
  * "small_attention", "layer_norm" or "glue". Waits for recorded launches. */
 int irx_profile_read(const char *family, irx_kernel_stats *out);
 
+/* ---- Regression summary on the GPU ---- */
+
+/* Regression outputs of a regressor's decoded quantiles, on the device
+ * (quantiles::summarize, src/models/tabicl_v2/quantiles.rs:80-213, which the
+ * reference runs on the host). decoded: device [ensembles, rows, quantiles]
+ * (2 <= quantiles <= 4096), e.g. irx_predictor_predict_device's output of a
+ * regressor. Per row, each estimator's quantiles are sorted and summarized in
+ * f64, then averaged over the estimators and rounded to f32, into device
+ * outputs (any may be null): mean [rows]; variance [rows] (unbiased);
+ * at_levels [rows, n_levels], the inverse CDF at each of the host array
+ * `levels` (finite, at most 64; 0.5 gives the median); raw [rows, quantiles],
+ * the sorted quantiles. Synchronous. */
+int irx_regression_summary(irx_device *device, const float *decoded, size_t ensembles, size_t rows,
+                           size_t quantiles, const float *levels, size_t n_levels, float *mean,
+                           float *variance, float *at_levels, float *raw);
+
 /* ---- Kernel harness (cuda/testing.rs:27-207): one kernel family on host data ---- */
 
 /* softmax(q k^T / 8) v for `pairs` (estimator, head) pairs: q [pairs, query_rows, 64],

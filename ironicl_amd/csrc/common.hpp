@@ -7,6 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 namespace irx {
 
@@ -140,6 +141,33 @@ struct Tail128 {
 };
 void tail128_pack(const float *wo, const float *w1, const float *w2, float *out);
 void tail128(const Tail128 &t, hipStream_t stream);
+
+// Regression outputs of decoded quantiles [b, q, k] (k <= 4096) on the device
+// (quantiles::summarize, quantiles.rs:80-213): per query row, averaged over
+// the b estimators, the mean, the unbiased variance, the inverse CDF at each
+// level and the sorted quantiles; null outputs are skipped. regression_tables
+// (host) prepares the tail fit's log levels and each level's case of the
+// inverse CDF.
+constexpr int kRegressionMaxLevels = 64;
+struct RegressionLevel {
+    int kind;     // 0 left tail, 1 right tail, 2 the last quantile, 3 between quantiles
+    int segment;  // kind 3: the lower quantile's index
+    double value; // kind 0 / 1: the difference of log levels; kind 3: the interpolation weight
+};
+struct RegressionSummary {
+    const float *decoded;
+    int b, q, k;
+    int tail;               // quantiles in each tail fit
+    const double *tail_x;   // [2 * tail]: ln of the left levels, then of one minus the right ones
+    int levels;
+    const RegressionLevel *level;  // [levels]
+    float *mean, *variance;        // [q]
+    float *at_levels;              // [q, levels]
+    float *raw;                    // [q, k]
+};
+void regression_tables(const float *alphas, int n_alphas, int k, int *tail, std::vector<double> &tail_x,
+                       std::vector<RegressionLevel> &levels);
+void regression_summary(const RegressionSummary &s, hipStream_t stream);
 
 // LayerNorm over `width` (128 or 512), eps 1e-5, two passes (reference.rs:223-252).
 void layer_norm(const float *x, long long ldx, const float *weight, const float *bias, float *y,

@@ -1427,6 +1427,39 @@ int irx_test_products(irx_device *device, const float *x, const float *w1, const
     });
 }
 
+int irx_regression_summary(irx_device *device, const float *decoded, size_t ensembles, size_t rows,
+                           size_t quantiles, const float *levels, size_t n_levels, float *mean, float *variance,
+                           float *at_levels, float *raw) {
+    return guarded("irx_regression_summary", [&] {
+        if (!device || (!decoded && rows) || (n_levels && !levels))
+            fail(IRX_INVALID_ARGUMENT, "regression summary needs a device, decoded quantiles and levels");
+        if (!ensembles || quantiles < 2 || quantiles > 4096)
+            fail(IRX_INVALID_ARGUMENT, "regression needs at least one estimator and 2 to 4096 quantiles");
+        if (n_levels > (size_t)kRegressionMaxLevels)
+            fail(IRX_INVALID_ARGUMENT, "at most " + std::to_string(kRegressionMaxLevels) + " quantile levels");
+        if (rows > (1u << 30)) fail(IRX_INVALID_ARGUMENT, "too many rows");
+        for (size_t i = 0; i < n_levels; ++i)
+            if (!std::isfinite(levels[i])) fail(IRX_INVALID_ARGUMENT, "quantile levels must be finite");
+        if (!rows) return;
+        set_device(device);
+        int tail = 0;
+        std::vector<double> tail_x;
+        std::vector<RegressionLevel> table;
+        regression_tables(levels, (int)n_levels, (int)quantiles, &tail, tail_x, table);
+        DevBuf dx(tail_x.size() * sizeof(double)), dl(std::max<size_t>(table.size(), 1) * sizeof(RegressionLevel));
+        IRX_HIP(hipMemcpy(dx.p, tail_x.data(), tail_x.size() * sizeof(double), hipMemcpyHostToDevice));
+        if (!table.empty())
+            IRX_HIP(hipMemcpy(dl.p, table.data(), table.size() * sizeof(RegressionLevel), hipMemcpyHostToDevice));
+        RegressionSummary rs{};
+        rs.decoded = decoded, rs.b = (int)ensembles, rs.q = (int)rows, rs.k = (int)quantiles;
+        rs.tail = tail, rs.tail_x = static_cast<const double *>(dx.p);
+        rs.levels = (int)n_levels, rs.level = static_cast<const RegressionLevel *>(dl.p);
+        rs.mean = mean, rs.variance = variance, rs.at_levels = n_levels ? at_levels : nullptr, rs.raw = raw;
+        regression_summary(rs, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+    });
+}
+
 int irx_test_block_tail(irx_device *device, int fused, const float *att, const float *state, size_t rows,
                         const float *wo, const float *bo, const float *n2w, const float *n2b, const float *w1,
                         const float *b1, const float *w2, const float *b2, size_t repeats, float *out) {

@@ -65,11 +65,10 @@ class TabICLRegressor:
         return self
 
     def predict(self, X, output_type: str = "mean", alphas=None):
-        """"mean" -> [Q]; "quantiles" -> [Q, len(alphas)] (alphas default 0.05, 0.5, 0.95)."""
+        """TabICLRegressor.predict's output types: "mean", "variance", "median"
+        -> [Q]; "quantiles" -> [Q, len(alphas)] (alphas default 0.05, 0.5,
+        0.95); "raw_quantiles" -> [Q, 999]; a list of names -> a dict of them."""
         alphas = (0.05, 0.5, 0.95) if alphas is None else tuple(alphas)
-        mean, quantiles = self.model_.predict_quantiles(X, alphas)
-        if output_type == "mean":
-            return mean
-        if output_type == "quantiles":
-            return quantiles
-        raise ValueError("output_type must be 'mean' or 'quantiles'")
+        names = [output_type] if isinstance(output_type, str) else list(output_type)
+        outs = self.model_.predict_regression_outputs(X, tuple(names), alphas)
+        return outs[0] if isinstance(output_type, str) else dict(zip(names, outs))

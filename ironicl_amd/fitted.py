@@ -20,7 +20,7 @@ from . import context_file as cf
 from . import hip, hipmem
 from . import manifest as mf
 from . import preprocess as pp
-from .tabicl import Executor, StaticExecutor, aggregate_classifier_probabilities, summarize_quantiles
+from .tabicl import Executor, StaticExecutor, aggregate_classifier_probabilities, summarize_regression
 
 
 class FittedModel:
@@ -56,9 +56,9 @@ class FittedModel:
 
     # ---- prediction (FittedModel::predict_*, fitted.rs:205-275) ----
 
-    def _logits(self, x) -> np.ndarray:
-        """Every member's decoder outputs [B, Q, width] for raw rows x, in
-        chunks of 8,192 rows transformed on the GPU into HBM."""
+    def _chunks(self, x):
+        """Yields (start, n, decoded outputs [B, n, width] in HBM) for raw rows
+        x, in chunks of 8,192 rows transformed on the GPU into HBM."""
         x = np.asarray(x)
         if x.ndim != 2 or x.shape[0] == 0:
             raise ValueError("X must be a nonempty matrix of features")
@@ -67,7 +67,6 @@ class FittedModel:
         b, h, width = p.member_count, p.n_features_out, self.executor.width
         q = x.shape[0]
         step = pp.PREDICT_CHUNK_ROWS
-        out = np.empty((b, q, width), np.float32)
         rows_dev = hipmem.DeviceArray((b, min(step, q), h))
         logits_dev = hipmem.DeviceArray((b, min(step, q), width))
         flags = np.zeros(min(step, q), np.uint8)
@@ -80,9 +79,38 @@ class FittedModel:
                 flags.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))))
             if flags[:n].any():
                 raise ValueError("a row is the all-missing marker, which this backend does not predict")
-            # The chunk's x and logits are [B, n, *] from the start of the buffers.
-            out[:, start:start + n] = logits_dev.to_host().reshape(-1)[: b * n * width].reshape(b, n, width)
+            # The chunk's x and outputs are [B, n, *] from the start of the buffers.
+            yield start, n, logits_dev
+
+    def _logits(self, x) -> np.ndarray:
+        """Every member's decoder outputs [B, Q, width] for raw rows x."""
+        b, width = self.preprocessor.member_count, self.executor.width
+        out = np.empty((b, np.asarray(x).shape[0], width), np.float32)
+        for start, n, dev in self._chunks(x):
+            out[:, start:start + n] = dev.to_host().reshape(-1)[: b * n * width].reshape(b, n, width)
         return out
+
+    def predict_regression_outputs(self, x, output_types=("mean",), alphas=()) -> list[np.ndarray]:
+        """Regression outputs (RegressionOutput, quantiles.rs:26-63) in the
+        targets' units, summarized on the GPU chunk by chunk: the
+        standardized values times the target scale plus its mean (unscale,
+        fitted.rs:158-177); the variance scales by the square of the scale."""
+        p = self.preprocessor
+        if p.target_scale is None:
+            raise ValueError("a classifier has no regression outputs")
+        b, width = p.member_count, self.executor.width
+        parts = [[] for _ in output_types]
+        for start, n, dev in self._chunks(x):
+            outs = summarize_regression(self.executor.device, dev.ptr, (b, n, width), output_types, alphas)
+            for acc, o in zip(parts, outs):
+                acc.append(o)
+        m, s = p.target_scale
+        result = []
+        for name, acc in zip(output_types, parts):
+            v = np.concatenate(acc).astype(np.float64)
+            v = v * (s * s) if name == "variance" else v * s + m
+            result.append(v.astype(np.float32))
+        return result
 
     def predict_proba(self, x, temperature: float = 0.9, average_logits: bool = True) -> np.ndarray:
         """Class probabilities [Q, C] from raw rows (predict_probabilities)."""
@@ -109,10 +137,8 @@ class FittedModel:
         p = self.preprocessor
         if p.target_scale is None:
             raise ValueError("a classifier has no regression outputs")
-        mean, quantiles = summarize_quantiles(self._logits(x), alphas)
-        m, s = p.target_scale
-        unscale = lambda v: (np.asarray(v, np.float64) * s + m).astype(np.float32)
-        return unscale(mean), unscale(quantiles)
+        mean, quantiles = self.predict_regression_outputs(x, ("mean", "quantiles"), alphas)
+        return mean, quantiles
 
     # ---- persistence ----
 

@@ -537,12 +537,39 @@ class StaticExecutor:
                                                   temperature, average_logits)
 
     def predict_regression(self, x: np.ndarray, alphas=(0.05, 0.5, 0.95)):
-        """(mean [Q], quantiles [Q, len(alphas)]) in standardized target units,
-        over 1024-row chunks (cpu.rs:2305-2329; quantiles.rs:80-213)."""
+        """(mean [Q], quantiles [Q, len(alphas)]) in standardized target units
+        (predict_regression, cpu.rs:2305-2329)."""
+        mean, quantiles = self.predict_regression_outputs(x, ("mean", "quantiles"), alphas)
+        return mean, quantiles
+
+    def predict_regression_outputs(self, x: np.ndarray, output_types=("mean",), alphas=()) -> list[np.ndarray]:
+        """The requested regression outputs (RegressionOutput, quantiles.rs:26-63),
+        in standardized target units: decoder outputs predicted into HBM and
+        summarized there (quantiles::summarize on the GPU); only the summaries
+        come back. Rows of the all-missing marker (cpu_rows) hold NaN."""
         if self.classes:
             raise ValueError("the context is a classification fit")
-        logits = self.predict_logits(x).logits
-        return summarize_quantiles(logits, alphas)
+        for name in output_types:
+            parse_regression_output(name, alphas)
+        from . import hipmem
+
+        x = _f32(x)
+        b, n, h = self.shape
+        if x.ndim != 3 or x.shape[0] != b or x.shape[2] != h:
+            raise ValueError(f"query shape {x.shape} does not match static context B={b} and H={h}")
+        q, width = x.shape[1], self.executor.width
+        if q == 0:
+            return [np.zeros((0,) + _regression_columns(t, alphas, width), np.float32) for t in output_types]
+        dx = hipmem.DeviceArray.from_host(x)
+        dl = hipmem.DeviceArray((b, q, width))
+        flags = np.zeros(q, np.uint8)
+        hip.check(hip.lib().irx_predictor_predict_device(self.handle, dx.ptr, q, dl.ptr,
+                                                         flags.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))))
+        outs = summarize_regression(self.executor.device, dl.ptr, (b, q, width), output_types, alphas)
+        rows = np.nonzero(flags)[0]
+        for o in outs:
+            o[rows] = np.nan
+        return outs
 
 
 def aggregate_classifier_probabilities(logits: np.ndarray, perms: np.ndarray, temperature: float = 0.9,
@@ -570,43 +597,47 @@ def aggregate_classifier_probabilities(logits: np.ndarray, perms: np.ndarray, te
     return (total / total.sum(axis=-1, keepdims=True)).astype(np.float32)
 
 
-def summarize_quantiles(logits: np.ndarray, alphas) -> tuple[np.ndarray, np.ndarray]:
-    """Mean and icdf at alphas of [B, Q, K] decoded quantiles, averaged over B
-    (quantiles::summarize, quantiles.rs:80-213)."""
-    b, q, k = logits.shape
-    tol = 1e-6
-    levels = (np.arange(1, k + 1, dtype=np.float64) / (k + 1)).astype(np.float32).astype(np.float64)
-    tk = max(1, min(20, k // 4))
-    xl = np.log(np.maximum(levels[:tk], tol))
-    xr = np.log(np.maximum(1.0 - levels[k - tk:], tol))
+REGRESSION_OUTPUTS = ("mean", "variance", "median", "quantiles", "raw_quantiles")
 
-    def slope(qv, x):
-        xm, qm = x.mean(), qv.mean(axis=-1, keepdims=True)
-        cov = ((qv - qm) * (x - xm)).mean(axis=-1)
-        var = ((x - xm) ** 2).mean()
-        return cov / max(var, tol)
 
-    alphas = np.asarray(alphas, dtype=np.float32).astype(np.float64)
-    mean = np.zeros(q)
-    quant = np.zeros((q, len(alphas)))
-    for e in range(b):
-        s = np.sort(logits[e].astype(np.float32), axis=-1).astype(np.float64)
-        mean += s.mean(axis=-1)
-        bl = np.clip(np.abs(slope(s[:, :tk], xl)), 0.01, 100.0)
-        br = np.clip(np.abs(-slope(s[:, k - tk:], xr)), 0.01, 100.0)
-        al, ar = levels[0], levels[-1]
-        for j, a in enumerate(alphas):
-            if a < al:
-                v = s[:, 0] + bl * (np.log(max(a, tol)) - np.log(max(al, tol)))
-            elif a > ar:
-                omr = 1.0 - min(ar, 1.0 - tol)
-                v = s[:, -1] - br * (np.log(max(1.0 - a, tol)) - np.log(omr))
-            elif a >= ar:
-                v = s[:, -1]
-            else:
-                seg = max(int(np.searchsorted(levels[:-1], a, side="right")) - 1, 0)
-                lo, hi = levels[seg], levels[seg + 1]
-                t = min(max((a - lo) / max(hi - lo, tol), 0.0), 1.0)
-                v = s[:, seg] + t * (s[:, seg + 1] - s[:, seg])
-            quant[:, j] += v
-    return (mean / b).astype(np.float32), (quant / b).astype(np.float32)
+def parse_regression_output(name: str, alphas=()) -> str:
+    """RegressionOutput::parse (quantiles.rs:43-63)."""
+    if name not in REGRESSION_OUTPUTS:
+        raise ValueError(f"unknown output_type {name!r}; expected mean, variance, median, quantiles, or raw_quantiles")
+    if name == "quantiles" and not all(math.isfinite(float(a)) for a in alphas):
+        raise ValueError("quantile levels must be finite")
+    return name
+
+
+def _regression_columns(name: str, alphas, width: int) -> tuple:
+    return {"quantiles": (len(alphas),), "raw_quantiles": (width,)}.get(name, ())
+
+
+def summarize_regression(device, decoded_ptr: int, shape, output_types, alphas=()) -> list[np.ndarray]:
+    """quantiles::summarize (quantiles.rs:80-213) on the GPU over decoded
+    quantiles [B, Q, K] already in HBM at `decoded_ptr`: one array per name in
+    `output_types` ("mean" [Q], "variance" [Q], "median" [Q], "quantiles"
+    [Q, len(alphas)], "raw_quantiles" [Q, K]), averaged over the B estimators."""
+    from . import hipmem
+
+    b, q, k = shape
+    for name in output_types:
+        parse_regression_output(name, alphas)
+    levels = [float(a) for a in alphas] if "quantiles" in output_types else []
+    if "median" in output_types:
+        levels.append(0.5)
+    levels = np.asarray(levels, np.float32)
+    mean = hipmem.DeviceArray((q,))
+    var = hipmem.DeviceArray((q,)) if "variance" in output_types else None
+    at = hipmem.DeviceArray((q, len(levels))) if len(levels) else None
+    raw = hipmem.DeviceArray((q, k)) if "raw_quantiles" in output_types else None
+    hip.check(hip.lib().irx_regression_summary(
+        device.handle, decoded_ptr, b, q, k, hip.fptr(levels) if len(levels) else None, len(levels), mean.ptr,
+        var.ptr if var else None, at.ptr if at else None, raw.ptr if raw else None))
+    at_host = at.to_host() if at else None
+    n_alpha = len(alphas) if "quantiles" in output_types else 0
+    got = {"mean": lambda: mean.to_host(), "variance": lambda: var.to_host(),
+           "median": lambda: np.ascontiguousarray(at_host[:, -1]),
+           "quantiles": lambda: np.ascontiguousarray(at_host[:, :n_alpha]),
+           "raw_quantiles": lambda: raw.to_host()}
+    return [got[name]() for name in output_types]

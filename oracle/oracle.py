@@ -66,6 +66,8 @@ def lib() -> ctypes.CDLL:
         L.ora_aggregate.restype = ctypes.c_int
         L.ora_regression_summary.argtypes = [_F, sz, sz, sz, _F, sz, _F, _F]
         L.ora_regression_summary.restype = ctypes.c_int
+        L.ora_regression_outputs.argtypes = [_F, sz, sz, sz, _F, sz, _F, _F, _F, _F]
+        L.ora_regression_outputs.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -231,6 +233,22 @@ def aggregate(logits, perms, temperature=0.9, average_logits=True):
     if st:
         raise ValueError("invalid aggregation")
     return out
+
+
+def regression_outputs(logits, alphas):
+    """(mean [Q], variance [Q], icdf at alphas [Q, A], sorted quantiles [Q, K]),
+    each averaged over the B estimators of logits [B, Q, K]."""
+    logits = f32(logits)
+    b, q, k = logits.shape
+    alphas = f32(alphas)
+    mean, var = np.zeros(q, np.float32), np.zeros(q, np.float32)
+    quant = np.zeros((q, len(alphas)), np.float32)
+    raw = np.zeros((q, k), np.float32)
+    st = lib().ora_regression_outputs(fp(logits), b, q, k, fp(alphas), len(alphas), fp(mean), fp(var), fp(quant),
+                                      fp(raw))
+    if st:
+        raise ValueError("regression needs at least two quantiles")
+    return mean, var, quant, raw
 
 
 def regression_summary(logits, alphas):

@@ -1041,13 +1041,22 @@ int ora_aggregate(const float *logits, size_t b, size_t q, size_t classes, const
     return 0;
 }
 
-static int cmp_float(const void *a, const void *b) {
-    float x = *(const float *)a, y = *(const float *)b;
+/* f32::total_cmp: integer keys ordered -NaN < -inf < ... < -0 < +0 < ... < +inf < +NaN. */
+static unsigned total_key(float v) {
+    unsigned u;
+    memcpy(&u, &v, 4);
+    return (u & 0x80000000u) ? ~u : u | 0x80000000u;
+}
+static int cmp_total(const void *a, const void *b) {
+    unsigned x = total_key(*(const float *)a), y = total_key(*(const float *)b);
     return (x > y) - (x < y);
 }
 
+/* The reference's f64 arithmetic is plain Rust: no multiply-add contraction. */
+#define ORA_NO_CONTRACT __attribute__((optimize("fp-contract=off")))
+
 /* tail_slope: quantiles.rs:202-213. */
-static double tail_slope(const float *q, const double *x, size_t n) {
+ORA_NO_CONTRACT static double tail_slope(const float *q, const double *x, size_t n) {
     double xm = 0, qm = 0;
     for (size_t i = 0; i < n; ++i) xm += x[i], qm += q[i];
     xm /= (double)n;
@@ -1061,16 +1070,26 @@ static double tail_slope(const float *q, const double *x, size_t n) {
     return (cov / (double)n) / (v > 1e-6 ? v : 1e-6);
 }
 
-/* quantiles::summarize (quantiles.rs:80-199): per estimator and row, sort the
- * decoded quantiles, fit exponential tails, evaluate; average over B. */
-int ora_regression_summary(const float *logits, size_t b, size_t q, size_t k, const float *alphas,
-                           size_t n_alphas, float *mean_out, float *quant_out) {
-    if (k < 2) return -1;
+/* f64::clamp of |beta| to [0.01, 100]; NaN stays NaN. */
+static double clamp_beta(double beta) {
+    double m = fabs(beta);
+    return m != m ? m : (m < 0.01 ? 0.01 : (m > 100.0 ? 100.0 : m));
+}
+
+/* quantiles::summarize (quantiles.rs:80-213): per estimator and row, sort the
+ * decoded quantiles (total order), then the mean, the unbiased variance, the
+ * inverse CDF at each alpha (exponential tails fitted to the outermost
+ * quantiles) and the sorted values; each averaged over B. Outputs may be null. */
+ORA_NO_CONTRACT int ora_regression_outputs(const float *logits, size_t b, size_t q, size_t k, const float *alphas,
+                                           size_t n_alphas, float *mean_out, float *var_out, float *quant_out,
+                                           float *raw_out) {
+    if (k < 2 || b < 1) return -1;
     const double TOL = 1e-6;
     double *levels = xcalloc(k, sizeof(double));
     for (size_t i = 0; i < k; ++i) levels[i] = (double)(float)((double)(i + 1) / (double)(k + 1));
-    double *msum = xcalloc(q, sizeof(double));
+    double *msum = xcalloc(q, sizeof(double)), *vsum = xcalloc(q, sizeof(double));
     double *qsum = xcalloc(q * (n_alphas ? n_alphas : 1), sizeof(double));
+    double *rsum = raw_out ? xcalloc(q * k, sizeof(double)) : NULL;
     float *sorted = xcalloc(k, sizeof(float));
     size_t tk = k / 4 < 20 ? k / 4 : 20;
     if (tk < 1) tk = 1;
@@ -1083,14 +1102,20 @@ int ora_regression_summary(const float *logits, size_t b, size_t q, size_t k, co
     for (size_t e = 0; e < b; ++e)
         for (size_t r = 0; r < q; ++r) {
             memcpy(sorted, logits + (e * q + r) * k, k * 4);
-            qsort(sorted, k, sizeof(float), cmp_float);
+            qsort(sorted, k, sizeof(float), cmp_total);
             double m = 0;
             for (size_t i = 0; i < k; ++i) m += sorted[i];
-            msum[r] += m / (double)k;
-            double left = tail_slope(sorted, xl, tk), right = tail_slope(sorted + k - tk, xr, tk);
-            double bl = fabs(left), br = fabs(-right);
-            bl = bl < 0.01 ? 0.01 : (bl > 100.0 ? 100.0 : bl);
-            br = br < 0.01 ? 0.01 : (br > 100.0 ? 100.0 : br);
+            const double mean = m / (double)k;
+            msum[r] += mean;
+            double sq = 0;
+            for (size_t i = 0; i < k; ++i) {
+                double d = (double)sorted[i] - mean;
+                sq += d * d;
+            }
+            vsum[r] += sq / (double)(k - 1);
+            if (rsum)
+                for (size_t i = 0; i < k; ++i) rsum[r * k + i] += (double)sorted[i];
+            double bl = clamp_beta(tail_slope(sorted, xl, tk)), br = clamp_beta(-tail_slope(sorted + k - tk, xr, tk));
             for (size_t a = 0; a < n_alphas; ++a) {
                 double alpha = alphas[a], al = levels[0], ar = levels[k - 1];
                 double ql = sorted[0], qr = sorted[k - 1], v;
@@ -1120,14 +1145,24 @@ int ora_regression_summary(const float *logits, size_t b, size_t q, size_t k, co
         }
     for (size_t r = 0; r < q; ++r) {
         if (mean_out) mean_out[r] = (float)(msum[r] / (double)b);
+        if (var_out) var_out[r] = (float)(vsum[r] / (double)b);
         for (size_t a = 0; a < n_alphas; ++a)
             if (quant_out) quant_out[r * n_alphas + a] = (float)(qsum[r * n_alphas + a] / (double)b);
+        if (rsum)
+            for (size_t i = 0; i < k; ++i) raw_out[r * k + i] = (float)(rsum[r * k + i] / (double)b);
     }
     free(levels);
     free(msum);
+    free(vsum);
     free(qsum);
+    free(rsum);
     free(sorted);
     free(xl);
     free(xr);
     return 0;
+}
+
+int ora_regression_summary(const float *logits, size_t b, size_t q, size_t k, const float *alphas,
+                           size_t n_alphas, float *mean_out, float *quant_out) {
+    return ora_regression_outputs(logits, b, q, k, alphas, n_alphas, mean_out, NULL, quant_out, NULL);
 }

@@ -115,6 +115,12 @@ int ora_aggregate(const float *logits, size_t b, size_t q, size_t classes,
  * quantiles at alphas (quantiles.rs:80-213). logits [B,Q,999]. */
 int ora_regression_summary(const float *logits, size_t b, size_t q, size_t width,
                            const float *alphas, size_t n_alphas, float *mean, float *quantiles);
+/* The same with every output of quantiles::summarize (any may be null): mean
+ * [Q], unbiased variance [Q], inverse CDF at alphas [Q, n_alphas] and the
+ * sorted quantiles [Q, width], each averaged over B. Sorting follows
+ * f32::total_cmp; f64 arithmetic is not contracted into fused multiply-adds. */
+int ora_regression_outputs(const float *logits, size_t b, size_t q, size_t width, const float *alphas,
+                           size_t n_alphas, float *mean, float *variance, float *quantiles, float *raw);
 
 #ifdef __cplusplus
 }

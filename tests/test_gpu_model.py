@@ -164,10 +164,16 @@ def test_regressor_quantiles(device, reg_weights):
     cpu = m.predict_uncached(x, y, xt)
     assert_parity(gpu, cpu, "regressor quantiles")
     alphas = [0.05, 0.5, 0.95]
-    gm, gq = tabicl.summarize_quantiles(gpu, alphas)
+    gm, gq = st.predict_regression(xt, alphas)
     cm, cq = O.regression_summary(cpu, alphas)
     assert_parity(gm, cm, "mean")
     assert_parity(gq, cq, "quantiles")
+    # Summaries of the same decoded outputs: the GPU's are the oracle's to the bit.
+    names = ("mean", "variance", "median", "quantiles", "raw_quantiles")
+    got = st.predict_regression_outputs(xt, names, alphas)
+    om, ov, oq, oraw = O.regression_outputs(gpu, list(alphas) + [0.5])
+    for g, want in zip(got, (om, ov, oq[:, -1], oq[:, :3], oraw)):
+        np.testing.assert_array_equal(g, want)
 
 
 def test_ensemble_with_feature_permutations(clf, clf_oracle):

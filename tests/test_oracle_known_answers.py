@@ -182,3 +182,35 @@ def test_quantile_linear_and_exponential_tails():
     row = f32(np.log(lv))
     _, quant = O.regression_summary(np.stack([row, row]).reshape(2, 1, k), [t["alpha"]])
     assert abs(float(quant[0, 0]) - t["expected"]) < t["tolerance"]
+
+
+def test_quantile_variance_raw_and_closed_forms():
+    """quantiles.rs:224-251: the unbiased variance of Q(alpha) = 10 alpha - 5
+    over the levels; sorted raw quantiles; float64 closed forms on random rows."""
+    c = KA["linear_quantiles"]
+    k = c["k"]
+    lv = _levels(k)
+    row = f32(10 * lv - 5)[::-1].copy()
+    mean, var, quant, raw = O.regression_outputs(row.reshape(1, 1, k), [0.25, 0.5, 0.75])
+    m = lv.sum() / k
+    assert abs(float(var[0]) - (100 * (lv - m) ** 2).sum() / (k - 1)) < 1e-4
+    np.testing.assert_array_equal(raw[0], np.sort(row))
+    np.testing.assert_allclose(quant[0], [-2.5, 0.0, 2.5], atol=1e-5)
+    x = np.random.default_rng(5).normal(size=(3, 4, 37)).astype(np.float32)
+    mean, var, quant, raw = O.regression_outputs(x, [])
+    s = np.sort(x.astype(np.float64), axis=-1)
+    np.testing.assert_allclose(mean, s.mean(-1).mean(0), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(var, s.var(-1, ddof=1).mean(0), rtol=1e-5)
+    np.testing.assert_allclose(raw, s.mean(0), rtol=1e-6, atol=1e-7)
+    assert quant.shape == (4, 0)
+
+
+def test_quantile_sort_follows_total_order():
+    """f32::total_cmp: -NaN first, +NaN last. (Raw sums start at +0.0, as the
+    reference's do, so both zeros come out as +0.0.)"""
+    neg_nan = np.array([0xFFC00000], np.uint32).view(np.float32)[0]
+    row = np.array([1.0, np.nan, -0.0, 0.0, -np.inf, neg_nan, 3.0, -2.0], np.float32)
+    _, _, _, raw = O.regression_outputs(row.reshape(1, 1, -1), [])
+    bits = raw[0].view(np.uint32)
+    assert bits[0] == 0xFFC00000 and np.isneginf(raw[0, 1]) and raw[0, 2] == -2.0
+    assert bits[3] == 0 and bits[4] == 0 and list(raw[0, 5:7]) == [1.0, 3.0] and np.isnan(raw[0, 7])
