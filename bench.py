@@ -17,7 +17,8 @@ CPU path) is timed on the host's cores on a bounded sample of the same rows.
 Passes of 1, 8, 16 and 32 rows, where streaming the cached K/V from HBM bounds
 the cross-attention, are timed after the steps and reported with their HBM
 fraction. The same workload at optimize="auto" (FP16 ICL cache, split-FP16
-attention) is reported beside the FP32 line, with its accuracy gate.
+attention) and optimize="fast" (FP8 ICL cache, FP16 attention products) is
+reported beside the FP32 line, each with its accuracy gate.
 
 Prints one JSON line.
 """
@@ -170,21 +171,37 @@ def bench_fitted(executor, x, y, xt, args) -> dict:
     return report
 
 
-def bench_auto(executor, x, y, q, dx, gpu_logits, args) -> dict:
-    """optimize="auto" on the same workload: FP16 ICL cache, split-FP16
-    attention products. Build ms, rows/s over timed steps (two streams), the
-    attention launch's rate (single-stream steps), and the accuracy gate
-    against the "safe" logits of the main run (max |logit| difference, labels
-    that differ where safe's top-2 margin exceeds 2e-2)."""
+# The reduced-precision levels: optimize -> (ICL cache bytes per value, FP16
+# products per FP32-equivalent product, gate on |logit - safe|
+# (docs/experiments.md:406-423), wide and decode kernels).
+LEVELS = {
+    "auto": (2, 2, 1e-2, "icl_attention_split_kernel (FP16 cache, queries and probabilities split hi + lo into "
+                         "one accumulator, 32x32x16 FP16 MFMA)",
+             "icl_decode16_kernel (FP16 cache, 16x16x32 FP16 MFMA)"),
+    "fast": (1, 1, 5e-2, "icl_attention_split_kernel<FP8> (E4M3 cache with per-dim scales, converted to FP16 after "
+                         "the LDS read; FP16 queries and probabilities, 32x32x16 FP16 MFMA)",
+             "icl_decode16_kernel<FP8> (E4M3 cache, 16x16x32 FP16 MFMA)"),
+}
+
+
+def bench_level(optimize, executor, x, y, q, dx, gpu_logits, args) -> dict:
+    """A reduced-precision optimize level on the same workload: "auto" (FP16
+    ICL cache, split-FP16 attention products) or "fast" (FP8 ICL cache, FP16
+    products). Build ms, rows/s over timed steps (two streams), the attention
+    launch's rate (single-stream steps), the small passes' HBM rate, and the
+    level's accuracy gate against the "safe" logits of the main run (max
+    |logit| difference, labels that differ where safe's top-2 margin exceeds
+    twice the gate)."""
     from ironicl_amd import hip, hipmem
 
+    elem, products, gate, wide_name, decode_name = LEVELS[optimize]
     ms = []
-    ctx = executor.build_context(x, y, optimize="auto")
+    ctx = executor.build_context(x, y, optimize=optimize)
     for _ in range(max(1, args.build_repeats)):
         del ctx
         hipmem.synchronize()
         t0 = time.perf_counter()
-        ctx = executor.build_context(x, y, optimize="auto")
+        ctx = executor.build_context(x, y, optimize=optimize)
         hipmem.synchronize()
         ms.append(1000 * (time.perf_counter() - t0))
     ctx.set_pass_rows(args.pass_rows)
@@ -211,10 +228,10 @@ def bench_auto(executor, x, y, q, dx, gpu_logits, args) -> dict:
     hipmem.synchronize()
     att = hip.profile_read("icl_attention")
     hip.profile_enable(False)
-    # Small passes over the FP16 cache (half the bytes of the FP32 one).
+    # Small passes: HBM-bound over the cache's K and V of one layer.
     small = {}
     n = x.shape[1]
-    kv_bytes = 2.0 * b * 8 * n * 64 * 2
+    kv_bytes = 2.0 * b * 8 * n * 64 * elem
     ctx.set_pass_rows(max(SMALL_PASSES))
     for qb in SMALL_PASSES:
         def small_step():
@@ -238,28 +255,28 @@ def bench_auto(executor, x, y, q, dx, gpu_logits, args) -> dict:
     launch_ms = att["milliseconds"] / max(att["launches"], 1)
     flops = att["flops"] / max(att["launches"], 1)
     safe = gpu_logits[..., :CLASSES]
-    auto = logits[..., :CLASSES]
+    got = logits[..., :CLASSES]
     top2 = np.sort(safe, axis=-1)[..., -2:]
-    decided = (top2[..., 1] - top2[..., 0]) > 2e-2
+    decided = (top2[..., 1] - top2[..., 0]) > 2 * gate
     report = {
         "rows_per_s": q * args.steps / elapsed,
         "ms_per_step": 1000 * elapsed / args.steps,
         "build_ms": float(np.median(ms)),
         "attention": {
-            "kernel": "icl_attention_split_kernel (FP16 cache, queries and probabilities split hi + lo into one "
-                      "accumulator, 32x32x16 FP16 MFMA)",
+            "kernel": wide_name,
             "avg_launch_ms": launch_ms,
             "algorithmic_tflops": flops / (launch_ms * 1e-3) / 1e12,
-            # Two FP16 products (hi and lo of Q, of P) per FP32-equivalent product.
-            "fp16_mfma_frac": 2 * flops / (launch_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
+            "fp16_products_per_product": products,
+            "fp16_mfma_frac": products * flops / (launch_ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
         },
-        "small_pass_hbm": {"kernel": "icl_decode16_kernel (FP16 cache, 16x16x32 FP16 MFMA)", "by_pass_rows": small},
-        "gate_vs_safe": {"max_abs_logit_diff": float(np.abs(auto - safe).max()),
-                         "tolerance": 1e-2,
-                         "labels_differing_beyond_near_ties": int((auto.argmax(-1) != safe.argmax(-1))[decided].sum())},
+        "small_pass_hbm": {"kernel": decode_name, "by_pass_rows": small},
+        "gate_vs_safe": {"max_abs_logit_diff": float(np.abs(got - safe).max()),
+                         "tolerance": gate,
+                         "labels_differing_beyond_near_ties": int((got.argmax(-1) != safe.argmax(-1))[decided].sum())},
     }
-    log(f"auto: build {report['build_ms']:.1f} ms, {report['rows_per_s']:.0f} rows/s, attention "
-        f"{1e3 * launch_ms:.1f} us, max |logit - safe| {report['gate_vs_safe']['max_abs_logit_diff']:.2e}")
+    log(f"{optimize}: build {report['build_ms']:.1f} ms, {report['rows_per_s']:.0f} rows/s, attention "
+        f"{1e3 * launch_ms:.1f} us, passes of <= 16 rows {1e3 * small['16']['avg_launch_ms']:.1f} us, "
+        f"max |logit - safe| {report['gate_vs_safe']['max_abs_logit_diff']:.2e}")
     del ctx
     return report
 
@@ -430,7 +447,8 @@ def main() -> int:
         os.remove(path)
         log(f"context export {export_s:.2f} s, verified reload {import_s:.2f} s ({size / 1e9:.2f} GB)")
 
-    auto_report = bench_auto(executor, x, y, q, dx, gpu_logits, args)
+    auto_report = bench_level("auto", executor, x, y, q, dx, gpu_logits, args)
+    fast_report = bench_level("fast", executor, x, y, q, dx, gpu_logits, args)
     fitted_report = bench_fitted(executor, x, y, xt, args) if args.fitted else None
 
     # The same prediction from host buffers (PCIe included), for reference.
@@ -502,6 +520,7 @@ def main() -> int:
             "bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s", "by_pass_rows": small,
         },
         "optimize_auto": auto_report,
+        "optimize_fast": fast_report,
         "context_io": context_io,
         "fitted": fitted_report,
         "kernel_ms_per_step": kernel_ms,

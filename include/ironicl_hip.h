@@ -50,8 +50,16 @@ typedef enum irx_status {
  * FP32: optimize="safe", FP32 everywhere, the ICL cache in FP32.
  * SPLIT: optimize="auto": the ICL cache in FP16 (cpu.rs:4038-4044) and the ICL
  * attention's products on FP16 MFMA with queries and probabilities split into
- * high and scaled low FP16 parts; other products in FP32. */
-typedef enum irx_precision { IRX_PRECISION_FP32 = 0, IRX_PRECISION_SPLIT = 1 } irx_precision;
+ * high and low FP16 parts; other products in FP32.
+ * HALF: optimize="fast": built as SPLIT (the context keeps FP16 K/V), then the
+ * resident ICL cache is FP8 E4M3 with a scale per (estimator, head, dim)
+ * (cuda/cache.rs:60-275) and the ICL attention's products take FP16 queries
+ * and probabilities, one FP16 product each; other products in FP32. */
+typedef enum irx_precision {
+    IRX_PRECISION_FP32 = 0,
+    IRX_PRECISION_SPLIT = 1,
+    IRX_PRECISION_HALF = 2
+} irx_precision;
 
 typedef enum irx_task { IRX_TASK_CLASSIFIER = 0, IRX_TASK_REGRESSOR = 1 } irx_task;
 
@@ -143,7 +151,7 @@ typedef struct irx_build_inputs {
 typedef struct irx_build_outputs {
     float *column_keys[3];   /* [B, H+4, 8, 128, 16] */
     float *column_values[3];
-    float *icl_keys[12];     /* [B, 8, N, 64]; FP16 bits (2 bytes each) at IRX_PRECISION_SPLIT */
+    float *icl_keys[12];     /* [B, 8, N, 64]; FP16 bits (2 bytes each) at IRX_PRECISION_SPLIT and HALF */
     float *icl_values[12];
 } irx_build_outputs;
 
@@ -164,7 +172,7 @@ typedef struct irx_context_tensors {
     const float *column_keys[3];    /* [B, H+4, 8, 128, 16]; may be NULL when adopting a built cache */
     const float *column_values[3];
     irx_icl_source icl;             /* may be NULL when adopting a built cache; at IRX_PRECISION_SPLIT
-                                     * its blocks are FP16 bits [B, 8, N, 64] */
+                                     * and HALF its blocks are FP16 bits [B, 8, N, 64] */
     void *icl_user;
     const float *base_scales[12];   /* [512] each */
     const float *rope_frequencies;  /* [8] */
@@ -200,7 +208,11 @@ int irx_predictor_set_streams(irx_predictor *predictor, int streams);
  * the reference's CUDA build always writes the tensors to host pages,
  * cpu.rs:744-805, where this backend keeps them in HBM until asked). Values
  * are FP32 (4 bytes), except the ICL tensors of an IRX_PRECISION_SPLIT
- * predictor, which are FP16 bits (2 bytes), as its context stores them. */
+ * predictor, which are FP16 bits (2 bytes), as its context stores them. An
+ * IRX_PRECISION_HALF predictor reads them as FP16 too when it adopted a build
+ * (which keeps its FP16 cache beside the FP8 one); one made from context
+ * tensors holds them only as FP8 and returns IRX_UNSUPPORTED (its caller has
+ * the FP16 tensors). */
 int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t offset, size_t floats,
                                void *dst);
 
@@ -303,9 +315,19 @@ int irx_regression_summary(irx_device *device, const float *decoded, size_t ense
  * k and v [pairs, rows, 64]; out [pairs, query_rows, 64]. */
 int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v,
                            size_t pairs, size_t query_rows, size_t rows, float *out);
-/* The same at `precision`: SPLIT packs k and v into the FP16 cache first. */
+/* The same at `precision`: SPLIT packs k and v into the FP16 cache first;
+ * HALF rounds them to FP16 and encodes the FP8 cache from those. */
 int irx_test_icl_attention_precision(irx_device *device, int precision, const float *q, const float *k,
                                      const float *v, size_t pairs, size_t query_rows, size_t rows, float *out);
+/* The FP8 cache block (IRX_PRECISION_HALF) of FP16 keys and values [pairs,
+ * rows, 64] (FP16 bits), as the predictor holds it: K [pairs, Np, 64] E4M3
+ * bytes (Np = rows rounded up to 64, zero rows after `rows`), V^T [pairs, Np /
+ * 64, 64 dims, 64 keys] bytes (keys of each group of 16 in the order 0..3,
+ * 8..11, 4..7, 12..15), key scales [pairs, 64] and value scales [pairs, 64]
+ * (FP32), then [2, pairs, 64] words of the encoder's own. `block` receives
+ * 2 * pairs * Np * 64 + 1024 * pairs bytes. */
+int irx_test_encode_icl8(irx_device *device, const uint16_t *k, const uint16_t *v, size_t pairs, size_t rows,
+                         void *block);
 /* first = gelu(x w1^T + b1); second = first w2^T + b2 (+ first when width2 == width).
  * x [rows, depth], w1 [width, depth], w2 [width2, width]. */
 int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1,

@@ -37,6 +37,8 @@
 //    through LDS in chunks of 64, optional RoPE on queries and keys.
 #include "common.hpp"
 
+#include <type_traits>
+
 #include <algorithm>
 
 namespace irx {
@@ -370,6 +372,33 @@ struct IclTile16 {
 
 __device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
+// FP8 tiles (IRX_PRECISION_HALF): K [64 keys x 64 bytes] and V^T [64 dims x
+// 64 keys] bytes, 4 KB each; the 16-byte chunk c of row r is stored at chunk
+// c ^ ((r / 4) % 4).
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+struct IclTile8 {
+    u32x4 k[kKeyTile * 4];
+    u32x4 v[kKeyTile * 4];
+};
+
+// Eight E4M3 values (OCP, bias 7) as FP16, exactly (v_cvt_scalef32_pk_f16_fp8, scale 1).
+__device__ __forceinline__ half8 fp8x8_to_half8(u32x2 w) {
+    typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+    const half2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0], 1.0f, false);
+    const half2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0], 1.0f, true);
+    const half2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[1], 1.0f, false);
+    const half2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[1], 1.0f, true);
+    return half8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Eight FP32 values rounded to FP16 (nearest even).
+__device__ __forceinline__ half8 round8(const float *x) {
+    half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (_Float16)x[e];
+    return h;
+}
+
 // Eight FP32 values split into high and low FP16 parts, x = hi + lo. The low
 // part is not rescaled: both products accumulate into one FP32 accumulator,
 // and a low part below FP16's normal range (only for |x| < 2^-3) loses bits
@@ -389,9 +418,15 @@ __device__ __forceinline__ void split8(const float *x, half8 &hi, half8 &lo) {
     lo = __builtin_bit_cast(half8, l);
 }
 
-template <bool SPLIT>
+// FP8 (IRX_PRECISION_HALF, the reference's optimize="fast"): the same
+// tiling over an E4M3 cache (K [pairs, Np, 64] bytes, V^T tiles as above in
+// bytes) with a scale per (pair, dim): the key scales are folded into the
+// queries, which are rounded once to FP16; each fragment is converted to FP16
+// after its LDS read; one FP16 product each (no low parts); the value scales
+// multiply the output.
+template <bool SPLIT, bool FP8 = false>
 __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(IclAttention p, IclLaunch g) {
-    __shared__ __attribute__((aligned(16))) IclTile16 tiles[2];
+    __shared__ __attribute__((aligned(16))) std::conditional_t<FP8, IclTile8, IclTile16> tiles[2];
 
     const int total = g.qtiles * p.pairs * g.splits;
     const int bid = blockIdx.x;
@@ -410,7 +445,8 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
     const int qrow0 = qt * kIclQueries + wave * 64 + r32;
 
     // The lane's queries, dims 16 m + 8 half .. +7 for m = 0..3, in the exp2
-    // domain, split into high and low FP16 parts.
+    // domain, split into high and low FP16 parts (FP8: times the key scales,
+    // rounded to FP16).
     half8 qh[2][4], ql[2][4];
     {
         const float scale = 0.125f * kLog2e;
@@ -430,7 +466,14 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
 #pragma unroll
                     for (int e = 0; e < 8; ++e) x[e] = 0.f;
                 }
-                split8(x, qh[j][m], ql[j][m]);
+                if constexpr (FP8) {
+                    const float *ks = p.kscale + pair * 64 + 16 * m + 8 * half;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] *= ks[e];
+                    qh[j][m] = round8(x);
+                } else {
+                    split8(x, qh[j][m], ql[j][m]);
+                }
             }
         }
     }
@@ -439,26 +482,49 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
     // of 8 fills LDS chunks 64 t .. 64 t + 63. Wave w issues K and V
     // instructions 2 w and 2 w + 1. Lane i of instruction t fills LDS row
     // 8 t + i / 8, stored chunk i % 8, i.e. source chunk (i % 8) ^ (row % 8).
-    const unsigned short *kbase = static_cast<const unsigned short *>(p.k16) + (long long)pair * n_pad * 64;
-    const unsigned short *vbase = static_cast<const unsigned short *>(p.v16) + (long long)pair * n_pad * 64;
+    // FP8: a tile of K (or V^T) is 4 KB; wave w's one instruction fills LDS
+    // rows 16 w .. 16 w + 15, lane i row 16 w + i / 4, stored chunk i % 4.
+    const unsigned short *kbase = p.k16 + (long long)pair * n_pad * 64;
+    const unsigned short *vbase = p.v16 + (long long)pair * n_pad * 64;
+    const unsigned char *kbase8 = p.k8 + (long long)pair * n_pad * 64;
+    const unsigned char *vbase8 = p.v8 + (long long)pair * n_pad * 64;
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     int src_off[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int t = 2 * wv + i, row = 8 * t + (lane >> 3);
-        src_off[i] = row * 64 + 8 * ((lane & 7) ^ (row & 7));  // halves
-    }
-    auto issue_tile = [&](int k0, int buf) {
-        const unsigned short *kt = kbase + (long long)k0 * 64, *vt = vbase + (long long)k0 * 64;
+    if constexpr (FP8) {
+        const int row = 16 * wv + (lane >> 2);
+        src_off[0] = row * 64 + 16 * ((lane & 3) ^ ((row >> 2) & 3));  // bytes
+        src_off[1] = 0;
+    } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int t = 2 * wv + i;
-            __builtin_amdgcn_global_load_lds(kt + src_off[i], (lds_void *)&tiles[buf].k[64 * t], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vt + src_off[i], (lds_void *)&tiles[buf].v[64 * t], 16, 0, 0);
+            const int t = 2 * wv + i, row = 8 * t + (lane >> 3);
+            src_off[i] = row * 64 + 8 * ((lane & 7) ^ (row & 7));  // halves
+        }
+    }
+    auto issue_tile = [&](int k0, int buf) {
+        if constexpr (FP8) {
+            const unsigned char *kt = kbase8 + (long long)k0 * 64, *vt = vbase8 + (long long)k0 * 64;
+            __builtin_amdgcn_global_load_lds(kt + src_off[0], (lds_void *)&tiles[buf].k[64 * wv], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vt + src_off[0], (lds_void *)&tiles[buf].v[64 * wv], 16, 0, 0);
+        } else {
+            const unsigned short *kt = kbase + (long long)k0 * 64, *vt = vbase + (long long)k0 * 64;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int t = 2 * wv + i;
+                __builtin_amdgcn_global_load_lds(kt + src_off[i], (lds_void *)&tiles[buf].k[64 * t], 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vt + src_off[i], (lds_void *)&tiles[buf].v[64 * t], 16, 0, 0);
+            }
         }
     };
-    // LDS chunk index of row `row`, chunk c.
-    auto at = [](int row, int c) { return row * 8 + (c ^ (row & 7)); };
+    // The FP16 operand of row `row`, 8-element group c2 (dims or keys 8 c2 .. +7).
+    auto frag = [](const u32x4 *tile, int row, int c2) {
+        if constexpr (FP8) {
+            const int c = c2 >> 1;
+            return fp8x8_to_half8(reinterpret_cast<const u32x2 *>(tile)[2 * (row * 4 + (c ^ ((row >> 2) & 3))) + (c2 & 1)]);
+        } else {
+            return as_half8(tile[row * 8 + (c2 ^ (row & 7))]);
+        }
+    };
 
     f32x16 o[2][2];  // [dim block][query block]
 #pragma unroll
@@ -487,12 +553,14 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
             s0 = init, s1 = init;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const half8 a0 = as_half8(kt[at(r32, 2 * m + half)]);
-                const half8 a1 = as_half8(kt[at(r32 + 32, 2 * m + half)]);
+                const half8 a0 = frag(kt, r32, 2 * m + half);
+                const half8 a1 = frag(kt, r32 + 32, 2 * m + half);
                 s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qh[j][m], s0, 0, 0, 0);
                 s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qh[j][m], s1, 0, 0, 0);
-                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, ql[j][m], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ql[j][m], s1, 0, 0, 0);
+                if constexpr (!FP8) {
+                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, ql[j][m], s0, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ql[j][m], s1, 0, 0, 0);
+                }
             }
             if (k0 + kKeyTile > k_end) {
 #pragma unroll
@@ -547,15 +615,18 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
                 float x[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] = s[j][kb][8 * g + e];
-                split8(x, ph[j], pl[j]);
+                if constexpr (FP8)
+                    ph[j] = round8(x);
+                else
+                    split8(x, ph[j], pl[j]);
             }
 #pragma unroll
             for (int d = 0; d < 2; ++d) {
-                const half8 a = as_half8(vt[at(32 * d + r32, 2 * t + half)]);
+                const half8 a = frag(vt, 32 * d + r32, 2 * t + half);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     o[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph[j], o[d][j], 0, 0, 0);
-                    o[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[j], o[d][j], 0, 0, 0);
+                    if constexpr (!FP8) o[d][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[j], o[d][j], 0, 0, 0);
                 }
             }
         }
@@ -585,6 +656,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
                 f32x4 v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = o[d][j][4 * a + e] * inv;
+                if constexpr (FP8) v *= *reinterpret_cast<const f32x4 *>(p.vscale + pair * 64 + 32 * d + 8 * a + 4 * half);
                 *reinterpret_cast<f32x4 *>(dst + 32 * d + 8 * a + 4 * half) = v;
             }
     }
@@ -853,7 +925,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
 //     load of V^T row dim.
 // Every K load is 64 contiguous bytes per four lanes, every V^T load 64
 // contiguous bytes of one dim row per four lanes.
-template <int QG, bool SPLIT>
+// FP8: the same over the E4M3 cache, each load half as wide (8 bytes per
+// lane) and converted to FP16 in registers; queries times the key scales
+// rounded once to FP16, one product each, outputs times the value scales.
+template <int QG, bool SPLIT, bool FP8 = false>
 __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclAttention p, IclLaunch g) {
     __shared__ float red_o[kDecodeWaves][QG * 16 * kDecodeOStride];
     __shared__ float red_m[kDecodeWaves][QG * 16], red_l[kDecodeWaves][QG * 16];
@@ -882,27 +957,58 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
 #pragma unroll
                     for (int e = 0; e < 8; ++e) x[e] = 0.f;
                 }
-                split8(x, qh[gq][m], ql[gq][m]);
+                if constexpr (FP8) {
+                    const float *ks = p.kscale + pair * 64 + 32 * m + 8 * grp;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] *= ks[e];
+                    qh[gq][m] = round8(x);
+                } else {
+                    split8(x, qh[gq][m], ql[gq][m]);
+                }
             }
         }
     }
     const unsigned short *kbase = p.k16 + (long long)pair * n_pad * 64;
     const unsigned short *vbase = p.v16 + (long long)pair * n_pad * 64;
+    const unsigned char *kbase8 = p.k8 + (long long)pair * n_pad * 64;
+    const unsigned char *vbase8 = p.v8 + (long long)pair * n_pad * 64;
+    // The block's operands as loaded: 16 bytes per lane and operand (FP16),
+    // or 8 (FP8, in the low half).
     // Block at k0 (a multiple of 32, at most n_pad - 32): K rows of S blocks
     // 0 and 1 (dims 32 m + 8 grp ..) and V^T rows 16 d + i16 at the block's
     // stored positions 8 grp ..
     auto load = [&](int k0, u32x4 *kd, u32x4 *vd) {
+        const long long vt = (long long)(k0 >> 6) * 4096 + 32 * ((k0 >> 5) & 1) + 8 * grp;
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const int key = k0 + 16 * (i16 >> 3) + 8 * b + (i16 & 7);
 #pragma unroll
-            for (int m = 0; m < 2; ++m)
-                kd[2 * b + m] = *reinterpret_cast<const u32x4 *>(kbase + (long long)key * 64 + 32 * m + 8 * grp);
+            for (int m = 0; m < 2; ++m) {
+                const long long off = (long long)key * 64 + 32 * m + 8 * grp;
+                if constexpr (FP8) {
+                    const u32x2 w = *reinterpret_cast<const u32x2 *>(kbase8 + off);
+                    kd[2 * b + m] = u32x4{w[0], w[1], 0u, 0u};
+                } else {
+                    kd[2 * b + m] = *reinterpret_cast<const u32x4 *>(kbase + off);
+                }
+            }
         }
-        const long long vt = (long long)(k0 >> 6) * 4096 + 32 * ((k0 >> 5) & 1) + 8 * grp;
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
-            vd[d] = *reinterpret_cast<const u32x4 *>(vbase + vt + (long long)(16 * d + i16) * 64);
+        for (int d = 0; d < 4; ++d) {
+            const long long off = vt + (long long)(16 * d + i16) * 64;
+            if constexpr (FP8) {
+                const u32x2 w = *reinterpret_cast<const u32x2 *>(vbase8 + off);
+                vd[d] = u32x4{w[0], w[1], 0u, 0u};
+            } else {
+                vd[d] = *reinterpret_cast<const u32x4 *>(vbase + off);
+            }
+        }
+    };
+    auto operand = [](const u32x4 &w) {
+        if constexpr (FP8)
+            return fp8x8_to_half8(u32x2{w[0], w[1]});
+        else
+            return as_half8(w);
     };
 
     f32x4 o[QG][4];
@@ -925,10 +1031,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
                 s0 = init, s1 = init;
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
-                    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), qh[gq][m], s0, 0, 0, 0);
-                    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[m]), ql[gq][m], s0, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), qh[gq][m], s1, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kf[2 + m]), ql[gq][m], s1, 0, 0, 0);
+                    const half8 a0 = operand(kf[m]), a1 = operand(kf[2 + m]);
+                    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[gq][m], s0, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[gq][m], s1, 0, 0, 0);
+                    if constexpr (!FP8) {
+                        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[gq][m], s0, 0, 0, 0);
+                        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[gq][m], s1, 0, 0, 0);
+                    }
                 }
                 if (tail) {
 #pragma unroll
@@ -976,11 +1085,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
 #pragma unroll
             for (int r = 0; r < 4; ++r) x[r] = s0[r], x[4 + r] = s1[r];
             half8 ph, pl;
-            split8(x, ph, pl);
+            if constexpr (FP8)
+                ph = round8(x);
+            else
+                split8(x, ph, pl);
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                o[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), ph, o[gq][d], 0, 0, 0);
-                o[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vf[d]), pl, o[gq][d], 0, 0, 0);
+                const half8 a = operand(vf[d]);
+                o[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, o[gq][d], 0, 0, 0);
+                if constexpr (!FP8) o[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[gq][d], 0, 0, 0);
             }
         }
     };
@@ -1033,7 +1146,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
             acc += wgt * *reinterpret_cast<const f32x4 *>(&red_o[w][qi * kDecodeOStride + d]);
             den += wgt * red_l[w][qi];
         }
-        const f32x4 out = acc * (1.0f / den);
+        f32x4 out = acc * (1.0f / den);
+        if constexpr (FP8) out *= *reinterpret_cast<const f32x4 *>(p.vscale + pair * 64 + d);
         if constexpr (!SPLIT) {
             const int b = pair / kHeads, head = pair - b * kHeads;
             *reinterpret_cast<f32x4 *>(p.o + ((long long)b * p.q_rows + qi) * p.ldo + head * 64 + d) = out;
@@ -1457,9 +1571,15 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         (reinterpret_cast<uintptr_t>(args.partial) & 15) || (args.q_pair_stride & 3) || (args.kv_pair_stride & 3) ||
         (args.ldo & 3))
         fail(3, "ICL attention operands must be 16-byte aligned");
-    const bool f16 = args.k16 != nullptr;
-    if (f16 && (!args.v16 || (reinterpret_cast<uintptr_t>(args.k16) & 15) || (reinterpret_cast<uintptr_t>(args.v16) & 15)))
+    const bool fp8 = args.k8 != nullptr;
+    if (args.k16 && (!args.v16 || (reinterpret_cast<uintptr_t>(args.k16) & 15) || (reinterpret_cast<uintptr_t>(args.v16) & 15)))
         fail(3, "ICL attention FP16 cache must be 16-byte aligned");
+    if (fp8 && (!args.v8 || !args.kscale || !args.vscale || (reinterpret_cast<uintptr_t>(args.k8) & 15) ||
+                (reinterpret_cast<uintptr_t>(args.v8) & 15) || (reinterpret_cast<uintptr_t>(args.kscale) & 15) ||
+                (reinterpret_cast<uintptr_t>(args.vscale) & 15)))
+        fail(3, "ICL attention FP8 cache and scales must be 16-byte aligned");
+    // The FP8 cache uses the FP16 cache's tiling.
+    const bool f16 = args.k16 != nullptr || fp8;
     IclLaunch g = plan_icl(args.pairs, args.q_rows, args.kv_rows, args.compute_units, f16);
     if (g.splits > 1) {
         size_t need = icl_attention_partial_floats(args.pairs, args.q_rows, g.splits, f16);
@@ -1467,28 +1587,41 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
     }
     {
         const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
-        const double kv_bytes = f16 ? 2.0 * 64.0 * pairs * 2.0 * kv : 4.0 * 64.0 * pairs * 2.0 * kv;
+        const double elem = fp8 ? 1.0 : f16 ? 2.0 : 4.0;
+        const double kv_bytes = elem * 64.0 * pairs * 2.0 * kv;
         KernelTimer timer(kFamIcl, stream, 4.0 * pairs * q * kv * 64.0, kv_bytes + 4.0 * 64.0 * pairs * 2.0 * q);
-        if (f16 && args.q_rows <= kDecodeQueries) {
+        auto decode16 = [&]<bool FP8>() {
             const dim3 blocks((unsigned)((long long)args.pairs * g.splits)), threads(kDecodeWaves * 64);
             if (args.q_rows <= 16) {
                 if (g.splits > 1)
-                    hipLaunchKernelGGL((icl_decode16_kernel<1, true>), blocks, threads, 0, stream, args, g);
+                    hipLaunchKernelGGL((icl_decode16_kernel<1, true, FP8>), blocks, threads, 0, stream, args, g);
                 else
-                    hipLaunchKernelGGL((icl_decode16_kernel<1, false>), blocks, threads, 0, stream, args, g);
+                    hipLaunchKernelGGL((icl_decode16_kernel<1, false, FP8>), blocks, threads, 0, stream, args, g);
             } else {
                 if (g.splits > 1)
-                    hipLaunchKernelGGL((icl_decode16_kernel<2, true>), blocks, threads, 0, stream, args, g);
+                    hipLaunchKernelGGL((icl_decode16_kernel<2, true, FP8>), blocks, threads, 0, stream, args, g);
                 else
-                    hipLaunchKernelGGL((icl_decode16_kernel<2, false>), blocks, threads, 0, stream, args, g);
+                    hipLaunchKernelGGL((icl_decode16_kernel<2, false, FP8>), blocks, threads, 0, stream, args, g);
             }
-        } else if (f16) {
+        };
+        auto wide16 = [&]<bool FP8>() {
             if (g.splits > 1)
-                hipLaunchKernelGGL((icl_attention_split_kernel<true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
-                                   stream, args, g);
+                hipLaunchKernelGGL((icl_attention_split_kernel<true, FP8>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64),
+                                   0, stream, args, g);
             else
-                hipLaunchKernelGGL((icl_attention_split_kernel<false>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0,
-                                   stream, args, g);
+                hipLaunchKernelGGL((icl_attention_split_kernel<false, FP8>), dim3(g.per_xcd * 8),
+                                   dim3(kIclWaves * 64), 0, stream, args, g);
+        };
+        if (f16 && args.q_rows <= kDecodeQueries) {
+            if (fp8)
+                decode16.template operator()<true>();
+            else
+                decode16.template operator()<false>();
+        } else if (f16) {
+            if (fp8)
+                wide16.template operator()<true>();
+            else
+                wide16.template operator()<false>();
         } else if (args.q_rows <= kDecodeQueries) {
             const dim3 blocks((unsigned)((long long)args.pairs * g.splits)), threads(kDecodeWaves * 64);
             if (args.q_rows <= 16) {

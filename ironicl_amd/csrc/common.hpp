@@ -209,6 +209,10 @@ struct IclAttention {
     // The FP16 cache (split-FP16 products) instead of k / v: K [pairs, Np, 64]
     // and tile-transposed V [pairs, Np / 64, 64, 64], Np = kv_rows rounded up to 64.
     const unsigned short *k16, *v16;
+    // Or the FP8 cache: K [pairs, Np, 64] and V^T tiles as the FP16 one, E4M3
+    // bytes, with the values' scales [pairs, 64] (value = byte * scale).
+    const unsigned char *k8, *v8;
+    const float *kscale, *vscale;
 };
 // Splits the ICL attention would use, and the partial floats it needs.
 int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units, bool f16 = false);
@@ -216,6 +220,23 @@ size_t icl_attention_partial_floats(int pairs, int q_rows, int splits, bool f16 
 void icl_attention(const IclAttention &args, hipStream_t stream);
 // Halves of one FP16 cache plane (K or V) for `pairs` x `rows` keys.
 inline size_t icl16_plane(long long pairs, long long rows) { return (size_t)pairs * ((rows + 63) / 64 * 64) * 64; }
+// One ICL block's FP8 cache (IRX_PRECISION_HALF), in one allocation: K
+// [pairs, Np, 64] and V^T tiles [pairs, Np / 64, 64, 64] as E4M3 bytes, then
+// the key and value scales [pairs, 64] and the encoder's peak words [2, pairs, 64].
+inline size_t icl8_plane(long long pairs, long long rows) { return (size_t)pairs * ((rows + 63) / 64 * 64) * 64; }
+inline size_t icl8_block_bytes(long long pairs, long long rows) {
+    return 2 * icl8_plane(pairs, rows) + 4 * (size_t)pairs * 64 * 4;
+}
+struct Icl8Block {
+    unsigned char *k, *v;
+    float *kscale, *vscale;
+    unsigned *kpeak, *vpeak;
+};
+Icl8Block icl8_block(void *base, long long pairs, long long rows);
+// FP16 K and V [pairs, rows, 64] (logical layout, FP16 bits) into the FP8
+// block at `block`; values that are not finite in FP16 are counted into `bad`.
+void encode_icl8(const unsigned short *k, const unsigned short *v, long long rows, int pairs, void *block,
+                 unsigned *bad, hipStream_t stream);
 // K and V [pairs, rows, 64] (FP32, or FP16 bits when src_f16) into the FP16
 // cache layout; adds the count of values not finite in FP16 to *bad.
 void pack_icl16(const void *k, const void *v, bool src_f16, long long rows, int pairs, unsigned short *k16,

@@ -231,7 +231,8 @@ struct irx_built_cache {
     irx_shape shape{};
     int precision = IRX_PRECISION_FP32;  // SPLIT: the ICL buffers hold the FP16 cache layout
     DevBuf column[kColumnBlocks];
-    DevBuf icl[kIclBlocks];
+    DevBuf icl[kIclBlocks];      // HALF: the FP8 blocks
+    DevBuf icl16[kIclBlocks];    // HALF: the FP16 cache the build made, kept for context reads
 };
 
 // Most HIP streams a predictor's passes rotate over (GPU_MAX_HW_QUEUES is 4).
@@ -244,6 +245,7 @@ struct irx_predictor {
     size_t pass_rows = 512;
     DevBuf column[kColumnBlocks];
     DevBuf icl[kIclBlocks];
+    DevBuf icl16[kIclBlocks];  // HALF, adopted from a build: its FP16 cache, for context reads
     DevBuf base_scales;   // [12, 512]
     DevBuf rope_cos, rope_sin;
     hipStream_t stream = nullptr;
@@ -412,7 +414,7 @@ struct Stages {
     // K/V [b, 8, kv_rows, 64] (or the FP16 cache k16 / v16).
     void icl_queries(int blk, float *x, int b, int rows, const float *k, const float *v, int kv_rows,
                      const float *base, const IclBuffers &r, const unsigned short *k16 = nullptr,
-                     const unsigned short *v16 = nullptr) const {
+                     const unsigned short *v16 = nullptr, const Icl8Block *c8 = nullptr) const {
         const BlockW &bw = w.icl[blk];
         const long long m = (long long)b * rows;
         layer_norm(x, 512, bw.n1w, bw.n1b, r.norm, 512, m, 512, s);
@@ -432,6 +434,7 @@ struct Stages {
         at.pairs = b * kHeads, at.q_rows = rows, at.kv_rows = kv_rows;
         at.partial = r.partial, at.partial_floats = r.partial_floats, at.compute_units = cus;
         at.k16 = k16, at.v16 = v16;
+        if (c8) at.k8 = c8->k, at.v8 = c8->v, at.kscale = c8->kscale, at.vscale = c8->vscale;
         icl_attention(at, s);
         tail(bw, x, m, r.att, r.norm, r.hid);
     }
@@ -574,11 +577,16 @@ size_t row_run_floats(long long seqs, int len) {
 BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus, int precision = IRX_PRECISION_FP32) {
     const long long n = sh.rows, h = sh.features, b = sh.ensembles;
     const int len = (int)h + kReserved;
-    const bool f16 = precision == IRX_PRECISION_SPLIT;
+    const bool f16 = precision != IRX_PRECISION_FP32;
     BuildPlan p{};
+    // HALF keeps the FP16 cache it builds and adds the FP8 blocks made from it
+    // (through one FP16 logical copy).
     p.keep_bytes = (size_t)kColumnBlocks * 2 * b * (h + 4) * kColumnCache * 4 +
                    (f16 ? (size_t)kIclBlocks * 2 * icl16_plane(b * kHeads, n) * 2
-                        : (size_t)kIclBlocks * 2 * b * kHeads * n * 64 * 4);
+                        : (size_t)kIclBlocks * 2 * b * kHeads * n * 64 * 4) +
+                   (precision == IRX_PRECISION_HALF
+                        ? (size_t)2 * b * kHeads * n * 64 * 2 + kIclBlocks * icl8_block_bytes(b * kHeads, n)
+                        : 0);
     size_t cap = std::min<size_t>(budget / 4, (size_t)24 << 30);
     int chunk = (int)h;
     while (chunk > 1 && column_chunk_floats(chunk, n) * 4 > cap) chunk = (chunk + 1) / 2;
@@ -609,7 +617,9 @@ int report(irx_progress_fn fn, void *user, int stage, size_t done, size_t total)
 
 void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *out, irx_built_cache **keep,
                 int precision) {
-    const bool f16 = precision == IRX_PRECISION_SPLIT;
+    // SPLIT and HALF build alike on the FP16 cache (the reference reads HALF's
+    // FP16 cache at Split precision during its build, cuda/build.rs:477-511).
+    const bool f16 = precision != IRX_PRECISION_FP32;
     const irx_shape sh = in->shape;
     if (!shape_ok(&sh)) fail(IRX_INVALID_ARGUMENT, "build shape must be nonempty");
     if (sh.rows < 64) fail(IRX_DOES_NOT_FIT, "the device builds contexts of at least 64 training rows");
@@ -795,9 +805,11 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
                     download(dst + off, cache->column[i].f() + part * col_plane + off, (size_t)H * kColumnCache * 4, s);
                 }
         }
-        DevBuf logical(f16 ? (size_t)2 * icl_plane * 2 : 0);
+        DevBuf logical(f16 && precision != IRX_PRECISION_HALF ? (size_t)2 * icl_plane * 2 : 0);
         for (int i = 0; i < kIclBlocks; ++i) {
-            if (!f16) {
+            if (precision == IRX_PRECISION_HALF) {
+                // Downloaded below, with the conversion to FP8.
+            } else if (!f16) {
                 if (out->icl_keys[i]) download(out->icl_keys[i], cache->icl[i].f(), icl_plane * 4, s);
                 if (out->icl_values[i]) download(out->icl_values[i], cache->icl[i].f() + icl_plane, icl_plane * 4, s);
             } else if (out->icl_keys[i] || out->icl_values[i]) {
@@ -811,6 +823,24 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
             }
         }
         IRX_HIP(hipStreamSynchronize(s));
+    }
+    if (precision == IRX_PRECISION_HALF) {
+        // Each block's FP16 cache -> logical FP16 (downloaded when asked) ->
+        // the FP8 cache the predictor reads (encode_fp8, cuda/build.rs:479-495).
+        // The FP16 cache stays beside it for context reads (exports).
+        DevBuf logical((size_t)2 * icl_plane * 2);
+        unsigned short *lk = static_cast<unsigned short *>(logical.p), *lv = lk + icl_plane;
+        for (int i = 0; i < kIclBlocks; ++i) {
+            const unsigned short *k16 = static_cast<const unsigned short *>(cache->icl[i].p);
+            unpack_icl16(k16, k16 + plane16, N, B * kHeads, lk, lv, s);
+            if (out && out->icl_keys[i]) download(out->icl_keys[i], lk, icl_plane * 2, s);
+            if (out && out->icl_values[i]) download(out->icl_values[i], lv, icl_plane * 2, s);
+            DevBuf fp8(icl8_block_bytes((long long)B * kHeads, N));
+            encode_icl8(lk, lv, N, B * kHeads, fp8.p, counter, s);
+            IRX_HIP(hipStreamSynchronize(s));
+            cache->icl16[i] = std::move(cache->icl[i]);
+            cache->icl[i] = std::move(fp8);
+        }
     }
     if (keep) {
         *keep = cache;
@@ -869,7 +899,7 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     Stages st{W, s, W.device->compute_units};
     Arena &ws = P->ws[slot];
     ws.used = 0;
-    const bool f16 = P->precision == IRX_PRECISION_SPLIT;
+    const bool f16 = P->precision != IRX_PRECISION_FP32;
     const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus, f16);
     uint8_t *flags = pb.flags;
     float *state = pb.state, *norm = pb.norm, *q = pb.q, *att = pb.att, *hid = pb.hid, *rows = pb.rows;
@@ -891,6 +921,10 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
         if (!f16) {
             const float *kc = P->icl[blk].f();
             st.icl_queries(blk, rows, B, R, kc, kc + icl_plane, N, P->base_scales.f() + blk * 512, ib);
+        } else if (P->precision == IRX_PRECISION_HALF) {
+            const Icl8Block c8 = icl8_block(P->icl[blk].p, (long long)B * kHeads, N);
+            st.icl_queries(blk, rows, B, R, nullptr, nullptr, N, P->base_scales.f() + blk * 512, ib, nullptr,
+                           nullptr, &c8);
         } else {
             const unsigned short *k16 = static_cast<const unsigned short *>(P->icl[blk].p);
             st.icl_queries(blk, rows, B, R, nullptr, nullptr, N, P->base_scales.f() + blk * 512, ib, k16,
@@ -919,7 +953,7 @@ void ensure_workspace(irx_predictor *P) {
     for (int i = 0; i < kMaxPassStreams; ++i)
         if (P->lane(i)) IRX_HIP(hipStreamSynchronize(P->lane(i)));
     size_t floats = predict_ws_floats(P->shape, P->pass_rows, P->weights->device->compute_units,
-                                      P->precision == IRX_PRECISION_SPLIT);
+                                      P->precision != IRX_PRECISION_FP32);
     // Workspaces of streams in use, at the current pass size; the others are released.
     for (int i = 0; i < kMaxPassStreams; ++i) {
         if (i < P->streams) {
@@ -1051,12 +1085,14 @@ int irx_weights_budget(const irx_weights *weights, uint64_t device_limit, size_t
 }
 
 size_t irx_context_bytes(int precision) {
-    return precision == IRX_PRECISION_FP32 ? 4 : precision == IRX_PRECISION_SPLIT ? 2 : 0;
+    // HALF contexts store FP16 K/V, as SPLIT ones; only the resident cache is FP8.
+    return precision == IRX_PRECISION_FP32 ? 4
+           : precision == IRX_PRECISION_SPLIT || precision == IRX_PRECISION_HALF ? 2
+                                                                                 : 0;
 }
 
 int irx_build_fits(size_t budget, int precision, const irx_shape *shape) {
-    if ((precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT) || !shape_ok(shape) ||
-        shape->rows < 64)
+    if (!irx_context_bytes(precision) || !shape_ok(shape) || shape->rows < 64)
         return 0;
     BuildPlan p = plan_build(*shape, budget, 256, precision);
     return p.ws_bytes + p.keep_bytes <= budget / 10 * 9;
@@ -1066,8 +1102,7 @@ int irx_build(irx_weights *weights, int precision, const irx_build_inputs *input
               irx_built_cache **keep) {
     return guarded("irx_build", [&] {
         if (!weights || !inputs) fail(IRX_INVALID_ARGUMENT, "null argument");
-        if (precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT)
-            fail(IRX_INVALID_ARGUMENT, "precision must be FP32 or SPLIT");
+        if (!irx_context_bytes(precision)) fail(IRX_INVALID_ARGUMENT, "precision must be FP32, SPLIT or HALF");
         if (keep) *keep = nullptr;
         if (inputs->shape.outputs == 0 || inputs->shape.outputs > (size_t)weights->width)
             fail(IRX_INVALID_ARGUMENT, "outputs exceed the decoder width");
@@ -1086,9 +1121,9 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
     irx_predictor *P = nullptr;
     int st = guarded("irx_predictor_new", [&] {
         if (!weights || !ctx || !out) fail(IRX_INVALID_ARGUMENT, "null argument");
-        if (precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT)
-            fail(IRX_INVALID_ARGUMENT, "precision must be FP32 or SPLIT");
-        const bool f16 = precision == IRX_PRECISION_SPLIT;
+        if (precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT && precision != IRX_PRECISION_HALF)
+            fail(IRX_INVALID_ARGUMENT, "precision must be FP32, SPLIT or HALF");
+        const bool f16 = precision != IRX_PRECISION_FP32, fp8 = precision == IRX_PRECISION_HALF;
         *out = nullptr;
         const irx_shape sh = ctx->shape;
         if (!shape_ok(&sh) || sh.outputs == 0 || sh.outputs > (size_t)weights->width)
@@ -1100,7 +1135,9 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         const long long B = sh.ensembles, H = sh.features, N = sh.rows, L = H + kReserved;
         const long long col_plane = B * L * kColumnCache, icl_plane = B * kHeads * N * 64;
         const size_t plane16 = icl16_plane(B * kHeads, N);
-        const size_t icl_bytes = f16 ? (size_t)kIclBlocks * 2 * plane16 * 2 : (size_t)kIclBlocks * 2 * icl_plane * 4;
+        const size_t icl_bytes = fp8   ? (size_t)kIclBlocks * icl8_block_bytes(B * kHeads, N)
+                                 : f16 ? (size_t)kIclBlocks * 2 * plane16 * 2
+                                       : (size_t)kIclBlocks * 2 * icl_plane * 4;
         const size_t cache_bytes = (size_t)kColumnBlocks * 2 * col_plane * 4 + icl_bytes;
         P = new irx_predictor();
         P->weights = weights;
@@ -1114,6 +1151,7 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
             if (adopt->precision != precision) fail(IRX_INVALID_ARGUMENT, "the built cache has another precision");
             for (int i = 0; i < kColumnBlocks; ++i) P->column[i] = std::move(adopt->column[i]);
             for (int i = 0; i < kIclBlocks; ++i) P->icl[i] = std::move(adopt->icl[i]);
+            for (int i = 0; i < kIclBlocks; ++i) P->icl16[i] = std::move(adopt->icl16[i]);
         } else {
             size_t ws = predict_ws_floats(sh, P->pass_rows, weights->device->compute_units, f16) * 4;
             if (cache_bytes + ws > ctx->budget / 10 * 9) fail(IRX_DOES_NOT_FIT, "the context does not fit the device");
@@ -1127,7 +1165,8 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
                 IRX_HIP(hipMemcpy(P->column[i].f() + col_plane, ctx->column_values[i], col_plane * 4,
                                   hipMemcpyHostToDevice));
             }
-            // FP16 contexts: the source gives FP16 bits [B, 8, N, 64], packed here.
+            // FP16 contexts: the source gives FP16 bits [B, 8, N, 64], packed here
+            // into the FP16 cache (SPLIT) or encoded into the FP8 one (HALF).
             DevBuf staging(f16 ? (size_t)2 * icl_plane * 2 : 0), bad(f16 ? 4 : 0);
             if (f16) IRX_HIP(hipMemset(bad.p, 0, 4));
             for (int i = 0; i < kIclBlocks; ++i) {
@@ -1142,10 +1181,15 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
                     unsigned short *sk = static_cast<unsigned short *>(staging.p), *sv = sk + icl_plane;
                     IRX_HIP(hipMemcpy(sk, k, icl_plane * 2, hipMemcpyHostToDevice));
                     IRX_HIP(hipMemcpy(sv, v, icl_plane * 2, hipMemcpyHostToDevice));
-                    P->icl[i].alloc(2 * plane16 * 2);
-                    unsigned short *k16 = static_cast<unsigned short *>(P->icl[i].p);
-                    pack_icl16(sk, sv, true, N, (int)(B * kHeads), k16, k16 + plane16, static_cast<unsigned *>(bad.p),
-                               nullptr);
+                    if (fp8) {
+                        P->icl[i].alloc(icl8_block_bytes(B * kHeads, N));
+                        encode_icl8(sk, sv, N, (int)(B * kHeads), P->icl[i].p, static_cast<unsigned *>(bad.p), nullptr);
+                    } else {
+                        P->icl[i].alloc(2 * plane16 * 2);
+                        unsigned short *k16 = static_cast<unsigned short *>(P->icl[i].p);
+                        pack_icl16(sk, sv, true, N, (int)(B * kHeads), k16, k16 + plane16,
+                                   static_cast<unsigned *>(bad.p), nullptr);
+                    }
                     IRX_HIP(hipDeviceSynchronize());
                 }
             }
@@ -1227,10 +1271,14 @@ int irx_predictor_read_context(irx_predictor *predictor, size_t tensor, size_t o
         const size_t plane = column ? col_plane : icl_plane;
         if (offset > plane || floats > plane - offset) fail(IRX_INVALID_ARGUMENT, "context read past the tensor's end");
         if (!floats) return;
-        const DevBuf &buf = column ? predictor->column[index / 2] : predictor->icl[index / 2];
+        const DevBuf &buf = column ? predictor->column[index / 2]
+                            : predictor->precision == IRX_PRECISION_HALF ? predictor->icl16[index / 2]
+                                                                         : predictor->icl[index / 2];
         std::lock_guard<std::mutex> lock(predictor->mu);
         set_device(predictor->weights->device);
-        if (!column && predictor->precision == IRX_PRECISION_SPLIT) {
+        if (!column && predictor->precision == IRX_PRECISION_HALF && !predictor->icl16[index / 2].p)
+            fail(IRX_UNSUPPORTED, "a fast (FP8) predictor made from context tensors keeps no FP16 ICL tensors");
+        if (!column && predictor->precision != IRX_PRECISION_FP32) {
             // FP16 bits in the logical layout, unpacked from the cache layout.
             const long long pairs = (long long)s.ensembles * kHeads;
             const size_t plane16 = icl16_plane(pairs, (long long)s.rows);
@@ -1350,9 +1398,8 @@ int irx_profile_read(const char *family, irx_kernel_stats *out) {
 int irx_test_icl_attention_precision(irx_device *device, int precision, const float *q, const float *k,
                                      const float *v, size_t pairs, size_t query_rows, size_t rows, float *out) {
     return guarded("irx_test_icl_attention", [&] {
-        if (precision != IRX_PRECISION_FP32 && precision != IRX_PRECISION_SPLIT)
-            fail(IRX_INVALID_ARGUMENT, "unsupported precision");
-        const bool f16 = precision == IRX_PRECISION_SPLIT;
+        if (!irx_context_bytes(precision)) fail(IRX_INVALID_ARGUMENT, "unsupported precision");
+        const bool f16 = precision != IRX_PRECISION_FP32, fp8 = precision == IRX_PRECISION_HALF;
         if (!device || !q || !k || !v || !out || !pairs || !query_rows || !rows)
             fail(IRX_INVALID_ARGUMENT, "ICL attention shapes do not match");
         if (pairs % kHeads) fail(IRX_INVALID_ARGUMENT, "pairs must be a multiple of 8 (estimators x heads)");
@@ -1366,6 +1413,7 @@ int irx_test_icl_attention_precision(irx_device *device, int precision, const fl
         size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, splits, f16);
         DevBuf part(pf * 4);
         DevBuf cache16(f16 ? 2 * icl16_plane((long long)pairs, (long long)rows) * 2 : 0), bad(f16 ? 4 : 0);
+        DevBuf logical(fp8 ? 2 * kn * 2 : 0), block8(fp8 ? icl8_block_bytes((long long)pairs, (long long)rows) : 0);
         IclAttention a{};
         if (f16) {
             unsigned short *k16 = static_cast<unsigned short *>(cache16.p);
@@ -1373,6 +1421,15 @@ int irx_test_icl_attention_precision(irx_device *device, int precision, const fl
             IRX_HIP(hipMemset(bad.p, 0, 4));
             pack_icl16(dk.p, dv.p, false, (long long)rows, (int)pairs, k16, v16, static_cast<unsigned *>(bad.p), nullptr);
             a.k16 = k16, a.v16 = v16;
+            if (fp8) {
+                // FP16 logical K/V (the context's values), then the FP8 cache from them.
+                unsigned short *lk = static_cast<unsigned short *>(logical.p), *lv = lk + kn;
+                unpack_icl16(k16, v16, (long long)rows, (int)pairs, lk, lv, nullptr);
+                encode_icl8(lk, lv, (long long)rows, (int)pairs, block8.p, static_cast<unsigned *>(bad.p), nullptr);
+                const Icl8Block c8 = icl8_block(block8.p, (long long)pairs, (long long)rows);
+                a.k16 = nullptr, a.v16 = nullptr;
+                a.k8 = c8.k, a.v8 = c8.v, a.kscale = c8.kscale, a.vscale = c8.vscale;
+            }
         }
         a.q = dq.f(), a.q_pair_stride = (long long)query_rows * 64, a.k = dk.f(), a.v = dv.f();
         a.kv_pair_stride = (long long)rows * 64, a.o = dout.f(), a.ldo = 512;
@@ -1388,6 +1445,26 @@ int irx_test_icl_attention_precision(irx_device *device, int precision, const fl
             for (size_t r = 0; r < query_rows; ++r)
                 std::memcpy(out + (p * query_rows + r) * 64, tok.data() + ((b * query_rows + r) * 512 + h * 64), 256);
         }
+    });
+}
+
+int irx_test_encode_icl8(irx_device *device, const uint16_t *k, const uint16_t *v, size_t pairs, size_t rows,
+                         void *block) {
+    return guarded("irx_test_encode_icl8", [&] {
+        if (!device || !k || !v || !block || !pairs || !rows) fail(IRX_INVALID_ARGUMENT, "FP8 encode shapes do not match");
+        set_device(device);
+        const size_t n = pairs * rows * 64, bytes = icl8_block_bytes((long long)pairs, (long long)rows);
+        DevBuf dk(n * 2), dv(n * 2), out(bytes), bad(4);
+        IRX_HIP(hipMemcpy(dk.p, k, n * 2, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dv.p, v, n * 2, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemset(bad.p, 0, 4));
+        encode_icl8(static_cast<const unsigned short *>(dk.p), static_cast<const unsigned short *>(dv.p),
+                    (long long)rows, (int)pairs, out.p, static_cast<unsigned *>(bad.p), nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+        unsigned nbad = 0;
+        IRX_HIP(hipMemcpy(&nbad, bad.p, 4, hipMemcpyDeviceToHost));
+        if (nbad) fail(IRX_NOT_FINITE, "a key or value is not finite");
+        IRX_HIP(hipMemcpy(block, out.p, bytes, hipMemcpyDeviceToHost));
     });
 }
 

@@ -20,6 +20,7 @@ STATUS_NAMES = ["OK", "NO_DEVICE", "OUT_OF_MEMORY", "INVALID_ARGUMENT", "DEVICE_
                 "DOES_NOT_FIT", "NOT_FINITE", "UNSUPPORTED"]
 PRECISION_FP32 = 0
 PRECISION_SPLIT = 1
+PRECISION_HALF = 2
 TASK_CLASSIFIER, TASK_REGRESSOR = 0, 1
 STAGE_BUILD, STAGE_PREDICT = 0, 1
 
@@ -104,6 +105,8 @@ SIGNATURES = {
     "irx_test_icl_attention": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
     "irx_test_icl_attention_precision": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _CF, _CF, _sz, _sz,
                                                         _sz, _F]),
+    "irx_test_encode_icl8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _sz, _sz,
+                                            ctypes.c_void_p]),
     "irx_test_products": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _CF, _CF, _sz, _sz, _sz, _sz, _F, _F]),
     "irx_regression_summary": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _sz, _sz, _sz, _CF, _sz,
                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),

@@ -31,8 +31,9 @@ _erf = np.frompyfunc(math.erf, 1, 1)
 
 # The optimize levels this backend builds and predicts at (Precision::for_optimize,
 # cuda/mod.rs:82-92): "safe" all FP32; "auto" an FP16 ICL cache with split-FP16
-# attention products.
-PRECISION = {"safe": hip.PRECISION_FP32, "auto": hip.PRECISION_SPLIT}
+# attention products; "fast" the same FP16 context, resident as an FP8 cache
+# read with single FP16 products.
+PRECISION = {"safe": hip.PRECISION_FP32, "auto": hip.PRECISION_SPLIT, "fast": hip.PRECISION_HALF}
 
 
 def _precision(optimize: str) -> int:
@@ -231,7 +232,9 @@ class Executor:
         file holds exactly this context, else build it and write it there.
         A missing, invalid or mismatched entry is rebuilt; a failed write
         leaves the context in HBM only (cpu.rs:645-672). ``optimize`` is "safe"
-        (all FP32) or "auto" (an FP16 ICL cache read by split-FP16 attention)."""
+        (all FP32), "auto" (an FP16 ICL cache read by split-FP16 attention) or
+        "fast" (the FP16 context kept on the host, its ICL cache resident as
+        FP8 with per-dim scales, read with single FP16 products)."""
         precision = _precision(optimize)
         meta = self.context_metadata(x, y_train, class_permutations, feature_permutations, optimize)
         directory = cf.resolve_cache_dir(cache_dir)
@@ -285,7 +288,7 @@ class Executor:
         if download:
             ck = [np.zeros((b, h + 4, 8, 128, 16), np.float32) for _ in range(3)]
             cv = [np.zeros_like(ck[0]) for _ in range(3)]
-            icl_dtype = np.float16 if precision == hip.PRECISION_SPLIT else np.float32
+            icl_dtype = np.float32 if precision == hip.PRECISION_FP32 else np.float16
             ik = [np.zeros((b, 8, n, 64), icl_dtype) for _ in range(12)]
             iv = [np.zeros_like(ik[0]) for _ in range(12)]
             for i in range(3):
@@ -303,18 +306,21 @@ class Executor:
     def _attach(self, context: cf.ContextFile, optimize: str | None = None) -> "StaticExecutor":
         """Upload a verified context for prediction (with_executor / with_cuda,
         cpu.rs:1745-1910). Its ICL storage decides the precision: FP32 caches
-        predict at "safe", FP16 caches at "auto"; an `optimize` that asks for
-        the other is an error (the reference's CUDA path would leave such a
-        context on its CPU, which this backend does not have)."""
+        predict at "safe", FP16 caches at "auto" (the default) or "fast" (the
+        file does not record which: the caller's level does); asking an FP32
+        context for "auto"/"fast" or an FP16 one for "safe" is an error (the
+        reference's CUDA path would leave such a context on its CPU, which
+        this backend does not have)."""
         meta = context.metadata
         b, n, _ = meta.shape
         icl = {context.tensor(f"icl.{i}.{kind}").dtype for i in range(12) for kind in ("key", "value")}
         cols = {context.tensor(f"column.{i}.{kind}").dtype for i in range(3) for kind in ("key", "value")}
         if cols != {np.dtype("<f4")} or len(icl) != 1:
             raise cf.ContextError("the context's column caches must be FP32 and its ICL caches of one type")
-        stored = "auto" if icl == {np.dtype("<f2")} else "safe"
-        if optimize is not None and optimize != stored:
-            raise cf.ContextError(f"the context stores its ICL cache for optimize={stored!r}, not {optimize!r}")
+        levels = ("auto", "fast") if icl == {np.dtype("<f2")} else ("safe",)
+        if optimize is not None and optimize not in levels:
+            raise cf.ContextError(f"the context stores its ICL cache for optimize={levels[0]!r}, not {optimize!r}")
+        stored = optimize if optimize is not None else levels[0]
         return StaticExecutor(self, meta.shape, meta.class_count, meta.class_permutations,
                               meta.feature_permutations, built=None, context=context.host_tensors(),
                               base_scales=self.icl_base_scales(n), metadata=meta, keep_alive=context,
@@ -404,7 +410,7 @@ class StaticExecutor:
         ctx.budget = executor.budget()
         keep_alive = []
         if built is None:
-            icl_dtype = np.float16 if precision == hip.PRECISION_SPLIT else np.float32
+            icl_dtype = np.float32 if precision == hip.PRECISION_FP32 else np.float16
             ck, cv = [[_f32(t) for t in part] for part in context[:2]]
             ik, iv = [[np.ascontiguousarray(t, dtype=icl_dtype) for t in part] for part in context[2:]]
             keep_alive = [ck, cv, ik, iv]
@@ -455,7 +461,8 @@ class StaticExecutor:
 
     def _tensor_source(self):
         """Values of each context tensor, from the host copy when there is one,
-        otherwise streamed out of HBM (irx_predictor_read_context)."""
+        otherwise streamed out of HBM (irx_predictor_read_context; a "fast"
+        build keeps its FP16 ICL cache there beside the FP8 one)."""
         if self.context is not None:
             ck, cv, ik, iv = self.context
             named = {}
@@ -489,13 +496,13 @@ class StaticExecutor:
         return self.metadata
 
     def _specs(self):
-        icl_dtype = np.float16 if self.precision == hip.PRECISION_SPLIT else np.float32
+        icl_dtype = np.float32 if self.precision == hip.PRECISION_FP32 else np.float16
         return cf.context_tensor_specs(*self.shape, icl_dtype)
 
     def save_context(self, path) -> None:
         """Write the context as an IRCNTXT file, atomically, streaming its
         tensors from HBM when no host copy exists (FP16 ICL tensors, version
-        2, for an optimize="auto" context)."""
+        2, for an optimize="auto" or "fast" context)."""
         meta = self._persistable()
         cf.write(path, meta, self._specs(), self._tensor_source())
 

@@ -10,6 +10,8 @@ import pytest
 
 from ironicl_amd import hip
 
+import fp8_np
+
 pytestmark = pytest.mark.gpu
 
 
@@ -110,6 +112,62 @@ def test_icl_attention_split_fp16_matches_float64(device, rows):
             worst16 = max(worst16, np.abs(out[pair, rows_sel] - want16).max())
             worst = max(worst, np.abs(out[pair, rows_sel] - want).max())
         assert worst16 < 2e-5, (rows, query_rows, worst16)
+        assert worst < 5e-3, (rows, query_rows, worst)
+
+
+@pytest.mark.parametrize("rows", [1, 63, 64, 65, 1000])
+def test_fp8_cache_encoding_matches_the_restatement(device, rows):
+    """The FP8 cache block (optimize="fast") byte for byte: E4M3 keys, V^T
+    tiles in the stored key order, zero padding, per-(pair, dim) scales."""
+    pairs = 8
+    rng = np.random.default_rng(rows)
+    k = (rng.normal(size=(pairs, rows, 64)) * rng.uniform(0.01, 30, size=(1, 1, 64))).astype(np.float16)
+    v = (rng.normal(size=(pairs, rows, 64)) * rng.uniform(0.01, 30, size=(1, 1, 64))).astype(np.float16)
+    k[:, :, 5] = 0  # an all-zero dim: scale 1
+    v[1, :, 7] = 2.0 ** -20  # subnormal FP16 values
+    n_pad = (rows + 63) // 64 * 64
+    block = np.zeros(2 * pairs * n_pad * 64 + 1024 * pairs, np.uint8)
+    hip.check(hip.lib().irx_test_encode_icl8(device.handle, k.ctypes.data, v.ctypes.data, pairs, rows,
+                                             block.ctypes.data))
+    plane = pairs * n_pad * 64
+    got_k = block[:plane].reshape(pairs, n_pad, 64)
+    got_vt = block[plane:2 * plane].reshape(pairs, n_pad // 64, 64, 64)
+    got_ks = block[2 * plane:2 * plane + 256 * pairs].view(np.float32).reshape(pairs, 64)
+    got_vs = block[2 * plane + 256 * pairs:2 * plane + 512 * pairs].view(np.float32).reshape(pairs, 64)
+    k8, vt, ks, vs = fp8_np.encode_block(k, v)
+    np.testing.assert_array_equal(got_ks, ks)
+    np.testing.assert_array_equal(got_vs, vs)
+    np.testing.assert_array_equal(got_k, k8)
+    np.testing.assert_array_equal(got_vt, vt)
+    assert np.all(got_ks[:, 5] == 1.0)
+
+
+@pytest.mark.parametrize("rows", [1, 63, 64, 65, 2000, 10007])
+def test_icl_attention_fp8_matches_float64(device, rows):
+    """Single FP16 products over the FP8 cache (optimize="fast"): against
+    float64 attention of the dequantized keys and values (byte x scale), within
+    the FP16 rounding of the scaled queries and of the probabilities."""
+    pairs = 16
+    k = fast_values(pairs * rows * 64, 2).reshape(pairs, rows, 64)
+    v = fast_values(pairs * rows * 64, 3).reshape(pairs, rows, 64)
+    k8, vt, ks, vs = fp8_np.encode_block(k.astype(np.float16), v.astype(np.float16))
+    kd = fp8_np.e4m3_value(k8[:, :rows]) * ks[:, None, :]
+    vq = np.zeros_like(k8)
+    key = np.arange(64)
+    pos = 16 * (key // 16) + fp8_np.stored_position(key % 16)
+    vq.reshape(pairs, -1, 64, 64)[:] = vt[:, :, :, pos].transpose(0, 1, 3, 2)
+    vd = fp8_np.e4m3_value(vq[:, :rows]) * vs[:, None, :]
+    for query_rows in (1, 5, 16, 17, 32, 40, 64, 300):
+        q = fast_values(pairs * query_rows * 64, 1, scale=3.0).reshape(pairs, query_rows, 64)
+        out = np.zeros_like(q)
+        F = hip.fptr
+        hip.check(hip.lib().irx_test_icl_attention_precision(device.handle, hip.PRECISION_HALF, F(q), F(k), F(v),
+                                                             pairs, query_rows, rows, F(out)))
+        worst = 0.0
+        for pair in (0, 7, 15):
+            rows_sel = sorted({0, query_rows // 2, query_rows - 1})
+            want = attention64(q[pair, rows_sel], kd[pair], vd[pair], 0.125)
+            worst = max(worst, np.abs(out[pair, rows_sel] - want).max())
         assert worst < 5e-3, (rows, query_rows, worst)
 
 
