@@ -343,6 +343,15 @@ int irx_test_block_tail(irx_device *device, int fused, const float *att, const f
                         const float *wo, const float *bo, const float *n2w, const float *n2b,
                         const float *w1, const float *b1, const float *w2, const float *b2,
                         size_t repeats, float *out);
+/* LayerNorm fused into a 512-wide product, x [m, 512], w [n, 512]:
+ * epilogue 1 (GELU): out [m, n] = gelu(LN(x) w^T + b); epilogue 2 (QASS, the
+ * ICL query path, n = 512): q = LN(x) w^T + b, then per head
+ * q * base[head] * (1 + tanh(gelu(q qm0w^T + qm0b) qm2w^T + qm2b)), into out
+ * head-major [m / rows, 8, rows, 64] (StaticExecutor::qass, cpu.rs:3798-3853). */
+int irx_test_ln_linear(irx_device *device, int epilogue, const float *x, size_t m, size_t rows,
+                       const float *lnw, const float *lnb, const float *w, const float *b, size_t n,
+                       const float *qm0w, const float *qm0b, const float *qm2w, const float *qm2b,
+                       const float *base, float *out);
 /* LayerNorm over width (128 or 512), eps 1e-5. */
 int irx_test_layer_norm(irx_device *device, const float *x, const float *weight, const float *bias,
                         size_t rows, size_t width, float *out);

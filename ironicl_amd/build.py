@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libironicl_hip.so")
-SOURCES = ["gemm.hip", "tail.hip", "attention.hip", "glue.hip", "preprocess.hip", "regression.hip", "cache8.hip", "runtime.hip"]
+SOURCES = ["gemm.hip", "tail.hip", "lnlinear.hip", "attention.hip", "glue.hip", "preprocess.hip", "regression.hip", "cache8.hip", "runtime.hip"]
 # The attention kernels take maxima of MFMA results; with IEEE mode off they
 # skip the NaN-quieting copy before every v_max (no NaN reaches a softmax:
 # inputs are checked finite and masked keys are -inf, not NaN).

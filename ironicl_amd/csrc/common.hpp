@@ -169,6 +169,25 @@ void regression_tables(const float *alphas, int n_alphas, int k, int *tail, std:
                        std::vector<RegressionLevel> &levels);
 void regression_summary(const RegressionSummary &s, hipStream_t stream);
 
+// epilogue(LN(x) W^T + b) over 512-wide rows x [m, 512] (W [n, 512]), the
+// LayerNorm in the product's prologue: kLnGelu writes gelu() row-major [m, n];
+// kLnQass (n = 512) runs each head's QASS query MLP and gate and writes
+// head-major [m / rows, 8, rows, 64]. For prediction-sized m.
+enum LnEpilogue : int { kLnGelu = 1, kLnQass = 2 };
+struct LnLinear {
+    const float *x;
+    long long ldx;
+    const float *lnw, *lnb;  // [512]; bias-free LayerNorms pass zeros
+    const float *w, *b;      // [n, 512], [n]
+    float *out;
+    long long ldo;           // kLnGelu: output row stride
+    int m, n;
+    const float *qm0w, *qm0b, *qm2w, *qm2b;  // kLnQass: [64, 64], [64] each
+    const float *base;                       // kLnQass: [8, 64]
+    int rows;                                // kLnQass: rows per estimator
+};
+void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream);
+
 // LayerNorm over `width` (128 or 512), eps 1e-5, two passes (reference.rs:223-252).
 void layer_norm(const float *x, long long ldx, const float *weight, const float *bias, float *y,
                 long long ldy, long long rows, int width, hipStream_t stream);

@@ -1,0 +1,178 @@
+// LayerNorm fused into the product that reads it, for 512-wide rows.
+//
+// y = epilogue(LN(x) W^T + b) over x [m, 512], with the LayerNorm of cpu.rs's
+// blocks (two-pass mean and variance, eps 1e-5, reference.rs:223-252) taken
+// in the product's prologue, and two epilogues:
+//   kLnGelu  gelu(y) into a row-major [m, n] output (LN2 + the FFN's first
+//            layer, cpu.rs:1585-1595; the decoder's, cpu.rs:2543-2580);
+//   kLnQass  the ICL query path, one 64-wide head per workgroup (n = 512):
+//            q = y, then the QASS query MLP per head, h = gelu(q Wm0^T + bm0),
+//            g = h Wm2^T + bm2, and the gate q * base[head] * (1 + tanh(g)),
+//            stored head-major [b, 8, rows, 64] (StaticExecutor::qass,
+//            cpu.rs:3798-3853; qassmax_f32, reference.rs:417-428).
+// It replaces, per ICL block of a prediction pass, LayerNorm + Q projection +
+// two QASS products (four launches), and LayerNorm + FFN up (two launches).
+//
+// A workgroup of four waves computes 16 rows x 64 columns; wave w reduces over
+// K = 128 w .. 128 w + 127 on v_mfma_f32_16x16x4f32 with the product
+// transposed (D = W x^T: lane (m, g) = (lane % 16, lane / 16) holds row m's
+// columns 16 b + 4 g + r in register r of block b). Each wave loads its rows'
+// quarter of x in that layout, the row statistics are summed over the four
+// waves through LDS, and the partial products are summed there too.
+#include "common.hpp"
+
+namespace irx {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 16;
+
+__device__ __forceinline__ f32x4 mfma(float a, float b, const f32x4 &acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
+    __shared__ float red[2][4][kRows];
+    __shared__ __attribute__((aligned(16))) float part[4][kRows][68];
+    __shared__ __attribute__((aligned(16))) float tile[2][kRows][68];  // QASS: q, then the hidden layer
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int m16 = lane & 15, g = lane >> 4;
+    const long long row0 = (long long)blockIdx.x * kRows;
+    const int col0 = 64 * blockIdx.y;
+    const long long row = row0 + m16;
+    const long long r = row < p.m ? row : p.m - 1;
+    const int k0 = 128 * w;
+
+    // x[row][k0 + 16 kb + 4 g + e], and every weight fragment of this wave's
+    // quarter up front (columns col0 + 16 ob + lane % 16): the loads' latency
+    // is paid once, under the LayerNorm.
+    f32x4 x[8], wf[8][4];
+    const float *xr = p.x + r * p.ldx + k0 + 4 * g;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) x[kb] = *reinterpret_cast<const f32x4 *>(xr + 16 * kb);
+    const float *wr = p.w + (long long)(col0 + m16) * 512 + k0 + 4 * g;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) wf[kb][ob] = *reinterpret_cast<const f32x4 *>(wr + ob * 16 * 512 + 16 * kb);
+    float s = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) s += (x[kb][0] + x[kb][1]) + (x[kb][2] + x[kb][3]);
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+    if (g == 0) red[0][w][m16] = s;
+    __syncthreads();
+    const float mean = ((red[0][0][m16] + red[0][1][m16]) + (red[0][2][m16] + red[0][3][m16])) / 512.f;
+    float sq = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float d = x[kb][e] - mean;
+            sq = fmaf(d, d, sq);
+        }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    if (g == 0) red[1][w][m16] = sq;
+    __syncthreads();
+    const float var = ((red[1][0][m16] + red[1][1][m16]) + (red[1][2][m16] + red[1][3][m16])) / 512.f;
+    const float rstd = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+        const f32x4 lw = *reinterpret_cast<const f32x4 *>(p.lnw + k0 + 16 * kb + 4 * g);
+        const f32x4 lb = *reinterpret_cast<const f32x4 *>(p.lnb + k0 + 16 * kb + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[kb][e] = (x[kb][e] - mean) * rstd * lw[e] + lb[e];
+    }
+
+    // This wave's quarter of the product: columns col0 + 16 ob + n, n = lane % 16.
+    f32x4 acc[4];
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int ob = 0; ob < 4; ++ob) acc[ob] = mfma(wf[kb][ob][e], x[kb][e], acc[ob]);
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob)
+        *reinterpret_cast<f32x4 *>(&part[w][m16][16 * ob + 4 * g]) = acc[ob];
+    __syncthreads();
+
+    // Thread t finishes row t / 16, columns 4 (t % 16) .. +3.
+    const int om = tid >> 4, oc = 4 * (tid & 15);
+    const long long orow = row0 + om;
+    f32x4 v = (*reinterpret_cast<const f32x4 *>(&part[0][om][oc]) + *reinterpret_cast<const f32x4 *>(&part[1][om][oc])) +
+              (*reinterpret_cast<const f32x4 *>(&part[2][om][oc]) + *reinterpret_cast<const f32x4 *>(&part[3][om][oc]));
+    v += *reinterpret_cast<const f32x4 *>(p.b + col0 + oc);
+    if constexpr (EPI == kLnGelu) {
+        if (orow < p.m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+            *reinterpret_cast<f32x4 *>(p.out + orow * p.ldo + col0 + oc) = v;
+        }
+    } else {
+        // The head's query tile, then its MLP: wave w computes columns 16 w .. 16 w + 15
+        // of each layer from the whole previous tile.
+        f32x4 mw[2][4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            mw[0][kb] = *reinterpret_cast<const f32x4 *>(p.qm0w + (16 * w + m16) * 64 + 16 * kb + 4 * g);
+            mw[1][kb] = *reinterpret_cast<const f32x4 *>(p.qm2w + (16 * w + m16) * 64 + 16 * kb + 4 * g);
+        }
+        *reinterpret_cast<f32x4 *>(&tile[0][om][oc]) = v;
+        __syncthreads();
+        auto layer = [&](const f32x4 *wt, const float *bias, int src) {
+            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const f32x4 xf = *reinterpret_cast<const f32x4 *>(&tile[src][m16][16 * kb + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a = mfma(wt[kb][e], xf[e], a);
+            }
+            return a + *reinterpret_cast<const f32x4 *>(bias + 16 * w + 4 * g);
+        };
+        f32x4 h = layer(mw[0], p.qm0b, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = gelu_erf(h[e]);
+        *reinterpret_cast<f32x4 *>(&tile[1][m16][16 * w + 4 * g]) = h;
+        __syncthreads();
+        const f32x4 gm = layer(mw[1], p.qm2b, 1);
+        if (row < p.m) {
+            const int head = blockIdx.y, col = 16 * w + 4 * g;
+            const f32x4 q = *reinterpret_cast<const f32x4 *>(&tile[0][m16][col]);
+            const f32x4 base = *reinterpret_cast<const f32x4 *>(p.base + head * 64 + col);
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = q[e] * base[e] * (1.0f + tanhf(gm[e]));
+            const long long b = row / p.rows, rr = row - b * p.rows;
+            *reinterpret_cast<f32x4 *>(p.out + (((b * kHeads + head) * p.rows + rr) * 64) + col) = o;
+        }
+    }
+}
+
+}  // namespace
+
+void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream) {
+    if (a.m <= 0) return;
+    if (a.n <= 0 || a.n % 64 || (epilogue == kLnQass && (a.n != 512 || a.rows <= 0)) ||
+        (epilogue != kLnQass && epilogue != kLnGelu))
+        fail(3, "ln_linear512: unsupported shape");
+    if ((a.ldx & 3) || (a.ldo & 3) || (reinterpret_cast<uintptr_t>(a.x) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.w) & 15) || (reinterpret_cast<uintptr_t>(a.out) & 15))
+        fail(3, "ln_linear512: rows must be 16-byte aligned");
+    const double m = a.m, n = a.n;
+    const double flops = 2.0 * m * n * 512 + (epilogue == kLnQass ? 2.0 * 2.0 * m * 8 * 64 * 64 : 0.0);
+    KernelTimer timer(kFamGemm, stream, flops, 4.0 * (m * 512 + n * 512 + m * n));
+    const dim3 grid((unsigned)ceil_div((size_t)a.m, kRows), (unsigned)(a.n / 64));
+    if (epilogue == kLnQass)
+        hipLaunchKernelGGL(ln_linear512_kernel<kLnQass>, grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(ln_linear512_kernel<kLnGelu>, grid, dim3(256), 0, stream, a);
+    IRX_HIP(hipGetLastError());
+}
+
+}  // namespace irx

@@ -267,6 +267,11 @@ void set_device(const irx_device *d) { IRX_HIP(hipSetDevice(d->ordinal)); }
 
 // ---- stages shared by the build and the predictor ----
 
+// Rows up to which 512-wide LayerNorms run fused into the product that reads
+// them (prediction passes); larger products (the build's N rows) keep the
+// tiled GEMMs, whose large tiles reuse the weights across rows.
+constexpr long long kLnLinearRows = 8192;
+
 struct Stages {
     const irx_weights &w;
     hipStream_t s;
@@ -300,6 +305,16 @@ struct Stages {
               int fused = -1) const {
         const int d = bw.dim;
         const bool use_fused = fused < 0 ? (d == 128 && bw.tail_pack && m >= 16384) : fused == 1;
+        if (d == 512 && m <= kLnLinearRows) {
+            // Prediction-sized 512-wide blocks: LN2 fused into the FFN's first product.
+            linear(att, d, m, d, bw.out.w, bw.out.b, d, state, d, kEpiResidual, state, d);
+            LnLinear f{};
+            f.x = state, f.ldx = d, f.lnw = bw.n2w, f.lnb = bw.n2b, f.w = bw.l1.w, f.b = bw.l1.b, f.out = hid;
+            f.ldo = 2 * d, f.m = (int)m, f.n = 2 * d;
+            ln_linear512(f, kLnGelu, s);
+            linear(hid, 2 * d, m, 2 * d, bw.l2.w, bw.l2.b, d, state, d, kEpiResidual, state, d);
+            return;
+        }
         if (use_fused) {
             if (d != 128 || !bw.tail_pack) fail(IRX_INVALID_ARGUMENT, "the fused tail needs a packed 128-wide block");
             Tail128 t{};
@@ -417,17 +432,26 @@ struct Stages {
                      const unsigned short *v16 = nullptr, const Icl8Block *c8 = nullptr) const {
         const BlockW &bw = w.icl[blk];
         const long long m = (long long)b * rows;
-        layer_norm(x, 512, bw.n1w, bw.n1b, r.norm, 512, m, 512, s);
-        // Q, head-major [b, 8, rows, 64].
-        OutMap qmap{64, kHeads, 0, (long long)rows * 64, rows, (long long)kHeads * rows * 64, 64};
-        linear_map(r.norm, 512, m, 512, bw.in_w, bw.in_b, 512, r.qh, qmap);
-        // QASSMax: q * base * (1 + tanh(MLP(q))) per head (reference.rs:417-428).
-        linear(r.qh, 64, m * kHeads, 64, bw.qm0.w, bw.qm0.b, 64, r.qhid, 64, kEpiGelu);
-        GemmArgs g{};
-        g.a = r.qhid, g.lda = 64, g.w = bw.qm2.w, g.bias = bw.qm2.b, g.residual = r.qh, g.ldr = 64;
-        g.qass_base = base, g.qass_rows = rows, g.c = r.qg, g.out = OutMap::row_major(64, 64);
-        g.m = (int)(m * kHeads), g.n = 64, g.k = 64, g.epilogue = kEpiQass;
-        gemm(g, s);
+        if (m <= kLnLinearRows) {
+            // LN1, Q projection and QASSMax in one launch, into qg head-major.
+            LnLinear f{};
+            f.x = x, f.ldx = 512, f.lnw = bw.n1w, f.lnb = bw.n1b, f.w = bw.in_w, f.b = bw.in_b, f.out = r.qg;
+            f.m = (int)m, f.n = 512, f.qm0w = bw.qm0.w, f.qm0b = bw.qm0.b, f.qm2w = bw.qm2.w, f.qm2b = bw.qm2.b;
+            f.base = base, f.rows = rows;
+            ln_linear512(f, kLnQass, s);
+        } else {
+            layer_norm(x, 512, bw.n1w, bw.n1b, r.norm, 512, m, 512, s);
+            // Q, head-major [b, 8, rows, 64].
+            OutMap qmap{64, kHeads, 0, (long long)rows * 64, rows, (long long)kHeads * rows * 64, 64};
+            linear_map(r.norm, 512, m, 512, bw.in_w, bw.in_b, 512, r.qh, qmap);
+            // QASSMax: q * base * (1 + tanh(MLP(q))) per head (reference.rs:417-428).
+            linear(r.qh, 64, m * kHeads, 64, bw.qm0.w, bw.qm0.b, 64, r.qhid, 64, kEpiGelu);
+            GemmArgs g{};
+            g.a = r.qhid, g.lda = 64, g.w = bw.qm2.w, g.bias = bw.qm2.b, g.residual = r.qh, g.ldr = 64;
+            g.qass_base = base, g.qass_rows = rows, g.c = r.qg, g.out = OutMap::row_major(64, 64);
+            g.m = (int)(m * kHeads), g.n = 64, g.k = 64, g.epilogue = kEpiQass;
+            gemm(g, s);
+        }
         IclAttention at{};
         at.q = r.qg, at.q_pair_stride = (long long)rows * 64, at.k = k, at.v = v;
         at.kv_pair_stride = (long long)kv_rows * 64, at.o = r.att, at.ldo = 512;
@@ -932,8 +956,15 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
         }
     }
     // Decoder (cached_icl_decoder, cpu.rs:2543-2580) into logits [B, Q, width].
-    layer_norm(rows, 512, W.ln_w, W.ln_b, ib.norm, 512, (long long)B * R, 512, s);
-    st.linear(ib.norm, 512, (long long)B * R, 512, W.dec0.w, W.dec0.b, 1024, ib.hid, 1024, kEpiGelu);
+    if ((long long)B * R <= kLnLinearRows) {
+        LnLinear f{};
+        f.x = rows, f.ldx = 512, f.lnw = W.ln_w, f.lnb = W.ln_b, f.w = W.dec0.w, f.b = W.dec0.b, f.out = ib.hid;
+        f.ldo = 1024, f.m = B * R, f.n = 1024;
+        ln_linear512(f, kLnGelu, s);
+    } else {
+        layer_norm(rows, 512, W.ln_w, W.ln_b, ib.norm, 512, (long long)B * R, 512, s);
+        st.linear(ib.norm, 512, (long long)B * R, 512, W.dec0.w, W.dec0.b, 1024, ib.hid, 1024, kEpiGelu);
+    }
     OutMap lmap{width, 1, 0, 0, R, (long long)Q * width, width};
     st.linear_map(ib.hid, 1024, (long long)B * R, 1024, W.dec2.w, W.dec2.b, width, d_logits + (size_t)q0 * width,
                   lmap);
@@ -1570,6 +1601,34 @@ int irx_test_block_tail(irx_device *device, int fused, const float *att, const f
         // Further applications (timing only) update the same state.
         for (size_t i = 1; i < repeats; ++i) st.tail(bw, dstate.f(), (long long)rows, datt.f(), dnorm.f(), dhid.f(), fused);
         IRX_HIP(hipDeviceSynchronize());
+    });
+}
+
+int irx_test_ln_linear(irx_device *device, int epilogue, const float *x, size_t m, size_t rows, const float *lnw,
+                       const float *lnb, const float *w, const float *b, size_t n, const float *qm0w,
+                       const float *qm0b, const float *qm2w, const float *qm2b, const float *base, float *out) {
+    return guarded("irx_test_ln_linear", [&] {
+        const bool qass = epilogue == kLnQass;
+        if (!device || !x || !m || !lnw || !lnb || !w || !b || !out || (epilogue != kLnGelu && !qass) ||
+            (qass && (n != 512 || !rows || m % rows || !qm0w || !qm0b || !qm2w || !qm2b || !base)) || !n || n % 64)
+            fail(IRX_INVALID_ARGUMENT, "LN-linear arguments do not match");
+        set_device(device);
+        auto up = [](const float *h, size_t count) {
+            DevBuf d(count * 4);
+            IRX_HIP(hipMemcpy(d.p, h, count * 4, hipMemcpyHostToDevice));
+            return d;
+        };
+        DevBuf dx = up(x, m * 512), dlw = up(lnw, 512), dlb = up(lnb, 512), dw = up(w, n * 512), db = up(b, n);
+        DevBuf d0w, d0b, d2w, d2b, dbase;
+        if (qass) d0w = up(qm0w, 64 * 64), d0b = up(qm0b, 64), d2w = up(qm2w, 64 * 64), d2b = up(qm2b, 64), dbase = up(base, 512);
+        DevBuf dout(m * n * 4);
+        LnLinear f{};
+        f.x = dx.f(), f.ldx = 512, f.lnw = dlw.f(), f.lnb = dlb.f(), f.w = dw.f(), f.b = db.f(), f.out = dout.f();
+        f.ldo = (long long)n, f.m = (int)m, f.n = (int)n;
+        if (qass) f.qm0w = d0w.f(), f.qm0b = d0b.f(), f.qm2w = d2w.f(), f.qm2b = d2b.f(), f.base = dbase.f(), f.rows = (int)rows;
+        ln_linear512(f, epilogue, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(out, dout.p, m * n * 4, hipMemcpyDeviceToHost));
     });
 }
 

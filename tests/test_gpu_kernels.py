@@ -231,6 +231,47 @@ def test_block_tail_matches_float64(device, rows, fused):
     assert np.abs(out.reshape(rows, 128) - want).max() < 2e-5
 
 
+def ln64(x, w, b):
+    x = x.astype(np.float64)
+    return (x - x.mean(1, keepdims=True)) / np.sqrt(x.var(1, keepdims=True) + 1e-5) * w + b
+
+
+@pytest.mark.parametrize("m,n", [(1, 512), (17, 1024), (512, 1024), (1000, 512)])
+def test_ln_linear_gelu_matches_float64(device, m, n):
+    """LN2 + FFN up (and the decoder's LN + first layer) in one kernel."""
+    x = fast_values(m * 512, 1, 3.0) + 0.25
+    lnw, lnb = fast_values(512, 2, 0.2) + 1.0, fast_values(512, 3, 0.1)
+    w, b = fast_values(n * 512, 4, 0.05), fast_values(n, 5, 0.1)
+    out = np.zeros(m * n, np.float32)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_ln_linear(device.handle, 1, F(x), m, 0, F(lnw), F(lnb), F(w), F(b), n,
+                                           None, None, None, None, None, F(out)))
+    want = gelu64(ln64(x.reshape(m, 512), lnw, lnb) @ w.reshape(n, 512).T.astype(np.float64) + b)
+    np.testing.assert_allclose(out.reshape(m, n), want, rtol=1e-4, atol=2e-5)
+
+
+@pytest.mark.parametrize("estimators,rows", [(1, 1), (1, 5), (2, 250), (3, 17)])
+def test_ln_linear_qass_matches_float64(device, estimators, rows):
+    """LN1 + Q projection + QASSMax (query MLP and gate per head), head-major."""
+    m = estimators * rows
+    x = fast_values(m * 512, 6, 3.0) - 0.1
+    lnw, lnb = fast_values(512, 7, 0.2) + 1.0, fast_values(512, 8, 0.1)
+    w, b = fast_values(512 * 512, 9, 0.05), fast_values(512, 10, 0.1)
+    m0w, m0b = fast_values(64 * 64, 11, 0.15), fast_values(64, 12, 0.1)
+    m2w, m2b = fast_values(64 * 64, 13, 0.15), fast_values(64, 14, 0.1)
+    base = fast_values(512, 15, 0.5) + 1.0
+    out = np.zeros(m * 512, np.float32)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_ln_linear(device.handle, 2, F(x), m, rows, F(lnw), F(lnb), F(w), F(b), 512,
+                                           F(m0w), F(m0b), F(m2w), F(m2b), F(base), F(out)))
+    q = ln64(x.reshape(m, 512), lnw, lnb) @ w.reshape(512, 512).T.astype(np.float64) + b
+    q = q.reshape(estimators, rows, 8, 64).transpose(0, 2, 1, 3)  # head-major
+    h = gelu64(q @ m0w.reshape(64, 64).T.astype(np.float64) + m0b)
+    g = h @ m2w.reshape(64, 64).T.astype(np.float64) + m2b
+    want = q * base.reshape(1, 8, 1, 64) * (1 + np.tanh(g))
+    np.testing.assert_allclose(out.reshape(estimators, 8, rows, 64), want, rtol=1e-4, atol=2e-5)
+
+
 @pytest.mark.parametrize("rows,width", [(1, 128), (333, 128), (1000, 512), (4, 512)])
 def test_layer_norm_matches_float64(device, rows, width):
     x = fast_values(rows * width, 4, 3.0) + 0.5
