@@ -333,6 +333,13 @@ int irx_test_encode_icl8(irx_device *device, const uint16_t *k, const uint16_t *
 int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1,
                       const float *w2, const float *b2, size_t rows, size_t width, size_t depth,
                       size_t width2, float *first, float *second);
+/* The pre-attention head of a 128-wide block on `rows` rows: out [rows,
+ * outputs] = LN1(x) w^T + b, LN1 with lnw / lnb, w [outputs, 128] (outputs
+ * 128, 256 or 384: the column blocks' queries, the CLS block's keys and
+ * values, the row blocks' Q/K/V). fused = 1 runs the one-kernel head, 0 a
+ * LayerNorm and a product. */
+int irx_test_block_head(irx_device *device, int fused, const float *x, size_t rows, const float *lnw,
+                        const float *lnb, const float *w, const float *b, size_t outputs, float *out);
 /* The post-attention half of a 128-wide block (cpu.rs:1555-1601) on `rows`
  * rows: s1 = state + (att wo^T + bo); out = s1 + (gelu(LN2(s1) w1^T + b1) w2^T + b2),
  * LN2 with n2w / n2b. fused = 1 runs the one-kernel tail, 0 the separate

@@ -142,6 +142,24 @@ struct Tail128 {
 void tail128_pack(const float *wo, const float *w1, const float *w2, float *out);
 void tail128(const Tail128 &t, hipStream_t stream);
 
+// Pre-attention head of a 128-wide block in one kernel: out = LN1(x) W^T + b
+// for nb = 8, 16 or 24 blocks of 16 outputs (W [16 nb, 128], packed by
+// head128_pack into head128_pack_floats(16 nb) floats).
+struct Head128 {
+    const float *x;  // [m, 128], row stride ldx
+    long long ldx;
+    const float *lnw, *lnb;  // [128]
+    const float *pack;
+    const float *b;          // [16 nb]
+    float *out;              // [m, 16 nb], row stride ldo
+    long long ldo;
+    long long m;
+    int nb;
+};
+size_t head128_pack_floats(int outputs);
+void head128_pack(const float *w, int outputs, float *out);
+void head128(const Head128 &h, hipStream_t stream);
+
 // Regression outputs of decoded quantiles [b, q, k] (k <= 4096) on the device
 // (quantiles::summarize, quantiles.rs:80-213): per query row, averaged over
 // the b estimators, the mean, the unbiased variance, the inverse CDF at each

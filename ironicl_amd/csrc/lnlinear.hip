@@ -16,11 +16,9 @@
 // A workgroup of four waves computes 16 rows x 64 columns; wave w reduces over
 // K = 128 w .. 128 w + 127 on v_mfma_f32_16x16x4f32 with the product
 // transposed (D = W x^T: lane (m, g) = (lane % 16, lane / 16) holds row m's
-// columns 16 b + 4 g + r in register r of block b). Each wave stages its
-// 32 KB of weights in LDS with coalesced direct loads (a fragment per lane
-// scattered over 16 rows fetched far slower), loads its rows' quarter of x
-// in that layout, the row statistics are summed over the four waves through
-// LDS, and the partial products are summed there too.
+// columns 16 b + 4 g + r in register r of block b). Each wave loads its rows'
+// quarter of x in that layout, the row statistics are summed over the four
+// waves through LDS, and the partial products are summed there too.
 #include "common.hpp"
 
 namespace irx {
@@ -34,13 +32,8 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, const f32x4 &acc) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 template <int EPI>
 __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
-    // Wave w's weights: columns col0 .. col0 + 63 (LDS rows) x K 128 w .. +127,
-    // 512-byte rows whose 16-byte chunk c is stored at c ^ (row % 16).
-    __shared__ __attribute__((aligned(16))) float wl[4][64 * 128];
     __shared__ float red[2][4][kRows];
     __shared__ __attribute__((aligned(16))) float part[4][kRows][68];
     __shared__ __attribute__((aligned(16))) float tile[2][kRows][68];  // QASS: q, then the hidden layer
@@ -52,25 +45,18 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
     const long long r = row < p.m ? row : p.m - 1;
     const int k0 = 128 * w;
 
-    // This wave's weights into LDS first (32 direct loads of 1 KB, two rows
-    // each: lane l fills row 2 i + l / 32, stored chunk l % 32), then
-    // x[row][k0 + 16 kb + 4 g + e]: the loads' latency is paid once, under
-    // the LayerNorm.
-    const int wv = __builtin_amdgcn_readfirstlane(w);
-    {
-        const int half = lane >> 5, c = lane & 31;
-        const float *src = p.w + (long long)col0 * 512 + 128 * wv;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int row = 2 * i + half;
-            __builtin_amdgcn_global_load_lds(src + row * 512 + 4 * (c ^ (row & 15)), (lds_void *)&wl[wv][i * 256], 16,
-                                             0, 0);
-        }
-    }
-    f32x4 x[8];
+    // x[row][k0 + 16 kb + 4 g + e], and every weight fragment of this wave's
+    // quarter up front (columns col0 + 16 ob + lane % 16): the loads' latency
+    // is paid once, under the LayerNorm.
+    f32x4 x[8], wf[8][4];
     const float *xr = p.x + r * p.ldx + k0 + 4 * g;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) x[kb] = *reinterpret_cast<const f32x4 *>(xr + 16 * kb);
+    const float *wr = p.w + (long long)(col0 + m16) * 512 + k0 + 4 * g;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) wf[kb][ob] = *reinterpret_cast<const f32x4 *>(wr + ob * 16 * 512 + 16 * kb);
     float s = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) s += (x[kb][0] + x[kb][1]) + (x[kb][2] + x[kb][3]);
@@ -101,24 +87,16 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
         for (int e = 0; e < 4; ++e) x[kb][e] = (x[kb][e] - mean) * rstd * lw[e] + lb[e];
     }
 
-    // This wave's quarter of the product: columns col0 + 16 ob + n, n = lane % 16,
-    // the weight fragment of (ob, kb) at LDS row 16 ob + n, chunk (4 kb + g) ^ n.
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's weights are in LDS
+    // This wave's quarter of the product: columns col0 + 16 ob + n, n = lane % 16.
     f32x4 acc[4];
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const float *wt = &wl[wv][m16 * 128];
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-        f32x4 wf[4];
-#pragma unroll
-        for (int ob = 0; ob < 4; ++ob)
-            wf[ob] = *reinterpret_cast<const f32x4 *>(wt + ob * 16 * 128 + 4 * ((4 * kb + g) ^ m16));
+    for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-            for (int ob = 0; ob < 4; ++ob) acc[ob] = mfma(wf[ob][e], x[kb][e], acc[ob]);
-    }
+            for (int ob = 0; ob < 4; ++ob) acc[ob] = mfma(wf[kb][ob][e], x[kb][e], acc[ob]);
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob)
         *reinterpret_cast<f32x4 *>(&part[w][m16][16 * ob + 4 * g]) = acc[ob];

@@ -206,6 +206,8 @@ struct BlockW {
     bool qass = false;
     Lin qm0, qm2;  // QASS query MLP, per head: hd -> 64 -> hd
     const float *tail_pack = nullptr;  // 128-wide blocks: out, linear1, linear2 packed for tail128
+    const float *head_pack = nullptr;  // 128-wide prediction blocks: the in_proj rows head128 needs
+    int head_nb = 0, head_row0 = 0;    // head128 output blocks of 16, first in_proj row
 };
 
 struct irx_weights {
@@ -286,6 +288,22 @@ struct Stages {
         gemm(g, s);
     }
 
+    // LN1 + the in_proj rows [head_row0, head_row0 + 16 head_nb) of a 128-wide
+    // block into out [m, ldo]: one fused launch from 16384 rows (as the tail),
+    // else LayerNorm into `norm` and a product.
+    void head(const BlockW &bw, const float *x, long long m, float *norm, float *out, long long ldo) const {
+        const int n = 16 * bw.head_nb;
+        if (bw.head_pack && m >= 16384) {
+            Head128 h{};
+            h.x = x, h.ldx = 128, h.lnw = bw.n1w, h.lnb = bw.n1b, h.pack = bw.head_pack;
+            h.b = bw.in_b + bw.head_row0, h.out = out, h.ldo = ldo, h.m = m, h.nb = bw.head_nb;
+            head128(h, s);
+            return;
+        }
+        layer_norm(x, 128, bw.n1w, bw.n1b, norm, 128, m, 128, s);
+        linear(norm, 128, m, 128, bw.in_w + (size_t)bw.head_row0 * 128, bw.in_b + bw.head_row0, n, out, ldo);
+    }
+
     void linear_map(const float *a, long long lda, long long m, int k, const float *wt, const float *b, int n,
                     float *c, const OutMap &map) const {
         GemmArgs g{};
@@ -337,8 +355,7 @@ struct Stages {
                        int group, long long group_stride, float *norm, float *q, float *att, float *hid) const {
         const BlockW &bw = w.col2[blk];
         const long long m = (long long)cols * rows;
-        layer_norm(state, kColumnDim, bw.n1w, bw.n1b, norm, kColumnDim, m, kColumnDim, s);
-        linear(norm, kColumnDim, m, kColumnDim, bw.in_w, bw.in_b, kColumnDim, q, kColumnDim);
+        head(bw, state, m, norm, q, kColumnDim);
         SmallAttention a{};
         a.q = q, a.q_seq = (long long)rows * kColumnDim, a.q_group = (long long)group * rows * kColumnDim;
         a.q_row = kColumnDim, a.q_head = kColumnHead;
@@ -375,8 +392,7 @@ struct Stages {
         build_rows(state, b, rows, h, w.cls, r.seq, s);
         for (int blk = 0; blk < 2; ++blk) {
             const BlockW &bw = w.row[blk];
-            layer_norm(r.seq, 128, bw.n1w, bw.n1b, r.norm, 128, m, 128, s);
-            linear(r.norm, 128, m, 128, bw.in_w, bw.in_b, 384, r.qkv, 384);
+            head(bw, r.seq, m, r.norm, r.qkv, 384);
             SmallAttention a{};
             a.q = r.qkv, a.k = r.qkv + 128, a.v = r.qkv + 256;
             a.q_seq = a.k_seq = a.v_seq = (long long)len * 384;
@@ -393,8 +409,7 @@ struct Stages {
         const BlockW &bw = w.row[2];
         const long long mc = seqs * kReserved;
         gather_cls(r.seq, seqs, len, r.cls, s);
-        layer_norm(r.seq, 128, bw.n1w, bw.n1b, r.norm, 128, m, 128, s);
-        linear(r.norm, 128, m, 128, bw.in_w + 128 * 128, bw.in_b + 128, 256, r.qkv, 256);
+        head(bw, r.seq, m, r.norm, r.qkv, 256);
         layer_norm(r.cls, 128, bw.n1w, bw.n1b, r.cnorm, 128, mc, 128, s);
         linear(r.cnorm, 128, mc, 128, bw.in_w, bw.in_b, 128, r.cq, 128);
         SmallAttention a{};
@@ -509,6 +524,16 @@ struct Loader {
         pending.push_back({&b.tail_pack, offset});
     }
 
+    // The in_proj rows [row0, row0 + outputs) of a 128-wide block in head128's fragment order.
+    void pack_head(BlockW &b, int row0, int outputs) {
+        const size_t w = offset_of(&b.in_w);
+        const size_t offset = (host.size() + 63) / 64 * 64;
+        host.resize(offset + head128_pack_floats(outputs), 0.f);
+        head128_pack(host.data() + w + (size_t)row0 * 128, outputs, host.data() + offset);
+        pending.push_back({&b.head_pack, offset});
+        b.head_nb = outputs / 16, b.head_row0 = row0;
+    }
+
     void block(BlockW &b, const std::string &prefix, int dim, bool qass) {
         const bool zb = task == IRX_TASK_REGRESSOR;  // bias-free LayerNorms (model.rs:273-280)
         b.dim = dim, b.qass = qass;
@@ -553,6 +578,10 @@ void weights_load(irx_weights *W, irx_tensor_lookup lookup, void *user) {
     }
     for (int b = 0; b < kRowBlocks; ++b)
         L.block(W->row[b], "row_interactor.tf_row.blocks." + std::to_string(b), 128, false);
+    // Heads fused with LN1 for prediction: the column blocks' queries, the row
+    // blocks' Q/K/V, the CLS block's K/V over every token.
+    for (int b = 0; b < kColumnBlocks; ++b) L.pack_head(W->col2[b], 0, 128);
+    for (int b = 0; b < kRowBlocks; ++b) L.pack_head(W->row[b], b + 1 < kRowBlocks ? 0 : 128, b + 1 < kRowBlocks ? 384 : 256);
     L.take("row_interactor.cls_tokens", 4 * 128, &W->cls);
     L.take("row_interactor.out_ln.weight", 128, &W->out_ln_w);
     L.take("row_interactor.out_ln.bias", 128, &W->out_ln_b, zb);
@@ -1565,6 +1594,40 @@ int irx_regression_summary(irx_device *device, const float *decoded, size_t ense
         rs.mean = mean, rs.variance = variance, rs.at_levels = n_levels ? at_levels : nullptr, rs.raw = raw;
         regression_summary(rs, nullptr);
         IRX_HIP(hipDeviceSynchronize());
+    });
+}
+
+int irx_test_block_head(irx_device *device, int fused, const float *x, size_t rows, const float *lnw,
+                        const float *lnb, const float *w, const float *b, size_t outputs, float *out) {
+    return guarded("irx_test_block_head", [&] {
+        if (!device || !x || !rows || !lnw || !lnb || !w || !b || !out || (fused != 0 && fused != 1) ||
+            (outputs != 128 && outputs != 256 && outputs != 384))
+            fail(IRX_INVALID_ARGUMENT, "block head arguments do not match");
+        set_device(device);
+        std::vector<float> pack(head128_pack_floats((int)outputs));
+        head128_pack(w, (int)outputs, pack.data());
+        auto up = [](const float *h, size_t count) {
+            DevBuf d(count * 4);
+            IRX_HIP(hipMemcpy(d.p, h, count * 4, hipMemcpyHostToDevice));
+            return d;
+        };
+        DevBuf dx = up(x, rows * 128), dlw = up(lnw, 128), dlb = up(lnb, 128), dw = up(w, outputs * 128);
+        DevBuf db = up(b, outputs), dp = up(pack.data(), pack.size()), dnorm(rows * 128 * 4), dout(rows * outputs * 4);
+        BlockW bw{};
+        bw.dim = 128, bw.n1w = dlw.f(), bw.n1b = dlb.f(), bw.in_w = dw.f(), bw.in_b = db.f();
+        bw.head_pack = fused ? dp.f() : nullptr, bw.head_nb = (int)outputs / 16, bw.head_row0 = 0;
+        irx_weights none;
+        Stages st{none, nullptr, device->compute_units};
+        if (fused) {
+            Head128 h{};
+            h.x = dx.f(), h.ldx = 128, h.lnw = dlw.f(), h.lnb = dlb.f(), h.pack = dp.f(), h.b = db.f();
+            h.out = dout.f(), h.ldo = (long long)outputs, h.m = (long long)rows, h.nb = (int)outputs / 16;
+            head128(h, nullptr);
+        } else {
+            st.head(bw, dx.f(), (long long)rows, dnorm.f(), dout.f(), (long long)outputs);
+        }
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(out, dout.p, rows * outputs * 4, hipMemcpyDeviceToHost));
     });
 }
 

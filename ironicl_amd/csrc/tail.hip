@@ -23,6 +23,8 @@
 // 16-byte read per lane of consecutive addresses (no bank conflicts).
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace irx {
 namespace {
 
@@ -192,7 +194,118 @@ __global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
     }
 }
 
+// The head of a 128-wide block: y = LN1(x) W^T + b over 16 NB outputs,
+// written row-major; the same per-wave layout as tail128, the fragments of W
+// in (k-block, output block) order streamed through the same LDS buffers.
+template <int NB>
+__global__ __launch_bounds__(256, 2) void head128_kernel(Head128 p) {
+    __shared__ __attribute__((aligned(16))) float buf[2][kChunkFloats];
+    constexpr int kFrags = 8 * NB, kHeadChunks = (kFrags + 31) / 32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
+    const long long row = (long long)blockIdx.x * kTailRows + wv * 16 + m16;
+    const bool live = row < p.m;
+    const long long r = live ? row : p.m - 1;
+    auto issue = [&](int chunk, int b) {
+        // A short last chunk still moves 32 KB: the pack is padded to whole chunks.
+        const float *src = p.pack + (long long)chunk * kChunkFloats + (8 * wv) * 256 + lane * 4;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_global_load_lds(src + i * 256, (lds_void *)&buf[b][(8 * wv + i) * 256], 16, 0, 0);
+    };
+    issue(0, 0);
+
+    f32x4 x[8];
+    const float *xr = p.x + r * p.ldx + 4 * g;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(xr + 16 * b);
+    // LN1 over the row's 128 features (lanes m, m + 16, m + 32, m + 48).
+    float sum = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) sum += (x[b][0] + x[b][1]) + (x[b][2] + x[b][3]);
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float mean = sum / 128.f;
+    float sq = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float d = x[b][e] - mean;
+            sq = fmaf(d, d, sq);
+        }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 w = *reinterpret_cast<const f32x4 *>(p.lnw + 16 * b + 4 * g);
+        const f32x4 bb = *reinterpret_cast<const f32x4 *>(p.lnb + 16 * b + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[b][e] = (x[b][e] - mean) * rstd * w[e] + bb[e];
+    }
+
+    f32x4 acc[NB];
+#pragma unroll
+    for (int ob = 0; ob < NB; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kHeadChunks; ++c) {
+        wait_vm();
+        __syncthreads();
+        if (c + 1 < kHeadChunks) issue(c + 1, (c + 1) & 1);
+        const float *frag = &buf[c & 1][lane * 4];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int f = 32 * c + i;
+            if (f < kFrags) {
+                const int kb = f / NB, ob = f % NB;
+                const f32x4 a = lds4(frag + i * 256);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[ob] = mfma(a[e], x[kb][e], acc[ob]);
+            }
+        }
+    }
+    if (!live) return;
+    float *out = p.out + row * p.ldo + 4 * g;
+#pragma unroll
+    for (int ob = 0; ob < NB; ++ob)
+        *reinterpret_cast<f32x4 *>(out + 16 * ob) = acc[ob] + *reinterpret_cast<const f32x4 *>(p.b + 16 * ob + 4 * g);
+}
+
 }  // namespace
+
+size_t head128_pack_floats(int outputs) { return (size_t)(8 * (outputs / 16) + 31) / 32 * kChunkFloats; }
+
+void head128_pack(const float *w, int outputs, float *out) {
+    const int nb = outputs / 16;
+    std::fill(out, out + head128_pack_floats(outputs), 0.f);
+    for (int kb = 0; kb < 8; ++kb)
+        for (int ob = 0; ob < nb; ++ob) {
+            float *dst = out + (size_t)(kb * nb + ob) * 256;
+            for (int l = 0; l < 64; ++l)
+                for (int e = 0; e < 4; ++e) dst[l * 4 + e] = w[(long long)(16 * ob + (l & 15)) * 128 + 16 * kb + 4 * (l >> 4) + e];
+        }
+}
+
+void head128(const Head128 &h, hipStream_t stream) {
+    if (h.m <= 0) return;
+    if (!h.x || !h.out || !h.pack || !h.lnw || !h.lnb || !h.b || (h.nb != 8 && h.nb != 16 && h.nb != 24))
+        fail(3, "head128: unsupported arguments");
+    if ((h.ldx & 3) || (h.ldo & 3) || (reinterpret_cast<uintptr_t>(h.x) & 15) ||
+        (reinterpret_cast<uintptr_t>(h.out) & 15) || (reinterpret_cast<uintptr_t>(h.pack) & 15))
+        fail(3, "head128: rows must be 16-byte aligned");
+    const double m = (double)h.m, n = 16.0 * h.nb;
+    KernelTimer timer(kFamGemm, stream, 2.0 * m * 128.0 * n, 4.0 * m * (128.0 + n) + 4.0 * 128.0 * n);
+    const dim3 grid((unsigned)ceil_div(h.m, (long long)kTailRows)), block(256);
+    if (h.nb == 8)
+        hipLaunchKernelGGL(head128_kernel<8>, grid, block, 0, stream, h);
+    else if (h.nb == 16)
+        hipLaunchKernelGGL(head128_kernel<16>, grid, block, 0, stream, h);
+    else
+        hipLaunchKernelGGL(head128_kernel<24>, grid, block, 0, stream, h);
+    IRX_HIP(hipGetLastError());
+}
 
 void tail128_pack(const float *wo, const float *w1, const float *w2, float *out) {
     // Fragment (rows r0.., columns c0..) of a row-major [.., ld] matrix:

@@ -110,6 +110,7 @@ SIGNATURES = {
     "irx_test_products": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _CF, _CF, _sz, _sz, _sz, _sz, _F, _F]),
     "irx_regression_summary": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _sz, _sz, _sz, _CF, _sz,
                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "irx_test_block_head": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _sz, _CF, _CF, _CF, _CF, _sz, _F]),
     "irx_test_block_tail": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _CF, _sz, _CF, _CF, _CF, _CF, _CF, _CF,
                                            _CF, _CF, _sz, _F]),
     "irx_test_ln_linear": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _sz, _sz, _CF, _CF, _CF, _CF, _sz, _CF,

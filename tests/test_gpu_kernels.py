@@ -212,6 +212,21 @@ def block_tail64(att, state, wo, bo, n2w, n2b, w1, b1, w2, b2):
     return s1 + (h @ w2.astype(np.float64).T + b2)
 
 
+@pytest.mark.parametrize("rows,outputs", [(1, 128), (65, 384), (1000, 256), (16411, 384), (17000, 128)])
+@pytest.mark.parametrize("fused", [0, 1])
+def test_block_head_matches_float64(device, rows, outputs, fused):
+    """LN1 + in_proj of a 128-wide block: the fused kernel and the two launches."""
+    x = fast_values(rows * 128, 21, 3.0) + 0.2
+    lnw, lnb = fast_values(128, 22, 0.2) + 1.0, fast_values(128, 23, 0.1)
+    w, b = fast_values(outputs * 128, 24, 0.09), fast_values(outputs, 25, 0.1)
+    out = np.zeros(rows * outputs, np.float32)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_block_head(device.handle, fused, F(x), rows, F(lnw), F(lnb), F(w), F(b), outputs,
+                                            F(out)))
+    want = ln64(x.reshape(rows, 128), lnw, lnb) @ w.reshape(outputs, 128).T.astype(np.float64) + b
+    np.testing.assert_allclose(out.reshape(rows, outputs), want, rtol=1e-4, atol=1e-5)
+
+
 @pytest.mark.parametrize("rows", [1, 17, 64, 65, 1000, 16411])
 @pytest.mark.parametrize("fused", [0, 1])
 def test_block_tail_matches_float64(device, rows, fused):
