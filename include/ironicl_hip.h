@@ -365,14 +365,23 @@ int irx_test_layer_norm(irx_device *device, const float *x, const float *weight,
 /* A plain device-to-device copy of `floats` floats by a one-float4-per-thread
  * kernel: the known-size reference for HBM traffic counters. */
 int irx_test_copy(irx_device *device, size_t floats);
-/* 16-wide-head attention: q [heads, query_rows, 16], k and v [heads, rows, 16]. */
 /* The Yeo-Johnson PowerTransformer fit alone (yeo_johnson.rs fit_power) on
  * each column of x [rows, columns] f64 as given: lambda_mean_scale [3, columns]
  * and, when not NULL, the fitted standardized values [rows, columns]. */
 int irx_test_power_fit(irx_device *device, const double *x, size_t rows, size_t columns, double *lambda_mean_scale,
                        double *fitted);
+/* 16-wide-head attention: q [heads, query_rows, 16], k and v [heads, rows, 16];
+ * more than 128 keys take the long-range kernel, with its key ranges split
+ * over workgroups when the heads do not fill the chip. */
 int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v,
                              size_t heads, size_t query_rows, size_t rows, float *out);
+/* The same with rotary position embedding of queries and keys (the row
+ * transformer's, rope_non_interleaved_f32, reference.rs:433-475): dim d of
+ * the token at position t becomes x[d] cos[t][d] + x[d ^ 8] sin[t][d], with
+ * tables [max(query_rows, rows), 16] (sin signed). */
+int irx_test_small_attention_rope(irx_device *device, const float *q, const float *k, const float *v,
+                                  const float *rope_cos, const float *rope_sin, size_t heads, size_t query_rows,
+                                  size_t rows, float *out);
 
 #ifdef __cplusplus
 }

@@ -1098,10 +1098,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
         }
     };
 
-    // Two register sets in turn; loads past the range re-read the last
-    // block of the padded cache (cached rows, results unused).
+    // Two register sets in turn; loads past the range re-read the range's
+    // own last block (just loaded, so served by the cache; results unused).
+    // Clamping to the end of the whole cache instead would fetch one round of
+    // the next range's keys per workgroup from HBM: a seventh more traffic at
+    // 896 keys per range.
     u32x4 k_a[4], v_a[4], k_b[4], v_b[4];
-    const int last = n_pad - 32;
+    const int last = min(n_pad, (k_end + 31) / 32 * 32) - 32;
     int k0 = k_begin + 32 * wave;
     load(min(k0, last), k_a, v_a);
     while (k0 < k_end) {
@@ -1264,119 +1267,226 @@ IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units, bool f
     return g;
 }
 
-// ---- 16-wide heads on the vector ALUs ----
+// ---- 16-wide heads on matrix cores, many keys ----
+//
+// The inducing points of the column stage (128 queries per column and head)
+// attend to every train row of the column (multihead_attn1 of the ISAB,
+// cpu.rs:1180-1207), and a row's tokens attend to each other when the row
+// has more than 128. One workgroup of four waves per (sequence, head, chunk
+// of up to 128 queries, key range): wave w takes the range's 16-key blocks
+// w, w + 4, ... for all of the chunk's queries, with the lazy running
+// softmax of the ICL decode kernel (exp2 against a reference maximum that is
+// raised only when a sum passes 2^64), and the four waves' results are
+// merged through LDS. Products on v_mfma_f32_16x16x4f32:
+//   S^T (16 keys x 16 queries): K-step st pairs lane group g with dim 4 g +
+//     st, so a lane's K operands over the four steps are one 16-byte load
+//     (key lane % 16, dims 4 g .. +3), and so are its Q operands; register r
+//     of lane (j, g) is key 4 g + r, query j;
+//   O^T (16 dims x 16 queries): step i puts key 4 g + i in k slot g, so the
+//     score registers are the B operand as they are and lane (d, g) loads
+//     V[4 g + i][d]; register r of lane (j, g) is dim 4 g + r of query j.
+// When the chunks do not fill the chip the keys are also split over
+// workgroups, which write normalised partial outputs and their log2 sums
+// into the caller's partial buffer for small_merge_kernel.
+constexpr int kLongWaves = 4;
+constexpr int kLongQueries = 128;
+constexpr int kLongOStride = 20;  // LDS rows of 16 outputs, padded
 
-constexpr int kSmallChunk = 64;
+template <int QG, bool ROPE>
+__global__ __launch_bounds__(64 * kLongWaves) void small_attention_long_kernel(SmallAttention p, int qchunks,
+                                                                               int splits, int keys_per_split) {
+    __shared__ __attribute__((aligned(16))) float red_o[kLongWaves][QG * 16 * kLongOStride];
+    __shared__ float red_m[kLongWaves][QG * 16], red_l[kLongWaves][QG * 16];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+    const int split = blockIdx.x % splits;
+    const int unit = blockIdx.x / splits;
+    const int qc = unit % qchunks, item = unit / qchunks;
+    const int head = item % p.heads, seq = item / p.heads;
+    const int gs = seq / p.group, sq = seq - gs * p.group;
+    const float *qb = p.q + gs * p.q_group + sq * p.q_seq + head * p.q_head;
+    const float *kb = p.k + gs * p.k_group + sq * p.k_seq + head * p.k_head;
+    const float *vb = p.v + gs * p.v_group + sq * p.v_seq + head * p.v_head;
+    const int k_begin = split * keys_per_split;
+    const int k_end = min(p.kv_rows, k_begin + keys_per_split);
+    const int q0 = qc * kLongQueries;
 
-__global__ __launch_bounds__(64) void small_attention_kernel(SmallAttention p, int qtiles) {
-    __shared__ __attribute__((aligned(16))) float Ks[kSmallChunk * 16];
-    __shared__ __attribute__((aligned(16))) float Vs[kSmallChunk * 16];
-    const int bid = blockIdx.x;
-    const int qt = bid % qtiles;
-    const int head = (bid / qtiles) % p.heads;
-    const int seq = bid / (qtiles * p.heads);
-    const int lane = threadIdx.x;
-    const int row = qt * 64 + lane;
-    const int gq = seq / p.group, sq = seq - gq * p.group;
-    const float *qb = p.q + gq * p.q_group + sq * p.q_seq + head * p.q_head;
-    const float *kb = p.k + gq * p.k_group + sq * p.k_seq + head * p.k_head;
-    const float *vb = p.v + gq * p.v_group + sq * p.v_seq + head * p.v_head;
-
-    float q[16], o[16];
-    const float scale = p.scale * kLog2e;
-    if (row < p.q_rows) {
-        const float *src = qb + (long long)row * p.q_row;
+    // Queries: lane (j, g) holds dims 4 g .. +3 of query q0 + 16 gq + j, RoPE'd and scaled.
+    f32x4 qf[QG];
+    {
+        const float scale = p.scale * kLog2e;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            f32x4 v = *reinterpret_cast<const f32x4 *>(src + 4 * c);
-            q[4 * c] = v[0], q[4 * c + 1] = v[1], q[4 * c + 2] = v[2], q[4 * c + 3] = v[3];
+        for (int gq = 0; gq < QG; ++gq) {
+            const int row = q0 + 16 * gq + l16;
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if (row < p.q_rows) {
+                const float *src = qb + (long long)row * p.q_row;
+                x = *reinterpret_cast<const f32x4 *>(src + 4 * g);
+                if constexpr (ROPE) {
+                    // dims (4 g + e) ^ 8 = (4 g ^ 8) + e
+                    const f32x4 y = *reinterpret_cast<const f32x4 *>(src + (4 * g ^ 8));
+                    const f32x4 c = *reinterpret_cast<const f32x4 *>(p.rope_cos + row * 16 + 4 * g);
+                    const f32x4 s = *reinterpret_cast<const f32x4 *>(p.rope_sin + row * 16 + 4 * g);
+                    x = x * c + y * s;
+                }
+            }
+            qf[gq] = x * scale;
         }
-        if (p.rope_cos) {
-            float r[16];
-            const float *cs = p.rope_cos + row * 16, *sn = p.rope_sin + row * 16;
-#pragma unroll
-            for (int d = 0; d < 16; ++d) r[d] = q[d] * cs[d] + q[d ^ 8] * sn[d];
-#pragma unroll
-            for (int d = 0; d < 16; ++d) q[d] = r[d];
+    }
+
+    // Block at kk: K dims 4 g .. +3 of key kk + lane % 16, and V dim lane % 16
+    // of keys kk + 4 g + i. Keys past the range repeat its last key (masked).
+    auto load = [&](int kk, f32x4 &kd, f32x4 &vd) {
+        const int key = min(kk + l16, k_end - 1);
+        const float *ks = kb + (long long)key * p.k_row;
+        kd = *reinterpret_cast<const f32x4 *>(ks + 4 * g);
+        if constexpr (ROPE) {
+            const f32x4 y = *reinterpret_cast<const f32x4 *>(ks + (4 * g ^ 8));
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(p.rope_cos + key * 16 + 4 * g);
+            const f32x4 s = *reinterpret_cast<const f32x4 *>(p.rope_sin + key * 16 + 4 * g);
+            kd = kd * c + y * s;
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vd[i] = vb[(long long)min(kk + 4 * g + i, k_end - 1) * p.v_row + l16];
+    };
+
+    f32x4 o[QG];
+    float neg_ref[QG], m_ref[QG], l_run[QG];
+#pragma unroll
+    for (int gq = 0; gq < QG; ++gq) {
+        o[gq] = f32x4{0.f, 0.f, 0.f, 0.f};
+        neg_ref[gq] = INFINITY, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
+    }
+    constexpr float kLazyLimit = 18446744073709551616.0f;  // 2^64
+    constexpr int kStride = 16 * kLongWaves;
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+    auto process = [&](int kk, const f32x4 &kf, const f32x4 &vf) {
+        const bool tail = kk + 16 > k_end;
+#pragma unroll
+        for (int gq = 0; gq < QG; ++gq) {
+            auto scores = [&](const f32x4 &init) {
+                f32x4 s = init;
+#pragma unroll
+                for (int st = 0; st < 4; ++st) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[gq][st], s, 0, 0, 0);
+                if (tail) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (kk + 4 * g + r >= k_end) s[r] = -INFINITY;
+                }
+                return s;
+            };
+            f32x4 s = scores(f32x4{neg_ref[gq], neg_ref[gq], neg_ref[gq], neg_ref[gq]});
+            float lsum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[r] = __builtin_amdgcn_exp2f(s[r]);
+                lsum += s[r];
+            }
+            if (__any(!(lsum <= kLazyLimit))) {
+                const f32x4 t = scores(zero4);
+                float mt = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
+                mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+                mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                const float m_new = fmaxf(m_ref[gq], mt);
+                const float alpha = __builtin_amdgcn_exp2f(m_ref[gq] - m_new);
+                l_run[gq] *= alpha;
+                o[gq] *= alpha;
+                neg_ref[gq] = -m_new;
+                m_ref[gq] = m_new;
+                lsum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    s[r] = __builtin_amdgcn_exp2f(t[r] - m_new);
+                    lsum += s[r];
+                }
+            }
+            l_run[gq] += lsum;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[gq] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[i], s[i], o[gq], 0, 0, 0);
+        }
+    };
+
+    // Two register sets in turn: the next block's loads are issued before the
+    // current block's products.
+    f32x4 k_a, v_a, k_b, v_b;
+    int kk = k_begin + 16 * wave;
+    load(kk, k_a, v_a);
+    while (kk < k_end) {
+        load(kk + kStride, k_b, v_b);
+        process(kk, k_a, v_a);
+        kk += kStride;
+        if (kk >= k_end) break;
+        load(kk + kStride, k_a, v_a);
+        process(kk, k_b, v_b);
+        kk += kStride;
+    }
+
+    // Each wave's (reference, sum, unnormalised output) per query to LDS.
+#pragma unroll
+    for (int gq = 0; gq < QG; ++gq) {
+        float l = l_run[gq];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const int qi = 16 * gq + l16;
+        if (g == 0) red_m[wave][qi] = m_ref[gq], red_l[wave][qi] = l;
+        *reinterpret_cast<f32x4 *>(&red_o[wave][qi * kLongOStride + 4 * g]) = o[gq];
+    }
+    __syncthreads();
+    // Merge: thread t takes query t / 2 of the chunk, dims 8 (t % 2) .. +7. A
+    // wave that got no block has reference -inf and sum 0; wave 0 always has one.
+    const int qi = threadIdx.x >> 1, d0 = 8 * (threadIdx.x & 1);
+    const int row = q0 + qi;
+    if (qi >= QG * 16 || row >= p.q_rows) return;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kLongWaves; ++w) mx = fmaxf(mx, red_m[w][qi]);
+    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+    float den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kLongWaves; ++w) {
+        const float wgt = __builtin_amdgcn_exp2f(red_m[w][qi] - mx);
+        a0 += wgt * *reinterpret_cast<const f32x4 *>(&red_o[w][qi * kLongOStride + d0]);
+        a1 += wgt * *reinterpret_cast<const f32x4 *>(&red_o[w][qi * kLongOStride + d0 + 4]);
+        den += wgt * red_l[w][qi];
+    }
+    const float inv = 1.0f / den;
+    float *dst;
+    if (splits == 1) {
+        dst = p.o + gs * p.o_group + sq * p.o_seq + (long long)row * p.o_row + head * p.o_head + d0;
     } else {
-#pragma unroll
-        for (int d = 0; d < 16; ++d) q[d] = 0.f;
+        const long long prow = ((long long)split * p.seqs * p.heads + item) * p.q_rows + row;
+        dst = p.partial + prow * 16 + d0;
+        if (d0 == 0) p.partial[(long long)splits * p.seqs * p.heads * p.q_rows * 16 + prow] = mx + log2f(den);
     }
-#pragma unroll
-    for (int d = 0; d < 16; ++d) q[d] *= scale, o[d] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    *reinterpret_cast<f32x4 *>(dst) = a0 * inv;
+    *reinterpret_cast<f32x4 *>(dst + 4) = a1 * inv;
+}
 
-    for (int k0 = 0; k0 < p.kv_rows; k0 += kSmallChunk) {
-        const int count = min(kSmallChunk, p.kv_rows - k0);
-        __syncthreads();
-        if (lane < count) {
-            const int key = k0 + lane;
-            const float *ks = kb + (long long)key * p.k_row;
-            const float *vs = vb + (long long)key * p.v_row;
-            float kr[16];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                f32x4 v = *reinterpret_cast<const f32x4 *>(ks + 4 * c);
-                kr[4 * c] = v[0], kr[4 * c + 1] = v[1], kr[4 * c + 2] = v[2], kr[4 * c + 3] = v[3];
-                *reinterpret_cast<f32x4 *>(&Vs[lane * 16 + 4 * c]) = *reinterpret_cast<const f32x4 *>(vs + 4 * c);
-            }
-            if (p.rope_cos) {
-                const float *cs = p.rope_cos + key * 16, *sn = p.rope_sin + key * 16;
-                float r[16];
-#pragma unroll
-                for (int d = 0; d < 16; ++d) r[d] = kr[d] * cs[d] + kr[d ^ 8] * sn[d];
-#pragma unroll
-                for (int d = 0; d < 16; ++d) kr[d] = r[d];
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                *reinterpret_cast<f32x4 *>(&Ks[lane * 16 + 4 * c]) =
-                    f32x4{kr[4 * c], kr[4 * c + 1], kr[4 * c + 2], kr[4 * c + 3]};
-        }
-        __syncthreads();
-        for (int j0 = 0; j0 < count; j0 += 16) {
-            const int nj = min(16, count - j0);
-            float s[16];
-            float mt = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                if (j < nj) {
-                    const float *kr = &Ks[(j0 + j) * 16];
-                    float acc = 0.f;
-#pragma unroll
-                    for (int d = 0; d < 16; ++d) acc = fmaf(q[d], kr[d], acc);
-                    s[j] = acc;
-                } else {
-                    s[j] = -INFINITY;
-                }
-                mt = fmaxf(mt, s[j]);
-            }
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int d = 0; d < 16; ++d) o[d] *= alpha;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                if (j < nj) {
-                    const float e = __builtin_amdgcn_exp2f(s[j] - m_new);
-                    l_run += e;
-                    const float *vr = &Vs[(j0 + j) * 16];
-#pragma unroll
-                    for (int d = 0; d < 16; ++d) o[d] = fmaf(e, vr[d], o[d]);
-                }
-            }
-        }
+// Combines the key ranges of small_attention_long_kernel: thread per (sequence
+// and head, query, four dims).
+__global__ __launch_bounds__(256) void small_merge_kernel(SmallAttention p, int splits) {
+    const long long items = (long long)p.seqs * p.heads;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int c = (int)(idx & 3);
+    const long long unit = idx >> 2;
+    if (unit >= items * p.q_rows) return;
+    const int row = (int)(unit % p.q_rows);
+    const long long item = unit / p.q_rows;
+    const long long stride = items * p.q_rows;
+    const float *lse = p.partial + (long long)splits * stride * 16;
+    float mx = -INFINITY;
+    for (int s = 0; s < splits; ++s) mx = fmaxf(mx, lse[s * stride + unit]);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    for (int s = 0; s < splits; ++s) {
+        const float wgt = __builtin_amdgcn_exp2f(lse[s * stride + unit] - mx);
+        acc += wgt * *reinterpret_cast<const f32x4 *>(p.partial + (s * stride + unit) * 16 + 4 * c);
+        den += wgt;
     }
-    if (row >= p.q_rows) return;
-    const float inv = 1.0f / l_run;
-    float *dst = p.o + gq * p.o_group + sq * p.o_seq + (long long)row * p.o_row + head * p.o_head;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<f32x4 *>(dst + 4 * c) =
-            f32x4{o[4 * c] * inv, o[4 * c + 1] * inv, o[4 * c + 2] * inv, o[4 * c + 3] * inv};
+    const int head = (int)(item % p.heads), seq = (int)(item / p.heads);
+    const int gs = seq / p.group, sq = seq - gs * p.group;
+    float *dst = p.o + gs * p.o_group + sq * p.o_seq + (long long)row * p.o_row + head * p.o_head + 4 * c;
+    *reinterpret_cast<f32x4 *>(dst) = acc * (1.0f / den);
 }
 
 // ---- 16-wide heads on matrix cores, up to 128 keys ----
@@ -1654,6 +1764,29 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
     }
 }
 
+// Launch shape of small_attention_long_kernel: one workgroup per (sequence,
+// head, query chunk), and the keys split until about two workgroups per CU
+// are in flight (ranges of at least 512 keys, in whole rounds of the four
+// waves' 16-key blocks).
+struct LongPlan {
+    long long units;
+    int qchunks, splits, keys_per_split;
+    long long partial_floats;
+};
+
+LongPlan plan_long(const SmallAttention &a) {
+    LongPlan p{};
+    p.qchunks = (int)ceil_div(a.q_rows, kLongQueries);
+    p.units = (long long)a.seqs * a.heads * p.qchunks;
+    const long long want = ceil_div(2LL * 256, p.units);
+    const int splits = (int)std::max<long long>(1, std::min<long long>({want, 64, a.kv_rows / 512}));
+    const int round = 16 * kLongWaves;
+    p.keys_per_split = (int)ceil_div(ceil_div(a.kv_rows, splits), round) * round;
+    p.splits = (int)ceil_div(a.kv_rows, p.keys_per_split);
+    p.partial_floats = (long long)p.splits * a.seqs * a.heads * a.q_rows * 17;
+    return p;
+}
+
 void small_attention(const SmallAttention &args, hipStream_t stream) {
     if (args.seqs <= 0 || args.q_rows <= 0) return;
     if (args.kv_rows <= 0 || args.group <= 0) fail(3, "small attention needs keys and a group size");
@@ -1698,12 +1831,42 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
         IRX_SMALL_CASE(4, 8, 4)
 #undef IRX_SMALL_CASE
     } else {
-        int qtiles = (int)ceil_div(args.q_rows, 64);
-        long long blocks = (long long)qtiles * args.heads * args.seqs;
+        const LongPlan plan = plan_long(args);
+        const bool split = plan.splits > 1 && args.partial && args.partial_floats >= plan.partial_floats;
+        const int splits = split ? plan.splits : 1;
+        const int per = split ? plan.keys_per_split : args.kv_rows;
+        const long long blocks = plan.units * splits;
         if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
-        hipLaunchKernelGGL(small_attention_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, args, qtiles);
+        const bool rope = args.rope_cos != nullptr;
+        const int qg = args.q_rows >= kLongQueries ? 8 : (args.q_rows > 32 ? 4 : (args.q_rows > 16 ? 2 : 1));
+#define IRX_LONG_CASE(QG)                                                                                      \
+    if (qg == QG) {                                                                                            \
+        if (rope)                                                                                              \
+            hipLaunchKernelGGL((small_attention_long_kernel<QG, true>), dim3((unsigned)blocks),                \
+                               dim3(64 * kLongWaves), 0, stream, args, plan.qchunks, splits, per);             \
+        else                                                                                                   \
+            hipLaunchKernelGGL((small_attention_long_kernel<QG, false>), dim3((unsigned)blocks),               \
+                               dim3(64 * kLongWaves), 0, stream, args, plan.qchunks, splits, per);             \
+    }
+        IRX_LONG_CASE(1)
+        IRX_LONG_CASE(2)
+        IRX_LONG_CASE(4)
+        IRX_LONG_CASE(8)
+#undef IRX_LONG_CASE
+        IRX_HIP(hipGetLastError());
+        if (split) {
+            const long long threads = (long long)args.seqs * args.heads * args.q_rows * 4;
+            hipLaunchKernelGGL(small_merge_kernel, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, stream, args,
+                               splits);
+        }
     }
     IRX_HIP(hipGetLastError());
+}
+
+long long small_attention_partial_floats(const SmallAttention &args) {
+    if (args.kv_rows <= kShortKeys || args.seqs <= 0 || args.q_rows <= 0) return 0;
+    const LongPlan plan = plan_long(args);
+    return plan.splits > 1 ? plan.partial_floats : 0;
 }
 
 void pack_icl16(const void *k, const void *v, bool src_f16, long long rows, int pairs, unsigned short *k16,

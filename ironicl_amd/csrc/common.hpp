@@ -225,8 +225,13 @@ struct SmallAttention {
     int q_rows, kv_rows;
     float scale;         // 1/sqrt(16)
     const float *rope_cos, *rope_sin;  // [positions, 16] tables or null
+    // More than 128 keys: room for key ranges split over workgroups (null: no
+    // split); small_attention_partial_floats gives the size that allows them.
+    float *partial;
+    long long partial_floats;
 };
 void small_attention(const SmallAttention &args, hipStream_t stream);
+long long small_attention_partial_floats(const SmallAttention &args);
 
 // ICL attention of 64-wide heads: Q [pairs, q_rows, 64] (head-major, q_stride
 // between pairs), K and V [pairs, kv_rows, 64]; the output goes to tokens

@@ -616,10 +616,18 @@ struct BuildPlan {
     size_t keep_bytes;
 };
 
+// Partial outputs of the inducing points' attention over `cols` columns when
+// its keys are split over workgroups: at most ceil(512 / units) splits of
+// units = cols x heads (sequence, head) items, 17 floats per query.
+size_t inducing_partial_floats(int cols) {
+    return (size_t)(512 + (long long)kHeads * cols) * kInducing * 17;
+}
+
 size_t column_chunk_floats(int cols, long long n) {
     long long cn = (long long)cols * n;
     // state is per estimator; chunk temporaries: norm, q, att (128) + kv, hid (256)
-    return (size_t)(cn * (128 * 3 + 256 * 2) + (long long)cols * 128 * (128 * 4 + 256));
+    return (size_t)(cn * (128 * 3 + 256 * 2) + (long long)cols * 128 * (128 * 4 + 256)) +
+           inducing_partial_floats(cols);
 }
 
 size_t row_run_floats(long long seqs, int len) {
@@ -758,6 +766,8 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
             float *kv = ws.take(cn * 256), *hid = ws.take(cn * 256);
             float *hidden = ws.take((size_t)C * 128 * 128), *hnorm = ws.take((size_t)C * 128 * 128);
             float *hatt = ws.take((size_t)C * 128 * 128), *hhid = ws.take((size_t)C * 128 * 256);
+            const size_t spart_floats = inducing_partial_floats(C);
+            float *spart = ws.take(spart_floats);
             column_input(d_x, 0, 1, N, H, W->in_w, W->in_b, d_ylab, d_state, nullptr, s);
             for (int f0 = 0; f0 < H; f0 += C) {
                 const int cols = std::min(C, H - f0);
@@ -775,6 +785,7 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
                     a.o = hatt, a.o_seq = 128 * 128, a.o_group = 0, a.o_row = 128, a.o_head = 16;
                     a.group = cols, a.seqs = cols, a.heads = kHeads, a.q_rows = kInducing, a.kv_rows = N;
                     a.scale = 0.25f;
+                    a.partial = spart, a.partial_floats = (long long)spart_floats;
                     small_attention(a, s);
                     repeat_rows(W->ind[blk], 128 * 128, cols, hidden, s);
                     st.tail(b1, hidden, (long long)cols * 128, hatt, hnorm, hhid);
@@ -1723,28 +1734,59 @@ int irx_test_copy(irx_device *device, size_t floats) {
     });
 }
 
+namespace {
+
+// Heads [heads, rows, 16] of one sequence; RoPE tables [max(query_rows, rows), 16] or null.
+void test_small_attention(irx_device *device, const float *q, const float *k, const float *v, const float *cos_t,
+                          const float *sin_t, size_t heads, size_t query_rows, size_t rows, float *out) {
+    if (!device || !q || !k || !v || !out || !heads || !query_rows || !rows || heads > 64 ||
+        query_rows > (1u << 20) || rows > (1u << 24) || (!cos_t) != (!sin_t))
+        fail(IRX_INVALID_ARGUMENT, "small attention shapes do not match");
+    set_device(device);
+    const size_t qn = heads * query_rows * 16, kn = heads * rows * 16, tn = std::max(query_rows, rows) * 16;
+    DevBuf dq(qn * 4), dk(kn * 4), dv(kn * 4), dout(qn * 4), dcos, dsin;
+    IRX_HIP(hipMemcpy(dq.p, q, qn * 4, hipMemcpyHostToDevice));
+    IRX_HIP(hipMemcpy(dk.p, k, kn * 4, hipMemcpyHostToDevice));
+    IRX_HIP(hipMemcpy(dv.p, v, kn * 4, hipMemcpyHostToDevice));
+    SmallAttention a{};
+    if (cos_t) {
+        dcos.alloc(tn * 4), dsin.alloc(tn * 4);
+        IRX_HIP(hipMemcpy(dcos.p, cos_t, tn * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dsin.p, sin_t, tn * 4, hipMemcpyHostToDevice));
+        a.rope_cos = dcos.f(), a.rope_sin = dsin.f();
+    }
+    a.q = dq.f(), a.k = dk.f(), a.v = dv.f(), a.o = dout.f();
+    a.q_seq = a.q_group = 0, a.q_row = 16, a.q_head = (long long)query_rows * 16;
+    a.k_seq = a.k_group = 0, a.k_row = 16, a.k_head = (long long)rows * 16;
+    a.v_seq = a.v_group = 0, a.v_row = 16, a.v_head = (long long)rows * 16;
+    a.o_seq = a.o_group = 0, a.o_row = 16, a.o_head = (long long)query_rows * 16;
+    a.group = 1, a.seqs = 1, a.heads = (int)heads, a.q_rows = (int)query_rows, a.kv_rows = (int)rows;
+    a.scale = 0.25f;
+    DevBuf part;
+    if (const long long pf = small_attention_partial_floats(a)) {
+        part.alloc((size_t)pf * 4);
+        a.partial = part.f(), a.partial_floats = pf;
+    }
+    small_attention(a, nullptr);
+    IRX_HIP(hipDeviceSynchronize());
+    IRX_HIP(hipMemcpy(out, dout.p, qn * 4, hipMemcpyDeviceToHost));
+}
+
+}  // namespace
+
 int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v, size_t heads,
                              size_t query_rows, size_t rows, float *out) {
     return guarded("irx_test_small_attention", [&] {
-        if (!device || !q || !k || !v || !out || !heads || !query_rows || !rows)
-            fail(IRX_INVALID_ARGUMENT, "small attention shapes do not match");
-        set_device(device);
-        const size_t qn = heads * query_rows * 16, kn = heads * rows * 16;
-        DevBuf dq(qn * 4), dk(kn * 4), dv(kn * 4), dout(qn * 4);
-        IRX_HIP(hipMemcpy(dq.p, q, qn * 4, hipMemcpyHostToDevice));
-        IRX_HIP(hipMemcpy(dk.p, k, kn * 4, hipMemcpyHostToDevice));
-        IRX_HIP(hipMemcpy(dv.p, v, kn * 4, hipMemcpyHostToDevice));
-        SmallAttention a{};
-        a.q = dq.f(), a.k = dk.f(), a.v = dv.f(), a.o = dout.f();
-        a.q_seq = a.q_group = 0, a.q_row = 16, a.q_head = (long long)query_rows * 16;
-        a.k_seq = a.k_group = 0, a.k_row = 16, a.k_head = (long long)rows * 16;
-        a.v_seq = a.v_group = 0, a.v_row = 16, a.v_head = (long long)rows * 16;
-        a.o_seq = a.o_group = 0, a.o_row = 16, a.o_head = (long long)query_rows * 16;
-        a.group = 1, a.seqs = 1, a.heads = (int)heads, a.q_rows = (int)query_rows, a.kv_rows = (int)rows;
-        a.scale = 0.25f;
-        small_attention(a, nullptr);
-        IRX_HIP(hipDeviceSynchronize());
-        IRX_HIP(hipMemcpy(out, dout.p, qn * 4, hipMemcpyDeviceToHost));
+        test_small_attention(device, q, k, v, nullptr, nullptr, heads, query_rows, rows, out);
+    });
+}
+
+int irx_test_small_attention_rope(irx_device *device, const float *q, const float *k, const float *v,
+                                  const float *rope_cos, const float *rope_sin, size_t heads, size_t query_rows,
+                                  size_t rows, float *out) {
+    return guarded("irx_test_small_attention_rope", [&] {
+        if (!rope_cos || !rope_sin) fail(IRX_INVALID_ARGUMENT, "RoPE tables are missing");
+        test_small_attention(device, q, k, v, rope_cos, rope_sin, heads, query_rows, rows, out);
     });
 }
 

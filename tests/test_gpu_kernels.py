@@ -315,6 +315,56 @@ def test_small_attention_matches_float64(device, query_rows, rows):
         assert np.abs(out[h] - attention64(q[h], k[h], v[h], 0.25)).max() < 1e-5
 
 
+@pytest.mark.parametrize("query_rows,rows,qscale", [(128, 50000, 3.0), (4, 3000, 3.0), (20, 2049, 3.0),
+                                                    (33, 777, 3.0), (300, 5000, 3.0), (128, 129, 40.0),
+                                                    (64, 5000, 40.0), (1, 100000, 40.0)])
+def test_small_attention_many_keys_matches_float64(device, query_rows, rows, qscale):
+    """More than 128 keys (the inducing points over a column's train rows):
+    every query-group width, key ranges split over workgroups and merged
+    (8 heads leave most of the chip idle), ragged last blocks, and peaked
+    scores that move the running reference many times."""
+    heads = 8
+    q = fast_values(heads * query_rows * 16, 4, qscale).reshape(heads, query_rows, 16)
+    k = fast_values(heads * rows * 16, 5).reshape(heads, rows, 16)
+    v = fast_values(heads * rows * 16, 6).reshape(heads, rows, 16)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_small_attention(device.handle, F(q), F(k), F(v), heads, query_rows, rows,
+                                                 F(out)))
+    worst = max(np.abs(out[h] - attention64(q[h], k[h], v[h], 0.25)).max() for h in range(heads))
+    assert worst < 1e-5, worst
+
+
+def rope64(x, cos_t, sin_t):
+    """x [rows, 16] at positions 0..rows-1: x[d] cos[t][d] + x[d ^ 8] sin[t][d]."""
+    x = x.astype(np.float64)
+    n = x.shape[0]
+    return x * cos_t[:n] + x[:, np.arange(16) ^ 8] * sin_t[:n]
+
+
+@pytest.mark.parametrize("query_rows,rows", [(68, 68), (130, 130), (20, 300), (128, 4000), (4, 133)])
+def test_small_attention_rope_matches_float64(device, query_rows, rows):
+    """The row transformer's attention with rotary embeddings, on the short
+    (<= 128 keys) and long kernels. Tables as the row stage builds them: cos
+    twice and [-sin, sin] of position x frequency."""
+    heads = 8
+    n = max(query_rows, rows)
+    freqs = 1.0 / (10000.0 ** (np.arange(8) / 8.0))
+    angle = np.arange(n)[:, None] * freqs[None, :]
+    cos_t = np.concatenate([np.cos(angle), np.cos(angle)], 1).astype(np.float32)
+    sin_t = np.concatenate([-np.sin(angle), np.sin(angle)], 1).astype(np.float32)
+    q = fast_values(heads * query_rows * 16, 7, 3.0).reshape(heads, query_rows, 16)
+    k = fast_values(heads * rows * 16, 8).reshape(heads, rows, 16)
+    v = fast_values(heads * rows * 16, 9).reshape(heads, rows, 16)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_small_attention_rope(device.handle, F(q), F(k), F(v), F(cos_t), F(sin_t), heads,
+                                                      query_rows, rows, F(out)))
+    worst = max(np.abs(out[h] - attention64(rope64(q[h], cos_t, sin_t), rope64(k[h], cos_t, sin_t), v[h],
+                                            0.25)).max() for h in range(heads))
+    assert worst < 1e-5, worst
+
+
 def test_harness_rejects_bad_shapes(device):
     z = np.zeros(64, np.float32)
     F = hip.fptr
