@@ -192,7 +192,48 @@ struct irx_device {
     int ordinal = 0;
     int compute_units = 0;
     std::atomic<int> refs{1};
+    // Idle non-blocking streams for builds, predictors and preprocessors to
+    // reuse: creating one costs about a millisecond.
+    std::mutex stream_mu;
+    std::vector<hipStream_t> idle_streams;
+    ~irx_device() {
+        if (idle_streams.empty()) return;
+        (void)hipSetDevice(ordinal);
+        for (hipStream_t s : idle_streams) (void)hipStreamDestroy(s);
+    }
 };
+
+namespace {
+
+constexpr size_t kIdleStreams = 16;
+
+// An idle stream of the device (current on this thread), or a new one.
+hipStream_t take_stream(irx_device *d) {
+    {
+        std::lock_guard<std::mutex> lock(d->stream_mu);
+        if (!d->idle_streams.empty()) {
+            hipStream_t s = d->idle_streams.back();
+            d->idle_streams.pop_back();
+            return s;
+        }
+    }
+    hipStream_t s = nullptr;
+    IRX_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    return s;
+}
+
+// Waits for the stream's work and keeps it for the next taker.
+void return_stream(irx_device *d, hipStream_t s) {
+    if (!s) return;
+    (void)hipStreamSynchronize(s);
+    std::lock_guard<std::mutex> lock(d->stream_mu);
+    if (d->idle_streams.size() < kIdleStreams)
+        d->idle_streams.push_back(s);
+    else
+        (void)hipStreamDestroy(s);
+}
+
+}  // namespace
 
 struct Lin {
     const float *w = nullptr, *b = nullptr;
@@ -704,15 +745,12 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     if (plan.ws_bytes + plan.keep_bytes > in->budget / 10 * 9)
         fail(IRX_DOES_NOT_FIT, "the context does not fit the device");
 
-    hipStream_t s;
-    IRX_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    hipStream_t s = take_stream(W->device);
     struct StreamGuard {
+        irx_device *d;
         hipStream_t s;
-        ~StreamGuard() {
-            (void)hipStreamSynchronize(s);
-            (void)hipStreamDestroy(s);
-        }
-    } guard{s};
+        ~StreamGuard() { return_stream(d, s); }
+    } guard{W->device, s};
 
     auto cache = new irx_built_cache();
     struct CacheGuard {
@@ -733,6 +771,22 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
 
     Arena ws;
     ws.buf.alloc(plan.ws_bytes);
+    // Each estimator's ICL labels go up on a side stream while its column
+    // stage runs (a pageable copy holds the host until it is done); events
+    // order the copy after the previous estimator's read and before the add.
+    struct SideUpload {
+        irx_device *d;
+        hipStream_t s = nullptr;
+        hipEvent_t ready = nullptr, free = nullptr;
+        ~SideUpload() {
+            return_stream(d, s);
+            if (ready) (void)hipEventDestroy(ready);
+            if (free) (void)hipEventDestroy(free);
+        }
+    } side{W->device};
+    side.s = take_stream(W->device);
+    IRX_HIP(hipEventCreateWithFlags(&side.ready, hipEventDisableTiming));
+    IRX_HIP(hipEventCreateWithFlags(&side.free, hipEventDisableTiming));
     Stages st{*W, s, cus};
     // Inputs shared by every estimator.
     float *d_ind_q = ws.take(3 * 128 * 128);
@@ -756,7 +810,6 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
         ws.used = mark;
         upload(d_x, in->x + (size_t)e * N * H, (size_t)N * H * 4, s);
         upload(d_ylab, in->column_labels + (size_t)e * N * 128, (size_t)N * 128 * 4, s);
-        upload(d_yicl, in->icl_labels + (size_t)e * N * 512, (size_t)N * 512 * 4, s);
         // Column stage, chunk by chunk of features (column_stream + isab, cpu.rs:1132-1207).
         {
             const size_t cmark = ws.used;
@@ -801,6 +854,9 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
             }
             ws.used = cmark;
         }
+        if (e > 0) IRX_HIP(hipStreamWaitEvent(side.s, side.free, 0));
+        upload(d_yicl, in->icl_labels + (size_t)e * N * 512, (size_t)N * 512 * 4, side.s);
+        IRX_HIP(hipEventRecord(side.ready, side.s));
         // Row stage in runs, into the ICL row states.
         float *rows = ws.take((size_t)N * 512);
         {
@@ -817,7 +873,9 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
             }
             ws.used = rmark;
         }
+        IRX_HIP(hipStreamWaitEvent(s, side.ready, 0));
         add_inplace(rows, d_yicl, (long long)N * 512, s);
+        IRX_HIP(hipEventRecord(side.free, s));
         // ICL stage: each block's K/V from the training rows, then their queries.
         {
             Stages::IclBuffers ib = Stages::icl_buffers(ws, N, 1, N, N, cus, f16);
@@ -1279,9 +1337,9 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         P->rope_sin.alloc(sin_t.size() * 4);
         IRX_HIP(hipMemcpy(P->rope_cos.p, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(P->rope_sin.p, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice));
-        IRX_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
+        P->stream = take_stream(weights->device);
         for (int i = 0; i < kMaxPassStreams - 1; ++i) {
-            IRX_HIP(hipStreamCreateWithFlags(&P->side[i], hipStreamNonBlocking));
+            P->side[i] = take_stream(weights->device);
             IRX_HIP(hipEventCreateWithFlags(&P->join[i], hipEventDisableTiming));
         }
         IRX_HIP(hipEventCreateWithFlags(&P->fork, hipEventDisableTiming));
@@ -1297,18 +1355,13 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
 void irx_predictor_free(irx_predictor *predictor) {
     if (!predictor) return;
     irx_weights *w = predictor->weights;
-    if (w) (void)hipSetDevice(w->device->ordinal);
-    if (predictor->stream) {
-        (void)hipStreamSynchronize(predictor->stream);
-        (void)hipStreamDestroy(predictor->stream);
+    if (w) {
+        (void)hipSetDevice(w->device->ordinal);
+        return_stream(w->device, predictor->stream);
+        for (int i = 0; i < kMaxPassStreams - 1; ++i) return_stream(w->device, predictor->side[i]);
     }
-    for (int i = 0; i < kMaxPassStreams - 1; ++i) {
-        if (predictor->side[i]) {
-            (void)hipStreamSynchronize(predictor->side[i]);
-            (void)hipStreamDestroy(predictor->side[i]);
-        }
+    for (int i = 0; i < kMaxPassStreams - 1; ++i)
         if (predictor->join[i]) (void)hipEventDestroy(predictor->join[i]);
-    }
     if (predictor->fork) (void)hipEventDestroy(predictor->fork);
     delete predictor;
     irx_weights_release(w);
@@ -1900,7 +1953,7 @@ int irx_preprocessor_new(irx_device *device, size_t columns, const uint32_t *kep
         IRX_HIP(hipMemcpy(P->stats.p, statistics, groups * 9 * kept_count * 8, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(P->member_groups.p, member_groups, members * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(P->orders.p, feature_orders, members * kept_count * 4, hipMemcpyHostToDevice));
-        IRX_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
+        P->stream = take_stream(device);
         device->refs.fetch_add(1);
         P->device = device;
         *out = P.release();
@@ -1910,10 +1963,7 @@ int irx_preprocessor_new(irx_device *device, size_t columns, const uint32_t *kep
 void irx_preprocessor_free(irx_preprocessor *p) {
     if (!p) return;
     (void)hipSetDevice(p->device->ordinal);
-    if (p->stream) {
-        (void)hipStreamSynchronize(p->stream);
-        (void)hipStreamDestroy(p->stream);
-    }
+    return_stream(p->device, p->stream);
     irx_device *d = p->device;
     delete p;
     device_release(d);

@@ -15,6 +15,7 @@ listed in ``Prediction.cpu_rows`` for the caller's own CPU path.
 
 from __future__ import annotations
 
+import concurrent.futures
 import ctypes
 import hashlib
 import math
@@ -101,6 +102,7 @@ class Executor:
             raise ValueError(f"unknown task {task!r}")
         self.task = task
         self.weights = {k: _f32(v) for k, v in weights.items()}
+        self._constants: dict[int, tuple] = {}
         self.width = mf.decoder_width(task)
         if source_sha256 is None:
             source_sha256 = weights_sha256(task, self.weights)
@@ -139,19 +141,34 @@ class Executor:
 
     # ---- host preparations the build and predictor take (cpu.rs:573-599, 763-771) ----
 
-    def target_embeddings(self, prefix: str, y: np.ndarray, width: int) -> np.ndarray:
-        """[N, width] label embeddings (target_embeddings, cpu.rs:1658-1680)."""
+    def target_embeddings(self, prefix: str, y: np.ndarray, width: int, out: np.ndarray | None = None) -> np.ndarray:
+        """[N, width] label embeddings (target_embeddings, cpu.rs:1658-1680):
+        weight[:, class] + bias for the classifier (one f32 sum per class,
+        gathered by row), target * weight + bias for the regressor (two f32
+        roundings, as the reference's loop)."""
         w = self.tensor(f"{prefix}.y_encoder.weight")
         b = self.tensor(f"{prefix}.y_encoder.bias")
+        if out is None:
+            out = np.empty((y.shape[0], width), np.float32)
         if self.task == mf.CLASSIFIER:
-            return _f32(w[:, y.astype(np.int64)].T + b[None, :])
-        return _f32(y[:, None].astype(np.float32) * w[:, 0][None, :] + b[None, :])
+            table = _f32(w.T + b[None, :])  # [classes, width]
+            # Labels are validated to 0..classes-1 before a build; "clip" lets
+            # take write into `out` unbuffered.
+            np.take(table, y.astype(np.intp), axis=0, out=out, mode="clip")
+        else:
+            np.multiply.outer(y.astype(np.float32), _f32(w[:, 0]), out=out)
+            out += _f32(b)
+        return out
 
     def label_embeddings(self, y: np.ndarray):
         """Column-stage [B, N, 128] and ICL-stage [B, N, 512] label embeddings."""
-        col = np.stack([self.target_embeddings("col_embedder", ye, 128) for ye in y])
-        icl = np.stack([self.target_embeddings("icl_predictor", ye, 512) for ye in y])
-        return _f32(col), _f32(icl)
+        b, n = y.shape
+        col = np.empty((b, n, 128), np.float32)
+        icl = np.empty((b, n, 512), np.float32)
+        for e in range(b):
+            self.target_embeddings("col_embedder", y[e], 128, col[e])
+            self.target_embeddings("icl_predictor", y[e], 512, icl[e])
+        return col, icl
 
     def qass_base_scale(self, prefix: str, source: int) -> np.ndarray:
         """base = W2 gelu(w1 ln(max(source,1)) + b1) + b2 (qass_base_scale, cpu.rs:3768-3791)."""
@@ -185,6 +202,18 @@ class Executor:
             out.append(_f32(gated.reshape(128, 128)))
         return out
 
+    def _row_count_constants(self, n: int):
+        """inducing_queries(n) and icl_base_scales(n): functions of the weights
+        and the train-row count only, kept for the last few counts (their
+        float64 GELU runs libm's erf per element)."""
+        hit = self._constants.get(n)
+        if hit is None:
+            hit = (self.inducing_queries(n), self.icl_base_scales(n))
+            if len(self._constants) >= 8:
+                self._constants.pop(next(iter(self._constants)))
+            self._constants[n] = hit
+        return hit
+
     def rope_frequencies(self) -> np.ndarray:
         return self.tensor("row_interactor.tf_row.rope.freqs")
 
@@ -198,6 +227,18 @@ class Executor:
         """Validate a context's inputs and describe it, with its cache identity
         (context_metadata, cpu.rs:809-869). Permutations default to the
         identity: class [B, C] (classifier) and feature [B, H]."""
+        meta, x, y_train = self._unhashed_metadata(x, y_train, class_permutations, feature_permutations)
+        meta.context_sha256 = cf.context_identity(self.source_sha256, optimize, x, y_train,
+                                                  meta.class_permutations, meta.feature_permutations)
+        try:
+            cf.validate_metadata(meta)
+        except cf.ContextError as e:
+            raise ValueError(str(e)) from None
+        return meta
+
+    def _unhashed_metadata(self, x, y_train, class_permutations, feature_permutations):
+        """context_metadata's checks and description with a placeholder
+        identity; also the f32 inputs the identity hashes."""
         x = _f32(x)
         y_train = _f32(y_train)
         if x.ndim != 3 or y_train.shape != x.shape[:2] or min(x.shape) == 0:
@@ -210,14 +251,12 @@ class Executor:
                  else np.tile(np.arange(classes, dtype=np.uint64), b))
         fperm = (np.asarray(feature_permutations, dtype=np.uint64).reshape(-1) if feature_permutations is not None
                  else np.tile(np.arange(h, dtype=np.uint64), b))
-        meta = cf.Metadata(bytes.fromhex(self.source_sha256),
-                           cf.context_identity(self.source_sha256, optimize, x, y_train, cperm, fperm),
-                           b, n, h, classes, cperm, fperm)
+        meta = cf.Metadata(bytes.fromhex(self.source_sha256), b"\1" * 32, b, n, h, classes, cperm, fperm)
         try:
             cf.validate_metadata(meta)
         except cf.ContextError as e:
             raise ValueError(str(e)) from None
-        return meta
+        return meta, x, y_train
 
     def build_context(self, x: np.ndarray, y_train: np.ndarray, class_permutations=None,
                       feature_permutations=None, download: bool = False, progress=None,
@@ -236,41 +275,49 @@ class Executor:
         "fast" (the FP16 context kept on the host, its ICL cache resident as
         FP8 with per-dim scales, read with single FP16 products)."""
         precision = _precision(optimize)
-        meta = self.context_metadata(x, y_train, class_permutations, feature_permutations, optimize)
         directory = cf.resolve_cache_dir(cache_dir)
-        if directory is not None:
-            path = cf.cache_path(directory, meta)
-            cached = cf.read_cached(path, meta)
-            if cached is not None:
-                try:
-                    cf.validate_for_model(cached, self.source_sha256, self.task)
-                except cf.ContextError:
-                    cached = None
-            if cached is not None:
-                try:
-                    os.utime(path)  # the entry's last use, for clear_cache
-                except OSError:
-                    pass
-                try:
-                    return self._attach(cached, optimize)
-                except cf.ContextError:
-                    pass  # stored at another precision: rebuilt below
-        executor = self._build(_f32(x), _f32(y_train), meta, download, progress, device_limit, precision)
-        if directory is not None:
-            # Caching is best effort: a context that cannot be written is still returned.
+        if directory is None:
+            # With no cache to look up, the identity (SHA-256 over x and
+            # y_train) is only kept with the context: hash it on a host thread
+            # while the GPU builds.
+            meta, xf, yf = self._unhashed_metadata(x, y_train, class_permutations, feature_permutations)
+            with concurrent.futures.ThreadPoolExecutor(1) as pool:
+                identity = pool.submit(cf.context_identity, self.source_sha256, optimize, xf, yf,
+                                       meta.class_permutations, meta.feature_permutations)
+                executor = self._build(xf, yf, meta, download, progress, device_limit, precision)
+                meta.context_sha256 = identity.result()
+            return executor
+        meta = self.context_metadata(x, y_train, class_permutations, feature_permutations, optimize)
+        path = cf.cache_path(directory, meta)
+        cached = cf.read_cached(path, meta)
+        if cached is not None:
             try:
-                directory.mkdir(parents=True, exist_ok=True)
-                executor.save_context(path)
-            except (OSError, ValueError):
+                cf.validate_for_model(cached, self.source_sha256, self.task)
+            except cf.ContextError:
+                cached = None
+        if cached is not None:
+            try:
+                os.utime(path)  # the entry's last use, for clear_cache
+            except OSError:
                 pass
+            try:
+                return self._attach(cached, optimize)
+            except cf.ContextError:
+                pass  # stored at another precision: rebuilt below
+        executor = self._build(_f32(x), _f32(y_train), meta, download, progress, device_limit, precision)
+        # Caching is best effort: a context that cannot be written is still returned.
+        try:
+            directory.mkdir(parents=True, exist_ok=True)
+            executor.save_context(path)
+        except (OSError, ValueError):
+            pass
         return executor
 
     def _build(self, x, y_train, meta: cf.Metadata, download: bool, progress, device_limit: int,
                precision: int = hip.PRECISION_FP32) -> "StaticExecutor":
         b, n, h = x.shape
         col_labels, icl_labels = self.label_embeddings(y_train)
-        ind_q = self.inducing_queries(n)
-        bases = self.icl_base_scales(n)
+        ind_q, bases = self._row_count_constants(n)
         freqs, cls = self.rope_frequencies(), self.cls_tokens()
         inp = hip.BuildInputs()
         inp.shape = hip.Shape(b, h, n, self.width)
