@@ -536,6 +536,27 @@ class StaticExecutor:
 
         return read
 
+    def estimator_tensors(self, member: int):
+        """One estimator's context tensors on the host, read out of HBM (or the
+        host copy): (column keys [3][H+4,8,128,16], column values, ICL keys
+        [12][8,N,64], ICL values), the slices of the context tensors
+        (cpu.rs:4106-4123) at ``member``. The ICL tensors are FP16 for an
+        optimize="auto" or "fast" context."""
+        b, n, h = self.shape
+        if not 0 <= member < b:
+            raise ValueError(f"estimator {member} is outside 0..{b - 1}")
+        read = self._tensor_source()
+        col, icl = (h + 4) * 8 * 128 * 16, 8 * n * 64
+
+        def take(name, size, shape):
+            return np.array(read(name, member * size, size)).reshape(shape)
+
+        ck = [take(f"column.{i}.key", col, (h + 4, 8, 128, 16)) for i in range(mf.COLUMN_BLOCKS)]
+        cv = [take(f"column.{i}.value", col, (h + 4, 8, 128, 16)) for i in range(mf.COLUMN_BLOCKS)]
+        ik = [take(f"icl.{i}.key", icl, (8, n, 64)) for i in range(mf.ICL_BLOCKS)]
+        iv = [take(f"icl.{i}.value", icl, (8, n, 64)) for i in range(mf.ICL_BLOCKS)]
+        return ck, cv, ik, iv
+
     def _persistable(self) -> cf.Metadata:
         if self.metadata is None:
             raise ValueError("this context has no identity metadata (built from bare tensors); "

@@ -48,6 +48,9 @@ def lib() -> ctypes.CDLL:
         L.ora_predict_cached.argtypes = [vp, sz, sz, sz, sz, _F, PF, PF, PF, PF, _F, cp, sz]
         L.ora_predict_uncached.argtypes = [vp, sz, sz, sz, sz, _F, _F, _F, cp, sz]
         L.ora_trace_uncached.argtypes = [vp, sz, sz, sz, sz, _F, _F, _F, _F, cp, sz]
+        PS = ctypes.POINTER(sz)
+        L.ora_context_columns.argtypes = [vp, sz, sz, _F, _F, PS, sz, PF, cp, sz]
+        L.ora_context_rows.argtypes = [vp, sz, sz, _F, _F, PS, sz, PF, PF, PF, PF, PF, PF, cp, sz]
         L.ora_affine.argtypes = [_F, sz, sz, _F, _F, sz, _F]
         L.ora_layer_norm.argtypes = [_F, sz, sz, _F, _F, _F]
         L.ora_gelu.argtypes = [ctypes.c_int, _F, sz, _F]
@@ -161,6 +164,43 @@ class OracleModel:
         if st:
             raise ValueError(err.value.decode())
         return out
+
+    def context_columns(self, x: np.ndarray, y: np.ndarray, features) -> list[np.ndarray]:
+        """One estimator (x [N,H], y [N]): the six column K/V tensors [nf,8,128,16]
+        (key, value per block) of the listed features, from the full N-row column
+        stream as build_context computes them."""
+        n, h = x.shape
+        feats = np.ascontiguousarray(features, dtype=np.uintp)
+        kv = [np.zeros((len(feats), 8, 128, 16), np.float32) for _ in range(6)]
+        err = ctypes.create_string_buffer(512)
+        x, y = f32(x), f32(y)
+        st = lib().ora_context_columns(self._handle, n, h, fp(x), fp(y),
+                                       feats.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), len(feats),
+                                       ptr_array(kv), err, 512)
+        if st:
+            raise ValueError(err.value.decode())
+        return kv
+
+    def context_rows(self, x: np.ndarray, y: np.ndarray, rows, ck, cv, ik, iv):
+        """One estimator (x [N,H], y [N], column K/V [H+4,8,128,16] x 3, ICL K/V
+        [8,N,64] x 12 of a built context): the ICL keys and values [8,nr,64] of the
+        listed training rows at every block, each block's computed from the given
+        context's earlier blocks (teacher forcing)."""
+        n, h = x.shape
+        idx = np.ascontiguousarray(rows, dtype=np.uintp)
+        keys = [np.zeros((8, len(idx), 64), np.float32) for _ in range(12)]
+        values = [np.zeros_like(keys[0]) for _ in range(12)]
+        err = ctypes.create_string_buffer(512)
+        # Contiguous float32 views kept alive for the call.
+        x, y = f32(x), f32(y)
+        ck, cv, ik, iv = ([f32(a) for a in t] for t in (ck, cv, ik, iv))
+        st = lib().ora_context_rows(self._handle, n, h, fp(x), fp(y),
+                                    idx.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), len(idx),
+                                    ptr_array(ck), ptr_array(cv), ptr_array(ik), ptr_array(iv),
+                                    ptr_array(keys), ptr_array(values), err, 512)
+        if st:
+            raise ValueError(err.value.decode())
+        return keys, values
 
     def trace_uncached(self, x_all, y, n):
         b, t, h = x_all.shape

@@ -885,6 +885,102 @@ int ora_build_context(const ora_model *m, size_t b, size_t n, size_t h, const fl
     return 0;
 }
 
+/* Spot check of one estimator's column tensors at full size: the three
+ * multihead_attn2 K/V pairs [8,128,16] of the listed features, each from the
+ * whole N-row column stream (column_stream + isab, cpu.rs:1132-1207) exactly
+ * as ora_build_context computes them. kv[2*block] / kv[2*block+1] are
+ * [nf, 8*128*16]. Features run on the oracle's threads. */
+int ora_context_columns(const ora_model *m, size_t n, size_t h, const float *x, const float *y,
+                        const size_t *features, size_t nf, float *const *kv, char *err, size_t errlen) {
+    if (validate_shapes(m, 1, n, h, y, err, errlen)) return -1;
+    for (size_t i = 0; i < nf; ++i)
+        if (features[i] >= h) {
+            set_err(err, errlen, "feature index out of range");
+            return -1;
+        }
+    size_t stream_el = (size_t)M * D;
+    float *ycol = xcalloc(n * D, sizeof(float));
+    target_embeddings(m, m->col_yw, m->col_yb, y, n, D, ycol);
+    int st = 0;
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic) reduction(| : st)
+    for (size_t i = 0; i < nf; ++i) {
+        float *emb = xcalloc(n * D, sizeof(float));
+        float *out[6];
+        for (int j = 0; j < 6; ++j) out[j] = kv[j] + i * stream_el;
+        st |= column_stream(m, x, ycol, n, h, n, features[i], emb, out) != 0;
+        free(emb);
+    }
+    free(ycol);
+    if (st) set_err(err, errlen, "column stream failed (all-missing column or non-finite softmax)");
+    return st ? -1 : 0;
+}
+
+/* Spot check of one estimator's ICL tensors at full size, by teacher forcing:
+ * for each listed training row, its column embeddings against the context's
+ * column K/V with its column label added (the attn2 half of isab,
+ * cpu.rs:1180-1207), its row representation (cpu.rs:1226-1266), its ICL label
+ * (cpu.rs:1270-1277), then per ICL block its K/V (LN1 + projections,
+ * cpu.rs:1356-1416) and its attention over the context's K/V of all N
+ * training rows of that block (cpu.rs:1278-1295). Each row's K/V at block b
+ * thus depends on the context only through blocks < b, so every block is
+ * checked against the same inputs the build used. ck/cv: [H+4,8,128,16]
+ * (one estimator); ik/iv: [8,N,64]; keys/values out: 12 x [8, nr, 64].
+ * Rows run on the oracle's threads, the row representation as in the build. */
+int ora_context_rows(const ora_model *m, size_t n, size_t h, const float *x, const float *y,
+                     const size_t *rows, size_t nr, const float *const *ck, const float *const *cv,
+                     const float *const *ik, const float *const *iv, float *const *keys,
+                     float *const *values, char *err, size_t errlen) {
+    if (validate_shapes(m, 1, n, h, y, err, errlen)) return -1;
+    for (size_t i = 0; i < nr; ++i)
+        if (rows[i] >= n) {
+            set_err(err, errlen, "row index out of range");
+            return -1;
+        }
+    size_t streams = h + RES, stream_el = (size_t)M * D, hd = E / HEADS;
+    float (*bases)[E] = xcalloc(ICLB, sizeof *bases);
+    for (int blk = 0; blk < ICLB; ++blk) qass_base(&m->icl[blk], n, bases[blk]);
+    int st = 0;
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic) reduction(| : st)
+    for (size_t i = 0; i < nr; ++i) {
+        size_t r = rows[i];
+        float ycol[D], yicl[E], emb[D], next[D], row[E], rnext[E], kh[E], vh[E];
+        float *columns = xcalloc(streams * D, sizeof(float));
+        memcpy(columns, m->cls, RES * D * 4);
+        target_embeddings(m, m->col_yw, m->col_yb, y + r, 1, D, ycol);
+        target_embeddings(m, m->icl_yw, m->icl_yb, y + r, 1, E, yicl);
+        int rs = 0;
+        for (size_t f = 0; f < h && !rs; ++f) {
+            column_input(m, x + r * h, 1, h, f, emb);
+            for (size_t c = 0; c < D; ++c) emb[c] += ycol[c];
+            for (int blk = 0; blk < COLB && !rs; ++blk) {
+                attend_opts o2 = {NULL, ORA_MATH_EXACT, 0, 1};
+                rs = attend(m, &m->col2[blk], emb, 1, ck[blk] + (RES + f) * stream_el,
+                            cv[blk] + (RES + f) * stream_el, M, &o2, next);
+                memcpy(emb, next, D * 4);
+            }
+            memcpy(columns + (RES + f) * D, emb, D * 4);
+        }
+        if (!rs) rs = row_embedding(m, columns, streams, row);
+        free(columns);
+        for (size_t c = 0; c < E; ++c) row[c] += yicl[c];
+        for (int blk = 0; blk < ICLB && !rs; ++blk) {
+            source_heads(m, &m->icl[blk], row, 1, 0, 1, kh, vh);
+            for (size_t hh = 0; hh < HEADS; ++hh) {
+                memcpy(keys[blk] + (hh * nr + i) * hd, kh + hh * hd, hd * 4);
+                memcpy(values[blk] + (hh * nr + i) * hd, vh + hh * hd, hd * 4);
+            }
+            if (blk + 1 == ICLB) break;
+            attend_opts o = {bases[blk], ORA_MATH_EXACT, 0, 1};
+            rs = attend(m, &m->icl[blk], row, 1, ik[blk], iv[blk], n, &o, rnext);
+            memcpy(row, rnext, E * 4);
+        }
+        st |= rs != 0;
+    }
+    free(bases);
+    if (st) set_err(err, errlen, "softmax normalization is not finite");
+    return st ? -1 : 0;
+}
+
 static int forward_uncached(const ora_model *m, size_t b, size_t t, size_t n, size_t h, const float *x,
                             const float *y, float *logits, float *trace_columns, float *trace_rows,
                             char *err, size_t errlen) {

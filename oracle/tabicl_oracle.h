@@ -63,6 +63,19 @@ int ora_build_context(const ora_model *model, size_t b, size_t n, size_t h, cons
                       const float *y, float *const *column_keys, float *const *column_values,
                       float *const *icl_keys, float *const *icl_values, char *err, size_t errlen);
 
+/* Spot checks of one estimator's built context at full size (x [N,H], y [N]).
+ * ora_context_columns: the column K/V of the listed features, as
+ * ora_build_context computes them; kv[2*block], kv[2*block+1] are [nf,8,128,16].
+ * ora_context_rows: the ICL K/V of the listed training rows, each block's from
+ * the given context's earlier blocks (teacher forcing); ck/cv [H+4,8,128,16],
+ * ik/iv [8,N,64] of that estimator; keys/values out 12 x [8,nr,64]. */
+int ora_context_columns(const ora_model *model, size_t n, size_t h, const float *x, const float *y,
+                        const size_t *features, size_t nf, float *const *kv, char *err, size_t errlen);
+int ora_context_rows(const ora_model *model, size_t n, size_t h, const float *x, const float *y,
+                     const size_t *rows, size_t nr, const float *const *ck, const float *const *cv,
+                     const float *const *ik, const float *const *iv, float *const *keys,
+                     float *const *values, char *err, size_t errlen);
+
 /* Cached prediction: StaticExecutor::predict_chunk per estimator
  * (cpu.rs:2200-2273), over 1024-row chunks (cpu.rs:2111-2153).
  * x [B,Q,H]; logits [B,Q,width] (every decoder output). */

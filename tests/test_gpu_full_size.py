@@ -1,0 +1,144 @@
+"""Full-size parity on the 10,000-row classifier (100 features, 20% log-normal
+columns, MLP labeller, 1,024 test rows) and the 20,000-row regressor (200
+features, 2,048 test rows), through the C ABI.
+
+The oracle cannot rebuild these contexts within a test (4.9 and 18.9 TFLOP of
+build work), so the GPU build is checked at full size by spot checks that the
+oracle computes exactly as its own build would (pinned bitwise against
+ora_build_context in test_oracle_model.py):
+
+- the column K/V of sampled features, from the oracle's full N-row column
+  stream of each feature (inducing points over all N rows, three blocks);
+- the ICL K/V of sampled training rows at all twelve blocks, each block's from
+  the GPU context's earlier blocks (teacher forcing), so no error compounds.
+
+Predictions: every test row on the GPU, the oracle's cached prediction of
+sampled rows against the GPU-built context, the HBM-bound small-pass kernels
+against the 512-row pass, and (classifier) invariance under a permutation of
+the training rows. The bar is the north star's: |gpu - cpu| <= 1e-5 +
+1e-4 |cpu| with identical argmax."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from ironicl_amd import hip
+from ironicl_amd import synthetic as S
+from ironicl_amd import tabicl
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-5, 1e-4
+
+
+def assert_parity(gpu, cpu, what=""):
+    gpu, cpu = np.asarray(gpu, np.float64), np.asarray(cpu, np.float64)
+    err = np.abs(gpu - cpu) - (ATOL + RTOL * np.abs(cpu))
+    worst = np.unravel_index(np.argmax(err), err.shape)
+    assert err.max() <= 0, f"{what}: |gpu-cpu| {abs(gpu[worst] - cpu[worst]):.3e} at {worst} (cpu {cpu[worst]:.6f})"
+
+
+def sample(count, total, seed):
+    """`count` sorted distinct indices of 0..total-1 including both ends."""
+    rest = np.random.default_rng(seed).choice(np.arange(1, total - 1), count - 2, replace=False)
+    return np.sort(np.concatenate([[0, total - 1], rest]))
+
+
+def check_context(oracle, x, y, ctx, what, features=4, rows=16):
+    """Spot checks of estimator 0 of a GPU-built context (host copy `ctx`)."""
+    ck, cv, ik, iv = ([t[0] for t in part] for part in ctx)
+    n, h = x.shape[1], x.shape[2]
+    feats = sample(features, h, 1)
+    kv = oracle.context_columns(x[0], y[0], feats)
+    for blk in range(3):
+        assert_parity(ck[blk][4 + feats], kv[2 * blk], f"{what} column.{blk}.key")
+        assert_parity(cv[blk][4 + feats], kv[2 * blk + 1], f"{what} column.{blk}.value")
+    idx = sample(rows, n, 2)
+    keys, values = oracle.context_rows(x[0], y[0], idx, ck, cv, ik, iv)
+    for blk in range(12):
+        assert_parity(ik[blk][:, idx], keys[blk], f"{what} icl.{blk}.key")
+        assert_parity(iv[blk][:, idx], values[blk], f"{what} icl.{blk}.value")
+
+
+@pytest.fixture(scope="module")
+def device():
+    return hip.Device(0)
+
+
+@pytest.fixture(scope="module")
+def clf_10k(device, clf_weights):
+    w = S.WORKLOADS["clf-10k"]
+    x, y, xt, meta = S.workload_data(w)
+    assert x.shape == (1, 10_000, 100) and xt.shape == (1, 1024, 100)
+    ex = tabicl.Executor("classifier", clf_weights, device)
+    st = ex.build_context(x, y, class_permutations=meta["class_permutations"], download=True)
+    O.set_threads(16)
+    return ex, st, x, y, xt, O.OracleModel("classifier", clf_weights, O.EXACT)
+
+
+def test_clf_10k_context_spot_checks(clf_10k):
+    _, st, x, y, _, oracle = clf_10k
+    check_context(oracle, x, y, st.context, "clf-10k")
+
+
+def test_clf_10k_predictions(clf_10k):
+    _, st, x, y, xt, oracle = clf_10k
+    gpu = st.predict_logits(xt).logits
+    assert gpu.shape == (1, 1024, 10) and np.isfinite(gpu).all()
+    rows = sample(48, xt.shape[1], 3)
+    cpu = oracle.predict_cached(st.context, np.ascontiguousarray(xt[:, rows]))[..., :10]
+    assert_parity(gpu[:, rows], cpu, "clf-10k logits")
+    assert np.array_equal(gpu[:, rows].argmax(-1), cpu.argmax(-1))
+    # Passes of <= 32 rows run the HBM-bound decode kernel over the same cache.
+    default = st.pass_rows()
+    st.set_pass_rows(32)
+    try:
+        small = st.predict_logits(np.ascontiguousarray(xt[:, :64])).logits
+        tiny = st.predict_logits(np.ascontiguousarray(xt[:, 64:80])).logits
+    finally:
+        st.set_pass_rows(default)
+    assert_parity(small, gpu[:, :64], "clf-10k 32-row passes")
+    assert_parity(tiny, gpu[:, 64:80], "clf-10k 16-row pass")
+
+
+def test_clf_10k_training_row_order_does_not_matter(clf_10k):
+    ex, st, x, y, xt, _ = clf_10k
+    perm = np.random.default_rng(4).permutation(x.shape[1])
+    st_p = ex.build_context(np.ascontiguousarray(x[:, perm]), np.ascontiguousarray(y[:, perm]),
+                            class_permutations=st.class_permutations)
+    q = np.ascontiguousarray(xt[:, :256])
+    a, b = st.predict_logits(q).logits, st_p.predict_logits(q).logits
+    assert_parity(b, a, "clf-10k permuted training rows")
+    assert np.array_equal(a.argmax(-1), b.argmax(-1))
+
+
+@pytest.fixture(scope="module")
+def reg_20k(device, reg_weights):
+    w = S.WORKLOADS["reg-20k"]
+    x, y, xt, meta = S.workload_data(w)
+    assert x.shape == (1, 20_000, 200) and xt.shape == (1, 2048, 200)
+    ex = tabicl.Executor("regressor", reg_weights, device)
+    st = ex.build_context(x, y, download=True)
+    O.set_threads(16)
+    return st, x, y, xt, O.OracleModel("regressor", reg_weights, O.EXACT)
+
+
+def test_reg_20k_context_spot_checks(reg_20k):
+    st, x, y, _, oracle = reg_20k
+    check_context(oracle, x, y, st.context, "reg-20k")
+
+
+def test_reg_20k_quantiles_mean_and_intervals(reg_20k):
+    st, _, _, xt, oracle = reg_20k
+    alphas = [0.05, 0.5, 0.95]
+    gpu = st.predict_logits(xt).logits
+    assert gpu.shape == (1, 2048, 999) and np.isfinite(gpu).all()
+    rows = sample(24, xt.shape[1], 5)
+    q = np.ascontiguousarray(xt[:, rows])
+    cpu = oracle.predict_cached(st.context, q)
+    assert_parity(gpu[:, rows], cpu, "reg-20k decoder quantiles")
+    gm, gq = st.predict_regression(q, alphas)
+    cm, cq = O.regression_summary(cpu, alphas)
+    assert_parity(gm, cm, "reg-20k mean")
+    assert_parity(gq, cq, "reg-20k quantiles at 0.05/0.5/0.95")
+    assert (gq[:, 0] <= gq[:, 1]).all() and (gq[:, 1] <= gq[:, 2]).all()

@@ -145,3 +145,38 @@ def test_missing_tensor_is_reported(clf_weights):
     del w["icl_predictor.ln.weight"]
     with pytest.raises(ValueError, match="icl_predictor.ln.weight"):
         O.OracleModel("classifier", w)
+
+
+def test_spot_checks_reproduce_the_build(lcg_case):
+    """The full-size spot checks (column K/V of chosen features, ICL K/V of chosen
+    training rows by teacher forcing) give the build's own tensors bitwise."""
+    m, x, y, _, (ck, cv, ik, iv) = lcg_case
+    feats, rows = [0, 3, 4], [0, 17, 239, 100]
+    for e in range(x.shape[0]):
+        kv = m.context_columns(x[e], y[e], feats)
+        for blk in range(3):
+            np.testing.assert_array_equal(kv[2 * blk], ck[blk][e, 4 + np.array(feats)])
+            np.testing.assert_array_equal(kv[2 * blk + 1], cv[blk][e, 4 + np.array(feats)])
+        keys, values = m.context_rows(x[e], y[e], rows, [c[e] for c in ck], [c[e] for c in cv],
+                                      [t[e] for t in ik], [t[e] for t in iv])
+        for blk in range(12):
+            np.testing.assert_array_equal(keys[blk], ik[blk][e][:, rows])
+            np.testing.assert_array_equal(values[blk], iv[blk][e][:, rows])
+
+
+def test_spot_checks_see_a_wrong_block(lcg_case):
+    """A value changed in one block of the context shows in the checked rows'
+    K/V of the next block only (teacher forcing), and a changed column cache
+    in every ICL block."""
+    m, x, y, _, (ck, cv, ik, iv) = lcg_case
+    rows = [5, 6]
+    bad_iv = [t[0].copy() for t in iv]
+    bad_iv[4] *= 1.01
+    keys, _ = m.context_rows(x[0], y[0], rows, [c[0] for c in ck], [c[0] for c in cv], [t[0] for t in ik], bad_iv)
+    for blk in range(12):
+        same = np.array_equal(keys[blk], ik[blk][0][:, rows])
+        assert same == (blk <= 4), blk
+    bad_cv = [c[0].copy() for c in cv]
+    bad_cv[2][4 + 1] *= 1.01
+    keys, _ = m.context_rows(x[0], y[0], rows, [c[0] for c in ck], bad_cv, [t[0] for t in ik], [t[0] for t in iv])
+    assert not np.array_equal(keys[0], ik[0][0][:, rows])
