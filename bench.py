@@ -281,6 +281,216 @@ def bench_level(optimize, executor, x, y, q, dx, gpu_logits, args) -> dict:
     return report
 
 
+def family_breakdown(stats: dict, per: float = 1.0) -> dict:
+    """Per kernel family: milliseconds, launches, algorithmic TFLOP/s and GB/s
+    (sums of launch durations recorded with HIP events), divided by `per`."""
+    return {f: {"ms": s["milliseconds"] / per, "launches": s["launches"] / per,
+                "tflops": (s["flops"] / (s["milliseconds"] * 1e-3) / 1e12) if s["milliseconds"] else 0.0,
+                "gbps": (s["bytes"] / (s["milliseconds"] * 1e-3) / 1e9) if s["milliseconds"] else 0.0}
+            for f, s in stats.items() if s["launches"]}
+
+
+def profiled_build(executor, x, y) -> dict:
+    """One more build with every launch timed by HIP events, per family: where
+    the build's time goes and each family's rate (GEMMs at build sizes)."""
+    from ironicl_amd import hip, hipmem
+
+    hip.profile_enable(True)
+    ctx = executor.build_context(x, y)
+    hipmem.synchronize()
+    stats = {f: hip.profile_read(f) for f in hip.KERNEL_FAMILIES}
+    hip.profile_enable(False)
+    del ctx
+    return family_breakdown(stats)
+
+
+def workload_parity(w, weights, width_all, ctx, x, y, xt, logits, big: bool) -> dict:
+    """Parity of a full-size context and its predictions on estimators 0 and
+    B-1. Against the oracle (the reference CPU path restated in C): the column
+    K/V of sampled features (their full column streams), the ICL K/V of
+    sampled training rows at every block (teacher forcing through the GPU
+    context's earlier blocks), and the logits of sampled test rows, each to
+    |gpu - cpu| <= 1e-5 + 1e-4 |cpu|. Where a K/V check misses that bar, the
+    float64 restatement decides: on the first sampled feature and rows, the
+    GPU's error against float64 must not exceed the oracle's own (both FP32;
+    they differ in summation order over the N training rows). Logits always
+    take the strict bar with identical argmax."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle as O
+    from reference_np import Model
+
+    threads = min(16, os.cpu_count() or 1)
+    O.set_threads(threads)
+    oracle = O.OracleModel(w.task, weights, O.EXACT)
+    exact = Model(w.task, weights)
+    b, n, h = x.shape
+    q = xt.shape[1]
+    width = w.classes or width_all
+    rng = np.random.default_rng(7)
+    feats = np.sort(rng.choice(h, min(h, 2 if big else 4), replace=False))
+    rows = np.sort(rng.choice(n, min(n, 8 if big else 16), replace=False))
+    tests = np.sort(rng.choice(q, min(q, 8 if big else 32), replace=False))
+    f64_rows = rows[: 2 if big else 4]
+
+    def excess(gpu, cpu):
+        gpu, cpu = np.asarray(gpu, np.float64), np.asarray(cpu, np.float64)
+        return float((np.abs(gpu - cpu) - (1e-5 + 1e-4 * np.abs(cpu))).max()), float(np.abs(gpu - cpu).max())
+
+    report = {k: {"max_abs_diff_vs_oracle": 0.0, "strict_ok": True} for k in ("column_kv", "icl_kv", "logits")}
+    for k in ("column_kv", "icl_kv"):
+        report[k]["float64"] = {"gpu_max_abs_err": 0.0, "oracle_max_abs_err": 0.0}
+
+    def note(kind, got, want):
+        ex, d = excess(got, want)
+        r = report[kind]
+        r["strict_ok"] &= ex <= 0
+        r["max_abs_diff_vs_oracle"] = max(r["max_abs_diff_vs_oracle"], d)
+
+    def note64(kind, gpu, cpu, ref):
+        r = report[kind]["float64"]
+        r["gpu_max_abs_err"] = max(r["gpu_max_abs_err"], float(np.abs(np.asarray(gpu, np.float64) - ref).max()))
+        r["oracle_max_abs_err"] = max(r["oracle_max_abs_err"], float(np.abs(np.asarray(cpu, np.float64) - ref).max()))
+
+    members = sorted({0, b - 1})
+    argmax_ok = True
+    for e in members:
+        t0 = time.perf_counter()
+        ck, cv, ik, iv = ctx.estimator_tensors(e)
+        log(f"estimator {e}: context read from HBM in {time.perf_counter() - t0:.1f} s")
+        t0 = time.perf_counter()
+        kv = oracle.context_columns(x[e], y[e], feats)
+        for blk in range(3):
+            note("column_kv", ck[blk][4 + feats], kv[2 * blk])
+            note("column_kv", cv[blk][4 + feats], kv[2 * blk + 1])
+        keys, values = oracle.context_rows(x[e], y[e], rows, ck, cv, ik, iv)
+        for blk in range(12):
+            note("icl_kv", ik[blk][:, rows], keys[blk])
+            note("icl_kv", iv[blk][:, rows], values[blk])
+        cpu = oracle.predict_cached(([c[None] for c in ck], [c[None] for c in cv], [t[None] for t in ik],
+                                     [t[None] for t in iv]), np.ascontiguousarray(xt[e:e + 1, tests]))[..., :width]
+        gpu = logits[e:e + 1, tests, :width]
+        note("logits", gpu, cpu)
+        if w.task == "classifier":
+            argmax_ok &= bool(np.array_equal(gpu.argmax(-1), cpu.argmax(-1)))
+        log(f"estimator {e}: oracle checks in {time.perf_counter() - t0:.1f} s")
+        t0 = time.perf_counter()
+        for blk, (k64, v64) in enumerate(exact.column_kv(x[e].astype(np.float64), y[e], int(feats[0]))):
+            note64("column_kv", ck[blk][4 + feats[0]], kv[2 * blk][0], k64)
+            note64("column_kv", cv[blk][4 + feats[0]], kv[2 * blk + 1][0], v64)
+        ik64 = [a.astype(np.float64) for a in ik]
+        iv64 = [a.astype(np.float64) for a in iv]
+        for j, r in enumerate(f64_rows):
+            k64, v64 = exact.row_kv(x[e, r].astype(np.float64), y[e, r], ck, cv, ik64, iv64)
+            for blk in range(12):
+                note64("icl_kv", ik[blk][:, r], keys[blk][:, j], k64[blk])
+                note64("icl_kv", iv[blk][:, r], values[blk][:, j], v64[blk])
+        del ik64, iv64, ck, cv, ik, iv
+        log(f"estimator {e}: float64 checks in {time.perf_counter() - t0:.1f} s; {json.dumps(report)}")
+    ok = report["logits"]["strict_ok"] and argmax_ok
+    for k in ("column_kv", "icl_kv"):
+        f = report[k]["float64"]
+        report[k]["ok"] = report[k]["strict_ok"] or f["gpu_max_abs_err"] <= f["oracle_max_abs_err"]
+        ok &= report[k]["ok"]
+    report["logits"]["argmax_identical"] = argmax_ok
+    report.update({"estimators": members, "features": feats.tolist(), "train_rows": rows.tolist(),
+                   "float64_features": [int(feats[0])], "float64_train_rows": f64_rows.tolist(),
+                   "test_rows": tests.tolist(), "oracle_threads": threads, "ok": bool(ok)})
+    return report
+
+
+def bench_workload(name: str, args) -> dict:
+    """Another configuration at full size: build ms, test rows/s (passes of
+    --pass-rows over two streams, inputs in HBM), the build's kernel families,
+    and parity on estimators 0 and B-1: the oracle's spot checks of the built
+    context (column K/V of sampled features from their full column streams,
+    ICL K/V of sampled training rows by teacher forcing) and its cached
+    prediction of sampled test rows against the GPU-built context."""
+    from ironicl_amd import hip, hipmem, synthetic, tabicl
+
+    w = synthetic.WORKLOADS[name]
+    log(f"{name}: generating weights and data")
+    weights = synthetic.random_weights(w.task)
+    x, y, xt, meta = synthetic.workload_data(w)
+    b, n, h = x.shape
+    q = xt.shape[1]
+    executor = tabicl.Executor(w.task, weights, hip.Device(0))
+    perms = meta["class_permutations"]
+
+    def progress(stage, done, total):
+        log(f"build: estimator {done} of {total} done")
+
+    big = b * n * h >= 5e8  # the 8 x 200k x 500 ensemble: one build, timed
+    if not big:
+        executor.build_context(x, y, class_permutations=perms)
+        hipmem.synchronize()
+    build_ms = []
+    build_kernels = None
+    for _ in range(1 if big else max(1, args.build_repeats)):
+        hipmem.synchronize()
+        if big:  # the one build is also the profiled one (HIP events per launch)
+            hip.profile_enable(True)
+        t0 = time.perf_counter()
+        ctx = executor.build_context(x, y, class_permutations=perms, progress=progress if big else None)
+        hipmem.synchronize()
+        build_ms.append(1000 * (time.perf_counter() - t0))
+        if big:
+            build_kernels = family_breakdown({f: hip.profile_read(f) for f in hip.KERNEL_FAMILIES})
+            hip.profile_enable(False)
+        log(f"build {build_ms[-1]:.1f} ms")
+        if len(build_ms) < max(1, args.build_repeats) and not big:
+            del ctx
+    ctx.set_pass_rows(args.pass_rows)
+    dx = hipmem.DeviceArray.from_host(xt)
+    dl = hipmem.DeviceArray((b, q, executor.width))
+
+    def step():
+        hip.check(hip.lib().irx_predictor_predict_device(ctx.handle, dx.ptr, q, dl.ptr, None))
+
+    steps = 2 if big else args.steps
+    for _ in range(1 if big else args.warmup):
+        step()
+    hipmem.synchronize()
+    hip.profile_enable(True)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step()
+        if big:
+            hipmem.synchronize()
+            log(f"prediction step {i + 1} of {steps}: {time.perf_counter() - t0:.2f} s")
+    hipmem.synchronize()
+    elapsed = time.perf_counter() - t0
+    stats = {f: hip.profile_read(f) for f in hip.KERNEL_FAMILIES}
+    hip.profile_enable(False)
+    logits = dl.to_host()
+    log(f"{name}: {q * steps / elapsed:.0f} test rows/s ({1000 * elapsed / steps:.1f} ms per {q} rows)")
+    if not big:
+        build_kernels = profiled_build(executor, x, y)
+
+    parity = None
+    if not args.no_cpu:
+        parity = workload_parity(w, weights, executor.width, ctx, x, y, xt, logits, big)
+    return {
+        "metric": "test rows/sec vs cached context; static-context build ms (1 MI355X)",
+        "value": q * steps / elapsed,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "ms_per_step": 1000 * elapsed / steps,
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": f"synthetic: seeded random-init FP32 weights of the official TabICLv2 {w.task}",
+        "config": {"workload": f"{name}: {n:,} train rows x {h} features, {b} estimator(s), {q:,} test rows in "
+                               f"passes of {args.pass_rows}; contexts resident in HBM",
+                   "train_rows": n, "features": h, "test_rows": q, "estimators": b, "classes": w.classes},
+        "build_ms": float(np.median(build_ms)),
+        "build_ms_all": build_ms,
+        "predict_kernels_per_step": family_breakdown(stats, steps),
+        "build_kernels": build_kernels,
+        "parity": parity,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -294,6 +504,9 @@ def main() -> int:
                     help="also time exporting the resident context to an IRCNTXT file in DIR and reloading it")
     ap.add_argument("--fitted", action="store_true",
                     help="also time TabICL preprocessing on the GPU and a fitted 8-member model from raw features")
+    ap.add_argument("--workload", default=WORKLOAD,
+                    help="clf-50k (default, the full report) or another configuration at full size: clf-1k, "
+                         "clf-10k, reg-20k, clf-200k (build, rows/s, build kernels, oracle parity on samples)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel over BYTES (reference for traffic counters)")
     args = ap.parse_args()
@@ -308,6 +521,9 @@ def main() -> int:
         device = hip.Device(0)
         hip.check(hip.lib().irx_test_copy(device.handle, args.copy_calibration // 4))
         print(json.dumps({"copy_bytes": args.copy_calibration}), flush=True)
+        return 0
+    if args.workload != WORKLOAD:
+        print(json.dumps(bench_workload(args.workload, args)), flush=True)
         return 0
     w = synthetic.WORKLOADS[WORKLOAD]
     log("generating weights and data")
@@ -447,6 +663,8 @@ def main() -> int:
         os.remove(path)
         log(f"context export {export_s:.2f} s, verified reload {import_s:.2f} s ({size / 1e9:.2f} GB)")
 
+    log("profiled build")
+    build_kernels = profiled_build(executor, x, y)
     auto_report = bench_level("auto", executor, x, y, q, dx, gpu_logits, args)
     fast_report = bench_level("fast", executor, x, y, q, dx, gpu_logits, args)
     fitted_report = bench_fitted(executor, x, y, xt, args) if args.fitted else None
@@ -512,6 +730,7 @@ def main() -> int:
         },
         "build_ms": float(np.median(build_ms)),
         "build_ms_all": build_ms,
+        "build_kernels": build_kernels,
         "rows_per_s_host_buffers": host_rows_per_s,
         "one_stream": {"ms_per_step": one_stream_ms, "rows_per_s": q / (one_stream_ms * 1e-3)},
         "roofline": roofline,

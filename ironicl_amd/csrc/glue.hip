@@ -68,9 +68,8 @@ __global__ __launch_bounds__(256) void column_input_kernel(const float *x, long 
                                                            const float *in_w, const float *in_b,
                                                            const float *labels, float *state,
                                                            uint8_t *missing) {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long total = (long long)b * h * rows * kColumnDim;
-    if (idx >= total) return;
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (long long)gridDim.x * 256) {
     const int ch = idx & (kColumnDim - 1);
     const long long cr = idx >> 7;
     const int r = (int)(cr % rows);
@@ -87,15 +86,15 @@ __global__ __launch_bounds__(256) void column_input_kernel(const float *x, long 
     }
     if (labels) v += labels[((long long)e * rows + r) * kColumnDim + ch];
     state[idx] = v;
+    }
 }
 
 // Row sequences: the 4 CLS tokens, then feature f's column state (cpu.rs:1226-1231).
 __global__ __launch_bounds__(256) void build_rows_kernel(const float *state, int b, int rows, int h,
                                                          const float *cls, float *seq) {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const int len = h + kReserved;
     const long long total = (long long)b * rows * len * kColumnDim;
-    if (idx >= total) return;
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (long long)gridDim.x * 256) {
     const int ch = idx & (kColumnDim - 1);
     const long long st = idx >> 7;
     const int t = (int)(st % len);
@@ -108,31 +107,34 @@ __global__ __launch_bounds__(256) void build_rows_kernel(const float *state, int
     else
         v = state[(((long long)e * h + (t - kReserved)) * rows + r) * kColumnDim + ch];
     seq[idx] = v;
+    }
 }
 
 __global__ __launch_bounds__(256) void gather_cls_kernel(const float *seq, long long seqs, int len, float *cls) {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long total = seqs * kReserved * kColumnDim;
-    if (idx >= total) return;
-    const long long s = idx / (kReserved * kColumnDim);
-    const int within = (int)(idx - s * (kReserved * kColumnDim));
-    cls[idx] = seq[s * len * kColumnDim + within];
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (long long)gridDim.x * 256) {
+        const long long s = idx / (kReserved * kColumnDim);
+        const int within = (int)(idx - s * (kReserved * kColumnDim));
+        cls[idx] = seq[s * len * kColumnDim + within];
+    }
 }
 
 __global__ __launch_bounds__(256) void add_kernel(float *y, const float *x, long long count) {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (idx < count) y[idx] += x[idx];
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long long)gridDim.x * 256)
+        y[idx] += x[idx];
 }
 
 __global__ __launch_bounds__(256) void repeat_kernel(const float *src, long long src_floats, long long copies,
                                                      float *dst) {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (idx < src_floats * copies) dst[idx] = src[idx % src_floats];
+    const long long total = src_floats * copies;
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (long long)gridDim.x * 256)
+        dst[idx] = src[idx % src_floats];
 }
 
 __global__ __launch_bounds__(256) void nonfinite_kernel(const float *x, long long count, unsigned *counter) {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    bool bad = idx < count && !isfinite(x[idx]);
+    bool bad = false;
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long long)gridDim.x * 256)
+        bad |= !isfinite(x[idx]);
     if (__any(bad) && (threadIdx.x & 63) == 0) atomicAdd(counter, 1u);
 }
 
@@ -144,8 +146,17 @@ __global__ __launch_bounds__(256) void copy_kernel(const float *src, float *dst,
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(float *x, long long count) {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (idx < count) x[idx] = 0.f;
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long long)gridDim.x * 256)
+        x[idx] = 0.f;
+}
+
+// Blocks of 256 threads for a 1D element loop of `total` items: the kernels
+// stride over the grid, so a launch stays far below the 2^32 work-items a
+// dispatch can hold (one estimator's column states at 200,000 rows x 500
+// features are 12.8G floats).
+dim3 grid_1d(long long total) {
+    constexpr long long kMaxBlocks = 1 << 20;
+    return dim3((unsigned)std::min<long long>((total + 255) / 256, kMaxBlocks));
 }
 
 }  // namespace
@@ -171,7 +182,7 @@ void column_input(const float *x, long long x_estimator_stride, int b, int rows,
     long long total = (long long)b * h * rows * kColumnDim;
     if (total <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * total + 4.0 * b * rows * h);
-    hipLaunchKernelGGL(column_input_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, x, x_estimator_stride, b, rows, h, in_w,
+    hipLaunchKernelGGL(column_input_kernel, grid_1d(total), dim3(256), 0, stream, x, x_estimator_stride, b, rows, h, in_w,
                        in_b, labels, state, missing_rows);
     IRX_HIP(hipGetLastError());
 }
@@ -180,7 +191,7 @@ void build_rows(const float *state, int b, int rows, int h, const float *cls, fl
     long long total = (long long)b * rows * (h + kReserved) * kColumnDim;
     if (total <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 8.0 * total);
-    hipLaunchKernelGGL(build_rows_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, state, b, rows, h, cls,
+    hipLaunchKernelGGL(build_rows_kernel, grid_1d(total), dim3(256), 0, stream, state, b, rows, h, cls,
                        seq);
     IRX_HIP(hipGetLastError());
 }
@@ -189,14 +200,14 @@ void gather_cls(const float *seq, long long seqs, int len, float *cls, hipStream
     long long total = seqs * kReserved * kColumnDim;
     if (total <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 8.0 * total);
-    hipLaunchKernelGGL(gather_cls_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, seq, seqs, len, cls);
+    hipLaunchKernelGGL(gather_cls_kernel, grid_1d(total), dim3(256), 0, stream, seq, seqs, len, cls);
     IRX_HIP(hipGetLastError());
 }
 
 void add_inplace(float *y, const float *x, long long count, hipStream_t stream) {
     if (count <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 12.0 * count);
-    hipLaunchKernelGGL(add_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, y, x, count);
+    hipLaunchKernelGGL(add_kernel, grid_1d(count), dim3(256), 0, stream, y, x, count);
     IRX_HIP(hipGetLastError());
 }
 
@@ -204,7 +215,7 @@ void repeat_rows(const float *src, long long src_floats, long long copies, float
     long long total = src_floats * copies;
     if (total <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * total + 4.0 * src_floats);
-    hipLaunchKernelGGL(repeat_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream, src, src_floats, copies,
+    hipLaunchKernelGGL(repeat_kernel, grid_1d(total), dim3(256), 0, stream, src, src_floats, copies,
                        dst);
     IRX_HIP(hipGetLastError());
 }
@@ -212,7 +223,7 @@ void repeat_rows(const float *src, long long src_floats, long long copies, float
 void count_nonfinite(const float *x, long long count, unsigned *counter, hipStream_t stream) {
     if (count <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * count);
-    hipLaunchKernelGGL(nonfinite_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, x, count, counter);
+    hipLaunchKernelGGL(nonfinite_kernel, grid_1d(count), dim3(256), 0, stream, x, count, counter);
     IRX_HIP(hipGetLastError());
 }
 
@@ -228,7 +239,7 @@ void copy_floats(const float *src, float *dst, long long count, hipStream_t stre
 void fill_zero(float *x, long long count, hipStream_t stream) {
     if (count <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * count);
-    hipLaunchKernelGGL(zero_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, stream, x, count);
+    hipLaunchKernelGGL(zero_kernel, grid_1d(count), dim3(256), 0, stream, x, count);
     IRX_HIP(hipGetLastError());
 }
 

@@ -672,7 +672,7 @@ static void column_input(const ora_model *m, const float *x, size_t t, size_t h,
  * multihead_attn2 K/V [8,128,16] (kv[2*block], kv[2*block+1]). Returns
  * non-zero for an all-missing column that a context cannot hold. */
 static int column_stream(const ora_model *m, const float *x, const float *ycol, size_t t, size_t h,
-                         size_t n, size_t f, float *emb, float **kv) {
+                         size_t n, size_t f, int workers, float *emb, float **kv) {
     column_input(m, x, t, h, f, emb);
     for (size_t r = 0; r < n; ++r)
         for (size_t c = 0; c < D; ++c) emb[r * D + c] += ycol[r * D + c];
@@ -690,18 +690,18 @@ static int column_stream(const ora_model *m, const float *x, const float *ycol, 
             continue;
         }
         /* multihead_attn1: inducing points attend to the n training rows, with QASS. */
-        source_heads(m, &m->col1[blk], emb, n, 0, 1, kh, vh);
+        source_heads(m, &m->col1[blk], emb, n, 0, workers, kh, vh);
         qass_base(&m->col1[blk], n, base);
-        attend_opts o1 = {base, ORA_MATH_EXACT, 0, 1};
+        attend_opts o1 = {base, ORA_MATH_EXACT, 0, workers};
         st = attend(m, &m->col1[blk], m->ind[blk], M, kh, vh, n, &o1, hidden);
         if (st) break;
         /* multihead_attn2: all t rows attend to the inducing state. */
-        source_heads(m, &m->col2[blk], hidden, M, 0, 1, kh, vh);
+        source_heads(m, &m->col2[blk], hidden, M, 0, workers, kh, vh);
         if (kv) {
             memcpy(kv[2 * blk], kh, M * D * 4);
             memcpy(kv[2 * blk + 1], vh, M * D * 4);
         }
-        attend_opts o2 = {NULL, ORA_MATH_EXACT, 0, 1};
+        attend_opts o2 = {NULL, ORA_MATH_EXACT, 0, workers};
         st = attend(m, &m->col2[blk], emb, t, kh, vh, M, &o2, next);
         memcpy(emb, next, t * D * 4);
     }
@@ -779,7 +779,7 @@ static int column_embeddings(const ora_model *m, const float *x, const float *y,
         float *emb = xcalloc(t * D, sizeof(float));
         float *kv[6];
         for (int i = 0; i < 6; ++i) kv[i] = feature_kv ? feature_kv[i] + f * M * D : NULL;
-        st |= column_stream(m, x, ycol, t, h, n, f, emb, feature_kv ? kv : NULL) != 0;
+        st |= column_stream(m, x, ycol, t, h, n, f, 1, emb, feature_kv ? kv : NULL) != 0;
         for (size_t r = 0; r < t; ++r) memcpy(columns + (r * streams + RES + f) * D, emb + r * D, D * 4);
         free(emb);
     }
@@ -902,12 +902,16 @@ int ora_context_columns(const ora_model *m, size_t n, size_t h, const float *x, 
     float *ycol = xcalloc(n * D, sizeof(float));
     target_embeddings(m, m->col_yw, m->col_yb, y, n, D, ycol);
     int st = 0;
-#pragma omp parallel for num_threads(g_threads) schedule(dynamic) reduction(| : st)
+    /* Fewer features than threads: one feature at a time, its products and
+     * attention on every thread (rows and heads split; each value is computed
+     * as on one thread). */
+    int outer = nf < (size_t)g_threads ? 1 : g_threads, inner = outer == 1 ? g_threads : 1;
+#pragma omp parallel for num_threads(outer) schedule(dynamic) reduction(| : st)
     for (size_t i = 0; i < nf; ++i) {
         float *emb = xcalloc(n * D, sizeof(float));
         float *out[6];
         for (int j = 0; j < 6; ++j) out[j] = kv[j] + i * stream_el;
-        st |= column_stream(m, x, ycol, n, h, n, features[i], emb, out) != 0;
+        st |= column_stream(m, x, ycol, n, h, n, features[i], inner, emb, out) != 0;
         free(emb);
     }
     free(ycol);

@@ -180,3 +180,20 @@ def test_spot_checks_see_a_wrong_block(lcg_case):
     bad_cv[2][4 + 1] *= 1.01
     keys, _ = m.context_rows(x[0], y[0], rows, [c[0] for c in ck], bad_cv, [t[0] for t in ik], [t[0] for t in iv])
     assert not np.array_equal(keys[0], ik[0][0][:, rows])
+
+
+def test_float64_spot_checks_match_the_oracle_build(lcg_case, clf_weights):
+    """The float64 restatement's spot checks (column K/V of a feature, a
+    training row's ICL K/V by teacher forcing) agree with the oracle's build."""
+    from reference_np import Model
+
+    _, x, y, _, (ck, cv, ik, iv) = lcg_case
+    m = Model("classifier", clf_weights)
+    for blk, (k, v) in enumerate(m.column_kv(x[1], y[1], 2)):
+        np.testing.assert_allclose(k, ck[blk][1, 6], atol=2e-5, rtol=1e-4)
+        np.testing.assert_allclose(v, cv[blk][1, 6], atol=2e-5, rtol=1e-4)
+    keys, values = m.row_kv(x[1, 33], y[1, 33], [c[1] for c in ck], [c[1] for c in cv], [t[1] for t in ik],
+                            [t[1] for t in iv])
+    for blk in range(12):
+        np.testing.assert_allclose(keys[blk], ik[blk][1][:, 33], atol=2e-5, rtol=1e-4)
+        np.testing.assert_allclose(values[blk], iv[blk][1][:, 33], atol=2e-5, rtol=1e-4)
