@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void column_input_kernel(const float *x, long 
     v = fmaf(in_w[ch * 3 + 2], s2, v);
     if (s0 == -100.0f && s1 == -100.0f && s2 == -100.0f) {
         v = -100.0f;
-        if (missing && ch == 0) missing[(long long)e * rows + r] = 1;
+        if (missing && ch == 0) missing[r] = 1;  // row r holds the marker in some estimator
     }
     if (labels) v += labels[((long long)e * rows + r) * kColumnDim + ch];
     state[idx] = v;

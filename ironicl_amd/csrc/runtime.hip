@@ -300,6 +300,9 @@ struct irx_predictor {
     int streams = 2;
     std::mutex mu;
     Arena ws[kMaxPassStreams];
+    // Host-buffer predictions: device inputs, outputs and missing-row flags,
+    // grown to the largest call so far.
+    DevBuf io_x, io_logits, io_flags;
     hipStream_t lane(int slot) const { return slot ? side[slot - 1] : stream; }
     size_t ws_rows = 0;
 };
@@ -976,7 +979,6 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
 // function sizes the workspace (counting arena) and carves it, so the two
 // always agree; a shorter last pass uses a prefix of each buffer.
 struct PassBuffers {
-    uint8_t *flags;
     float *state, *norm, *q, *att, *hid, *rows;
     Stages::RowBuffers rb;
     Stages::IclBuffers ib;
@@ -985,7 +987,6 @@ struct PassBuffers {
 PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus, bool f16) {
     const long long B = sh.ensembles, H = sh.features, cr = B * H * (long long)R;
     PassBuffers p{};
-    p.flags = a.take_bytes(B * R);
     p.state = a.take(cr * 128), p.norm = a.take(cr * 128), p.q = a.take(cr * 128), p.att = a.take(cr * 128);
     p.hid = a.take(cr * 256);
     p.rb = Stages::row_buffers(a, B * (long long)R, (int)H + kReserved);
@@ -1011,8 +1012,11 @@ size_t predict_ws_floats(const irx_shape &sh, size_t R, int cus, bool f16) {
     return count.used / 4;
 }
 
+// One pass of R query rows starting at row q0 of x [B, Q, H] (row stride
+// x_stride between estimators) into logits [B, Q, width]; rows holding the
+// all-missing marker set d_flags[q0 + r] (device, [Q], or null).
 void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stride, int q0, int R, float *d_logits,
-                  int Q, uint8_t *flags_host) {
+                  int Q, uint8_t *d_flags) {
     const irx_weights &W = *P->weights;
     const irx_shape &sh = P->shape;
     const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
@@ -1023,13 +1027,12 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     ws.used = 0;
     const bool f16 = P->precision != IRX_PRECISION_FP32;
     const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus, f16);
-    uint8_t *flags = pb.flags;
     float *state = pb.state, *norm = pb.norm, *q = pb.q, *att = pb.att, *hid = pb.hid, *rows = pb.rows;
     const Stages::RowBuffers &rb = pb.rb;
     Stages::IclBuffers ib = pb.ib;
 
-    IRX_HIP(hipMemsetAsync(flags, 0, (size_t)B * R, s));
-    column_input(d_x + (size_t)q0 * H, x_stride, B, R, H, W.in_w, W.in_b, nullptr, state, flags, s);
+    column_input(d_x + (size_t)q0 * H, x_stride, B, R, H, W.in_w, W.in_b, nullptr, state,
+                 d_flags ? d_flags + q0 : nullptr, s);
     const long long col_plane = (long long)B * L * kColumnCache;
     for (int blk = 0; blk < kColumnBlocks; ++blk) {
         const float *kc = P->column[blk].f() + kReserved * kColumnCache;
@@ -1066,13 +1069,6 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     OutMap lmap{width, 1, 0, 0, R, (long long)Q * width, width};
     st.linear_map(ib.hid, 1024, (long long)B * R, 1024, W.dec2.w, W.dec2.b, width, d_logits + (size_t)q0 * width,
                   lmap);
-    if (flags_host) {
-        std::vector<uint8_t> f((size_t)B * R);
-        download(f.data(), flags, f.size(), s);
-        IRX_HIP(hipStreamSynchronize(s));
-        for (int b = 0; b < B; ++b)
-            for (int r = 0; r < R; ++r) flags_host[q0 + r] |= f[(size_t)b * R + r];
-    }
 }
 
 void ensure_workspace(irx_predictor *P) {
@@ -1433,10 +1429,18 @@ int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows) {
     });
 }
 
+// Every pass of a prediction of q rows. With cpu_rows (host, [q]), the rows
+// holding the all-missing marker are flagged there: the passes set device
+// flags, read back once after the last pass, so passes never wait on the host.
 static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *d_logits, uint8_t *cpu_rows,
                            irx_progress_fn progress, void *user) {
     const size_t R = P->pass_rows;
-    if (cpu_rows) std::memset(cpu_rows, 0, q);
+    uint8_t *d_flags = nullptr;
+    if (cpu_rows) {
+        if (P->io_flags.bytes < q) P->io_flags.alloc(q);
+        d_flags = static_cast<uint8_t *>(P->io_flags.p);
+        IRX_HIP(hipMemsetAsync(d_flags, 0, q, P->stream));
+    }
     // Side streams start after everything already queued on the main one (the
     // inputs' upload), and the main stream ends after the side streams' passes.
     const int lanes = P->streams;
@@ -1445,7 +1449,7 @@ static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *
     int slot = 0;
     for (size_t q0 = 0; q0 < q; q0 += R, slot = (slot + 1) % lanes) {
         const int len = (int)std::min(R, q - q0);
-        predict_pass(P, slot, d_x, (long long)q * P->shape.features, (int)q0, len, d_logits, (int)q, cpu_rows);
+        predict_pass(P, slot, d_x, (long long)q * P->shape.features, (int)q0, len, d_logits, (int)q, d_flags);
         if (progress) {
             IRX_HIP(hipStreamSynchronize(P->lane(slot)));
             report(progress, user, IRX_STAGE_PREDICT, q0 + len, q);
@@ -1455,6 +1459,7 @@ static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *
         IRX_HIP(hipEventRecord(P->join[i - 1], P->lane(i)));
         IRX_HIP(hipStreamWaitEvent(P->stream, P->join[i - 1], 0));
     }
+    if (cpu_rows) download(cpu_rows, d_flags, q, P->stream);  // complete at the caller's synchronisation
 }
 
 int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, float *logits, uint8_t *cpu_rows,
@@ -1466,10 +1471,13 @@ int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, fl
         set_device(predictor->weights->device);
         const irx_shape &sh = predictor->shape;
         const size_t xn = sh.ensembles * q * sh.features, ln = sh.ensembles * q * sh.outputs;
-        DevBuf dx(xn * 4), dl(ln * 4);
-        upload(dx.p, x, xn * 4, predictor->stream);
-        predict_common(predictor, dx.f(), q, dl.f(), cpu_rows, progress, progress_user);
-        download(logits, dl.p, ln * 4, predictor->stream);
+        // Device copies of the inputs and outputs, kept and grown across calls.
+        if (predictor->io_x.bytes < xn * 4) predictor->io_x.alloc(xn * 4);
+        if (predictor->io_logits.bytes < ln * 4) predictor->io_logits.alloc(ln * 4);
+        upload(predictor->io_x.p, x, xn * 4, predictor->stream);
+        predict_common(predictor, predictor->io_x.f(), q, predictor->io_logits.f(), cpu_rows, progress,
+                       progress_user);
+        download(logits, predictor->io_logits.p, ln * 4, predictor->stream);
         IRX_HIP(hipStreamSynchronize(predictor->stream));
     });
 }

@@ -141,6 +141,20 @@ def test_missing_marker_rows_are_flagged(lcg):
     p = ctx_gpu.predict_raw(xt)
     assert p.cpu_rows == [7]
     assert np.all(np.isnan(p.logits[:, 7])) and np.all(np.isfinite(np.delete(p.logits, 7, axis=1)))
+    # Over several passes on two streams, in both estimators, and again after
+    # a call without marked rows (the flags start from zero on every call).
+    xt = lcg[2][:, :200].copy()
+    xt[0, 3, :] = -100.0
+    xt[1, 150, :] = -100.0
+    xt[0, 199, :] = -100.0
+    default = ctx_gpu.pass_rows()
+    ctx_gpu.set_pass_rows(64)
+    try:
+        assert ctx_gpu.predict_raw(lcg[2][:, :200]).cpu_rows == []
+        assert ctx_gpu.predict_raw(xt).cpu_rows == [3, 150, 199]
+        assert ctx_gpu.predict_raw(lcg[2][:, :200]).cpu_rows == []
+    finally:
+        ctx_gpu.set_pass_rows(default)
 
 
 def test_config_clf_1k_end_to_end(clf, clf_oracle):
