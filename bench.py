@@ -451,7 +451,6 @@ def bench_workload(name: str, args) -> dict:
     for _ in range(1 if big else args.warmup):
         step()
     hipmem.synchronize()
-    hip.profile_enable(True)
     t0 = time.perf_counter()
     for i in range(steps):
         step()
@@ -460,9 +459,14 @@ def bench_workload(name: str, args) -> dict:
             log(f"prediction step {i + 1} of {steps}: {time.perf_counter() - t0:.2f} s")
     hipmem.synchronize()
     elapsed = time.perf_counter() - t0
+    logits = dl.to_host()
+    # Kernel families of one more step, every launch timed (passes then launch
+    # kernel by kernel rather than from their graphs).
+    hip.profile_enable(True)
+    step()
+    hipmem.synchronize()
     stats = {f: hip.profile_read(f) for f in hip.KERNEL_FAMILIES}
     hip.profile_enable(False)
-    logits = dl.to_host()
     log(f"{name}: {q * steps / elapsed:.0f} test rows/s ({1000 * elapsed / steps:.1f} ms per {q} rows)")
     if not big:
         build_kernels = profiled_build(executor, x, y)
@@ -485,7 +489,7 @@ def bench_workload(name: str, args) -> dict:
                    "train_rows": n, "features": h, "test_rows": q, "estimators": b, "classes": w.classes},
         "build_ms": float(np.median(build_ms)),
         "build_ms_all": build_ms,
-        "predict_kernels_per_step": family_breakdown(stats, steps),
+        "predict_kernels_per_step": family_breakdown(stats),
         "build_kernels": build_kernels,
         "parity": parity,
     }
@@ -611,12 +615,19 @@ def main() -> int:
 
         small_step()
         hipmem.synchronize()
+        # Whole-pass latency, each pass replayed from its HIP graph.
+        t0 = time.perf_counter()
+        for _ in range(SMALL_PASS_REPEATS):
+            small_step()
+            hipmem.synchronize()
+        pass_ms = 1000 * (time.perf_counter() - t0) / SMALL_PASS_REPEATS
+        # Kernel timing (HIP events) launches the passes kernel by kernel.
         hip.profile_enable(["icl_attention", "icl_merge"])
         t0 = time.perf_counter()
         for _ in range(SMALL_PASS_REPEATS):
             small_step()
         hipmem.synchronize()
-        pass_ms = 1000 * (time.perf_counter() - t0) / SMALL_PASS_REPEATS
+        launched_ms = 1000 * (time.perf_counter() - t0) / SMALL_PASS_REPEATS
         att = hip.profile_read("icl_attention")
         mrg = hip.profile_read("icl_merge")
         hip.profile_enable(False)
@@ -631,6 +642,7 @@ def main() -> int:
             "frac": algo / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
             "frac_with_merge": algo / ((launch_ms + merge_ms) * 1e-3) / 1e9 / HBM_PEAK_GBPS,
             "ms_per_pass": pass_ms,
+            "ms_per_pass_launched_with_timing": launched_ms,
             "launches": att["launches"],
         }
         log(f"pass of {qb:2d} rows: {pass_ms:.2f} ms, attention {1e3 * launch_ms:.1f} us/launch, "

@@ -199,6 +199,13 @@ int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows);
  * Results are identical either way. No counterpart in the reference (its
  * predictor runs passes in order, predictor.rs:224-271). */
 int irx_predictor_set_streams(irx_predictor *predictor, int streams);
+/* Whether prediction passes replay HIP graphs (1, the default; the environment
+ * variable IRONICL_NO_GRAPHS=1 makes 0 the default) or launch their kernels one
+ * by one (0). A graph is captured per stream and pass size on first use; each
+ * replay reads the pass's rows from a copy in the stream's workspace. Passes
+ * launch one by one while kernel timing (irx_profile_enable) is on. Results are
+ * identical either way. No counterpart in the reference. */
+int irx_predictor_set_graphs(irx_predictor *predictor, int enable);
 /* Copies floats [offset, offset + floats) of one resident context tensor to
  * host memory, after every pass issued before the call. `tensor` indexes the
  * reference's context tensor order (context_tensors, cpu.rs:4106-4123):

@@ -303,6 +303,19 @@ struct irx_predictor {
     // Host-buffer predictions: device inputs, outputs and missing-row flags,
     // grown to the largest call so far.
     DevBuf io_x, io_logits, io_flags;
+    // Passes replayed from HIP graphs, one per (stream slot, rows), captured on
+    // first use over the slot's workspace; dropped when a workspace moves.
+    struct PassGraph {
+        int slot;
+        int rows;
+        hipGraphExec_t exec;
+    };
+    std::vector<PassGraph> graphs;
+    bool use_graphs = true;
+    void drop_graphs() {
+        for (auto &g : graphs) (void)hipGraphExecDestroy(g.exec);
+        graphs.clear();
+    }
     hipStream_t lane(int slot) const { return slot ? side[slot - 1] : stream; }
     size_t ws_rows = 0;
 };
@@ -979,6 +992,10 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
 // function sizes the workspace (counting arena) and carves it, so the two
 // always agree; a shorter last pass uses a prefix of each buffer.
 struct PassBuffers {
+    // A graph-replayed pass reads its rows from xin [B, R, H], writes logits
+    // [B, R, width] to lout and missing-row flags [R] to fin (fixed addresses).
+    float *xin, *lout;
+    uint8_t *fin;
     float *state, *norm, *q, *att, *hid, *rows;
     Stages::RowBuffers rb;
     Stages::IclBuffers ib;
@@ -987,6 +1004,8 @@ struct PassBuffers {
 PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus, bool f16) {
     const long long B = sh.ensembles, H = sh.features, cr = B * H * (long long)R;
     PassBuffers p{};
+    p.xin = a.take(B * H * (long long)R), p.lout = a.take(B * (long long)R * (long long)sh.outputs);
+    p.fin = reinterpret_cast<uint8_t *>(a.take((R + 3) / 4));
     p.state = a.take(cr * 128), p.norm = a.take(cr * 128), p.q = a.take(cr * 128), p.att = a.take(cr * 128);
     p.hid = a.take(cr * 256);
     p.rb = Stages::row_buffers(a, B * (long long)R, (int)H + kReserved);
@@ -1012,27 +1031,23 @@ size_t predict_ws_floats(const irx_shape &sh, size_t R, int cus, bool f16) {
     return count.used / 4;
 }
 
-// One pass of R query rows starting at row q0 of x [B, Q, H] (row stride
-// x_stride between estimators) into logits [B, Q, width]; rows holding the
-// all-missing marker set d_flags[q0 + r] (device, [Q], or null).
-void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stride, int q0, int R, float *d_logits,
-                  int Q, uint8_t *d_flags) {
+// The kernels of one pass over the slot's workspace `pb`: R rows of x [B, ., H]
+// (row stride x_stride between estimators) into logits [B, ., width] (Q rows
+// per estimator), flags [R] (or null) set for rows holding the marker.
+void issue_pass(irx_predictor *P, int slot, const PassBuffers &pb, const float *x, long long x_stride, int R,
+                float *logits, int Q, uint8_t *flags) {
     const irx_weights &W = *P->weights;
     const irx_shape &sh = P->shape;
     const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
     const int width = (int)sh.outputs;
     hipStream_t s = P->lane(slot);
     Stages st{W, s, W.device->compute_units};
-    Arena &ws = P->ws[slot];
-    ws.used = 0;
     const bool f16 = P->precision != IRX_PRECISION_FP32;
-    const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, st.cus, f16);
     float *state = pb.state, *norm = pb.norm, *q = pb.q, *att = pb.att, *hid = pb.hid, *rows = pb.rows;
     const Stages::RowBuffers &rb = pb.rb;
     Stages::IclBuffers ib = pb.ib;
 
-    column_input(d_x + (size_t)q0 * H, x_stride, B, R, H, W.in_w, W.in_b, nullptr, state,
-                 d_flags ? d_flags + q0 : nullptr, s);
+    column_input(x, x_stride, B, R, H, W.in_w, W.in_b, nullptr, state, flags, s);
     const long long col_plane = (long long)B * L * kColumnCache;
     for (int blk = 0; blk < kColumnBlocks; ++blk) {
         const float *kc = P->column[blk].f() + kReserved * kColumnCache;
@@ -1067,8 +1082,57 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
         st.linear(ib.norm, 512, (long long)B * R, 512, W.dec0.w, W.dec0.b, 1024, ib.hid, 1024, kEpiGelu);
     }
     OutMap lmap{width, 1, 0, 0, R, (long long)Q * width, width};
-    st.linear_map(ib.hid, 1024, (long long)B * R, 1024, W.dec2.w, W.dec2.b, width, d_logits + (size_t)q0 * width,
-                  lmap);
+    st.linear_map(ib.hid, 1024, (long long)B * R, 1024, W.dec2.w, W.dec2.b, width, logits, lmap);
+}
+
+// One pass of R query rows starting at row q0 of x [B, Q, H] (row stride
+// x_stride between estimators) into logits [B, Q, width]; rows holding the
+// all-missing marker set d_flags[q0 + r] (device, [Q], or null). Unless kernel
+// timing is on (or graphs are off), the pass replays a HIP graph captured over
+// the slot's workspace: its rows are first copied into the workspace and its
+// logits and flags copied out after, so one graph serves every call.
+void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stride, int q0, int R, float *d_logits,
+                  int Q, uint8_t *d_flags) {
+    const irx_shape &sh = P->shape;
+    const int B = (int)sh.ensembles, H = (int)sh.features, width = (int)sh.outputs;
+    hipStream_t s = P->lane(slot);
+    Arena &ws = P->ws[slot];
+    ws.used = 0;
+    const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, P->weights->device->compute_units,
+                                       P->precision != IRX_PRECISION_FP32);
+    if (!P->use_graphs || g_profiling.load(std::memory_order_relaxed)) {
+        issue_pass(P, slot, pb, d_x + (size_t)q0 * H, x_stride, R, d_logits + (size_t)q0 * width, Q,
+                   d_flags ? d_flags + q0 : nullptr);
+        return;
+    }
+    IRX_HIP(hipMemcpy2DAsync(pb.xin, (size_t)R * H * 4, d_x + (size_t)q0 * H, (size_t)x_stride * 4, (size_t)R * H * 4,
+                             B, hipMemcpyDeviceToDevice, s));
+    hipGraphExec_t exec = nullptr;
+    for (const auto &g : P->graphs)
+        if (g.slot == slot && g.rows == R) exec = g.exec;
+    if (!exec) {
+        if (P->graphs.size() >= 16) P->drop_graphs();
+        hipGraph_t graph = nullptr;
+        IRX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        try {
+            // Flags start from zero on every replay: a fill kernel, not a memset node.
+            fill_zero(reinterpret_cast<float *>(pb.fin), (R + 3) / 4, s);
+            issue_pass(P, slot, pb, pb.xin, (long long)R * H, R, pb.lout, R, pb.fin);
+        } catch (...) {
+            (void)hipStreamEndCapture(s, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            throw;
+        }
+        IRX_HIP(hipStreamEndCapture(s, &graph));
+        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        IRX_HIP(e);
+        P->graphs.push_back({slot, R, exec});
+    }
+    IRX_HIP(hipGraphLaunch(exec, s));
+    IRX_HIP(hipMemcpy2DAsync(d_logits + (size_t)q0 * width, (size_t)Q * width * 4, pb.lout, (size_t)R * width * 4,
+                             (size_t)R * width * 4, B, hipMemcpyDeviceToDevice, s));
+    if (d_flags) IRX_HIP(hipMemcpyAsync(d_flags + q0, pb.fin, R, hipMemcpyDeviceToDevice, s));
 }
 
 void ensure_workspace(irx_predictor *P) {
@@ -1077,6 +1141,7 @@ void ensure_workspace(irx_predictor *P) {
     if (ready) return;
     for (int i = 0; i < kMaxPassStreams; ++i)
         if (P->lane(i)) IRX_HIP(hipStreamSynchronize(P->lane(i)));
+    P->drop_graphs();  // they hold the old workspaces' addresses
     size_t floats = predict_ws_floats(P->shape, P->pass_rows, P->weights->device->compute_units,
                                       P->precision != IRX_PRECISION_FP32);
     // Workspaces of streams in use, at the current pass size; the others are released.
@@ -1269,6 +1334,8 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         irx_weights_retain(weights);
         P->shape = sh;
         P->precision = precision;
+        const char *no_graphs = std::getenv("IRONICL_NO_GRAPHS");
+        P->use_graphs = !(no_graphs && *no_graphs && std::strcmp(no_graphs, "0") != 0);
         if (adopt) {
             if (adopt->shape.ensembles != sh.ensembles || adopt->shape.features != sh.features ||
                 adopt->shape.rows != sh.rows)
@@ -1353,6 +1420,9 @@ void irx_predictor_free(irx_predictor *predictor) {
     irx_weights *w = predictor->weights;
     if (w) {
         (void)hipSetDevice(w->device->ordinal);
+        for (int i = 0; i < kMaxPassStreams; ++i)
+            if (predictor->lane(i)) (void)hipStreamSynchronize(predictor->lane(i));
+        predictor->drop_graphs();
         return_stream(w->device, predictor->stream);
         for (int i = 0; i < kMaxPassStreams - 1; ++i) return_stream(w->device, predictor->side[i]);
     }
@@ -1366,6 +1436,18 @@ void irx_predictor_free(irx_predictor *predictor) {
 int irx_predictor_streamed(const irx_predictor *) { return 0; }
 
 size_t irx_predictor_pass_rows(const irx_predictor *predictor) { return predictor ? predictor->pass_rows : 0; }
+
+int irx_predictor_set_graphs(irx_predictor *predictor, int enable) {
+    return guarded("irx_predictor_set_graphs", [&] {
+        if (!predictor) fail(IRX_INVALID_ARGUMENT, "null predictor");
+        std::lock_guard<std::mutex> lock(predictor->mu);
+        set_device(predictor->weights->device);
+        for (int i = 0; i < kMaxPassStreams; ++i)
+            if (predictor->lane(i)) IRX_HIP(hipStreamSynchronize(predictor->lane(i)));
+        predictor->drop_graphs();
+        predictor->use_graphs = enable != 0;
+    });
+}
 
 int irx_predictor_set_streams(irx_predictor *predictor, int streams) {
     return guarded("irx_predictor_set_streams", [&] {

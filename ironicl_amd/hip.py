@@ -84,6 +84,7 @@ SIGNATURES = {
     "irx_predictor_pass_rows": (_sz, [ctypes.c_void_p]),
     "irx_predictor_set_pass_rows": (ctypes.c_int, [ctypes.c_void_p, _sz]),
     "irx_predictor_set_streams": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "irx_predictor_set_graphs": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "irx_predictor_read_context": (ctypes.c_int, [ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p]),
     "irx_preprocess_fit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _sz, _sz,
                                           ctypes.c_void_p, _sz, ctypes.c_void_p, _sz, ctypes.c_double,

@@ -497,6 +497,11 @@ class StaticExecutor:
     def set_pass_rows(self, rows: int) -> None:
         hip.check(hip.lib().irx_predictor_set_pass_rows(self.handle, rows))
 
+    def set_graphs(self, enable: bool) -> None:
+        """Replay prediction passes from HIP graphs (the default) or launch
+        their kernels one by one; results are identical."""
+        hip.check(hip.lib().irx_predictor_set_graphs(self.handle, int(bool(enable))))
+
     def set_streams(self, streams: int) -> None:
         """Passes rotate over `streams` (1 to 4) HIP streams; results are identical."""
         hip.check(hip.lib().irx_predictor_set_streams(self.handle, streams))

@@ -117,6 +117,32 @@ def test_stream_counts_give_identical_results(lcg):
             ctx_gpu.set_streams(bad)
 
 
+def test_graph_replays_match_launched_passes(lcg):
+    """Passes replayed from HIP graphs give the logits of passes launched
+    kernel by kernel, bitwise, with new rows on every replay (three inputs,
+    twice round), at 512-, 64- and 32-row passes with a ragged last pass, on
+    one and two streams."""
+    *_, ctx = lcg
+    xt = lcg[2]
+    inputs = [np.ascontiguousarray(xt[:, a:a + 200]) for a in (0, 50, 25)]
+    default = ctx.pass_rows()
+    try:
+        for rows in (512, 64, 32):
+            ctx.set_pass_rows(rows)
+            for streams in (1, 2):
+                ctx.set_streams(streams)
+                ctx.set_graphs(False)
+                eager = [ctx.predict_raw(x).logits for x in inputs]
+                ctx.set_graphs(True)
+                for _ in range(2):
+                    for x, want in zip(inputs, eager):
+                        np.testing.assert_array_equal(ctx.predict_raw(x).logits, want)
+    finally:
+        ctx.set_graphs(True)
+        ctx.set_streams(2)
+        ctx.set_pass_rows(default)
+
+
 def test_kernel_timing_records_launches(lcg):
     *_, ctx_gpu = lcg
     hip.profile_enable(True)
