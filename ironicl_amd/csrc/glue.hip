@@ -61,6 +61,35 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, long lo
     }
 }
 
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+    for (int offset = 16; offset >= 1; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+// 128-wide rows (layer_norm_f32, reference.rs:223-252: two-pass mean and
+// variance, eps 1e-5): 32 lanes per row, each moving 16 bytes, two rows per
+// wave and eight per workgroup, so every load and store instruction of a wave
+// covers 1 KB of contiguous rows. Shuffles stay within a row's half-wave.
+__global__ __launch_bounds__(256) void layer_norm128_kernel(const float *x, long long ldx, const float *w,
+                                                            const float *b, float *y, long long ldy, long long rows) {
+    const long long row = (long long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (row >= rows) return;  // a whole half-wave: its shuffles never read the other half
+    const int c = (threadIdx.x & 31) * 4;
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(x + row * ldx + c);
+    const float mean = half_wave_sum((v[0] + v[1]) + (v[2] + v[3])) / 128.0f;
+    const f32x4 d = v - mean;
+    float sq = d[0] * d[0];
+    sq = fmaf(d[1], d[1], sq);
+    sq = fmaf(d[2], d[2], sq);
+    sq = fmaf(d[3], d[3], sq);
+    const float rstd = 1.0f / sqrtf(half_wave_sum(sq) / 128.0f + 1e-5f);
+    const f32x4 g = *reinterpret_cast<const f32x4 *>(w + c);
+    f32x4 o = d * rstd * g;
+    if (b) o += *reinterpret_cast<const f32x4 *>(b + c);
+    *reinterpret_cast<f32x4 *>(y + row * ldy + c) = o;
+}
+
 // Grouped features (f+1, f+2, f+4) mod H through the 3 -> 128 input affine
 // (cpu.rs:1144-1157, 2461-2473), the -100 all-missing marker, and the
 // column-stage label embeddings of training rows.
@@ -166,12 +195,13 @@ void layer_norm(const float *x, long long ldx, const float *weight, const float 
     if (rows <= 0) return;
     if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(y) & 15) || (ldx & 3) || (ldy & 3))
         fail(3, "layer norm operands must be 16-byte aligned");
-    dim3 grid(ceil_div(rows, 4));
     KernelTimer timer(kFamNorm, stream, 8.0 * rows * width, 8.0 * rows * width);
     if (width == 128)
-        hipLaunchKernelGGL(layer_norm_kernel<128>, grid, dim3(256), 0, stream, x, ldx, weight, bias, y, ldy, rows);
+        hipLaunchKernelGGL(layer_norm128_kernel, dim3(ceil_div(rows, 8)), dim3(256), 0, stream, x, ldx, weight, bias,
+                           y, ldy, rows);
     else if (width == 512)
-        hipLaunchKernelGGL(layer_norm_kernel<512>, grid, dim3(256), 0, stream, x, ldx, weight, bias, y, ldy, rows);
+        hipLaunchKernelGGL(layer_norm_kernel<512>, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, ldx, weight,
+                           bias, y, ldy, rows);
     else
         fail(3, "layer norm width must be 128 or 512");
     IRX_HIP(hipGetLastError());

@@ -638,6 +638,7 @@ void weights_load(irx_weights *W, irx_tensor_lookup lookup, void *user) {
     // Heads fused with LN1 for prediction: the column blocks' queries, the row
     // blocks' Q/K/V, the CLS block's K/V over every token.
     for (int b = 0; b < kColumnBlocks; ++b) L.pack_head(W->col2[b], 0, 128);
+    for (int b = 0; b < kColumnBlocks; ++b) L.pack_head(W->col1[b], 128, 256);  // the build's attn1 K/V
     for (int b = 0; b < kRowBlocks; ++b) L.pack_head(W->row[b], b + 1 < kRowBlocks ? 0 : 128, b + 1 < kRowBlocks ? 384 : 256);
     L.take("row_interactor.cls_tokens", 4 * 128, &W->cls);
     L.take("row_interactor.out_ln.weight", 128, &W->out_ln_w);
@@ -845,8 +846,7 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
                 for (int blk = 0; blk < kColumnBlocks; ++blk) {
                     // multihead_attn1: the inducing points attend to the column's N rows, QASS'd queries.
                     const BlockW &b1 = W->col1[blk];
-                    layer_norm(state, 128, b1.n1w, b1.n1b, norm, 128, m, 128, s);
-                    st.linear(norm, 128, m, 128, b1.in_w + 128 * 128, b1.in_b + 128, 256, kv, 256);
+                    st.head(b1, state, m, norm, kv, 256);  // LN1 + the K/V rows of in_proj
                     SmallAttention a{};
                     a.q = d_ind_q + blk * 128 * 128, a.q_seq = 0, a.q_group = 0, a.q_row = 128, a.q_head = 16;
                     a.k = kv, a.v = kv + 128, a.k_seq = a.v_seq = (long long)N * 256, a.k_group = a.v_group = 0;
