@@ -92,50 +92,61 @@ __global__ __launch_bounds__(256) void layer_norm128_kernel(const float *x, long
 
 // Grouped features (f+1, f+2, f+4) mod H through the 3 -> 128 input affine
 // (cpu.rs:1144-1157, 2461-2473), the -100 all-missing marker, and the
-// column-stage label embeddings of training rows.
+// column-stage label embeddings of training rows. One thread per four channels
+// of an (estimator, feature, row); the launcher keeps b * h * rows below 2^32
+// so the index arithmetic is 32-bit.
 __global__ __launch_bounds__(256) void column_input_kernel(const float *x, long long xs, int b, int rows, int h,
                                                            const float *in_w, const float *in_b,
                                                            const float *labels, float *state,
                                                            uint8_t *missing) {
-    const long long total = (long long)b * h * rows * kColumnDim;
-    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (long long)gridDim.x * 256) {
-    const int ch = idx & (kColumnDim - 1);
-    const long long cr = idx >> 7;
-    const int r = (int)(cr % rows);
-    const int c = (int)(cr / rows);
-    const int e = c / h, f = c - e * h;
-    const float *xr = x + (long long)e * xs + (long long)r * h;
-    const float s0 = xr[(f + 1) % h], s1 = xr[(f + 2) % h], s2 = xr[(f + 4) % h];
-    float v = fmaf(in_w[ch * 3 + 0], s0, in_b[ch]);
-    v = fmaf(in_w[ch * 3 + 1], s1, v);
-    v = fmaf(in_w[ch * 3 + 2], s2, v);
-    if (s0 == -100.0f && s1 == -100.0f && s2 == -100.0f) {
-        v = -100.0f;
-        if (missing && ch == 0) missing[r] = 1;  // row r holds the marker in some estimator
-    }
-    if (labels) v += labels[((long long)e * rows + r) * kColumnDim + ch];
-    state[idx] = v;
+    const long long total4 = (long long)b * h * rows * (kColumnDim / 4);
+    const unsigned urows = (unsigned)rows, uh = (unsigned)h;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total4; i += (long long)gridDim.x * 256) {
+        const int ch = (int)(i & (kColumnDim / 4 - 1)) * 4;
+        const unsigned cr = (unsigned)(i / (kColumnDim / 4));
+        const unsigned r = cr % urows, c = cr / urows;
+        const unsigned e = c / uh, f = c - e * uh;
+        const float *xr = x + (long long)e * xs + (long long)r * h;
+        const float s0 = xr[(f + 1) % uh], s1 = xr[(f + 2) % uh], s2 = xr[(f + 4) % uh];
+        // in_w [128, 3]: the 12 weights of channels ch..ch+3 are contiguous.
+        const f32x4 wa = *reinterpret_cast<const f32x4 *>(in_w + ch * 3);
+        const f32x4 wb = *reinterpret_cast<const f32x4 *>(in_w + ch * 3 + 4);
+        const f32x4 wc = *reinterpret_cast<const f32x4 *>(in_w + ch * 3 + 8);
+        const float w[12] = {wa[0], wa[1], wa[2], wa[3], wb[0], wb[1], wb[2], wb[3], wc[0], wc[1], wc[2], wc[3]};
+        const f32x4 bias = *reinterpret_cast<const f32x4 *>(in_b + ch);
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float t = fmaf(w[3 * j + 0], s0, bias[j]);
+            t = fmaf(w[3 * j + 1], s1, t);
+            v[j] = fmaf(w[3 * j + 2], s2, t);
+        }
+        if (s0 == -100.0f && s1 == -100.0f && s2 == -100.0f) {
+            v = f32x4{-100.0f, -100.0f, -100.0f, -100.0f};
+            if (missing && ch == 0) missing[r] = 1;  // row r holds the marker in some estimator
+        }
+        if (labels) v += *reinterpret_cast<const f32x4 *>(labels + ((long long)e * rows + r) * kColumnDim + ch);
+        *reinterpret_cast<f32x4 *>(state + (long long)cr * kColumnDim + ch) = v;
     }
 }
 
-// Row sequences: the 4 CLS tokens, then feature f's column state (cpu.rs:1226-1231).
+// Row sequences: the 4 CLS tokens, then feature f's column state
+// (cpu.rs:1226-1231). One thread per four channels of a token; the launcher
+// keeps b * rows * (h + 4) below 2^32.
 __global__ __launch_bounds__(256) void build_rows_kernel(const float *state, int b, int rows, int h,
                                                          const float *cls, float *seq) {
-    const int len = h + kReserved;
-    const long long total = (long long)b * rows * len * kColumnDim;
-    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (long long)gridDim.x * 256) {
-    const int ch = idx & (kColumnDim - 1);
-    const long long st = idx >> 7;
-    const int t = (int)(st % len);
-    const long long s = st / len;
-    const int r = (int)(s % rows);
-    const int e = (int)(s / rows);
-    float v;
-    if (t < kReserved)
-        v = cls[t * kColumnDim + ch];
-    else
-        v = state[(((long long)e * h + (t - kReserved)) * rows + r) * kColumnDim + ch];
-    seq[idx] = v;
+    const unsigned len = (unsigned)h + kReserved, urows = (unsigned)rows;
+    const long long total4 = (long long)b * rows * len * (kColumnDim / 4);
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total4; i += (long long)gridDim.x * 256) {
+        const int ch = (int)(i & (kColumnDim / 4 - 1)) * 4;
+        const unsigned st = (unsigned)(i / (kColumnDim / 4));
+        const unsigned t = st % len, s = st / len;
+        const unsigned r = s % urows, e = s / urows;
+        const f32x4 v = t < kReserved
+                            ? *reinterpret_cast<const f32x4 *>(cls + t * kColumnDim + ch)
+                            : *reinterpret_cast<const f32x4 *>(
+                                  state + (((long long)e * h + (t - kReserved)) * rows + r) * kColumnDim + ch);
+        *reinterpret_cast<f32x4 *>(seq + (long long)st * kColumnDim + ch) = v;
     }
 }
 
@@ -211,8 +222,12 @@ void column_input(const float *x, long long x_estimator_stride, int b, int rows,
                   const float *in_b, const float *labels, float *state, uint8_t *missing_rows, hipStream_t stream) {
     long long total = (long long)b * h * rows * kColumnDim;
     if (total <= 0) return;
+    if ((long long)b * h * rows >= (1LL << 32)) fail(3, "column input: more than 2^32 columns x rows");
+    if ((reinterpret_cast<uintptr_t>(state) | reinterpret_cast<uintptr_t>(labels) | reinterpret_cast<uintptr_t>(in_w) |
+         reinterpret_cast<uintptr_t>(in_b)) & 15)
+        fail(3, "column input: operands must be 16-byte aligned");
     KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * total + 4.0 * b * rows * h);
-    hipLaunchKernelGGL(column_input_kernel, grid_1d(total), dim3(256), 0, stream, x, x_estimator_stride, b, rows, h, in_w,
+    hipLaunchKernelGGL(column_input_kernel, grid_1d(total / 4), dim3(256), 0, stream, x, x_estimator_stride, b, rows, h, in_w,
                        in_b, labels, state, missing_rows);
     IRX_HIP(hipGetLastError());
 }
@@ -220,8 +235,11 @@ void column_input(const float *x, long long x_estimator_stride, int b, int rows,
 void build_rows(const float *state, int b, int rows, int h, const float *cls, float *seq, hipStream_t stream) {
     long long total = (long long)b * rows * (h + kReserved) * kColumnDim;
     if (total <= 0) return;
+    if ((long long)b * rows * (h + kReserved) >= (1LL << 32)) fail(3, "row sequences: more than 2^32 tokens");
+    if ((reinterpret_cast<uintptr_t>(state) | reinterpret_cast<uintptr_t>(cls) | reinterpret_cast<uintptr_t>(seq)) & 15)
+        fail(3, "row sequences: operands must be 16-byte aligned");
     KernelTimer timer(kFamGlue, stream, 0.0, 8.0 * total);
-    hipLaunchKernelGGL(build_rows_kernel, grid_1d(total), dim3(256), 0, stream, state, b, rows, h, cls,
+    hipLaunchKernelGGL(build_rows_kernel, grid_1d(total / 4), dim3(256), 0, stream, state, b, rows, h, cls,
                        seq);
     IRX_HIP(hipGetLastError());
 }
