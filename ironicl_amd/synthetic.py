@@ -184,6 +184,8 @@ def workload_data(w: Workload, train_rows: int | None = None, test_rows: int | N
             y = y.astype(np.float32)
             break
         attempt += 1
+        if attempt == 100:
+            raise ValueError(f"{w.name}: no seeded labeller covers all {c} classes at {h} features")
     xs, ys, xts, perms, fperms = [], [], [], [], []
     for e in range(b):
         fp = np.arange(h) if e == 0 else Stream(_key(w.data_seed, 0xFE0 + e)).permutation(h)
