@@ -1155,6 +1155,33 @@ void ensure_workspace(irx_predictor *P) {
     P->ws_rows = P->pass_rows;
 }
 
+// The pass workspaces beside the caches within `budget` (bytes the predictor
+// may use, caches included): when those of every stream at pass_rows do not
+// fit, or a hipMalloc runs out, one stream, then halved passes (multiples of
+// 32), as Predictor::predict halves its run rows on out-of-memory
+// (predictor.rs:248-258); IRX_DOES_NOT_FIT below one 32-row pass.
+void fit_workspace(irx_predictor *P, size_t cache_bytes, size_t budget) {
+    const bool f16 = P->precision != IRX_PRECISION_FP32;
+    const int cus = P->weights->device->compute_units;
+    for (;;) {
+        const size_t ws = (size_t)P->streams * predict_ws_floats(P->shape, P->pass_rows, cus, f16) * 4;
+        if (cache_bytes + ws <= budget / 10 * 9) {
+            try {
+                ensure_workspace(P);
+                return;
+            } catch (const Failure &f) {
+                if (f.status != IRX_OUT_OF_MEMORY) throw;
+            }
+        }
+        if (P->streams > 1)
+            P->streams = 1;
+        else if (P->pass_rows > 32)
+            P->pass_rows = std::max<size_t>(32, P->pass_rows / 64 * 32);
+        else
+            fail(IRX_DOES_NOT_FIT, "the prediction workspace does not fit the device");
+    }
+}
+
 int guarded(const char *where, auto &&fn) {
     try {
         fn();
@@ -1274,6 +1301,13 @@ int irx_weights_budget(const irx_weights *weights, uint64_t device_limit, size_t
     });
 }
 
+size_t irx_predict_workspace_bytes(const irx_shape *shape, int precision, size_t pass_rows) {
+    if (!shape_ok(shape) || !irx_context_bytes(precision) || pass_rows < 1 || pass_rows > (1u << 20)) return 0;
+    int cus = 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
+    return predict_ws_floats(*shape, pass_rows, cus, precision != IRX_PRECISION_FP32) * 4;
+}
+
 size_t irx_context_bytes(int precision) {
     // HALF contexts store FP16 K/V, as SPLIT ones; only the resident cache is FP8.
     return precision == IRX_PRECISION_FP32 ? 4
@@ -1345,7 +1379,8 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
             for (int i = 0; i < kIclBlocks; ++i) P->icl[i] = std::move(adopt->icl[i]);
             for (int i = 0; i < kIclBlocks; ++i) P->icl16[i] = std::move(adopt->icl16[i]);
         } else {
-            size_t ws = predict_ws_floats(sh, P->pass_rows, weights->device->compute_units, f16) * 4;
+            // Even one 32-row pass must fit beside the caches (fit_workspace settles the rest).
+            size_t ws = predict_ws_floats(sh, 32, weights->device->compute_units, f16) * 4;
             if (cache_bytes + ws > ctx->budget / 10 * 9) fail(IRX_DOES_NOT_FIT, "the context does not fit the device");
             if (!ctx->icl) fail(IRX_INVALID_ARGUMENT, "ICL source is missing");
             for (int i = 0; i < kColumnBlocks; ++i)
@@ -1406,7 +1441,8 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
             IRX_HIP(hipEventCreateWithFlags(&P->join[i], hipEventDisableTiming));
         }
         IRX_HIP(hipEventCreateWithFlags(&P->fork, hipEventDisableTiming));
-        ensure_workspace(P);
+        // An adopted cache is already resident: the caller's budget (free memory) excludes it.
+        fit_workspace(P, adopt ? 0 : cache_bytes, ctx->budget);
         *out = P;
         P = nullptr;
     });

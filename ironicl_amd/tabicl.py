@@ -388,12 +388,16 @@ class Executor:
         return self._attach(context, optimize)
 
     def load_context_tensors(self, context, shape, classes: int, class_permutations=None,
-                             feature_permutations=None) -> "StaticExecutor":
+                             feature_permutations=None, device_limit: int = 0) -> "StaticExecutor":
         """Upload host context tensors (column K/V [B,H+4,8,128,16] x 3 each, ICL
-        K/V [B,8,N,64] x 12 each) for prediction, without a file."""
+        K/V [B,8,N,64] x 12 each) for prediction, without a file. ``device_limit``
+        (bytes, 0 = none) caps the device memory the model may use
+        (ModelWeights::budget, cuda/weights.rs:286-292): the predictor takes one
+        stream and halves its passes until its workspace fits beside the caches."""
         b, n, h = shape
         return StaticExecutor(self, (b, n, h), classes, class_permutations, feature_permutations,
-                              built=None, context=context, base_scales=self.icl_base_scales(n))
+                              built=None, context=context, base_scales=self.icl_base_scales(n),
+                              device_limit=device_limit)
 
 
 def weights_sha256(task: str, weights: dict[str, np.ndarray]) -> str:
@@ -433,7 +437,7 @@ class StaticExecutor:
 
     def __init__(self, executor: Executor, shape, classes: int, class_permutations, feature_permutations,
                  built, context, base_scales, metadata: cf.Metadata | None = None, keep_alive=None,
-                 precision: int = hip.PRECISION_FP32):
+                 precision: int = hip.PRECISION_FP32, device_limit: int = 0):
         self.executor = executor
         self.shape = shape
         self.classes = classes
@@ -454,7 +458,7 @@ class StaticExecutor:
             ctx.base_scales[i] = hip.fptr(self._bases[i])
         ctx.rope_frequencies = hip.fptr(executor.rope_frequencies())
         ctx.cls_tokens = hip.fptr(executor.cls_tokens())
-        ctx.budget = executor.budget()
+        ctx.budget = executor.budget(device_limit)
         keep_alive = []
         if built is None:
             icl_dtype = np.float32 if precision == hip.PRECISION_FP32 else np.float16

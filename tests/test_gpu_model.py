@@ -143,6 +143,33 @@ def test_graph_replays_match_launched_passes(lcg):
         ctx.set_pass_rows(default)
 
 
+def test_predictor_fits_its_workspace_to_the_budget(clf, lcg):
+    """A device limit with room for the caches and one stream's workspace at
+    128-row passes, but not at 256, gives one stream of 128-row passes
+    (Predictor::predict halves its run rows when memory runs out,
+    predictor.rs:248-258) with the unconstrained predictor's results; without
+    room for one 32-row pass the context does not fit (the CPU path's case)."""
+    import ctypes
+
+    x, _, xt, shifts, _, ctx_gpu = lcg
+    b, n, h = x.shape
+    shape = hip.Shape(b, h, n, clf.width)
+    ws = lambda rows: hip.lib().irx_predict_workspace_bytes(ctypes.byref(shape), hip.PRECISION_FP32, rows)
+    assert 0 < ws(32) < ws(128) < ws(256) < ws(512)
+    cache = sum(t.nbytes for part in ctx_gpu.context for t in part)
+    weights = hip.lib().irx_weights_bytes(clf.handle)
+    budget = (cache + ws(128)) * 10 // 9 + 20
+    assert budget // 10 * 9 < cache + ws(256)
+    small = clf.load_context_tensors(ctx_gpu.context, (b, n, h), 3, shifts, device_limit=weights + budget)
+    assert small.pass_rows() == 128
+    full = clf.load_context_tensors(ctx_gpu.context, (b, n, h), 3, shifts)
+    assert full.pass_rows() == 512
+    assert_parity(small.predict_logits(xt).logits, full.predict_logits(xt).logits, "128-row passes")
+    with pytest.raises(hip.HipError) as e:
+        clf.load_context_tensors(ctx_gpu.context, (b, n, h), 3, shifts, device_limit=weights + cache + ws(32) // 2)
+    assert e.value.status == hip.DOES_NOT_FIT
+
+
 def test_kernel_timing_records_launches(lcg):
     *_, ctx_gpu = lcg
     hip.profile_enable(True)
