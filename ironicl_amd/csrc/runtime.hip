@@ -1435,9 +1435,22 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         P->rope_sin.alloc(sin_t.size() * 4);
         IRX_HIP(hipMemcpy(P->rope_cos.p, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(P->rope_sin.p, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice));
-        P->stream = take_stream(weights->device);
+        // The pass streams each get a hardware queue of their own: passes on
+        // two streams that share one of the runtime's pooled queues run in
+        // turn (measured: two-stream steps then as slow as one-stream ones,
+        // depending on which pooled streams a predictor happened to get). A
+        // stream created with a CU mask is given its own queue; the mask
+        // enables every CU.
+        std::vector<uint32_t> all_cus((weights->device->compute_units + 31) / 32, 0xffffffffu);
+        auto lane_stream = [&](hipStream_t *out) {
+            if (hipExtStreamCreateWithCUMask(out, (uint32_t)all_cus.size(), all_cus.data()) != hipSuccess) {
+                (void)hipGetLastError();
+                IRX_HIP(hipStreamCreateWithFlags(out, hipStreamNonBlocking));
+            }
+        };
+        lane_stream(&P->stream);
         for (int i = 0; i < kMaxPassStreams - 1; ++i) {
-            P->side[i] = take_stream(weights->device);
+            lane_stream(&P->side[i]);
             IRX_HIP(hipEventCreateWithFlags(&P->join[i], hipEventDisableTiming));
         }
         IRX_HIP(hipEventCreateWithFlags(&P->fork, hipEventDisableTiming));
@@ -1459,8 +1472,9 @@ void irx_predictor_free(irx_predictor *predictor) {
         for (int i = 0; i < kMaxPassStreams; ++i)
             if (predictor->lane(i)) (void)hipStreamSynchronize(predictor->lane(i));
         predictor->drop_graphs();
-        return_stream(w->device, predictor->stream);
-        for (int i = 0; i < kMaxPassStreams - 1; ++i) return_stream(w->device, predictor->side[i]);
+        if (predictor->stream) (void)hipStreamDestroy(predictor->stream);
+        for (int i = 0; i < kMaxPassStreams - 1; ++i)
+            if (predictor->side[i]) (void)hipStreamDestroy(predictor->side[i]);
     }
     for (int i = 0; i < kMaxPassStreams - 1; ++i)
         if (predictor->join[i]) (void)hipEventDestroy(predictor->join[i]);
