@@ -1135,7 +1135,19 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     if (d_flags) IRX_HIP(hipMemcpyAsync(d_flags + q0, pb.fin, R, hipMemcpyDeviceToDevice, s));
 }
 
+// A pass stream with a hardware queue of its own: a stream created with a CU
+// mask (here every CU) gets one, where plain streams share the runtime's pool.
+void create_lane_stream(irx_predictor *P, hipStream_t *out) {
+    std::vector<uint32_t> all_cus((P->weights->device->compute_units + 31) / 32, 0xffffffffu);
+    if (hipExtStreamCreateWithCUMask(out, (uint32_t)all_cus.size(), all_cus.data()) != hipSuccess) {
+        (void)hipGetLastError();
+        IRX_HIP(hipStreamCreateWithFlags(out, hipStreamNonBlocking));
+    }
+}
+
 void ensure_workspace(irx_predictor *P) {
+    for (int i = 1; i < P->streams; ++i)
+        if (!P->side[i - 1]) create_lane_stream(P, &P->side[i - 1]);
     bool ready = P->ws_rows == P->pass_rows;
     for (int i = 0; i < P->streams; ++i) ready = ready && P->ws[i].buf.p;
     if (ready) return;
@@ -1441,18 +1453,12 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         // depending on which pooled streams a predictor happened to get). A
         // stream created with a CU mask is given its own queue; the mask
         // enables every CU.
-        std::vector<uint32_t> all_cus((weights->device->compute_units + 31) / 32, 0xffffffffu);
-        auto lane_stream = [&](hipStream_t *out) {
-            if (hipExtStreamCreateWithCUMask(out, (uint32_t)all_cus.size(), all_cus.data()) != hipSuccess) {
-                (void)hipGetLastError();
-                IRX_HIP(hipStreamCreateWithFlags(out, hipStreamNonBlocking));
-            }
-        };
-        lane_stream(&P->stream);
-        for (int i = 0; i < kMaxPassStreams - 1; ++i) {
-            lane_stream(&P->side[i]);
+        // Side streams are created when a stream count first asks for them
+        // (ensure_workspace): every queue the process holds costs the command
+        // processor scheduling time.
+        create_lane_stream(P, &P->stream);
+        for (int i = 0; i < kMaxPassStreams - 1; ++i)
             IRX_HIP(hipEventCreateWithFlags(&P->join[i], hipEventDisableTiming));
-        }
         IRX_HIP(hipEventCreateWithFlags(&P->fork, hipEventDisableTiming));
         // An adopted cache is already resident: the caller's budget (free memory) excludes it.
         fit_workspace(P, adopt ? 0 : cache_bytes, ctx->budget);
