@@ -196,9 +196,18 @@ struct irx_device {
     // reuse: creating one costs about a millisecond.
     std::mutex stream_mu;
     std::vector<hipStream_t> idle_streams;
+    // Builds upload their ICL labels on this stream while the column stage
+    // runs; it has a hardware queue of its own (a CU-masked stream), so the
+    // copy never waits behind the build's kernels on a shared queue.
+    hipStream_t upload = nullptr;
+    // Idle streams with a hardware queue each, for predictors' passes: creating
+    // one takes milliseconds (a new queue), so they are kept for reuse.
+    std::vector<hipStream_t> idle_lanes;
     ~irx_device() {
-        if (idle_streams.empty()) return;
+        if (idle_streams.empty() && idle_lanes.empty() && !upload) return;
         (void)hipSetDevice(ordinal);
+        if (upload) (void)hipStreamDestroy(upload);
+        for (hipStream_t s : idle_lanes) (void)hipStreamDestroy(s);
         for (hipStream_t s : idle_streams) (void)hipStreamDestroy(s);
     }
 };
@@ -223,6 +232,48 @@ hipStream_t take_stream(irx_device *d) {
 }
 
 // Waits for the stream's work and keeps it for the next taker.
+// A stream with a hardware queue of its own: a stream created with a CU mask
+// (here every CU) gets one, where plain streams share the runtime's pool of
+// queues, on which work of two streams runs in turn.
+hipStream_t own_queue_stream(const irx_device *d) {
+    std::vector<uint32_t> all_cus((d->compute_units + 31) / 32, 0xffffffffu);
+    hipStream_t s = nullptr;
+    if (hipExtStreamCreateWithCUMask(&s, (uint32_t)all_cus.size(), all_cus.data()) != hipSuccess) {
+        (void)hipGetLastError();
+        s = nullptr;
+        IRX_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    }
+    return s;
+}
+
+hipStream_t upload_stream(irx_device *d) {
+    std::lock_guard<std::mutex> lock(d->stream_mu);
+    if (!d->upload) d->upload = own_queue_stream(d);
+    return d->upload;
+}
+
+hipStream_t take_lane(irx_device *d) {
+    {
+        std::lock_guard<std::mutex> lock(d->stream_mu);
+        if (!d->idle_lanes.empty()) {
+            hipStream_t s = d->idle_lanes.back();
+            d->idle_lanes.pop_back();
+            return s;
+        }
+    }
+    return own_queue_stream(d);
+}
+
+void return_lane(irx_device *d, hipStream_t s) {
+    if (!s) return;
+    (void)hipStreamSynchronize(s);
+    std::lock_guard<std::mutex> lock(d->stream_mu);
+    if (d->idle_lanes.size() < kIdleStreams)
+        d->idle_lanes.push_back(s);
+    else
+        (void)hipStreamDestroy(s);
+}
+
 void return_stream(irx_device *d, hipStream_t s) {
     if (!s) return;
     (void)hipStreamSynchronize(s);
@@ -792,16 +843,15 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     // stage runs (a pageable copy holds the host until it is done); events
     // order the copy after the previous estimator's read and before the add.
     struct SideUpload {
-        irx_device *d;
         hipStream_t s = nullptr;
         hipEvent_t ready = nullptr, free = nullptr;
         ~SideUpload() {
-            return_stream(d, s);
+            if (s) (void)hipStreamSynchronize(s);
             if (ready) (void)hipEventDestroy(ready);
             if (free) (void)hipEventDestroy(free);
         }
-    } side{W->device};
-    side.s = take_stream(W->device);
+    } side;
+    side.s = upload_stream(W->device);
     IRX_HIP(hipEventCreateWithFlags(&side.ready, hipEventDisableTiming));
     IRX_HIP(hipEventCreateWithFlags(&side.free, hipEventDisableTiming));
     Stages st{*W, s, cus};
@@ -1135,19 +1185,9 @@ void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stri
     if (d_flags) IRX_HIP(hipMemcpyAsync(d_flags + q0, pb.fin, R, hipMemcpyDeviceToDevice, s));
 }
 
-// A pass stream with a hardware queue of its own: a stream created with a CU
-// mask (here every CU) gets one, where plain streams share the runtime's pool.
-void create_lane_stream(irx_predictor *P, hipStream_t *out) {
-    std::vector<uint32_t> all_cus((P->weights->device->compute_units + 31) / 32, 0xffffffffu);
-    if (hipExtStreamCreateWithCUMask(out, (uint32_t)all_cus.size(), all_cus.data()) != hipSuccess) {
-        (void)hipGetLastError();
-        IRX_HIP(hipStreamCreateWithFlags(out, hipStreamNonBlocking));
-    }
-}
-
 void ensure_workspace(irx_predictor *P) {
     for (int i = 1; i < P->streams; ++i)
-        if (!P->side[i - 1]) create_lane_stream(P, &P->side[i - 1]);
+        if (!P->side[i - 1]) P->side[i - 1] = take_lane(P->weights->device);
     bool ready = P->ws_rows == P->pass_rows;
     for (int i = 0; i < P->streams; ++i) ready = ready && P->ws[i].buf.p;
     if (ready) return;
@@ -1447,16 +1487,14 @@ int irx_predictor_new(irx_weights *weights, int precision, const irx_context_ten
         P->rope_sin.alloc(sin_t.size() * 4);
         IRX_HIP(hipMemcpy(P->rope_cos.p, cos_t.data(), cos_t.size() * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(P->rope_sin.p, sin_t.data(), sin_t.size() * 4, hipMemcpyHostToDevice));
-        // The pass streams each get a hardware queue of their own: passes on
-        // two streams that share one of the runtime's pooled queues run in
-        // turn (measured: two-stream steps then as slow as one-stream ones,
-        // depending on which pooled streams a predictor happened to get). A
-        // stream created with a CU mask is given its own queue; the mask
-        // enables every CU.
-        // Side streams are created when a stream count first asks for them
+        // The pass streams each have a hardware queue of their own (take_lane):
+        // passes on two streams that share one of the runtime's pooled queues
+        // run in turn (measured: two-stream steps then as slow as one-stream
+        // ones, depending on which streams a predictor happened to get). Side
+        // streams are taken when a stream count first asks for them
         // (ensure_workspace): every queue the process holds costs the command
         // processor scheduling time.
-        create_lane_stream(P, &P->stream);
+        P->stream = take_lane(weights->device);
         for (int i = 0; i < kMaxPassStreams - 1; ++i)
             IRX_HIP(hipEventCreateWithFlags(&P->join[i], hipEventDisableTiming));
         IRX_HIP(hipEventCreateWithFlags(&P->fork, hipEventDisableTiming));
@@ -1478,9 +1516,8 @@ void irx_predictor_free(irx_predictor *predictor) {
         for (int i = 0; i < kMaxPassStreams; ++i)
             if (predictor->lane(i)) (void)hipStreamSynchronize(predictor->lane(i));
         predictor->drop_graphs();
-        if (predictor->stream) (void)hipStreamDestroy(predictor->stream);
-        for (int i = 0; i < kMaxPassStreams - 1; ++i)
-            if (predictor->side[i]) (void)hipStreamDestroy(predictor->side[i]);
+        return_lane(w->device, predictor->stream);
+        for (int i = 0; i < kMaxPassStreams - 1; ++i) return_lane(w->device, predictor->side[i]);
     }
     for (int i = 0; i < kMaxPassStreams - 1; ++i)
         if (predictor->join[i]) (void)hipEventDestroy(predictor->join[i]);
