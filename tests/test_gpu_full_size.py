@@ -142,3 +142,22 @@ def test_reg_20k_quantiles_mean_and_intervals(reg_20k):
     assert_parity(gm, cm, "reg-20k mean")
     assert_parity(gq, cq, "reg-20k quantiles at 0.05/0.5/0.95")
     assert (gq[:, 0] <= gq[:, 1]).all() and (gq[:, 1] <= gq[:, 2]).all()
+
+
+def test_clf_50k_context_spot_checks_and_predictions(device, clf_weights):
+    """The benchmark's 50,000-row, 64-feature context at full size: spot checks
+    of its column and ICL tensors and the oracle's cached prediction of sampled
+    test rows against it."""
+    w = S.WORKLOADS["clf-50k"]
+    x, y, xt, _ = S.workload_data(w)
+    assert x.shape == (1, 50_000, 64) and xt.shape == (1, 4096, 64)
+    st = tabicl.Executor("classifier", clf_weights, device).build_context(x, y, download=True)
+    O.set_threads(16)
+    oracle = O.OracleModel("classifier", clf_weights, O.EXACT)
+    check_context(oracle, x, y, st.context, "clf-50k", features=2, rows=8)
+    rows = sample(16, xt.shape[1], 9)
+    q = np.ascontiguousarray(xt[:, rows])
+    gpu = st.predict_logits(q).logits
+    cpu = oracle.predict_cached(st.context, q)[..., :10]
+    assert_parity(gpu, cpu, "clf-50k logits")
+    assert np.array_equal(gpu.argmax(-1), cpu.argmax(-1))
