@@ -15,52 +15,6 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-template <int W>
-__global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, long long ldx, const float *w,
-                                                         const float *b, float *y, long long ldy,
-                                                         long long rows) {
-    constexpr int PER = W / 64;
-    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const int lane = threadIdx.x & 63;
-    const float *xr = x + row * ldx + lane * PER;
-    float v[PER];
-    if constexpr (PER == 2) {
-        f32x2 t = *reinterpret_cast<const f32x2 *>(xr);
-        v[0] = t[0], v[1] = t[1];
-    } else {
-#pragma unroll
-        for (int c = 0; c < PER / 4; ++c) {
-            f32x4 t = *reinterpret_cast<const f32x4 *>(xr + 4 * c);
-            v[4 * c] = t[0], v[4 * c + 1] = t[1], v[4 * c + 2] = t[2], v[4 * c + 3] = t[3];
-        }
-    }
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) s += v[i];
-    const float mean = wave_sum(s) / (float)W;
-    float sq = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        float d = v[i] - mean;
-        sq = fmaf(d, d, sq);
-    }
-    const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)W + 1e-5f);
-    float *yr = y + row * ldy + lane * PER;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int c = lane * PER + i;
-        v[i] = (v[i] - mean) * rstd * w[c] + (b ? b[c] : 0.f);
-    }
-    if constexpr (PER == 2) {
-        *reinterpret_cast<f32x2 *>(yr) = f32x2{v[0], v[1]};
-    } else {
-#pragma unroll
-        for (int c = 0; c < PER / 4; ++c)
-            *reinterpret_cast<f32x4 *>(yr + 4 * c) = f32x4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
-    }
-}
-
 __device__ __forceinline__ float half_wave_sum(float v) {
 #pragma unroll
     for (int offset = 16; offset >= 1; offset >>= 1) v += __shfl_xor(v, offset, 64);
@@ -88,6 +42,62 @@ __global__ __launch_bounds__(256) void layer_norm128_kernel(const float *x, long
     f32x4 o = d * rstd * g;
     if (b) o += *reinterpret_cast<const f32x4 *>(b + c);
     *reinterpret_cast<f32x4 *>(y + row * ldy + c) = o;
+}
+
+// 512-wide rows (layer_norm_f32, reference.rs:223-252: two-pass mean and
+// variance, eps 1e-5): one wave takes two rows, each lane eight values of
+// each, with all four 16-byte loads issued before the two rows' reduction
+// chains run side by side; eight rows per workgroup.
+__global__ __launch_bounds__(256) void layer_norm512_kernel(const float *x, long long ldx, const float *w,
+                                                            const float *b, float *y, long long ldy, long long rows) {
+    const long long r0 = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
+    if (r0 >= rows) return;
+    const bool two = r0 + 1 < rows;
+    const int c = (threadIdx.x & 63) * 8;
+    f32x4 v[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float *xr = x + (r0 + (two ? i : 0)) * ldx + c;
+        v[i][0] = *reinterpret_cast<const f32x4 *>(xr);
+        v[i][1] = *reinterpret_cast<const f32x4 *>(xr + 4);
+    }
+    float s[2], mean[2], sq[2], rstd[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) s[i] = ((v[i][0][0] + v[i][0][1]) + (v[i][0][2] + v[i][0][3])) +
+                                       ((v[i][1][0] + v[i][1][1]) + (v[i][1][2] + v[i][1][3]));
+#pragma unroll
+    for (int offset = 32; offset >= 1; offset >>= 1)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) s[i] += __shfl_xor(s[i], offset, 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        mean[i] = s[i] / 512.0f;
+        v[i][0] -= mean[i];
+        v[i][1] -= mean[i];
+        float q = v[i][0][0] * v[i][0][0];
+        q = fmaf(v[i][0][1], v[i][0][1], q);
+        q = fmaf(v[i][0][2], v[i][0][2], q);
+        q = fmaf(v[i][0][3], v[i][0][3], q);
+        q = fmaf(v[i][1][0], v[i][1][0], q);
+        q = fmaf(v[i][1][1], v[i][1][1], q);
+        q = fmaf(v[i][1][2], v[i][1][2], q);
+        sq[i] = fmaf(v[i][1][3], v[i][1][3], q);
+    }
+#pragma unroll
+    for (int offset = 32; offset >= 1; offset >>= 1)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) sq[i] += __shfl_xor(sq[i], offset, 64);
+    const f32x4 g0 = *reinterpret_cast<const f32x4 *>(w + c), g1 = *reinterpret_cast<const f32x4 *>(w + c + 4);
+    f32x4 b0 = {0.f, 0.f, 0.f, 0.f}, b1 = b0;
+    if (b) b0 = *reinterpret_cast<const f32x4 *>(b + c), b1 = *reinterpret_cast<const f32x4 *>(b + c + 4);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (i == 1 && !two) break;
+        rstd[i] = 1.0f / sqrtf(sq[i] / 512.0f + 1e-5f);
+        float *yr = y + (r0 + i) * ldy + c;
+        *reinterpret_cast<f32x4 *>(yr) = v[i][0] * rstd[i] * g0 + b0;
+        *reinterpret_cast<f32x4 *>(yr + 4) = v[i][1] * rstd[i] * g1 + b1;
+    }
 }
 
 // Grouped features (f+1, f+2, f+4) mod H through the 3 -> 128 input affine
@@ -211,7 +221,7 @@ void layer_norm(const float *x, long long ldx, const float *weight, const float 
         hipLaunchKernelGGL(layer_norm128_kernel, dim3(ceil_div(rows, 8)), dim3(256), 0, stream, x, ldx, weight, bias,
                            y, ldy, rows);
     else if (width == 512)
-        hipLaunchKernelGGL(layer_norm_kernel<512>, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, ldx, weight,
+        hipLaunchKernelGGL(layer_norm512_kernel, dim3(ceil_div(rows, 8)), dim3(256), 0, stream, x, ldx, weight,
                            bias, y, ldy, rows);
     else
         fail(3, "layer norm width must be 128 or 512");
