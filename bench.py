@@ -81,7 +81,10 @@ def profiled_traffic() -> int | None:
 
 def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target_s: float) -> dict:
     """The oracle's cached prediction on the host cores, on a bounded sample of
-    the workload's test rows (sized for about target_s seconds of CPU work)."""
+    the workload's test rows (sized for about target_s seconds of CPU work), at
+    the reference's default thread count and native-approximation math; then,
+    on a third of that sample, all logical cores, and on a sixth, exact math as
+    the control."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
@@ -101,6 +104,23 @@ def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target
     gpu = gpu_logits[:, :rows, : logits.shape[2]]
     cpu = logits[..., : gpu.shape[2]]
     excess = np.abs(gpu - cpu) - (1e-5 + 1e-4 * np.abs(cpu))
+
+    def variant(model, workers, sample_rows):
+        # A shorter sample of the same rows: the all-logical-cores variant and
+        # the exact-math control of the reference's CPU path.
+        O.set_threads(workers)
+        t0 = time.perf_counter()
+        out = model.predict_cached(context_host, np.ascontiguousarray(x_test[:, :sample_rows]))
+        dt_v = time.perf_counter() - t0
+        O.set_threads(threads)
+        return {"value": sample_rows / dt_v, "cores": workers, "rows": sample_rows, "seconds": dt_v,
+                "max_abs_diff_vs_gpu": float(np.abs(gpu_logits[:, :sample_rows, : out.shape[2]]
+                                                    - out[..., : gpu.shape[2]]).max())}
+
+    sample = max(8, min(rows, rows // 3))
+    logical = os.cpu_count() or threads
+    all_cores = variant(m, logical, sample)
+    exact = variant(O.OracleModel("classifier", weights, O.EXACT), threads, max(8, sample // 2))
     return {
         "value": rows / dt,
         "unit": "rows/s",
@@ -113,6 +133,8 @@ def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target
         "parity_rows": rows,
         "parity_max_abs_diff": float(np.abs(gpu - cpu).max()),
         "parity_ok": bool(excess.max() <= 0 and np.array_equal(gpu.argmax(-1), cpu.argmax(-1))),
+        "all_logical_cores": all_cores,
+        "exact_math_control": exact,
     }
 
 
