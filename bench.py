@@ -138,6 +138,36 @@ def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target
     }
 
 
+def cpu_build_baseline(weights, x, y, threads: int, sample_rows: int = 2000) -> dict:
+    """The oracle's static-context build (the reference CPU path's
+    build_tensors_cpu) on the host cores, extrapolated to the workload's N: the
+    build is timed at `sample_rows` training rows; its twelve ICL self-attentions
+    (serial per estimator, as in the reference) are timed alone at that shape
+    and scaled by N^2, the rest of the build by N."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    O.set_threads(threads)
+    m = O.OracleModel("classifier", weights, O.NATIVE)
+    n_full, n = x.shape[1], min(sample_rows, x.shape[1])
+    t0 = time.perf_counter()
+    m.build_context(np.ascontiguousarray(x[:, :n]), np.ascontiguousarray(y[:, :n]))
+    build_s = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    qkv = [rng.standard_normal((8, n, 64)).astype(np.float32) * 0.3 for _ in range(3)]
+    t0 = time.perf_counter()
+    O.attention(*qkv, math=O.NATIVE)
+    att_s = 12 * (time.perf_counter() - t0)
+    linear_s = max(build_s - att_s, 0.0)
+    scale = n_full / n
+    estimate = linear_s * scale + att_s * scale * scale
+    return {"value_ms": 1000 * estimate, "kind": "port", "extrapolated": True, "cores": threads,
+            "sample": f"oracle build (native math, {threads} threads) of the first {n} training rows: "
+                      f"{build_s:.2f} s, of which the 12 serial ICL self-attentions {att_s:.2f} s (timed alone); "
+                      f"extrapolated to {n_full:,} rows as the rest x N and the attentions x N^2",
+            "sample_seconds": build_s}
+
+
 def bench_fitted(executor, x, y, xt, args) -> dict:
     """TabICL preprocessing on the GPU and a fitted model predicting from raw
     features: the workload's rows as raw features with every fifth column
@@ -788,6 +818,9 @@ def main() -> int:
         log(f"CPU baseline on {threads} threads")
         result["cpu_baseline"] = cpu_baseline(weights, context_host, xt, gpu_logits, threads, args.cpu_seconds)
         result["cpu_baseline"].update(host_facts())
+        log("CPU build baseline (extrapolated)")
+        result["cpu_baseline"]["build"] = cpu_build_baseline(weights, x, y, threads)
+        log(f"CPU build estimate {result['cpu_baseline']['build']['value_ms'] / 1000:.1f} s")
     print(json.dumps(result), flush=True)
     return 0
 
