@@ -125,14 +125,16 @@ int irx_weights_budget(const irx_weights *weights, uint64_t device_limit, size_t
 
 /* Bytes per cached ICL key or value at `precision` (context_bytes, build.rs:92-97). */
 size_t irx_context_bytes(int precision);
-/* Device bytes of one stream's prediction workspace for passes of `pass_rows`
- * rows (0 for an invalid shape). A predictor holds one per stream beside its
- * caches; irx_predictor_new fits them into the budget by taking one stream,
- * then halving the passes (Predictor::predict's out-of-memory fallback,
- * predictor.rs:248-258). No counterpart in the reference. */
-size_t irx_predict_workspace_bytes(const irx_shape *shape, int precision, size_t pass_rows);
+/* Device bytes of one stream's prediction workspace on `device` for passes of
+ * `pass_rows` rows (0 for an invalid shape; the attention's split plan, and so
+ * its partials, follow the device's compute units). A predictor holds one per
+ * stream beside its caches; irx_predictor_new fits them into the budget by
+ * taking one stream, then halving the passes (Predictor::predict's
+ * out-of-memory fallback, predictor.rs:248-258). No counterpart in the
+ * reference. */
+size_t irx_predict_workspace_bytes(irx_device *device, const irx_shape *shape, int precision, size_t pass_rows);
 /* Whether a context of `shape` builds on the device within `budget` bytes
- * (fits, build.rs:158-160). */
+ * (fits, build.rs:158-160), planned for the calling thread's current device. */
 int irx_build_fits(size_t budget, int precision, const irx_shape *shape);
 
 /* BuildInputs (build.rs:42-63). */

@@ -14,6 +14,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/ironicl_hip.h"
@@ -331,6 +332,17 @@ struct irx_built_cache {
 
 // Most HIP streams a predictor's passes rotate over (GPU_MAX_HW_QUEUES is 4).
 constexpr int kMaxPassStreams = 4;
+// Most pass graphs a predictor keeps: 4 streams x the 47 pass shapes of the
+// default 512-row passes (larger passes evict the oldest).
+constexpr size_t kMaxPassGraphs = 192;
+
+// A pass replayed from a HIP graph: one per (stream slot, rows), captured on
+// first use over the slot's workspace; dropped when a workspace moves.
+struct PassGraphEntry {
+    int slot;
+    int rows;
+    hipGraphExec_t exec;
+};
 
 struct irx_predictor {
     irx_weights *weights = nullptr;
@@ -354,14 +366,8 @@ struct irx_predictor {
     // Host-buffer predictions: device inputs, outputs and missing-row flags,
     // grown to the largest call so far.
     DevBuf io_x, io_logits, io_flags;
-    // Passes replayed from HIP graphs, one per (stream slot, rows), captured on
-    // first use over the slot's workspace; dropped when a workspace moves.
-    struct PassGraph {
-        int slot;
-        int rows;
-        hipGraphExec_t exec;
-    };
-    std::vector<PassGraph> graphs;
+    // Passes replayed from HIP graphs, oldest first.
+    std::vector<PassGraphEntry> graphs;
     bool use_graphs = true;
     void drop_graphs() {
         for (auto &g : graphs) (void)hipGraphExecDestroy(g.exec);
@@ -780,6 +786,38 @@ bool shape_ok(const irx_shape *s) {
            s->rows < (size_t)(1u << 30) && s->ensembles < 4096;
 }
 
+// Whether any of `rows` rows of x [rows, h] holds a grouped all-missing
+// triple, scanned by host threads over row ranges (the reference scans with
+// par_chunks; 8 x 200,000 rows of 500 features is 800M triples).
+bool has_missing_marker(const float *x, long long rows, int h) {
+    const long long work = rows * h;
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const int threads = (int)std::min<long long>(std::min(16u, hw), std::max(1LL, work >> 22));
+    std::atomic<bool> found{false};
+    auto scan = [&](long long r0, long long r1) {
+        for (long long r = r0; r < r1 && !found.load(std::memory_order_relaxed); ++r) {
+            const float *row = x + r * h;
+            for (int f = 0; f < h; ++f)
+                if (row[(f + 1) % h] == -100.0f && row[(f + 2) % h] == -100.0f && row[(f + 4) % h] == -100.0f) {
+                    found.store(true, std::memory_order_relaxed);
+                    break;
+                }
+        }
+    };
+    if (threads <= 1) {
+        scan(0, rows);
+        return found.load();
+    }
+    std::vector<std::thread> pool;
+    const long long per = (rows + threads - 1) / threads;
+    for (int t = 0; t < threads; ++t) {
+        const long long r0 = t * per, r1 = std::min(rows, r0 + per);
+        if (r0 < r1) pool.emplace_back(scan, r0, r1);
+    }
+    for (auto &th : pool) th.join();
+    return found.load();
+}
+
 int report(irx_progress_fn fn, void *user, int stage, size_t done, size_t total) {
     if (fn && fn(user, stage, done, total) != 0) fail(IRX_INTERRUPTED, "interrupted by the progress hook");
     return 0;
@@ -800,13 +838,10 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     for (int i = 0; i < kIclBlocks; ++i)
         if (!in->base_scales[i]) fail(IRX_INVALID_ARGUMENT, "base scales are missing");
     const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
-    // A grouped all-missing triple is the CPU path's (has_missing_marker, cpu.rs:4072-4084).
-    for (long long r = 0; r < (long long)B * N; ++r) {
-        const float *row = in->x + r * H;
-        for (int f = 0; f < H; ++f)
-            if (row[(f + 1) % H] == -100.0f && row[(f + 2) % H] == -100.0f && row[(f + 4) % H] == -100.0f)
-                fail(IRX_UNSUPPORTED, "a grouped feature triple is the all-missing marker");
-    }
+    // A grouped all-missing triple is the CPU path's (has_missing_marker,
+    // cpu.rs:4072-4084): the caller routes such a context to its CPU build.
+    if (has_missing_marker(in->x, (long long)B * N, H))
+        fail(IRX_UNSUPPORTED, "a grouped feature triple is the all-missing marker");
     set_device(W->device);
     const int cus = W->device->compute_units;
     BuildPlan plan = plan_build(sh, in->budget, cus, precision);
@@ -1137,50 +1172,75 @@ void issue_pass(irx_predictor *P, int slot, const PassBuffers &pb, const float *
 
 // One pass of R query rows starting at row q0 of x [B, Q, H] (row stride
 // x_stride between estimators) into logits [B, Q, width]; rows holding the
-// all-missing marker set d_flags[q0 + r] (device, [Q], or null). Unless kernel
-// timing is on (or graphs are off), the pass replays a HIP graph captured over
-// the slot's workspace: its rows are first copied into the workspace and its
-// logits and flags copied out after, so one graph serves every call.
+// all-missing marker set d_flags[q0 + r] (device, [Q], or null).
+//
+// A pass of more than 32 rows computes a multiple of 32 rows, Rp = R rounded
+// up: its rows are staged in the slot's workspace (xin) with zero rows after
+// them, and only the first R rows of its logits and flags are copied out.
+// Passes of up to 32 rows (the HBM-bound decode passes of serving) compute
+// exactly R rows. Every pass length thus maps onto one of 31 + pass_rows / 32
+// shapes, launched the same way whether replayed or not (the split plan of the
+// attention follows the row count, so a row's logits are the same either
+// way). Unless kernel timing is on (or graphs are off), the pass replays a HIP
+// graph captured over the slot's workspace for (slot, Rp). A pass with
+// Rp == R that launches its kernels one by one reads x in place.
 void predict_pass(irx_predictor *P, int slot, const float *d_x, long long x_stride, int q0, int R, float *d_logits,
                   int Q, uint8_t *d_flags) {
     const irx_shape &sh = P->shape;
     const int B = (int)sh.ensembles, H = (int)sh.features, width = (int)sh.outputs;
+    const int Rp = R <= 32 ? R : (R + 31) / 32 * 32;
     hipStream_t s = P->lane(slot);
     Arena &ws = P->ws[slot];
     ws.used = 0;
     const PassBuffers pb = pass_layout(ws, sh, P->ws_rows, P->weights->device->compute_units,
                                        P->precision != IRX_PRECISION_FP32);
-    if (!P->use_graphs || g_profiling.load(std::memory_order_relaxed)) {
+    const bool replay = P->use_graphs && !g_profiling.load(std::memory_order_relaxed);
+    if (!replay && Rp == R) {
         issue_pass(P, slot, pb, d_x + (size_t)q0 * H, x_stride, R, d_logits + (size_t)q0 * width, Q,
                    d_flags ? d_flags + q0 : nullptr);
         return;
     }
-    IRX_HIP(hipMemcpy2DAsync(pb.xin, (size_t)R * H * 4, d_x + (size_t)q0 * H, (size_t)x_stride * 4, (size_t)R * H * 4,
+    IRX_HIP(hipMemcpy2DAsync(pb.xin, (size_t)Rp * H * 4, d_x + (size_t)q0 * H, (size_t)x_stride * 4, (size_t)R * H * 4,
                              B, hipMemcpyDeviceToDevice, s));
-    hipGraphExec_t exec = nullptr;
-    for (const auto &g : P->graphs)
-        if (g.slot == slot && g.rows == R) exec = g.exec;
-    if (!exec) {
-        if (P->graphs.size() >= 16) P->drop_graphs();
-        hipGraph_t graph = nullptr;
-        IRX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-        try {
-            // Flags start from zero on every replay: a fill kernel, not a memset node.
-            fill_zero(reinterpret_cast<float *>(pb.fin), (R + 3) / 4, s);
-            issue_pass(P, slot, pb, pb.xin, (long long)R * H, R, pb.lout, R, pb.fin);
-        } catch (...) {
-            (void)hipStreamEndCapture(s, &graph);
-            if (graph) (void)hipGraphDestroy(graph);
-            throw;
+    if (Rp != R)
+        IRX_HIP(hipMemset2DAsync(pb.xin + (size_t)R * H, (size_t)Rp * H * 4, 0, (size_t)(Rp - R) * H * 4, B, s));
+    if (!replay) {
+        fill_zero(reinterpret_cast<float *>(pb.fin), (Rp + 3) / 4, s);
+        issue_pass(P, slot, pb, pb.xin, (long long)Rp * H, Rp, pb.lout, Rp, pb.fin);
+    } else {
+        hipGraphExec_t exec = nullptr;
+        for (const auto &g : P->graphs)
+            if (g.slot == slot && g.rows == Rp) exec = g.exec;
+        if (!exec) {
+            // At most streams x pass_rows / 32 shapes exist; past the cap the
+            // oldest graph goes, once the lane it was launched on is idle
+            // (earlier passes of this call may still be running it).
+            if (P->graphs.size() >= kMaxPassGraphs) {
+                const PassGraphEntry victim = P->graphs.front();
+                IRX_HIP(hipStreamSynchronize(P->lane(victim.slot)));
+                (void)hipGraphExecDestroy(victim.exec);
+                P->graphs.erase(P->graphs.begin());
+            }
+            hipGraph_t graph = nullptr;
+            IRX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            try {
+                // Flags start from zero on every replay: a fill kernel, not a memset node.
+                fill_zero(reinterpret_cast<float *>(pb.fin), (Rp + 3) / 4, s);
+                issue_pass(P, slot, pb, pb.xin, (long long)Rp * H, Rp, pb.lout, Rp, pb.fin);
+            } catch (...) {
+                (void)hipStreamEndCapture(s, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            IRX_HIP(hipStreamEndCapture(s, &graph));
+            const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            IRX_HIP(e);
+            P->graphs.push_back({slot, Rp, exec});
         }
-        IRX_HIP(hipStreamEndCapture(s, &graph));
-        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(graph);
-        IRX_HIP(e);
-        P->graphs.push_back({slot, R, exec});
+        IRX_HIP(hipGraphLaunch(exec, s));
     }
-    IRX_HIP(hipGraphLaunch(exec, s));
-    IRX_HIP(hipMemcpy2DAsync(d_logits + (size_t)q0 * width, (size_t)Q * width * 4, pb.lout, (size_t)R * width * 4,
+    IRX_HIP(hipMemcpy2DAsync(d_logits + (size_t)q0 * width, (size_t)Q * width * 4, pb.lout, (size_t)Rp * width * 4,
                              (size_t)R * width * 4, B, hipMemcpyDeviceToDevice, s));
     if (d_flags) IRX_HIP(hipMemcpyAsync(d_flags + q0, pb.fin, R, hipMemcpyDeviceToDevice, s));
 }
@@ -1353,11 +1413,12 @@ int irx_weights_budget(const irx_weights *weights, uint64_t device_limit, size_t
     });
 }
 
-size_t irx_predict_workspace_bytes(const irx_shape *shape, int precision, size_t pass_rows) {
-    if (!shape_ok(shape) || !irx_context_bytes(precision) || pass_rows < 1 || pass_rows > (1u << 20)) return 0;
-    int cus = 256;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
-    return predict_ws_floats(*shape, pass_rows, cus, precision != IRX_PRECISION_FP32) * 4;
+size_t irx_predict_workspace_bytes(irx_device *device, const irx_shape *shape, int precision, size_t pass_rows) {
+    if (!device || !shape_ok(shape) || !irx_context_bytes(precision) || pass_rows < 1 || pass_rows > (1u << 20))
+        return 0;
+    // The split plan of the ICL attention, and with it the partials, follows
+    // the device's compute units.
+    return predict_ws_floats(*shape, pass_rows, device->compute_units, precision != IRX_PRECISION_FP32) * 4;
 }
 
 size_t irx_context_bytes(int precision) {
@@ -1370,7 +1431,15 @@ size_t irx_context_bytes(int precision) {
 int irx_build_fits(size_t budget, int precision, const irx_shape *shape) {
     if (!irx_context_bytes(precision) || !shape_ok(shape) || shape->rows < 64)
         return 0;
-    BuildPlan p = plan_build(*shape, budget, 256, precision);
+    // fits (build.rs:158-160) takes no device: the caller's current one, as
+    // the reference's single CUDA device, sets the split plan.
+    int ordinal = 0, cus = 256;
+    if (hipGetDevice(&ordinal) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ordinal) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();
+        cus = 256;
+    }
+    BuildPlan p = plan_build(*shape, budget, cus, precision);
     return p.ws_bytes + p.keep_bytes <= budget / 10 * 9;
 }
 

@@ -7,6 +7,8 @@ counterpart here."""
 
 from __future__ import annotations
 
+from numbers import Integral, Real
+
 import numpy as np
 
 from . import preprocess as pp
@@ -15,14 +17,22 @@ from .tabicl import Executor
 
 
 def _options(n_estimators, norm_methods, outlier_threshold, random_state) -> pp.PreprocessOptions:
+    """The drop-ins' option checks (python/ironicl/base.py:252-258): an
+    unseeded ensemble is refused rather than silently seeded, and the numbers
+    must have the types the Rust side converts."""
+    if random_state is None:
+        raise NotImplementedError("random_state=None is not supported")
+    for name, value, kind in (("n_estimators", n_estimators, Integral), ("random_state", random_state, Integral),
+                              ("outlier_threshold", outlier_threshold, Real)):
+        if isinstance(value, bool) or not isinstance(value, kind):
+            raise ValueError(f"{name} must be a{'n integer' if kind is Integral else ' number'}, not {value!r}")
     if norm_methods is None:
         methods = (pp.NONE, pp.POWER)
     elif isinstance(norm_methods, str):
         methods = (norm_methods,)
     else:
         methods = tuple(norm_methods)
-    return pp.PreprocessOptions(n_estimators, 42 if random_state is None else int(random_state), methods,
-                                float(outlier_threshold))
+    return pp.PreprocessOptions(int(n_estimators), int(random_state), methods, float(outlier_threshold))
 
 
 class TabICLClassifier:

@@ -73,7 +73,7 @@ SIGNATURES = {
     "irx_weights_bytes": (_sz, [ctypes.c_void_p]),
     "irx_weights_budget": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.POINTER(_sz)]),
     "irx_context_bytes": (_sz, [ctypes.c_int]),
-    "irx_predict_workspace_bytes": (_sz, [ctypes.c_void_p, ctypes.c_int, _sz]),
+    "irx_predict_workspace_bytes": (_sz, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, _sz]),
     "irx_build_fits": (ctypes.c_int, [_sz, ctypes.c_int, ctypes.POINTER(Shape)]),
     "irx_build": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(BuildInputs),
                                  ctypes.POINTER(BuildOutputs), ctypes.POINTER(ctypes.c_void_p)]),

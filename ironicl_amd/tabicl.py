@@ -125,6 +125,18 @@ class Executor:
         hip.check(hip.lib().irx_weights_upload(self.device.handle, t, lookup, None, ctypes.byref(handle)))
         self.handle = handle.value
 
+    @classmethod
+    def from_model_file(cls, path, device: hip.Device | None = None) -> "Executor":
+        """Weights from an IRMODEL artifact (ModelArtifact::load, src/format/model.rs:225-250;
+        an official profile only), uploaded through irx_weights_upload; the
+        artifact's source SHA-256 becomes the model identity contexts carry."""
+        from . import model_file
+
+        artifact = model_file.load(path)
+        executor = cls(artifact.task, artifact.tensors, device, source_sha256=artifact.source_sha256)
+        executor.artifact = artifact.summary
+        return executor
+
     def __del__(self):
         h = getattr(self, "handle", None)
         if h:
@@ -171,11 +183,26 @@ class Executor:
         return col, icl
 
     def qass_base_scale(self, prefix: str, source: int) -> np.ndarray:
-        """base = W2 gelu(w1 ln(max(source,1)) + b1) + b2 (qass_base_scale, cpu.rs:3768-3791)."""
+        """base = W2 gelu(w1 ln(max(source,1)) + b1) + b2 in the reference's FP32
+        arithmetic (qass_base_scale, cpu.rs:3768-3791): ln of the count rounded
+        to f32, w1 * ln + b1 as one fused multiply-add, the GELU in f32, and
+        the affine as a bias-initialized chain of fused multiply-adds
+        (affine_f32, reference.rs:83-120). A large w1 makes the scale
+        sensitive to the count, so its rounding is the reference's, not a
+        float64 one's."""
         n = lambda part: self.tensor(f"{prefix}.ssmax_layer.{part}")
-        log_source = math.log(max(source, 1))
-        hidden = _gelu64(n("base_mlp.0.weight")[:, 0].astype(np.float64) * log_source + n("base_mlp.0.bias"))
-        return _f32(n("base_mlp.2.weight").astype(np.float64) @ hidden + n("base_mlp.2.bias"))
+        log_source = np.float32(math.log(max(source, 1)))
+        w1 = n("base_mlp.0.weight")[:, 0].astype(np.float64)
+        # A product of two f32 values is exact in f64, so one rounding to f32
+        # after the add is the fused multiply-add (up to a rare double rounding).
+        value = (w1 * np.float64(log_source) + n("base_mlp.0.bias").astype(np.float64)).astype(np.float32)
+        hidden = (np.float32(0.5) * value *
+                  (np.float32(1.0) + _erf(value / np.float32(math.sqrt(2.0))).astype(np.float32))).astype(np.float32)
+        w2 = n("base_mlp.2.weight").astype(np.float64)
+        acc = n("base_mlp.2.bias").astype(np.float32)
+        for k in range(hidden.shape[0]):
+            acc = (acc.astype(np.float64) + np.float64(hidden[k]) * w2[:, k]).astype(np.float32)
+        return _f32(acc)
 
     def icl_base_scales(self, n: int) -> list[np.ndarray]:
         return [self.qass_base_scale(f"icl_predictor.tf_icl.blocks.{b}.attn", n) for b in range(12)]
@@ -617,8 +644,13 @@ class StaticExecutor:
         """Aggregated class probabilities [Q, C] (cpu.rs:2338-2348, 3873-3932)."""
         if not self.classes:
             raise ValueError("the context is a regression fit")
-        return aggregate_classifier_probabilities(self.predict_logits(x).logits, self.class_permutations,
-                                                  temperature, average_logits)
+        p = self.predict_logits(x)
+        if p.cpu_rows:
+            # The reference re-runs these rows on its CPU path (cpu.rs:2072-2106);
+            # this backend has none, so it refuses rather than return NaN.
+            raise ValueError(f"rows {p.cpu_rows[:8]} hold the all-missing marker, which this backend does not "
+                             "predict; use predict_logits and the CPU path for them")
+        return aggregate_classifier_probabilities(p.logits, self.class_permutations, temperature, average_logits)
 
     def predict_regression(self, x: np.ndarray, alphas=(0.05, 0.5, 0.95)):
         """(mean [Q], quantiles [Q, len(alphas)]) in standardized target units

@@ -16,11 +16,13 @@ Predictions: every test row on the GPU, the oracle's cached prediction of
 sampled rows against the GPU-built context, the HBM-bound small-pass kernels
 against the 512-row pass, and (classifier) invariance under a permutation of
 the training rows. The bar is the north star's: |gpu - cpu| <= 1e-5 +
-1e-4 |cpu| with identical argmax."""
+1e-4 |cpu| with identical argmax. The benchmark's 50,000-row workload and
+the 8 x 200,000 x 500 ensemble run the same checks (tests/full_size.py)."""
 
 import numpy as np
 import pytest
 
+import full_size
 import oracle as O
 from ironicl_amd import hip
 from ironicl_amd import synthetic as S
@@ -145,19 +147,54 @@ def test_reg_20k_quantiles_mean_and_intervals(reg_20k):
 
 
 def test_clf_50k_context_spot_checks_and_predictions(device, clf_weights):
-    """The benchmark's 50,000-row, 64-feature context at full size: spot checks
-    of its column and ICL tensors and the oracle's cached prediction of sampled
-    test rows against it."""
+    """The benchmark's workload at full size: 50,000 training rows x 64
+    features, all 4,096 test rows predicted as the benchmark does (eight passes
+    of 512 rows over two streams, the 512-query attention kernel), then the
+    oracle's spot checks of the context (2 features, 8 training rows) and its
+    cached prediction of 32 sampled test rows against the GPU-built context."""
     w = S.WORKLOADS["clf-50k"]
     x, y, xt, _ = S.workload_data(w)
     assert x.shape == (1, 50_000, 64) and xt.shape == (1, 4096, 64)
-    st = tabicl.Executor("classifier", clf_weights, device).build_context(x, y, download=True)
-    O.set_threads(16)
-    oracle = O.OracleModel("classifier", clf_weights, O.EXACT)
-    check_context(oracle, x, y, st.context, "clf-50k", features=2, rows=8)
-    rows = sample(16, xt.shape[1], 9)
-    q = np.ascontiguousarray(xt[:, rows])
-    gpu = st.predict_logits(q).logits
-    cpu = oracle.predict_cached(st.context, q)[..., :10]
-    assert_parity(gpu, cpu, "clf-50k logits")
-    assert np.array_equal(gpu.argmax(-1), cpu.argmax(-1))
+    st = tabicl.Executor("classifier", clf_weights, device).build_context(x, y)
+    assert st.pass_rows() == 512
+    gpu = st.predict_logits(xt).logits
+    assert gpu.shape == (1, 4096, 10) and np.isfinite(gpu).all()
+    report = full_size.spot_checks("classifier", clf_weights, 10, st, x, y, xt, gpu, features=2, train_rows=8,
+                                   test_rows=32, float64_rows=2)
+    assert report["column_kv"]["strict_ok"] and report["icl_kv"]["strict_ok"], report
+    assert report["logits"]["strict_ok"] and report["logits"]["argmax_identical"], report
+
+
+@pytest.mark.timeout(1200)
+def test_clf_200k_ensemble_full_size(device, clf_weights):
+    """8 estimators x 200,000 training rows x 500 features, 16,384 test rows
+    (80 GB of contexts resident in HBM): the full build, every test row
+    predicted in passes of 512 over two streams, then on estimators 0 and 7
+    the oracle's spot checks (2 features, 8 training rows) and its cached
+    prediction of 32 sampled test rows each.
+
+    The logits take the strict bar with identical argmax. The K/V spot checks
+    may miss it (by up to about 6e-5 absolute, measured): the oracle
+    accumulates each attention over 200,000 keys in one sequential FP32 order.
+    Then the float64 restatement (tests/reference_np.py) arbitrates on the
+    first sampled feature and two rows: the GPU's error against float64 must
+    not exceed the oracle's (measured: column K/V 1.9e-6 for the GPU against
+    2.9e-5 for the oracle, ICL K/V 2.8e-5 against 3.4e-5)."""
+    w = S.WORKLOADS["clf-200k"]
+    print("clf-200k: generating data", flush=True)
+    x, y, xt, meta = S.workload_data(w)
+    assert x.shape == (8, 200_000, 500) and xt.shape == (8, 16_384, 500)
+    ex = tabicl.Executor("classifier", clf_weights, device)
+
+    def progress(stage, done, total):
+        print(f"clf-200k build: estimator {done} of {total}", flush=True)
+
+    st = ex.build_context(x, y, class_permutations=meta["class_permutations"], progress=progress)
+    print("clf-200k: predicting 16,384 rows", flush=True)
+    gpu = st.predict_logits(xt).logits
+    assert gpu.shape == (8, 16_384, 10) and np.isfinite(gpu).all()
+    report = full_size.spot_checks("classifier", clf_weights, 10, st, x, y, xt, gpu, features=2, train_rows=8,
+                                   test_rows=32, float64_rows=2,
+                                   log=lambda m: print(f"clf-200k {m}", flush=True))
+    assert report["logits"]["strict_ok"] and report["logits"]["argmax_identical"], report
+    assert report["column_kv"]["ok"] and report["icl_kv"]["ok"], report

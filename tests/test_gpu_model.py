@@ -143,7 +143,29 @@ def test_graph_replays_match_launched_passes(lcg):
         ctx.set_pass_rows(default)
 
 
-def test_predictor_fits_its_workspace_to_the_budget(clf, lcg):
+def test_many_ragged_lengths_replay_safely(clf, lcg):
+    """Serving calls of many lengths on two streams: a pass of more than 32
+    rows computes a multiple of 32 rows, so the predictor keeps one graph per
+    (stream, shape): 32 shapes up to 32 rows, then one per 32 rows. With
+    3,072-row passes that is 2 x 127 shapes, past the 192 it keeps, so graphs
+    are evicted while earlier passes of the same call may still run them.
+    Every call matches kernel-by-kernel launches bitwise."""
+    x, _, _, shifts, ctx_cpu, _ = lcg
+    st = clf.load_context_tensors(ctx_cpu, x.shape, 3, shifts)
+    rng = np.random.default_rng(5)
+    xt = rng.uniform(-2, 2, size=(2, 2 * 3072, 5)).astype(np.float32)
+    tails = list(range(1, 33)) + [32 * t - 5 for t in range(2, 97)]
+    lengths = tails + [3072 + t for t in tails]
+    st.set_pass_rows(3072)
+    st.set_graphs(False)
+    eager = {q: st.predict_raw(np.ascontiguousarray(xt[:, :q])).logits for q in lengths}
+    st.set_graphs(True)
+    for q in lengths + lengths[::-1]:
+        np.testing.assert_array_equal(st.predict_raw(np.ascontiguousarray(xt[:, :q])).logits, eager[q],
+                                      err_msg=f"{q} rows")
+
+
+def test_predictor_fits_its_workspace_to_the_budget(clf, lcg, device):
     """A device limit with room for the caches and one stream's workspace at
     128-row passes, but not at 256, gives one stream of 128-row passes
     (Predictor::predict halves its run rows when memory runs out,
@@ -154,7 +176,8 @@ def test_predictor_fits_its_workspace_to_the_budget(clf, lcg):
     x, _, xt, shifts, _, ctx_gpu = lcg
     b, n, h = x.shape
     shape = hip.Shape(b, h, n, clf.width)
-    ws = lambda rows: hip.lib().irx_predict_workspace_bytes(ctypes.byref(shape), hip.PRECISION_FP32, rows)
+    ws = lambda rows: hip.lib().irx_predict_workspace_bytes(device.handle, ctypes.byref(shape), hip.PRECISION_FP32,
+                                                             rows)
     assert 0 < ws(32) < ws(128) < ws(256) < ws(512)
     cache = sum(t.nbytes for part in ctx_gpu.context for t in part)
     weights = hip.lib().irx_weights_bytes(clf.handle)
@@ -181,7 +204,8 @@ def test_kernel_timing_records_launches(lcg):
         hip.profile_enable(False)
     assert icl["launches"] == 12 and icl["milliseconds"] > 0
     assert 0 < icl["busy_milliseconds"] <= icl["milliseconds"] * (1 + 1e-6)
-    assert icl["flops"] == pytest.approx(12 * 4.0 * 16 * 250 * 240 * 64)
+    # 250 rows run as one pass of 256 (passes over 32 rows compute multiples of 32).
+    assert icl["flops"] == pytest.approx(12 * 4.0 * 16 * 256 * 240 * 64)
     assert gemm["launches"] > 50 and gemm["flops"] > 0
     with pytest.raises(hip.HipError):
         hip.profile_read("nonsense")
@@ -194,6 +218,9 @@ def test_missing_marker_rows_are_flagged(lcg):
     p = ctx_gpu.predict_raw(xt)
     assert p.cpu_rows == [7]
     assert np.all(np.isnan(p.logits[:, 7])) and np.all(np.isfinite(np.delete(p.logits, 7, axis=1)))
+    # Probabilities of such a row would be NaN: refused, not returned.
+    with pytest.raises(ValueError, match="all-missing marker"):
+        ctx_gpu.predict_probabilities(xt)
     # Over several passes on two streams, in both estimators, and again after
     # a call without marked rows (the flags start from zero on every call).
     xt = lcg[2][:, :200].copy()
