@@ -524,6 +524,36 @@ def bench_workload(name: str, args) -> dict:
     }
 
 
+def profile_leg(args) -> dict:
+    """The kernels of the headline's prediction alone, for a profiler's
+    per-kernel statistics: one build, then single-stream prediction steps (or
+    small passes) with inputs in HBM, every pass launched kernel by kernel."""
+    from ironicl_amd import hip, hipmem, synthetic, tabicl
+
+    w = synthetic.WORKLOADS[WORKLOAD]
+    x, y, xt, _ = synthetic.workload_data(w)
+    q = xt.shape[1]
+    executor = tabicl.Executor("classifier", synthetic.random_weights("classifier"), hip.Device(0))
+    ctx = executor.build_context(x, y)
+    ctx.set_pass_rows(args.pass_rows)
+    ctx.set_streams(1)
+    ctx.set_graphs(False)
+    dx = hipmem.DeviceArray.from_host(xt)
+    dl = hipmem.DeviceArray((1, q, executor.width))
+    sizes = [q] if args.profile_leg == "predict" else list(SMALL_PASSES)
+    if args.profile_leg == "small":
+        ctx.set_pass_rows(max(SMALL_PASSES))
+    out = {}
+    for rows in sizes:
+        def call():
+            hip.check(hip.lib().irx_predictor_predict_device(ctx.handle, dx.ptr, rows, dl.ptr, None))
+
+        samples = timed_calls(call, args.warmup, args.steps)
+        out[str(rows)] = latency_stats(samples)
+        log(f"profile leg: {rows} rows, p50 {out[str(rows)]['p50_ms']:.3f} ms")
+    return {"profile_leg": args.profile_leg, "steps": args.steps, "by_rows": out}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -540,6 +570,10 @@ def main() -> int:
     ap.add_argument("--workload", default=WORKLOAD,
                     help="clf-50k (default, the full report) or another configuration at full size: clf-1k, "
                          "clf-10k, reg-20k, clf-200k (build, rows/s, build kernels, oracle parity on samples)")
+    ap.add_argument("--profile-leg", choices=["predict", "small"], default=None,
+                    help="only the leg a profiler reads: one build, then --steps single-stream prediction steps "
+                         "of the 4,096 rows (predict) or passes of 1, 8, 16 and 32 rows (small), kernels launched "
+                         "one by one")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel over BYTES (reference for traffic counters)")
     args = ap.parse_args()
@@ -557,6 +591,9 @@ def main() -> int:
         return 0
     if args.workload != WORKLOAD:
         print(json.dumps(bench_workload(args.workload, args)), flush=True)
+        return 0
+    if args.profile_leg:
+        print(json.dumps(profile_leg(args)), flush=True)
         return 0
     w = synthetic.WORKLOADS[WORKLOAD]
     log("generating weights and data")

@@ -53,11 +53,20 @@ static void *xcalloc(size_t count, size_t size) {
 /* Elementwise math                                                    */
 /* ------------------------------------------------------------------ */
 
+/* Rust never contracts a * b + c into a fused multiply-add, so this file is
+ * built with -ffp-contract=off and every fused operation of the reference
+ * (mul_add, _mm512_fmadd_ps / _mm512_fnmadd_ps) is an explicit fmaf. Rust's
+ * f32::round() rounds halves away from zero (roundf); the AVX-512 kernels'
+ * _mm512_cvt_roundps_epi32 with _MM_FROUND_TO_NEAREST_INT rounds them to
+ * even (rintf under the default rounding mode). */
+#define ORA_LOG2E 1.44269504088896340736f
+#define ORA_LN2 0.693147180559945309417f
+
 /* bounded_exp: src/kernels/cpu/ops/pointwise.rs:49-74. */
 float ora_bounded_exp(float value) {
     float v = value < -40.0f ? -40.0f : (value > 20.0f ? 20.0f : value);
-    int exponent = (int)rintf(v * 1.44269504088896340736f);
-    float r = fmaf((float)(-exponent), 0.693147180559945309417f, v);
+    int exponent = (int)roundf(v * ORA_LOG2E);
+    float r = fmaf((float)(-exponent), ORA_LN2, v);
     float p = fmaf(r, 1.0f / 5040.0f, 1.0f / 720.0f);
     p = fmaf(r, p, 1.0f / 120.0f);
     p = fmaf(r, p, 1.0f / 24.0f);
@@ -70,17 +79,35 @@ float ora_bounded_exp(float value) {
     return p * pw.f;
 }
 
-/* fast_exp_negative / softmax_exp_sum_avx512: src/kernels/cpu/arch/x86_64.rs:40-51,610-660. */
-float ora_fast_exp_negative(float value) {
-    float v = value < -87.0f ? -87.0f : value;
-    int exponent = (int)rintf(v * 1.44269504088896340736f);
-    float r = v - (float)exponent * 0.693147180559945309417f;
+static inline float exp_polynomial(float r) {
     float p = 1.0f / 5040.0f;
     const float c[7] = {1.0f / 720.0f, 1.0f / 120.0f, 1.0f / 24.0f, 1.0f / 6.0f, 0.5f, 1.0f, 1.0f};
     for (int i = 0; i < 7; ++i) p = fmaf(p, r, c[i]);
+    return p;
+}
+
+static inline float pow2i(int exponent) {
     union { unsigned u; float f; } pw;
     pw.u = (unsigned)(exponent + 127) << 23;
-    return p * pw.f;
+    return pw.f;
+}
+
+/* fast_exp_negative, the scalar form: src/kernels/cpu/arch/x86_64.rs:40-51
+ * (half away from zero; exponent * LN_2 rounded before the subtraction). */
+float ora_fast_exp_negative(float value) {
+    float v = value < -87.0f ? -87.0f : value;
+    int exponent = (int)roundf(v * ORA_LOG2E);
+    float r = v - (float)exponent * ORA_LN2;
+    return exp_polynomial(r) * pow2i(exponent);
+}
+
+/* One lane of the AVX-512 exp in softmax_exp_sum_avx512 and gelu_avx512
+ * (x86_64.rs:610-660, 1394-1441): ties to even, the remainder one fnmadd. */
+static inline float vector_exp_negative(float value) {
+    float v = value < -87.0f ? -87.0f : value;
+    int exponent = (int)rintf(v * ORA_LOG2E);
+    float r = fmaf(-(float)exponent, ORA_LN2, v);
+    return exp_polynomial(r) * pow2i(exponent);
 }
 
 /* fast_erf: pointwise.rs:76-91 (Abramowitz-Stegun 7.1.26). */
@@ -101,15 +128,59 @@ static float fast_erf(float value) {
 static inline float gelu_exact(float x) { return 0.5f * x * (1.0f + erff(x / 1.41421356237309504880f)); }
 static inline float gelu_native(float x) { return 0.5f * x * (1.0f + fast_erf(x / 1.41421356237309504880f)); }
 
-void ora_gelu(int math, const float *input, size_t len, float *output) {
-    if (math == ORA_MATH_NATIVE)
-        for (size_t i = 0; i < len; ++i) output[i] = gelu_native(input[i]);
-    else
-        for (size_t i = 0; i < len; ++i) output[i] = gelu_exact(input[i]);
+/* One lane of gelu_avx512 (x86_64.rs:1394-1441): its own erf, with the
+ * vector exp clamped at -87 rather than bounded_exp. */
+static inline float gelu_vector(float x) {
+    float scaled = x * 0.707106781186547524401f;
+    float mag = fmaxf(scaled, 0.0f - scaled);
+    float t = 1.0f / fmaf(0.3275911f, mag, 1.0f);
+    float p = 1.0614054f;
+    const float c[4] = {-1.4531521f, 1.4214138f, -0.28449672f, 0.2548296f};
+    for (int i = 0; i < 4; ++i) p = fmaf(p, t, c[i]);
+    p = p * t;
+    float e = vector_exp_negative(0.0f - mag * mag);
+    float erf = fmaf(-p, e, 1.0f);
+    if (scaled < 0.0f) erf = 0.0f - erf;
+    if (mag < 1e-4f) erf = scaled * 1.12837916709551257390f;
+    if (mag >= 6.0f) erf = scaled < 0.0f ? -1.0f : 1.0f;
+    return 0.5f * x * (1.0f + erf);
 }
 
-static inline float softmax_exp(int math, float x) {
-    return math == ORA_MATH_NATIVE ? ora_fast_exp_negative(x) : expf(x);
+/* gelu_f32 (reference.rs:256-266): native math is gelu_avx512 over whole
+ * groups of 16 and fast_gelu on the rest (x86_64.rs:1347-1441). */
+void ora_gelu(int math, const float *input, size_t len, float *output) {
+    if (math == ORA_MATH_NATIVE) {
+        size_t body = len / 16 * 16;
+        for (size_t i = 0; i < body; ++i) output[i] = gelu_vector(input[i]);
+        for (size_t i = body; i < len; ++i) output[i] = gelu_native(input[i]);
+    } else {
+        for (size_t i = 0; i < len; ++i) output[i] = gelu_exact(input[i]);
+    }
+}
+
+/* The softmax numerators of one score row against its maximum, in place,
+ * added into *denominator. Native: softmax_exp_sum_avx512
+ * (x86_64.rs:610-660): 16 lane sums over whole groups of 16, reduced
+ * pairwise, then the scalar fast_exp_negative of the rest added in order, the
+ * total added once. Exact (the exact-math feature): libm expf, each numerator
+ * added to the denominator in order (reference.rs:963-969). */
+static void softmax_numerators(int math, float *scores, size_t n, float maximum, float *denominator) {
+    if (math != ORA_MATH_NATIVE) {
+        for (size_t i = 0; i < n; ++i) *denominator += (scores[i] = expf(scores[i] - maximum));
+        return;
+    }
+    float lanes[16] = {0};
+    size_t body = n / 16 * 16;
+    for (size_t i = 0; i < body; i += 16)
+        for (int l = 0; l < 16; ++l) {
+            float x = scores[i + l] - maximum;
+            lanes[l] += (scores[i + l] = vector_exp_negative(x));
+        }
+    for (int w = 8; w >= 1; w >>= 1)
+        for (int l = 0; l < w; ++l) lanes[l] += lanes[l + w];
+    float total = lanes[0];
+    for (size_t i = body; i < n; ++i) total += (scores[i] = ora_fast_exp_negative(scores[i] - maximum));
+    *denominator += total;
 }
 
 /* ------------------------------------------------------------------ */
@@ -233,66 +304,99 @@ static void heads_to_tokens(const float *in, size_t rows, size_t dim, float *out
 /* Attention                                                           */
 /* ------------------------------------------------------------------ */
 
-/* Source-major online attention for `heads` heads: reference.rs:792-1024.
- * Per key tile of 128, every query row updates its running maximum and
- * denominator, rescaling its partial output by exp(old - new). */
+/* Source-major online attention for `heads` heads, as the reference's x86-64
+ * path runs it (source_major_online_attention_with_backend_f32,
+ * reference.rs:792-1024, with the AVX-512 tiles of x86_64.rs): key tiles of
+ * 128 outermost; per head, the tile's keys packed dimension-major and padded
+ * to 16 sources; per block of 16 query rows, the score tile with one lane per
+ * source (each score a sequential fused chain over the dimensions, times the
+ * scale: attention_score_packed_key_padded_tile_avx512, x86_64.rs:866-915);
+ * per row the running maximum, the rescale by exp(old - new) and the
+ * numerators' sum; then the value tile, one fused multiply-add per source in
+ * order (attention_value_tile_fma). */
+#define QUERY_BLOCK 16 /* ATTENTION_QUERY_BLOCK_ROWS, cpu.rs:48 */
 static int attention_heads(int math, const float *query, size_t query_rows, const float *key,
                            const float *value, size_t source_rows, size_t heads, size_t head_dim,
                            float *output) {
-    float scale = 1.0f / sqrtf((float)head_dim);
-    float *scores = xcalloc(KEY_TILE, sizeof(float));
-    float *maximum = xcalloc(query_rows, sizeof(float));
-    float *denominator = xcalloc(query_rows, sizeof(float));
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    const size_t packed_tile = (KEY_TILE + 15) / 16 * 16;
+    float *packed = xcalloc(packed_tile * head_dim, sizeof(float));
+    float *scores = xcalloc(QUERY_BLOCK * KEY_TILE, sizeof(float));
+    float *qd = xcalloc(QUERY_BLOCK * head_dim, sizeof(float));
+    float *maximum = xcalloc(heads * query_rows, sizeof(float));
+    float *denominator = xcalloc(heads * query_rows, sizeof(float));
     int status = 0;
-    for (size_t h = 0; h < heads && !status; ++h) {
-        const float *qh = query + h * query_rows * head_dim;
-        const float *kh = key + h * source_rows * head_dim;
-        const float *vh = value + h * source_rows * head_dim;
-        float *oh = output + h * query_rows * head_dim;
-        for (size_t r = 0; r < query_rows; ++r) maximum[r] = -INFINITY, denominator[r] = 0.0f;
-        memset(oh, 0, query_rows * head_dim * sizeof(float));
-        for (size_t s0 = 0; s0 < source_rows; s0 += KEY_TILE) {
-            size_t ns = source_rows - s0 < KEY_TILE ? source_rows - s0 : KEY_TILE;
-            for (size_t r = 0; r < query_rows; ++r) {
-                const float *q = qh + r * head_dim;
-                float tile_max = -INFINITY;
-                for (size_t s = 0; s < ns; ++s) {
-                    scores[s] = dot16(q, kh + (s0 + s) * head_dim, head_dim) * scale;
-                    if (scores[s] != scores[s]) { status = -1; break; }
-                    if (scores[s] > tile_max) tile_max = scores[s];
+    for (size_t i = 0; i < heads * query_rows; ++i) maximum[i] = -INFINITY;
+    memset(output, 0, heads * query_rows * head_dim * sizeof(float));
+    for (size_t s0 = 0; s0 < source_rows && !status; s0 += KEY_TILE) {
+        const size_t ns = source_rows - s0 < KEY_TILE ? source_rows - s0 : KEY_TILE;
+        const size_t ps = (ns + 15) / 16 * 16;
+        for (size_t h = 0; h < heads && !status; ++h) {
+            const float *kt = key + (h * source_rows + s0) * head_dim;
+            const float *vt = value + (h * source_rows + s0) * head_dim;
+            memset(packed, 0, ps * head_dim * sizeof(float));
+            for (size_t d = 0; d < head_dim; ++d)
+                for (size_t s = 0; s < ns; ++s) packed[d * ps + s] = kt[s * head_dim + d];
+            for (size_t q0 = 0; q0 < query_rows && !status; q0 += QUERY_BLOCK) {
+                const size_t rows = query_rows - q0 < QUERY_BLOCK ? query_rows - q0 : QUERY_BLOCK;
+                const float *qt = query + (h * query_rows + q0) * head_dim;
+                /* The block's queries dimension-major, zero rows past `rows`,
+                 * so the tile loop has constant bounds (one register per row). */
+                for (size_t d = 0; d < head_dim; ++d)
+                    for (size_t r = 0; r < QUERY_BLOCK; ++r) qd[d * QUERY_BLOCK + r] = r < rows ? qt[r * head_dim + d] : 0.0f;
+                for (size_t s = 0; s < ps; s += 16) {
+                    float acc[QUERY_BLOCK][16];
+                    memset(acc, 0, sizeof acc);
+                    for (size_t d = 0; d < head_dim; ++d) {
+                        const float *kd = packed + d * ps + s;
+                        const float *qv = qd + d * QUERY_BLOCK;
+                        for (int r = 0; r < QUERY_BLOCK; ++r)
+                            for (int l = 0; l < 16; ++l) acc[r][l] = fmaf(kd[l], qv[r], acc[r][l]);
+                    }
+                    const size_t lanes = ns - s < 16 ? ns - s : 16;
+                    for (size_t r = 0; r < rows; ++r)
+                        for (size_t l = 0; l < lanes; ++l) scores[r * ns + s + l] = acc[r][l] * scale;
+                }
+                for (size_t r = 0; r < rows; ++r) {
+                    float *sc = scores + r * ns;
+                    const size_t state = h * query_rows + q0 + r;
+                    float tile_max = -INFINITY;
+                    for (size_t s = 0; s < ns; ++s) {
+                        if (sc[s] != sc[s]) status = -1;
+                        if (sc[s] > tile_max) tile_max = sc[s];
+                    }
+                    float mx = maximum[state] > tile_max ? maximum[state] : tile_max;
+                    if (status || (isinf(mx) && mx > 0)) { status = -1; break; }
+                    if (mx == -INFINITY) continue;
+                    float *o = output + state * head_dim;
+                    if (denominator[state] != 0.0f) {
+                        const float old = expf(maximum[state] - mx);
+                        for (size_t d = 0; d < head_dim; ++d) o[d] *= old;
+                        denominator[state] *= old;
+                    }
+                    softmax_numerators(math, sc, ns, mx, &denominator[state]);
+                    maximum[state] = mx;
                 }
                 if (status) break;
-                float mx = maximum[r] > tile_max ? maximum[r] : tile_max;
-                if (isinf(mx) && mx > 0) { status = -1; break; }
-                if (mx == -INFINITY) continue;
-                float *o = oh + r * head_dim;
-                if (denominator[r] != 0.0f) {
-                    float old = expf(maximum[r] - mx);
-                    for (size_t d = 0; d < head_dim; ++d) o[d] *= old;
-                    denominator[r] *= old;
-                }
-                float sum = 0.0f;
-                for (size_t s = 0; s < ns; ++s) {
-                    scores[s] = softmax_exp(math, scores[s] - mx);
-                    sum += scores[s];
-                }
-                denominator[r] += sum;
-                maximum[r] = mx;
-                for (size_t s = 0; s < ns; ++s) {
-                    const float *v = vh + (s0 + s) * head_dim;
-                    float w = scores[s];
-                    for (size_t d = 0; d < head_dim; ++d) o[d] = fmaf(w, v[d], o[d]);
+                for (size_t r = 0; r < rows; ++r) {
+                    float *o = output + (h * query_rows + q0 + r) * head_dim;
+                    const float *w = scores + r * ns;
+                    for (size_t s = 0; s < ns; ++s) {
+                        const float *v = vt + s * head_dim;
+                        for (size_t d = 0; d < head_dim; ++d) o[d] = fmaf(w[s], v[d], o[d]);
+                    }
                 }
             }
-            if (status) break;
-        }
-        for (size_t r = 0; r < query_rows && !status; ++r) {
-            float den = denominator[r];
-            if (!isfinite(den) || den == 0.0f) { status = -1; break; }
-            for (size_t d = 0; d < head_dim; ++d) oh[r * head_dim + d] /= den;
         }
     }
+    for (size_t i = 0; i < heads * query_rows && !status; ++i) {
+        const float den = denominator[i];
+        if (!isfinite(den) || den == 0.0f) { status = -1; break; }
+        for (size_t d = 0; d < head_dim; ++d) output[i * head_dim + d] /= den;
+    }
+    free(packed);
     free(scores);
+    free(qd);
     free(maximum);
     free(denominator);
     return status;

@@ -14,12 +14,16 @@ each checked estimator of a GPU-built context gets:
 - the logits of sampled test rows, the oracle's cached prediction against the
   GPU-built context.
 
-Each to |gpu - cpu| <= 1e-5 + 1e-4 |cpu|. Where a K/V check misses that bar
-(at 200,000 training rows the oracle accumulates each attention over the
-keys in one sequential FP32 order), the float64 restatement
-(tests/reference_np.py) decides on the first sampled feature and rows: the
-GPU's error against float64 must not exceed the oracle's own. Logits always
-take the strict bar, with identical argmax for a classifier.
+Each to |gpu - cpu| <= 1e-5 + 1e-4 |cpu|, with identical argmax for a
+classifier's logits. Where a check misses that bar, the float64 restatement
+(tests/reference_np.py) decides: at 200,000 training rows the reference's
+FP32 CPU path itself strays from exact arithmetic by more than the bar (each
+attention accumulates its output, and in exact math its softmax denominator,
+over the 200,000 keys one key at a time, cpu.rs:963-969). For K/V, on the
+first sampled feature and rows, the GPU's error against float64 must not
+exceed the oracle's own. For logits, on every sampled test row, the GPU must
+meet the strict bar against float64 itself and be no further from it than
+the oracle; the argmax must still equal the oracle's.
 """
 
 from __future__ import annotations
@@ -56,8 +60,9 @@ def spot_checks(task, weights, width, ctx, x, y, xt, logits, features=4, train_r
         return float((np.abs(gpu - cpu) - (1e-5 + 1e-4 * np.abs(cpu))).max()), float(np.abs(gpu - cpu).max())
 
     report = {k: {"max_abs_diff_vs_oracle": 0.0, "strict_ok": True} for k in ("column_kv", "icl_kv", "logits")}
-    for k in ("column_kv", "icl_kv"):
+    for k in ("column_kv", "icl_kv", "logits"):
         report[k]["float64"] = {"gpu_max_abs_err": 0.0, "oracle_max_abs_err": 0.0}
+    report["logits"]["float64"]["gpu_strict_vs_float64"] = True
 
     def note(kind, got, want):
         ex, d = excess(got, want)
@@ -92,6 +97,12 @@ def spot_checks(task, weights, width, ctx, x, y, xt, logits, features=4, train_r
         if task == "classifier":
             argmax_ok &= bool(np.array_equal(gpu.argmax(-1), cpu.argmax(-1)))
         log(f"estimator {e}: oracle checks in {time.perf_counter() - t0:.1f} s")
+        if excess(gpu, cpu)[0] > 0:
+            t0 = time.perf_counter()
+            ref = exact.cached_logits(xt[e, tests].astype(np.float64), ck, cv, ik, iv)[None, :, :width]
+            note64("logits", gpu, cpu, ref)
+            report["logits"]["float64"]["gpu_strict_vs_float64"] &= excess(gpu, ref)[0] <= 0
+            log(f"estimator {e}: float64 logits in {time.perf_counter() - t0:.1f} s")
         if not (report["column_kv"]["strict_ok"] and report["icl_kv"]["strict_ok"]):
             t0 = time.perf_counter()
             for blk, (k64, v64) in enumerate(exact.column_kv(x[e].astype(np.float64), y[e], int(feats[0]))):
@@ -108,10 +119,11 @@ def spot_checks(task, weights, width, ctx, x, y, xt, logits, features=4, train_r
             log(f"estimator {e}: float64 checks in {time.perf_counter() - t0:.1f} s")
         del ck, cv, ik, iv
         log(f"estimator {e}: {json.dumps(report)}")
-    ok = report["logits"]["strict_ok"] and argmax_ok
-    for k in ("column_kv", "icl_kv"):
+    ok = argmax_ok
+    for k in ("column_kv", "icl_kv", "logits"):
         f = report[k]["float64"]
-        report[k]["ok"] = report[k]["strict_ok"] or f["gpu_max_abs_err"] <= f["oracle_max_abs_err"]
+        report[k]["ok"] = report[k]["strict_ok"] or (f["gpu_max_abs_err"] <= f["oracle_max_abs_err"] and
+                                                     f.get("gpu_strict_vs_float64", True))
         ok &= report[k]["ok"]
     report["logits"]["argmax_identical"] = argmax_ok
     report.update({"estimators": members, "features": feats.tolist(), "train_rows": rows.tolist(),

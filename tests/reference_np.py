@@ -139,6 +139,32 @@ class Model:
                                   qass_source=n)
         return keys, values
 
+    def cached_logits(self, xq, ck, cv, ik, iv):
+        """Test rows xq [Q, H] against a built context (column K/V
+        [3][H+4,8,128,16], ICL K/V [12][8,N,64]), cached prediction in float64
+        (StaticExecutor::predict_chunk, cpu.rs:2200-2273): decoder outputs [Q, width]."""
+        t = self.t
+        q, h = xq.shape
+        n = ik[0].shape[1]
+        seq = np.zeros((q, h + 4, 128))
+        seq[:, :4] = t("row_interactor.cls_tokens")
+        for f in range(h):
+            e = self.column_input(xq, f)
+            for blk in range(3):
+                p = f"col_embedder.tf_col.blocks.{blk}.multihead_attn2"
+                e = self.attend(p, e, np.asarray(ck[blk][4 + f], np.float64), np.asarray(cv[blk][4 + f], np.float64))
+            seq[:, 4 + f] = e
+        for blk in range(2):
+            seq = self.block(f"row_interactor.tf_row.blocks.{blk}", seq, seq, rope=True)
+        final = self.block("row_interactor.tf_row.blocks.2", seq[:, :4], seq, rope=True)
+        rows = layer_norm(final, t("row_interactor.out_ln.weight"), t("row_interactor.out_ln.bias")).reshape(q, 512)
+        for blk in range(12):
+            rows = self.attend(f"icl_predictor.tf_icl.blocks.{blk}", rows, np.asarray(ik[blk], np.float64),
+                               np.asarray(iv[blk], np.float64), qass_source=n)
+        hid = gelu(layer_norm(rows, t("icl_predictor.ln.weight"), t("icl_predictor.ln.bias")) @
+                   t("icl_predictor.decoder.0.weight").T + t("icl_predictor.decoder.0.bias"))
+        return hid @ t("icl_predictor.decoder.2.weight").T + t("icl_predictor.decoder.2.bias")
+
     def target(self, prefix, y):
         w, b = self.t(f"{prefix}.y_encoder.weight"), self.t(f"{prefix}.y_encoder.bias")
         if self.task == "classifier":

@@ -173,13 +173,17 @@ def test_clf_200k_ensemble_full_size(device, clf_weights):
     the oracle's spot checks (2 features, 8 training rows) and its cached
     prediction of 32 sampled test rows each.
 
-    The logits take the strict bar with identical argmax. The K/V spot checks
-    may miss it (by up to about 6e-5 absolute, measured): the oracle
-    accumulates each attention over 200,000 keys in one sequential FP32 order.
-    Then the float64 restatement (tests/reference_np.py) arbitrates on the
-    first sampled feature and two rows: the GPU's error against float64 must
-    not exceed the oracle's (measured: column K/V 1.9e-6 for the GPU against
-    2.9e-5 for the oracle, ICL K/V 2.8e-5 against 3.4e-5)."""
+    At 200,000 training rows the reference's FP32 CPU path strays from exact
+    arithmetic by more than the parity bar: each attention accumulates over
+    the 200,000 keys one key at a time (in exact math its softmax denominator
+    too, cpu.rs:963-969). Measured against the oracle: column K/V up to 5.6e-5,
+    ICL K/V 9.3e-5, logits 1.8e-5 apart. The float64 restatement
+    (tests/reference_np.py) then decides: for K/V (first sampled feature, two
+    rows) the GPU's error against float64 must not exceed the oracle's
+    (measured: column 2.1e-6 against 5.6e-5, ICL 2.8e-5 against 8.5e-5); for
+    logits (every sampled row) the GPU must meet the strict bar against float64
+    itself and be no further from it than the oracle, with the oracle's
+    argmax."""
     w = S.WORKLOADS["clf-200k"]
     print("clf-200k: generating data", flush=True)
     x, y, xt, meta = S.workload_data(w)
@@ -196,5 +200,5 @@ def test_clf_200k_ensemble_full_size(device, clf_weights):
     report = full_size.spot_checks("classifier", clf_weights, 10, st, x, y, xt, gpu, features=2, train_rows=8,
                                    test_rows=32, float64_rows=2,
                                    log=lambda m: print(f"clf-200k {m}", flush=True))
-    assert report["logits"]["strict_ok"] and report["logits"]["argmax_identical"], report
+    assert report["logits"]["ok"] and report["logits"]["argmax_identical"], report
     assert report["column_kv"]["ok"] and report["icl_kv"]["ok"], report

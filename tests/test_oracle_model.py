@@ -197,3 +197,18 @@ def test_float64_spot_checks_match_the_oracle_build(lcg_case, clf_weights):
     for blk in range(12):
         np.testing.assert_allclose(keys[blk], ik[blk][1][:, 33], atol=2e-5, rtol=1e-4)
         np.testing.assert_allclose(values[blk], iv[blk][1][:, 33], atol=2e-5, rtol=1e-4)
+
+
+def test_float64_cached_prediction_matches_the_oracle(clf_weights):
+    """reference_np's cached prediction (the float64 arbiter of the full-size
+    logit checks) against the oracle's, on an oracle-built context."""
+    rng = np.random.default_rng(12)
+    n, q, h = 64, 6, 5
+    x = rng.normal(size=(n + q, h)).astype(np.float32)
+    y = (np.arange(n) % 3).astype(np.float32)
+    m = O.OracleModel("classifier", clf_weights, O.EXACT)
+    ck, cv, ik, iv = m.build_context(x[None, :n], y[None])
+    want = m.predict_cached((ck, cv, ik, iv), x[None, n:])[0]
+    got = Model("classifier", clf_weights).cached_logits(x[n:].astype(np.float64), [c[0] for c in ck],
+                                                        [c[0] for c in cv], [t[0] for t in ik], [t[0] for t in iv])
+    np.testing.assert_allclose(got, want, atol=1e-5, rtol=1e-4)
