@@ -330,6 +330,22 @@ int irx_regression_summary(irx_device *device, const float *decoded, size_t ense
  * k and v [pairs, rows, 64]; out [pairs, query_rows, 64]. */
 int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v,
                            size_t pairs, size_t query_rows, size_t rows, float *out);
+/* The FP32 attention of irx_test_icl_attention on device buffers, allocating
+ * nothing. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops).
+ * q [pairs, query_rows, 64], k and v [pairs, rows, 64] and out are device
+ * memory, 16-byte aligned; out receives token rows [pairs / 8, query_rows,
+ * 512] (head h of estimator b at columns 64 h .. 64 h + 63 of row b,
+ * query). The kernels' split-K partials live in a 64 MiB scratch array that
+ * the library holds on each device from irx_device_open until the process
+ * ends; a shape whose partials exceed it is refused with
+ * IRX_INVALID_ARGUMENT. The work is enqueued on `stream` (a hipStream_t, or
+ * NULL for the null stream) and the call returns without waiting. Every call
+ * on one device shares its scratch array: calls whose work overlaps on one
+ * device (on different streams, or from different threads) race. Results are
+ * bitwise those of irx_test_icl_attention on the same device. */
+int irx_icl_attention_noalloc(irx_device *device, const float *q, const float *k, const float *v, size_t pairs,
+                              size_t query_rows, size_t rows, float *out, void *stream);
 /* The same at `precision`: SPLIT packs k and v into the FP16 cache first;
  * HALF rounds them to FP16 and encodes the FP8 cache from those. */
 int irx_test_icl_attention_precision(irx_device *device, int precision, const float *q, const float *k,

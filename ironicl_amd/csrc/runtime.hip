@@ -187,11 +187,23 @@ void rope_tables(const float *freqs, int len, std::vector<float> &cos_t, std::ve
 
 using namespace irx;
 
+// ---- the no-allocation entry point's scratch ----
+
+// Split-K partials of irx_icl_attention_noalloc, for callers that cannot
+// allocate (code under HIP graph capture, tight serving loops). Every GPU the
+// library runs on holds its own copy until the process ends; host code never
+// uses this name as an address, only the per-device pointer that
+// hipGetSymbolAddress returns (irx_device::scratch).
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
 // ---- opaque ABI objects ----
 
 struct irx_device {
     int ordinal = 0;
     int compute_units = 0;
+    // This device's copy of `scratch`, looked up once when the device is opened.
+    float *scratch = nullptr;
     std::atomic<int> refs{1};
     // Idle non-blocking streams for builds, predictors and preprocessors to
     // reuse: creating one costs about a millisecond.
@@ -1339,9 +1351,14 @@ int irx_device_open(int ordinal, irx_device **out) {
         if (std::strncmp(props.gcnArchName, "gfx950", 6) != 0)
             fail(IRX_NO_DEVICE, std::string("kernels are built for gfx950, not ") + props.gcnArchName);
         IRX_HIP(hipSetDevice(ordinal));
+        // The device address of this device's scratch array (the array's name
+        // in host code is no device address).
+        float *scratch_ptr = nullptr;
+        IRX_HIP(hipGetSymbolAddress(reinterpret_cast<void **>(&scratch_ptr), HIP_SYMBOL(scratch)));
         auto d = new irx_device();
         d->ordinal = ordinal;
         d->compute_units = props.multiProcessorCount;
+        d->scratch = scratch_ptr;
         *out = d;
     });
 }
@@ -1847,6 +1864,35 @@ int irx_test_encode_icl8(irx_device *device, const uint16_t *k, const uint16_t *
 int irx_test_icl_attention(irx_device *device, const float *q, const float *k, const float *v, size_t pairs,
                            size_t query_rows, size_t rows, float *out) {
     return irx_test_icl_attention_precision(device, IRX_PRECISION_FP32, q, k, v, pairs, query_rows, rows, out);
+}
+
+int irx_icl_attention_noalloc(irx_device *device, const float *q, const float *k, const float *v, size_t pairs,
+                              size_t query_rows, size_t rows, float *out, void *stream) {
+    return guarded("irx_icl_attention_noalloc", [&] {
+        if (!device || !q || !k || !v || !out || !pairs || !query_rows || !rows)
+            fail(IRX_INVALID_ARGUMENT, "ICL attention shapes do not match");
+        if (pairs % kHeads) fail(IRX_INVALID_ARGUMENT, "pairs must be a multiple of 8 (estimators x heads)");
+        if (pairs > (size_t)1 << 20 || query_rows > (size_t)1 << 24 || rows > (size_t)1 << 30)
+            fail(IRX_INVALID_ARGUMENT, "ICL attention shape is out of range");
+        if (!device->scratch) fail(IRX_DEVICE_ERROR, "the device's scratch array was not set up");
+        // The same split plan as irx_test_icl_attention on this device, so the
+        // results are the same bit for bit; its partials must fit the scratch.
+        const int splits = icl_attention_splits((int)pairs, (int)query_rows, (int)rows, device->compute_units);
+        const size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, splits);
+        if (pf * sizeof(float) > kNoAllocScratchBytes)
+            fail(IRX_INVALID_ARGUMENT, "ICL attention of " + std::to_string(pairs) + " pairs x " +
+                                           std::to_string(query_rows) + " queries x " + std::to_string(rows) +
+                                           " keys needs " + std::to_string(pf * sizeof(float)) +
+                                           " bytes of partials; the no-allocation entry point holds " +
+                                           std::to_string(kNoAllocScratchBytes));
+        set_device(device);
+        IclAttention a{};
+        a.q = q, a.q_pair_stride = (long long)query_rows * 64, a.k = k, a.v = v;
+        a.kv_pair_stride = (long long)rows * 64, a.o = out, a.ldo = 512;
+        a.pairs = (int)pairs, a.q_rows = (int)query_rows, a.kv_rows = (int)rows;
+        a.partial = pf ? device->scratch : nullptr, a.partial_floats = pf, a.compute_units = device->compute_units;
+        icl_attention(a, static_cast<hipStream_t>(stream));
+    });
 }
 
 int irx_test_products(irx_device *device, const float *x, const float *w1, const float *b1, const float *w2,

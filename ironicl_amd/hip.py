@@ -105,6 +105,8 @@ SIGNATURES = {
     "irx_profile_enable": (ctypes.c_int, [ctypes.c_uint]),
     "irx_profile_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(KernelStats)]),
     "irx_test_icl_attention": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
+    "irx_icl_attention_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                 _sz, _sz, _sz, ctypes.c_void_p, ctypes.c_void_p]),
     "irx_test_icl_attention_precision": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _CF, _CF, _sz, _sz,
                                                         _sz, _F]),
     "irx_test_encode_icl8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _sz, _sz,
