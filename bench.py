@@ -132,6 +132,18 @@ def profiled_traffic() -> int | None:
     return int(m.group(1)) if m else None
 
 
+def predict_flops_per_row(n: int, h: int, width: int) -> float:
+    """Algorithmic FLOPs of one test row's cached prediction against an
+    N-row, H-feature context: column stage 3 H (12 D^2 + 4 M D), row stage
+    36 L D^2 + 8 L^2 D + 16 L D + 48 D^2, ICL 12 (12 E^2 + 131,072) + 48 N E,
+    decoder 2 E 1,024 + 2,048 width (D = M = 128, E = 512, L = H + 4)."""
+    d, m, e, length = 128, 128, 512, h + 4
+    column = 3 * h * (12 * d * d + 4 * m * d)
+    row = 36 * length * d * d + 8 * length * length * d + 16 * length * d + 48 * d * d
+    icl = 12 * (12 * e * e + 131072) + 12 * 4 * n * e
+    return float(column + row + icl + 2 * e * 1024 + 2 * 1024 * width)
+
+
 def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target_s: float) -> dict:
     """The oracle's cached prediction on the host cores, on a bounded sample of
     the workload's test rows (sized for about target_s seconds of CPU work), at
@@ -174,9 +186,15 @@ def cpu_baseline(weights, context_host, x_test, gpu_logits, threads: int, target
     logical = os.cpu_count() or threads
     all_cores = variant(m, logical, sample)
     exact = variant(O.OracleModel("classifier", weights, O.EXACT), threads, max(8, sample // 2))
+    n, h = context_host[2][0].shape[2], x_test.shape[2]
+    per_row = predict_flops_per_row(n, h, CLASSES)
+    all_cores["gflops"] = all_cores["value"] * per_row / 1e9
+    exact["gflops"] = exact["value"] * per_row / 1e9
     return {
         "value": rows / dt,
         "unit": "rows/s",
+        "gflops": rows / dt * per_row / 1e9,
+        "flops_per_row": per_row,
         "cores": threads,
         "kind": "port",
         "sample": f"cached prediction of the first {rows} of the {x_test.shape[1]} test rows against the same "
