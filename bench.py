@@ -132,6 +132,61 @@ def profiled_traffic() -> int | None:
     return int(m.group(1)) if m else None
 
 
+def attention_back_to_back(device, pairs: int, n: int, rows_list, layers: int = 12, rounds: int = 4) -> dict:
+    """The whole KV-streaming cross-attention of a pass of few rows (the
+    attention kernel and its split-K merge, as a pass issues them), launched
+    back to back through irx_icl_attention_noalloc over `layers` K/V buffers
+    of one ICL layer's shape ([pairs, n, 64] each; rotated, so every call
+    streams its K/V from HBM past the 256 MB MALL) and timed with one pair of
+    HIP events around rounds x layers calls: no event between the two
+    launches of a call, so neither carries a timed launch's overhead."""
+    from ironicl_amd import hip, hipmem
+
+    rt = hipmem.runtime()
+    kv = np.random.default_rng(11).standard_normal(pairs * n * 64, dtype=np.float32)
+    ks = [hipmem.DeviceArray.from_host(kv) for _ in range(layers)]
+    vs = [hipmem.DeviceArray.from_host(kv[::-1]) for _ in range(layers)]
+    del kv
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    hipmem._ok(rt.hipEventCreate(ctypes.byref(e0)), "hipEventCreate")
+    hipmem._ok(rt.hipEventCreate(ctypes.byref(e1)), "hipEventCreate")
+    out = {}
+    try:
+        for rows in rows_list:
+            qd = hipmem.DeviceArray.from_host(
+                (np.random.default_rng(rows).standard_normal((pairs, rows, 64)) * 0.5).astype(np.float32))
+            od = hipmem.DeviceArray((pairs // 8, rows, 512))
+
+            def call(i):
+                hip.check(hip.lib().irx_icl_attention_noalloc(device.handle, qd.ptr, ks[i].ptr, vs[i].ptr, pairs, rows,
+                                                              n, od.ptr, None))
+
+            for i in range(layers):
+                call(i)
+            hipmem.synchronize()
+            best = float("inf")
+            for _ in range(3):
+                hipmem._ok(rt.hipEventRecord(e0, None), "hipEventRecord")
+                for _ in range(rounds):
+                    for i in range(layers):
+                        call(i)
+                hipmem._ok(rt.hipEventRecord(e1, None), "hipEventRecord")
+                hipmem._ok(rt.hipEventSynchronize(e1), "hipEventSynchronize")
+                ms = ctypes.c_float()
+                hipmem._ok(rt.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
+                best = min(best, ms.value / (rounds * layers))
+            algo = 2.0 * pairs * n * 64 * 4 + 2.0 * pairs * rows * 64 * 4
+            out[str(rows)] = {"ms_per_layer": best, "achieved_gbps": algo / (best * 1e-3) / 1e9,
+                              "frac": algo / (best * 1e-3) / 1e9 / HBM_PEAK_GBPS}
+            del qd, od
+    finally:
+        rt.hipEventDestroy(e0)
+        rt.hipEventDestroy(e1)
+        for a in ks + vs:
+            a.free()
+    return out
+
+
 def predict_flops_per_row(n: int, h: int, width: int) -> float:
     """Algorithmic FLOPs of one test row's cached prediction against an
     N-row, H-feature context: column stage 3 H (12 D^2 + 4 M D), row stage
@@ -755,6 +810,11 @@ def main() -> int:
         }
         log(f"pass of {qb:2d} rows: {pass_ms:.2f} ms, attention {1e3 * launch_ms:.1f} us/launch, "
             f"{small[str(qb)]['achieved_gbps']:.0f} GB/s")
+    whole = attention_back_to_back(device, b * 8, n, SMALL_PASSES)
+    for qb in SMALL_PASSES:
+        small[str(qb)]["attention_with_merge_back_to_back"] = whole[str(qb)]
+        log(f"pass of {qb:2d} rows: attention + merge back to back {1e3 * whole[str(qb)]['ms_per_layer']:.1f} us "
+            f"per layer = {whole[str(qb)]['frac']:.3f} of HBM peak")
     context.set_pass_rows(args.pass_rows)
     context.set_streams(2)
 
@@ -861,6 +921,10 @@ def main() -> int:
         "small_pass_hbm": {
             "kernel": "icl_decode_kernel (passes of <= 32 rows against the 2.46 GB cached K/V, one stream)",
             "bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s", "by_pass_rows": small,
+            "timing": "avg_launch_ms / merge_ms_per_launch: HIP events around each launch inside whole passes "
+                      "(each carries a timed launch's overhead); attention_with_merge_back_to_back: the attention "
+                      "kernel and its merge as one call, 12 layer-sized K/V buffers rotated, one event pair "
+                      "around 48 calls (irx_icl_attention_noalloc)",
         },
         "optimize_auto": auto_report,
         "optimize_fast": fast_report,
