@@ -141,6 +141,29 @@ struct DevBuf {
     float *f() const { return static_cast<float *>(p); }
 };
 
+// Pinned host memory (hipHostMalloc), grown on demand: copies between it and
+// the device are asynchronous, where copies from pageable memory block the
+// host until the stream reaches them.
+struct PinnedBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    PinnedBuf() = default;
+    PinnedBuf(const PinnedBuf &) = delete;
+    PinnedBuf &operator=(const PinnedBuf &) = delete;
+    ~PinnedBuf() { release(); }
+    void reserve(size_t b) {
+        if (b <= bytes) return;
+        release();
+        IRX_HIP(hipHostMalloc(&p, b, hipHostMallocDefault));
+        bytes = b;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr, bytes = 0;
+    }
+    float *f() const { return static_cast<float *>(p); }
+};
+
 // Bump allocator over one device allocation. With `counting`, only sums sizes.
 struct Arena {
     DevBuf buf;
@@ -376,8 +399,10 @@ struct irx_predictor {
     std::mutex mu;
     Arena ws[kMaxPassStreams];
     // Host-buffer predictions: device inputs, outputs and missing-row flags,
-    // grown to the largest call so far.
+    // and pinned staging for the inputs and logits, grown to the largest call
+    // so far.
     DevBuf io_x, io_logits, io_flags;
+    PinnedBuf pin_x, pin_logits;
     // Passes replayed from HIP graphs, oldest first.
     std::vector<PassGraphEntry> graphs;
     bool use_graphs = true;
@@ -1690,11 +1715,23 @@ int irx_predictor_set_pass_rows(irx_predictor *predictor, size_t rows) {
     });
 }
 
+// Host buffers of a prediction: each pass's rows are copied into pinned
+// staging and go up on the pass's stream just before it, and its logits come
+// back into pinned staging on the same stream right after it, so the first
+// pass waits for its own rows only and the copies overlap other passes.
+struct HostIo {
+    const float *x;    // [B, q, H], the caller's
+    float *pin_x;      // [B, q, H], pinned
+    float *pin_logits; // [B, q, width], pinned
+};
+
 // Every pass of a prediction of q rows. With cpu_rows (host, [q]), the rows
 // holding the all-missing marker are flagged there: the passes set device
 // flags, read back once after the last pass, so passes never wait on the host.
+// With io, the inputs start on the host and d_x / d_logits are the
+// predictor's device copies of them.
 static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *d_logits, uint8_t *cpu_rows,
-                           irx_progress_fn progress, void *user) {
+                           irx_progress_fn progress, void *user, const HostIo *io = nullptr) {
     const size_t R = P->pass_rows;
     uint8_t *d_flags = nullptr;
     if (cpu_rows) {
@@ -1707,10 +1744,21 @@ static void predict_common(irx_predictor *P, const float *d_x, size_t q, float *
     const int lanes = P->streams;
     IRX_HIP(hipEventRecord(P->fork, P->stream));
     for (int i = 1; i < lanes; ++i) IRX_HIP(hipStreamWaitEvent(P->lane(i), P->fork, 0));
+    const size_t B = P->shape.ensembles, H = P->shape.features, width = P->shape.outputs;
     int slot = 0;
     for (size_t q0 = 0; q0 < q; q0 += R, slot = (slot + 1) % lanes) {
         const int len = (int)std::min(R, q - q0);
-        predict_pass(P, slot, d_x, (long long)q * P->shape.features, (int)q0, len, d_logits, (int)q, d_flags);
+        if (io) {  // the pass's rows of every estimator
+            for (size_t e = 0; e < B; ++e)
+                std::memcpy(io->pin_x + (e * q + q0) * H, io->x + (e * q + q0) * H, (size_t)len * H * 4);
+            IRX_HIP(hipMemcpy2DAsync(const_cast<float *>(d_x) + q0 * H, q * H * 4, io->pin_x + q0 * H, q * H * 4,
+                                     (size_t)len * H * 4, B, hipMemcpyHostToDevice, P->lane(slot)));
+        }
+        predict_pass(P, slot, d_x, (long long)q * H, (int)q0, len, d_logits, (int)q, d_flags);
+        if (io)
+            IRX_HIP(hipMemcpy2DAsync(io->pin_logits + q0 * width, q * width * 4, d_logits + q0 * width,
+                                     q * width * 4, (size_t)len * width * 4, B, hipMemcpyDeviceToHost,
+                                     P->lane(slot)));
         if (progress) {
             IRX_HIP(hipStreamSynchronize(P->lane(slot)));
             report(progress, user, IRX_STAGE_PREDICT, q0 + len, q);
@@ -1735,11 +1783,13 @@ int irx_predictor_predict(irx_predictor *predictor, const float *x, size_t q, fl
         // Device copies of the inputs and outputs, kept and grown across calls.
         if (predictor->io_x.bytes < xn * 4) predictor->io_x.alloc(xn * 4);
         if (predictor->io_logits.bytes < ln * 4) predictor->io_logits.alloc(ln * 4);
-        upload(predictor->io_x.p, x, xn * 4, predictor->stream);
+        predictor->pin_x.reserve(xn * 4);
+        predictor->pin_logits.reserve(ln * 4);
+        const HostIo io{x, predictor->pin_x.f(), predictor->pin_logits.f()};
         predict_common(predictor, predictor->io_x.f(), q, predictor->io_logits.f(), cpu_rows, progress,
-                       progress_user);
-        download(logits, predictor->io_logits.p, ln * 4, predictor->stream);
+                       progress_user, &io);
         IRX_HIP(hipStreamSynchronize(predictor->stream));
+        std::memcpy(logits, predictor->pin_logits.p, ln * 4);
     });
 }
 
