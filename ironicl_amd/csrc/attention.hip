@@ -299,12 +299,20 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
             l_run[j] += lsum;
         }
         // O^T += V^T P^T: register r of s[j][b] is key b*32 + half*4 + (r&3) + 8*(r>>2);
-        // the lane fetches that key's dims 2*r32 and 2*r32 + 1.
+        // the lane fetches that key's dims 2*r32 and 2*r32 + 1, one key ahead
+        // of its products (scheduling fences keep the reads there: left to
+        // itself the compiler moves each read next to its first use).
+        auto vrow = [&](int r) { return vt + (half * 4 + (r & 3) + 8 * (r >> 2)) * 64 + 2 * r32; };
+        f32x2 v0 = *reinterpret_cast<const f32x2 *>(vrow(0));
+        f32x2 v1 = *reinterpret_cast<const f32x2 *>(vrow(0) + 32 * 64);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int key = half * 4 + (r & 3) + 8 * (r >> 2);
-            const f32x2 v0 = *reinterpret_cast<const f32x2 *>(vt + key * 64 + 2 * r32);
-            const f32x2 v1 = *reinterpret_cast<const f32x2 *>(vt + (key + 32) * 64 + 2 * r32);
+            f32x2 n0 = v0, n1 = v1;
+            if (r < 15) {
+                n0 = *reinterpret_cast<const f32x2 *>(vrow(r + 1));
+                n1 = *reinterpret_cast<const f32x2 *>(vrow(r + 1) + 32 * 64);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 o[j][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[0], s[j][0][r], o[j][0], 0, 0, 0);
@@ -312,6 +320,8 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
                 o[j][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[0], s[j][1][r], o[j][0], 0, 0, 0);
                 o[j][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[1], s[j][1][r], o[j][1], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            v0 = n0, v1 = n1;
         }
         buf ^= 1;
     }
