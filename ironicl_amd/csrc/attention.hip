@@ -549,12 +549,11 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
     for (int r = 0; r < 16; ++r) neg_ref[0][r] = INFINITY, neg_ref[1][r] = INFINITY, zero[r] = 0.f;
     constexpr float kLazyLimit16 = 32768.0f;  // 2^15: probabilities stay FP16-representable
 
-    issue_tile(k_begin, 0);
-    int buf = 0;
-    for (int k0 = k_begin; k0 < k_end; k0 = __builtin_amdgcn_readfirstlane(k0 + kKeyTile)) {
-        wait_loads();
-        __syncthreads();
-        if (k0 + kKeyTile < k_end) issue_tile(k0 + kKeyTile, buf ^ 1);
+    // One tile at k0 from LDS buffer `buf`. Only a range's last tile can hold
+    // keys past it (RAGGED): full tiles carry no masking code at all (left to
+    // itself the compiler computes every key's bound check on every tile).
+    auto tile = [&](int k0, int buf, auto ragged) {
+        constexpr bool RAGGED = decltype(ragged)::value;
         const u32x4 *kt = tiles[buf].k;
         const u32x4 *vt = tiles[buf].v;
 
@@ -572,7 +571,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
                     s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, ql[j][m], s1, 0, 0, 0);
                 }
             }
-            if (k0 + kKeyTile > k_end) {
+            if constexpr (RAGGED) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -640,7 +639,24 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
                 }
             }
         }
+    };
+
+    issue_tile(k_begin, 0);
+    int buf = 0;
+    // Full tiles, then the range's ragged last tile if it has one.
+    const int k_full = __builtin_amdgcn_readfirstlane(k_begin + (k_end - k_begin) / kKeyTile * kKeyTile);
+    int k0 = k_begin;
+    for (; k0 < k_full; k0 = __builtin_amdgcn_readfirstlane(k0 + kKeyTile)) {
+        wait_loads();
+        __syncthreads();
+        if (k0 + kKeyTile < k_end) issue_tile(k0 + kKeyTile, buf ^ 1);
+        tile(k0, buf, std::false_type{});
         buf ^= 1;
+    }
+    if (k0 < k_end) {
+        wait_loads();
+        __syncthreads();
+        tile(k0, buf, std::true_type{});
     }
 
 #pragma unroll
