@@ -750,13 +750,14 @@ __global__ __launch_bounds__(256) void unpack_icl16_kernel(const unsigned short 
 // stream it front to back. Products run on the 16x16x4 FP32 MFMA over QG
 // groups of 16 queries, which pads a pass to 16 or 32 queries rather than 64.
 // Operands go straight from global memory into registers in MFMA order:
-//   scores S^T (key x query): A = K[key = lane % 16][dim 16 (lane / 16) + m],
-//     B = Q[query = lane % 16][same dim], for m = 0..15; lane l's result
-//     register r is key 4 (l / 16) + r, query l % 16;
+//   scores S^T (key x query): A = K[key = lane % 16][dim 16 (m / 4) +
+//     4 (lane / 16) + m % 4], B = Q[query = lane % 16][same dim], for
+//     m = 0..15; lane l's result register r is key 4 (l / 16) + r, query l % 16;
 //   output O^T (dim x query), tile t: A = V[key 4 (l / 16) + r][dim 4 (l % 16)
 //     + t], B = that lane's own probability r: no data moves between lanes.
-// Every K load is a lane's 64 contiguous bytes of one key and every V load
-// four whole 256-byte rows per instruction. The next block's loads are issued
+// Each K load instruction reads 64 contiguous bytes of each of 16 keys (the
+// four lanes of a key take its consecutive 16-byte chunks) and every V load
+// four whole 256-byte rows. The next block's loads are issued
 // before the current block's products, into the other of two register sets.
 // The softmax is the lazy-reference form above; the waves' partial results
 // are merged through LDS at the end.
@@ -780,10 +781,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
         for (int gq = 0; gq < QG; ++gq) {
             const int row = 16 * gq + i16;
             if (row < p.q_rows) {
-                const float *src = p.q + pair * p.q_pair_stride + (long long)row * 64 + 16 * grp;
+                const float *src = p.q + pair * p.q_pair_stride + (long long)row * 64 + 4 * grp;
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const f32x4 v = *reinterpret_cast<const f32x4 *>(src + 4 * c);
+                    const f32x4 v = *reinterpret_cast<const f32x4 *>(src + 16 * c);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) q[gq][4 * c + e] = v[e] * scale;
                 }
@@ -795,13 +796,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
     }
     const float *kbase = p.k + pair * p.kv_pair_stride;
     const float *vbase = p.v + pair * p.kv_pair_stride;
-    // Block at k0: K dims 16 grp .. +15 of key k0 + i16, and V dims 4 i16 ..
-    // +3 of keys k0 + 4 grp + r. Keys past the range repeat its last key
-    // (masked below).
+    // Block at k0: K dims 16 c + 4 grp .. +3 (c = 0..3) of key k0 + i16, and
+    // V dims 4 i16 .. +3 of keys k0 + 4 grp + r. Keys past the range repeat
+    // its last key (masked below).
     auto load = [&](int k0, f32x4 *kd, f32x4 *vd) {
         const int key = min(k0 + i16, k_end - 1);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) kd[c] = *reinterpret_cast<const f32x4 *>(kbase + (long long)key * 64 + 16 * grp + 4 * c);
+        for (int c = 0; c < 4; ++c) kd[c] = *reinterpret_cast<const f32x4 *>(kbase + (long long)key * 64 + 16 * c + 4 * grp);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int vk = min(k0 + 4 * grp + r, k_end - 1);
@@ -1255,12 +1256,17 @@ IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units, bool f
     IclLaunch g{};
     if (q_rows <= kDecodeQueries) {
         // One workgroup per (pair, key range), about two per CU, at least 256
-        // keys each; ranges in whole rounds of the waves' 16-key (FP16: 32-key) blocks.
+        // keys each. FP32 ranges are whole 16-key blocks, so the ranges come
+        // out even and the grid is exactly two workgroups per CU where the keys
+        // allow (50,000 keys x 8 pairs: 64 ranges of 784 keys; in whole rounds
+        // of the four waves' blocks it was 61 and 12 CUs took one workgroup);
+        // FP16 ranges are whole rounds of the waves' 32-key blocks (the
+        // transposed V tiles hold 64 keys).
         g.qtiles = 1;
         g.q_padded = kDecodeQueries;
         const int want = std::max(1, (int)ceil_div(2LL * compute_units, pairs));
         const int splits = std::max(1, std::min(want, kv_rows / 256));
-        const int round = (f16 ? 32 : 16) * kDecodeWaves;
+        const int round = f16 ? 32 * kDecodeWaves : 16;
         const int per = (int)ceil_div(ceil_div(kv_rows, splits), round) * round;
         g.keys_per_split = per;
         g.splits = (int)ceil_div(kv_rows, per);

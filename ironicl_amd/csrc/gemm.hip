@@ -17,6 +17,8 @@
 // of M, whose A rows then stay in that XCD's L2 for all N tiles.
 #include "common.hpp"
 
+#include <atomic>
+
 namespace irx {
 namespace {
 
@@ -76,6 +78,18 @@ __device__ __forceinline__ void store_rows(const GemmArgs &p, int row0, int col,
         dst[dr * ldc] = v;
     };
     if (full_rows) {
+        if constexpr (EPI == kEpiResidual) {
+            // The residual may be the output itself (an in-place update), so
+            // the compiler cannot move a residual load above an earlier store:
+            // load all 16 first (each lane reads only the elements it writes),
+            // or every load's latency is paid in turn.
+            float rv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) rv[r] = res[((r & 3) + 8 * (r >> 2)) * p.ldr];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dst[((r & 3) + 8 * (r >> 2)) * ldc] = acc[r] + bias + rv[r];
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) one(r);
     } else {
@@ -282,6 +296,25 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
     }
 }
 
+// Compute units of the current device, looked up once per device ordinal.
+int device_compute_units() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cached[kMaxDevices] = {};
+    int ordinal = 0;
+    if (hipGetDevice(&ordinal) != hipSuccess || ordinal < 0 || ordinal >= kMaxDevices) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    int cus = cached[ordinal].load(std::memory_order_relaxed);
+    if (cus > 0) return cus;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ordinal) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    cached[ordinal].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
 struct Flops {
     double flops, bytes;
 };
@@ -356,12 +389,34 @@ void gemm(const GemmArgs &args, hipStream_t stream) {
     // prediction pass's products).
     const long long small_tiles = (long long)ceil_div(args.m, 64) * ceil_div(args.n, 64);
     const long long big_tiles = (long long)ceil_div(args.m, 128) * ceil_div(args.n, 128);
-    if (small_tiles < 256)
+    if (small_tiles < 256) {
         launch_splitk(args, stream);
-    else if (big_tiles >= 1024 || (args.epilogue == kEpiGelu && big_tiles >= 512))
-        launch<128, 128>(args, stream);
-    else
+    } else if (big_tiles >= 1024 || (args.epilogue == kEpiGelu && big_tiles >= 512)) {
+        // 128 x 128 tiles run in rounds of two per CU. When the last round
+        // would be mostly empty (the build's 50,000-row products: 1,564 tiles
+        // at N = 512 are 3.05 rounds of 512), the whole rounds take the first
+        // rows and the rows left over run as 64 x 64 tiles, a quarter of the
+        // work each, spread over the chip.
+        const long long slots = 2LL * device_compute_units();
+        const long long tiles_n = ceil_div(args.n, 128);
+        const long long main_tm = big_tiles / slots * slots / tiles_n;
+        const bool plain_rows = args.out.rows_per_group >= args.m && args.epilogue != kEpiQass;
+        if (plain_rows && big_tiles % slots < slots / 2 && main_tm > 0 && main_tm * 128 < args.m) {
+            GemmArgs head = args, rest = args;
+            const long long rows = main_tm * 128;
+            head.m = (int)rows;
+            rest.m = args.m - (int)rows;
+            rest.a = args.a + rows * args.lda;
+            rest.c = args.c + rows * args.out.ldc;
+            if (args.residual) rest.residual = args.residual + rows * args.ldr;
+            launch<128, 128>(head, stream);
+            launch<64, 64>(rest, stream);
+        } else {
+            launch<128, 128>(args, stream);
+        }
+    } else {
         launch<64, 64>(args, stream);
+    }
 }
 
 }  // namespace irx
