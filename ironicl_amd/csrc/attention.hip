@@ -1252,6 +1252,50 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
     *reinterpret_cast<f32x4 *>(p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64 + d) = num * (1.0f / den);
 }
 
+// Few splits (the build's self-attention, passes of many rows): a 16-lane
+// group per (pair, query row), lane d4 taking dims 4 d4 .. +3, with every
+// split's log2-sum-exp and partial row loaded at once; consecutive groups take
+// consecutive rows of one pair, so a workgroup's loads of one split are one
+// contiguous 4 KB run. A wave per row (icl_merge_kernel) leaves too few bytes
+// in flight for these launches (the build's 5-split merge of 50,000 rows ran
+// at 2.7 TB/s).
+template <int MAXS>
+__global__ __launch_bounds__(256) void icl_merge_rows_kernel(IclAttention p, int splits, int q_padded) {
+    const long long pq = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (pq >= (long long)p.pairs * p.q_rows) return;
+    const int d = (threadIdx.x & 15) * 4;
+    const int qrow = (int)(pq % p.q_rows);
+    const int pair = (int)(pq / p.q_rows);
+    const long long step = (long long)p.pairs * q_padded;
+    const long long row0 = (long long)pair * q_padded + qrow;
+    const float *lse = p.partial + (long long)splits * step * 64 + row0;
+    float l[MAXS];
+    f32x4 v[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+        if (s < splits) {
+            l[s] = lse[s * step];
+            v[s] = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + s * step) * 64 + d);
+        } else {
+            l[s] = -INFINITY;
+            v[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    float m = l[0];
+#pragma unroll
+    for (int s = 1; s < MAXS; ++s) m = fmaxf(m, l[s]);
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+        const float w = __builtin_amdgcn_exp2f(l[s] - m);  // 0 past the splits
+        num += w * v[s];
+        den += w;
+    }
+    const int b = pair / kHeads, head = pair - b * kHeads;
+    *reinterpret_cast<f32x4 *>(p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64 + d) = num * (1.0f / den);
+}
+
 IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units, bool f16 = false) {
     IclLaunch g{};
     if (q_rows <= kDecodeQueries) {
@@ -1790,8 +1834,15 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         long long rows = (long long)args.pairs * args.q_rows;
         KernelTimer timer(kFamIclMerge, stream, 0.0,
                           4.0 * ((double)g.splits * rows * 65.0 + (double)rows * 64.0));
-        hipLaunchKernelGGL(icl_merge_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, args, g.splits,
-                           g.q_padded);
+        if (g.splits <= 8)
+            hipLaunchKernelGGL(icl_merge_rows_kernel<8>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args,
+                               g.splits, g.q_padded);
+        else if (g.splits <= 16)
+            hipLaunchKernelGGL(icl_merge_rows_kernel<16>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args,
+                               g.splits, g.q_padded);
+        else
+            hipLaunchKernelGGL(icl_merge_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, args, g.splits,
+                               g.q_padded);
         IRX_HIP(hipGetLastError());
     }
 }

@@ -64,6 +64,28 @@ def test_products_match_float64(device, m, n, k, n2):
     assert rel(first, y) < 1e-5 and rel(second, z) < 1e-5, (rel(first, y), rel(second, z))
 
 
+def test_large_products_with_a_split_last_round(device):
+    """70,000 rows: 2,188 tiles of 128 x 128 are 4.3 rounds of two per CU on
+    256 CUs, so both products (GELU, then residual) run the first 65,536 rows
+    as whole rounds and the 4,464 rows after them as 64 x 64 tiles. Rows on
+    both sides of that boundary and the last rows against float64."""
+    m, n, k = 70_000, 512, 512
+    x = fast_values(m * k, 11)
+    w1, b1 = fast_values(n * k, 12, 0.05), fast_values(n, 13)
+    w2, b2 = fast_values(n * n, 14, 0.05), fast_values(n, 15)
+    first = np.zeros(m * n, np.float32)
+    second = np.zeros(m * n, np.float32)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_products(device.handle, F(x), F(w1), F(b1), F(w2), F(b2), m, n, k, n,
+                                          F(first), F(second)))
+    rows = np.r_[0:64, 65_472:65_600, m - 64:m]
+    y = gelu64(x.reshape(m, k)[rows].astype(np.float64) @ w1.reshape(n, k).T.astype(np.float64) + b1)
+    z = y @ w2.reshape(n, n).T.astype(np.float64) + b2 + y
+    got1, got2 = first.reshape(m, n)[rows], second.reshape(m, n)[rows]
+    assert np.abs(got1 - y).max() / np.abs(y).max() < 1e-5
+    assert np.abs(got2 - z).max() / np.abs(z).max() < 1e-5
+
+
 def attention64(q, k, v, scale):
     s = (q.astype(np.float64) @ k.astype(np.float64).T) * scale
     p = np.exp(s - s.max(-1, keepdims=True))
