@@ -1581,8 +1581,12 @@ constexpr int kShortKStride = 20;   // K rows padded to 20 floats
 
 template <int QB, int KB, bool ROPE, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallAttention p, int groups_per_seq) {
-    constexpr int KEYS = KB * 16, VSTRIDE = KEYS + 4;
-    __shared__ __attribute__((aligned(16))) float Ks[KEYS * kShortKStride];
+    // Rows are padded against bank conflicts, except for 80 keys (the
+    // 68-token rows of 64 features): unpadded, one item's K and V^T take
+    // exactly 10 KB, so sixteen single-wave workgroups fit a CU's LDS and a
+    // 512-row pass (4,096 items) runs in one round.
+    constexpr int KEYS = KB * 16, KSTRIDE = KB == 5 ? 16 : kShortKStride, VSTRIDE = KB == 5 ? KEYS : KEYS + 4;
+    __shared__ __attribute__((aligned(16))) float Ks[KEYS * KSTRIDE];
     __shared__ __attribute__((aligned(16))) float Vt[16 * VSTRIDE];
     // Workgroup j of a (sequence, head) item: its WAVES waves take query chunks
     // (j * WAVES + wave) + k * groups_per_seq * WAVES and share the staged keys.
@@ -1628,7 +1632,7 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
             f32x4 a;
 #pragma unroll
             for (int e = 0; e < 4; ++e) a[e] = kr[4 * c + e];
-            *reinterpret_cast<f32x4 *>(&Ks[key * kShortKStride + 4 * c]) = a;
+            *reinterpret_cast<f32x4 *>(&Ks[key * KSTRIDE + 4 * c]) = a;
         }
 #pragma unroll
         for (int d = 0; d < 16; ++d) Vt[d * VSTRIDE + key] = vr[d];
@@ -1636,14 +1640,17 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
     __syncthreads();
 
     const float scale = p.scale * kLog2e;
-    const int chunks = (p.q_rows + 16 * QB - 1) / (16 * QB);
-    for (int c = c_first; c < chunks; c += c_step) {
-        const int q0 = c * 16 * QB;
-        // This lane's query operands: dims 4g .. 4g+3 of query q0 + 16 j + l16.
-        f32x4 qf[QB];
+    // Query blocks J0 .. J0 + NJ - 1 of the chunk at q0: scores, softmax and
+    // output. A chunk of more than three blocks runs in two such groups, so
+    // the scores of at most three blocks are live at once (at five, the
+    // 80-query chunk of a 68-token row held 148 registers, three waves per
+    // SIMD, and a 512-row pass's 4,096 workgroups took a second round).
+    auto blocks_of = [&]<int J0, int NJ>(int q0) {
+        // This lane's query operands: dims 4g .. 4g+3 of query q0 + 16 (J0 + j) + l16.
+        f32x4 qf[NJ];
 #pragma unroll
-        for (int j = 0; j < QB; ++j) {
-            const int row = q0 + 16 * j + l16;
+        for (int j = 0; j < NJ; ++j) {
+            const int row = q0 + 16 * (J0 + j) + l16;
             f32x4 q = {0.f, 0.f, 0.f, 0.f};
             if (row < p.q_rows) {
                 const float *src = qb + (long long)row * p.q_row;
@@ -1659,13 +1666,13 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
             qf[j] = q * scale;
         }
         // Scores S^T for every key block.
-        f32x4 s[QB][KB];
+        f32x4 s[NJ][KB];
 #pragma unroll
         for (int b = 0; b < KB; ++b) {
             if (b < kblocks) {
-                const f32x4 kf = *reinterpret_cast<const f32x4 *>(&Ks[(16 * b + l16) * kShortKStride + 4 * g]);
+                const f32x4 kf = *reinterpret_cast<const f32x4 *>(&Ks[(16 * b + l16) * KSTRIDE + 4 * g]);
 #pragma unroll
-                for (int j = 0; j < QB; ++j) {
+                for (int j = 0; j < NJ; ++j) {
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int st = 0; st < 4; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[j][st], acc, 0, 0, 0);
@@ -1673,7 +1680,7 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < QB; ++j) s[j][b] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                for (int j = 0; j < NJ; ++j) s[j][b] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             }
         }
         if (kv < kblocks * 16) {
@@ -1685,13 +1692,13 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
                 for (int r = 0; r < 4; ++r)
                     if (16 * bb + 4 * g + r >= kv)
 #pragma unroll
-                        for (int j = 0; j < QB; ++j) s[j][bb][r] = -INFINITY;
+                        for (int j = 0; j < NJ; ++j) s[j][bb][r] = -INFINITY;
             }
         }
         // Exact softmax per query: lanes l16, l16 + 16, l16 + 32, l16 + 48 share a query.
-        float inv[QB];
+        float inv[NJ];
 #pragma unroll
-        for (int j = 0; j < QB; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             float m = -INFINITY;
 #pragma unroll
             for (int b = 0; b < KB; ++b)
@@ -1714,24 +1721,35 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
             inv[j] = 1.0f / l;
         }
         // O^T = V^T P^T.
-        f32x4 o[QB];
+        f32x4 o[NJ];
 #pragma unroll
-        for (int j = 0; j < QB; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int b = 0; b < KB; ++b) {
             if (b < kblocks) {
                 const f32x4 vf = *reinterpret_cast<const f32x4 *>(&Vt[l16 * VSTRIDE + 16 * b + 4 * g]);
 #pragma unroll
-                for (int j = 0; j < QB; ++j)
+                for (int j = 0; j < NJ; ++j)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[i], s[j][b][i], o[j], 0, 0, 0);
             }
         }
-        // Lane l holds O[query q0 + 16 j + l16][dims 4g .. 4g+3].
+        // Lane l holds O[query q0 + 16 (J0 + j) + l16][dims 4g .. 4g+3].
 #pragma unroll
-        for (int j = 0; j < QB; ++j) {
-            const int row = q0 + 16 * j + l16;
+        for (int j = 0; j < NJ; ++j) {
+            const int row = q0 + 16 * (J0 + j) + l16;
             if (row < p.q_rows) *reinterpret_cast<f32x4 *>(ob + (long long)row * p.o_row + 4 * g) = o[j] * inv[j];
+        }
+    };
+    const int chunks = (p.q_rows + 16 * QB - 1) / (16 * QB);
+    for (int c = c_first; c < chunks; c += c_step) {
+        const int q0 = c * 16 * QB;
+        if constexpr (QB <= 3) {
+            blocks_of.template operator()<0, QB>(q0);
+        } else {
+            constexpr int kFirst = (QB + 1) / 2;
+            blocks_of.template operator()<0, kFirst>(q0);
+            blocks_of.template operator()<kFirst, QB - kFirst>(q0);
         }
     }
 }
