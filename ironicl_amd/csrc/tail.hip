@@ -18,9 +18,11 @@
 // The weights are packed once (tail128_pack) into A-operand fragments, 1 KB
 // per 16 x 16 block, lane after lane, in the order the kernel consumes them:
 // ten 32 KB chunks (Wo in two, then per 32-unit slice of the hidden layer the
-// W1 rows and W2 columns it touches). A workgroup streams the chunks through
-// two LDS buffers with direct global -> LDS loads; every LDS read is one
-// 16-byte read per lane of consecutive addresses (no bank conflicts).
+// W1 rows and W2 columns it touches). A workgroup streams each chunk as two
+// 16 KB halves (out-projection k-blocks, or a slice's W1 rows then its W2
+// columns) through two 16 KB LDS buffers with direct global -> LDS loads, so
+// three workgroups share a CU; every LDS read is one 16-byte read per lane
+// of consecutive addresses (no bank conflicts).
 #include "common.hpp"
 
 #include <algorithm>
@@ -31,8 +33,12 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kChunkFloats = 8192;  // 32 KB
+constexpr int kChunkFloats = 8192;  // 32 KB: the packing unit
 constexpr int kChunks = 10;
+// Chunks stream through LDS in halves of 16 KB (two 16 KB buffers), so a
+// workgroup takes 32 KB and three fit a CU.
+constexpr int kHalfFloats = kChunkFloats / 2;
+constexpr int kHalves = 2 * kChunks;
 constexpr int kTailWaves = 4;
 constexpr int kTailRows = 16 * kTailWaves;  // rows per workgroup
 
@@ -47,8 +53,8 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, const f32x4 &acc) {
 
 __device__ __forceinline__ f32x4 lds4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
 
-__global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
-    __shared__ __attribute__((aligned(16))) float buf[2][kChunkFloats];
+__global__ __launch_bounds__(256, 3) void tail128_kernel(Tail128 p) {
+    __shared__ __attribute__((aligned(16))) float buf[2][kHalfFloats];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m16 = lane & 15, g = lane >> 4;
@@ -56,14 +62,23 @@ __global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
     const bool live = row < p.m;
     const long long r = live ? row : p.m - 1;
 
-    // Wave w moves 1 KB blocks 8 w .. 8 w + 7 of each chunk.
-    auto issue = [&](int chunk, int b) {
-        const float *src = p.pack + (long long)chunk * kChunkFloats + (8 * wv) * 256 + lane * 4;
+    // Half-chunk hc (16 KB) goes to buffer hc % 2; wave w moves its 1 KB
+    // blocks 4 w .. 4 w + 3.
+    auto issue = [&](int hc) {
+        const float *src = p.pack + (long long)hc * kHalfFloats + (4 * wv) * 256 + lane * 4;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_global_load_lds(src + i * 256, (lds_void *)&buf[b][(8 * wv + i) * 256], 16, 0, 0);
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(src + i * 256, (lds_void *)&buf[hc & 1][(4 * wv + i) * 256], 16, 0, 0);
     };
-    issue(0, 0);
+    // Before half-chunk hc is read: its loads done, every wave past the
+    // previous one (whose buffer the next half-chunk then overwrites).
+    auto next = [&](int hc) {
+        wait_vm();
+        __syncthreads();
+        if (hc + 1 < kHalves) issue(hc + 1);
+        return &buf[hc & 1][lane * 4];
+    };
+    issue(0);
 
     // x: row m's features 16 kb + 4 g + e (att now, LN2(s1) later).
     f32x4 x[8], s1[8], acc[8];
@@ -76,29 +91,26 @@ __global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
 #pragma unroll
     for (int b = 0; b < 8; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Out-projection: chunks 0 and 1 hold k-blocks 4c .. 4c + 3, each with
-    // the eight output blocks' fragments. The fragments of the next k-block
-    // are read while the current one's 32 products (8 independent
+    // Out-projection: half-chunks 0 .. 3 hold k-blocks 2 hc and 2 hc + 1,
+    // each with the eight output blocks' fragments. The second k-block's
+    // fragments are read while the first one's 32 products (8 independent
     // accumulators) run.
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        wait_vm();
-        __syncthreads();
-        issue(c + 1, (c + 1) & 1);
-        const float *frag = &buf[c & 1][lane * 4];
+    for (int hc = 0; hc < 4; ++hc) {
+        const float *frag = next(hc);
         f32x4 fa[2][8];
 #pragma unroll
         for (int ob = 0; ob < 8; ++ob) fa[0][ob] = lds4(frag + ob * 256);
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            if (kb < 3) {
+        for (int kb = 0; kb < 2; ++kb) {
+            if (kb == 0) {
 #pragma unroll
-                for (int ob = 0; ob < 8; ++ob) fa[(kb + 1) & 1][ob] = lds4(frag + ((kb + 1) * 8 + ob) * 256);
+                for (int ob = 0; ob < 8; ++ob) fa[1][ob] = lds4(frag + (8 + ob) * 256);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(fa[kb & 1][ob][e], x[4 * c + kb][e], acc[ob]);
+                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(fa[kb][ob][e], x[2 * hc + kb][e], acc[ob]);
         }
     }
 
@@ -137,15 +149,13 @@ __global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
         acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // FFN, 32 hidden units per chunk: h = gelu(W1 x + b1) for units 32 c + 16 hb
-    // + 4 g + e (even and odd k-blocks in separate accumulators, four
-    // independent chains), then acc += W2 h.
+    // FFN, 32 hidden units per slice c: h = gelu(W1 x + b1) for units 32 c +
+    // 16 hb + 4 g + e from half-chunk 4 + 2 c (even and odd k-blocks in
+    // separate accumulators, four independent chains), then acc += W2 h from
+    // half-chunk 5 + 2 c.
 #pragma unroll 1
     for (int c = 0; c < 8; ++c) {
-        wait_vm();
-        __syncthreads();
-        if (c + 3 < kChunks) issue(c + 3, (c + 3) & 1);
-        const float *frag = &buf[c & 1][lane * 4];
+        const float *frag = next(4 + 2 * c);
         f32x4 h[2][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i) h[i >> 1][i & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -162,9 +172,6 @@ __global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
 #pragma unroll
                 for (int hb = 0; hb < 2; ++hb) h[hb][kb & 1] = mfma(fw[kb & 1][hb][e], x[kb][e], h[hb][kb & 1]);
         }
-        f32x4 f2[2][8];
-#pragma unroll
-        for (int ob = 0; ob < 8; ++ob) f2[0][ob] = lds4(frag + 4096 + ob * 256);
         f32x4 hg[2];
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) {
@@ -172,8 +179,12 @@ __global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) hg[hb][e] = gelu_erf((h[hb][0][e] + h[hb][1][e]) + b1[e]);
         }
+        const float *frag2 = next(5 + 2 * c);
+        f32x4 f2[2][8];
 #pragma unroll
-        for (int ob = 0; ob < 8; ++ob) f2[1][ob] = lds4(frag + 4096 + (8 + ob) * 256);
+        for (int ob = 0; ob < 8; ++ob) f2[0][ob] = lds4(frag2 + ob * 256);
+#pragma unroll
+        for (int ob = 0; ob < 8; ++ob) f2[1][ob] = lds4(frag2 + (8 + ob) * 256);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -198,23 +209,26 @@ __global__ __launch_bounds__(256, 2) void tail128_kernel(Tail128 p) {
 // written row-major; the same per-wave layout as tail128, the fragments of W
 // in (k-block, output block) order streamed through the same LDS buffers.
 template <int NB>
-__global__ __launch_bounds__(256, 2) void head128_kernel(Head128 p) {
-    __shared__ __attribute__((aligned(16))) float buf[2][kChunkFloats];
-    constexpr int kFrags = 8 * NB, kHeadChunks = (kFrags + 31) / 32;
+__global__ __launch_bounds__(256, 3) void head128_kernel(Head128 p) {
+    // 16 KB halves of the packed chunks, as tail128 streams them: 32 KB of LDS
+    // per workgroup, so three (four at 8 and 16 output blocks, whose
+    // registers allow it) share a CU.
+    __shared__ __attribute__((aligned(16))) float buf[2][kHalfFloats];
+    constexpr int kFrags = 8 * NB, kHeadHalves = (kFrags + 15) / 16;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m16 = lane & 15, g = lane >> 4;
     const long long row = (long long)blockIdx.x * kTailRows + wv * 16 + m16;
     const bool live = row < p.m;
     const long long r = live ? row : p.m - 1;
-    auto issue = [&](int chunk, int b) {
-        // A short last chunk still moves 32 KB: the pack is padded to whole chunks.
-        const float *src = p.pack + (long long)chunk * kChunkFloats + (8 * wv) * 256 + lane * 4;
+    auto issue = [&](int hc) {
+        // A short last half still moves 16 KB: the pack is padded to whole chunks.
+        const float *src = p.pack + (long long)hc * kHalfFloats + (4 * wv) * 256 + lane * 4;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_global_load_lds(src + i * 256, (lds_void *)&buf[b][(8 * wv + i) * 256], 16, 0, 0);
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(src + i * 256, (lds_void *)&buf[hc & 1][(4 * wv + i) * 256], 16, 0, 0);
     };
-    issue(0, 0);
+    issue(0);
 
     f32x4 x[8];
     const float *xr = p.x + r * p.ldx + 4 * g;
@@ -250,14 +264,14 @@ __global__ __launch_bounds__(256, 2) void head128_kernel(Head128 p) {
 #pragma unroll
     for (int ob = 0; ob < NB; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < kHeadChunks; ++c) {
+    for (int c = 0; c < kHeadHalves; ++c) {
         wait_vm();
         __syncthreads();
-        if (c + 1 < kHeadChunks) issue(c + 1, (c + 1) & 1);
+        if (c + 1 < kHeadHalves) issue(c + 1);
         const float *frag = &buf[c & 1][lane * 4];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int f = 32 * c + i;
+        for (int i = 0; i < 16; ++i) {
+            const int f = 16 * c + i;
             if (f < kFrags) {
                 const int kb = f / NB, ob = f % NB;
                 const f32x4 a = lds4(frag + i * 256);
