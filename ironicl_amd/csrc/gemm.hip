@@ -26,7 +26,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 32;
-constexpr int kLdsStride = 36;
+// Workgroups per CU of the 128 x 128 tiles with 32-deep K steps (73.7 KB of
+// LDS) and with 16-deep ones (40 KB, 128 registers).
+constexpr long long kDeepPerCu = 2, kShallowPerCu = 4;
 
 __device__ __forceinline__ long long col_offset(const OutMap &o, int n) {
     int seg = n / o.col_seg;
@@ -103,12 +105,13 @@ __device__ __forceinline__ void store_rows(const GemmArgs &p, int row0, int col,
 // (BM/2) x (BN/2)), K in 32-deep steps through double-buffered LDS. Within a
 // step lanes 0-31 feed k = 0..15 and lanes 32-63 k = 16..31, one k from each
 // half per MFMA, so a lane reads its 16 operands as four 16-byte LDS loads.
-template <int BM, int BN, int EPI, bool GROUPED>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
+template <int BM, int BN, int EPI, bool GROUPED, int BK = kBK>
+__global__ __launch_bounds__(256, BK == 16 ? 3 : 2) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
     constexpr int MI = BM / 64, NI = BN / 64;
-    constexpr int A_LOADS = BM * kBK / 4 / 256, B_LOADS = BN * kBK / 4 / 256;
-    __shared__ __attribute__((aligned(16))) float As[2][BM * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BN * kLdsStride];
+    constexpr int STRIDE = BK + 4, KQ = BK / 8;  // LDS row floats; 16-byte operand loads per lane and block
+    constexpr int A_LOADS = BM * BK / 4 / 256, B_LOADS = BN * BK / 4 / 256;
+    __shared__ __attribute__((aligned(16))) float As[2][BM * STRIDE];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BN * STRIDE];
 
     const int bid = blockIdx.x;
     const int tile = (bid % 8) * per_xcd + bid / 8;
@@ -124,17 +127,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, i
     int a_lds[A_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-        int idx = tid + 256 * i, row = idx >> 3, k4 = idx & 7;
+        int idx = tid + 256 * i, row = idx / (BK / 4), k4 = idx % (BK / 4);
         a_src[i] = p.a + (long long)min(m0 + row, p.m - 1) * p.lda + k4 * 4;
-        a_lds[i] = row * kLdsStride + k4 * 4;
+        a_lds[i] = row * STRIDE + k4 * 4;
     }
     const float *b_src[B_LOADS];
     int b_lds[B_LOADS];
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-        int idx = tid + 256 * i, row = idx >> 3, k4 = idx & 7;
+        int idx = tid + 256 * i, row = idx / (BK / 4), k4 = idx % (BK / 4);
         b_src[i] = p.w + (long long)min(n0 + row, p.n - 1) * p.k + k4 * 4;
-        b_lds[i] = row * kLdsStride + k4 * 4;
+        b_lds[i] = row * STRIDE + k4 * 4;
     }
     f32x4 a_reg[A_LOADS], b_reg[B_LOADS];
     auto load_tile = [&](int k0) {
@@ -158,29 +161,29 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs p, int tiles_m, i
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int ktiles = p.k / kBK;
+    const int ktiles = p.k / BK;
     load_tile(0);
     store_tile(0);
     __syncthreads();
-    const int a_row = (wm * (BM / 2) + r32) * kLdsStride + 16 * half;
-    const int b_row = (wn * (BN / 2) + r32) * kLdsStride + 16 * half;
+    const int a_row = (wm * (BM / 2) + r32) * STRIDE + (BK / 2) * half;
+    const int b_row = (wn * (BN / 2) + r32) * STRIDE + (BK / 2) * half;
     for (int kt = 0; kt < ktiles; ++kt) {
         const int buf = kt & 1;
         const bool more = kt + 1 < ktiles;
-        if (more) load_tile((kt + 1) * kBK);
-        f32x4 af[MI][4], bf[NI][4];
+        if (more) load_tile((kt + 1) * BK);
+        f32x4 af[MI][KQ], bf[NI][KQ];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                af[i][c] = *reinterpret_cast<const f32x4 *>(&As[buf][a_row + i * 32 * kLdsStride + 4 * c]);
+            for (int c = 0; c < KQ; ++c)
+                af[i][c] = *reinterpret_cast<const f32x4 *>(&As[buf][a_row + i * 32 * STRIDE + 4 * c]);
 #pragma unroll
         for (int j = 0; j < NI; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                bf[j][c] = *reinterpret_cast<const f32x4 *>(&Bs[buf][b_row + j * 32 * kLdsStride + 4 * c]);
+            for (int c = 0; c < KQ; ++c)
+                bf[j][c] = *reinterpret_cast<const f32x4 *>(&Bs[buf][b_row + j * 32 * STRIDE + 4 * c]);
 #pragma unroll
-        for (int t = 0; t < 16; ++t)
+        for (int t = 0; t < 4 * KQ; ++t)
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -348,11 +351,11 @@ void dispatch_epilogue(const GemmArgs &args, dim3 grid, hipStream_t stream, int 
     fail(3, "gemm: unknown epilogue");
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int BK>
 struct Tiled {
     template <int E, bool G>
     struct K {
-        static constexpr auto kernel = gemm_kernel<BM, BN, E, G>;
+        static constexpr auto kernel = gemm_kernel<BM, BN, E, G, BK>;
     };
 };
 
@@ -361,11 +364,11 @@ struct SplitK {
     static constexpr auto kernel = gemm_splitk_kernel<E, G>;
 };
 
-template <int BM, int BN>
+template <int BM, int BN, int BK = kBK>
 void launch(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, BM), tiles_n = (int)ceil_div(args.n, BN);
     int per_xcd = (tiles_m * tiles_n + 7) / 8;
-    dispatch_epilogue<Tiled<BM, BN>::template K>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
+    dispatch_epilogue<Tiled<BM, BN, BK>::template K>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
 }
 
 void launch_splitk(const GemmArgs &args, hipStream_t stream) {
@@ -392,15 +395,26 @@ void gemm(const GemmArgs &args, hipStream_t stream) {
     if (small_tiles < 256) {
         launch_splitk(args, stream);
     } else if (big_tiles >= 1024 || (args.epilogue == kEpiGelu && big_tiles >= 512)) {
-        // 128 x 128 tiles run in rounds of two per CU. When the last round
-        // would be mostly empty (the build's 50,000-row products: 1,564 tiles
-        // at N = 512 are 3.05 rounds of 512), the whole rounds take the first
-        // rows and the rows left over run as 64 x 64 tiles, a quarter of the
-        // work each, spread over the chip.
-        const long long slots = 2LL * device_compute_units();
+        // 128 x 128 tiles: 16-deep K steps (40 KB of LDS, 128 registers: four
+        // workgroups per CU) when there are at least two such rounds of
+        // tiles, else 32-deep steps at two per CU (the 50,000-row build's
+        // products: N = 1,024 and 1,536 take the first, N = 512 the second,
+        // whose 1,564 tiles are 1.5 rounds of four per CU). When the last
+        // round would be mostly empty (at N = 512: 3.05 rounds of two per CU)
+        // the whole rounds take the first rows and the rows left over run as
+        // 64 x 64 tiles, a quarter of the work each, spread over the chip.
+        const long long cus = device_compute_units();
+        const bool deep = big_tiles < 2 * kShallowPerCu * cus;
+        const long long slots = (deep ? kDeepPerCu : kShallowPerCu) * cus;
         const long long tiles_n = ceil_div(args.n, 128);
         const long long main_tm = big_tiles / slots * slots / tiles_n;
         const bool plain_rows = args.out.rows_per_group >= args.m && args.epilogue != kEpiQass;
+        auto big = [&](const GemmArgs &a) {
+            if (deep)
+                launch<128, 128, 32>(a, stream);
+            else
+                launch<128, 128, 16>(a, stream);
+        };
         if (plain_rows && big_tiles % slots < slots / 2 && main_tm > 0 && main_tm * 128 < args.m) {
             GemmArgs head = args, rest = args;
             const long long rows = main_tm * 128;
@@ -409,10 +423,10 @@ void gemm(const GemmArgs &args, hipStream_t stream) {
             rest.a = args.a + rows * args.lda;
             rest.c = args.c + rows * args.out.ldc;
             if (args.residual) rest.residual = args.residual + rows * args.ldr;
-            launch<128, 128>(head, stream);
+            big(head);
             launch<64, 64>(rest, stream);
         } else {
-            launch<128, 128>(args, stream);
+            big(args);
         }
     } else {
         launch<64, 64>(args, stream);

@@ -65,10 +65,11 @@ def test_products_match_float64(device, m, n, k, n2):
 
 
 def test_large_products_with_a_split_last_round(device):
-    """70,000 rows: 2,188 tiles of 128 x 128 are 4.3 rounds of two per CU on
-    256 CUs, so both products (GELU, then residual) run the first 65,536 rows
-    as whole rounds and the 4,464 rows after them as 64 x 64 tiles. Rows on
-    both sides of that boundary and the last rows against float64."""
+    """70,000 rows: 2,188 tiles of 128 x 128 fill whole rounds on 256 CUs up to
+    row 65,536 (two rounds of four workgroups per CU, or four of two), so both
+    products (GELU, then residual) run those rows as 128 x 128 tiles and the
+    4,464 rows after them as 64 x 64 tiles. Rows on both sides of that
+    boundary and the last rows against float64."""
     m, n, k = 70_000, 512, 512
     x = fast_values(m * k, 11)
     w1, b1 = fast_values(n * k, 12, 0.05), fast_values(n, 13)
