@@ -600,13 +600,18 @@ def bench_workload(name: str, args) -> dict:
 def profile_leg(args) -> dict:
     """The kernels of the headline's prediction alone, for a profiler's
     per-kernel statistics: one build, then single-stream prediction steps (or
-    small passes) with inputs in HBM, every pass launched kernel by kernel."""
+    small passes) with inputs in HBM, every pass launched kernel by kernel;
+    or ("build") `warmup` untimed builds, then `steps` timed builds."""
     from ironicl_amd import hip, hipmem, synthetic, tabicl
 
     w = synthetic.WORKLOADS[WORKLOAD]
     x, y, xt, _ = synthetic.workload_data(w)
     q = xt.shape[1]
     executor = tabicl.Executor("classifier", synthetic.random_weights("classifier"), hip.Device(0))
+    if args.profile_leg == "build":
+        stats = latency_stats(timed_calls(lambda: executor.build_context(x, y), args.warmup, args.steps))
+        log(f"profile leg: build p50 {stats['p50_ms']:.1f} ms")
+        return {"profile_leg": "build", "steps": args.steps, "build": stats}
     ctx = executor.build_context(x, y)
     ctx.set_pass_rows(args.pass_rows)
     ctx.set_streams(1)
@@ -643,10 +648,10 @@ def main() -> int:
     ap.add_argument("--workload", default=WORKLOAD,
                     help="clf-50k (default, the full report) or another configuration at full size: clf-1k, "
                          "clf-10k, reg-20k, clf-200k (build, rows/s, build kernels, oracle parity on samples)")
-    ap.add_argument("--profile-leg", choices=["predict", "small"], default=None,
+    ap.add_argument("--profile-leg", choices=["predict", "small", "build"], default=None,
                     help="only the leg a profiler reads: one build, then --steps single-stream prediction steps "
                          "of the 4,096 rows (predict) or passes of 1, 8, 16 and 32 rows (small), kernels launched "
-                         "one by one")
+                         "one by one; or --warmup untimed then --steps timed builds (build)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel over BYTES (reference for traffic counters)")
     args = ap.parse_args()

@@ -150,6 +150,13 @@ typedef struct irx_build_inputs {
     size_t budget;                     /* device bytes the build may use */
     irx_progress_fn progress;          /* may be NULL */
     void *progress_user;
+    /* No counterpart in the reference's BuildInputs: [B, N] targets (a
+     * classifier's class indices 0..9 as floats, a regressor's targets), or
+     * NULL. When column_labels and icl_labels are both NULL, the device
+     * computes those embeddings from the targets through the uploaded
+     * y_encoder weights, bitwise as target_embeddings (cpu.rs:1658-1680) does
+     * on the host, instead of receiving 640 floats per training row. */
+    const float *targets;
 } irx_build_inputs;
 
 /* BuildOutputs (build.rs:66-74), host buffers owned by the caller. A NULL

@@ -342,6 +342,11 @@ void build_rows(const float *state, int b, int rows, int h, const float *cls, fl
                 hipStream_t stream);
 void gather_cls(const float *seq, long long seqs, int len, float *cls, hipStream_t stream);
 void add_inplace(float *y, const float *x, long long count, hipStream_t stream);
+// Label embeddings [n, width] of targets [n] from a y_encoder's weight [width,
+// classes] and bias [width]: column `class` + bias (classifier), or target *
+// weight + bias (regressor, classes = 1).
+void label_embeddings(const float *targets, long long n, const float *w, const float *b, int classes, int width,
+                      bool classifier, float *out, hipStream_t stream);
 void repeat_rows(const float *src, long long src_floats, long long copies, float *dst,
                  hipStream_t stream);
 void count_nonfinite(const float *x, long long count, unsigned *counter, hipStream_t stream);

@@ -169,6 +169,31 @@ __global__ __launch_bounds__(256) void gather_cls_kernel(const float *seq, long 
     }
 }
 
+// Label embeddings [n, width] from targets [n] (target_embeddings,
+// cpu.rs:1658-1680): a classifier's row takes column `class` of w [width,
+// classes] plus the bias, one FP32 sum; a regressor's is target * w[:, 0] +
+// bias with both roundings (never a fused multiply-add), as the reference's
+// loop computes it. Classes outside 0 .. classes - 1 are clamped (the host
+// validates labels first).
+__global__ __launch_bounds__(256) void label_embedding_kernel(const float *targets, long long n, const float *w,
+                                                              const float *b, int classes, int width,
+                                                              bool classifier, float *out) {
+    const long long count = n * width;
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long long)gridDim.x * 256) {
+        const long long row = idx / width;
+        const int c = (int)(idx - row * width);
+        const float t = targets[row];
+        float v;
+        if (classifier) {
+            const int k = min(max((int)t, 0), classes - 1);
+            v = __fadd_rn(w[(long long)c * classes + k], b[c]);
+        } else {
+            v = __fadd_rn(__fmul_rn(t, w[c]), b[c]);
+        }
+        out[idx] = v;
+    }
+}
+
 __global__ __launch_bounds__(256) void add_kernel(float *y, const float *x, long long count) {
     for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long long)gridDim.x * 256)
         y[idx] += x[idx];
@@ -259,6 +284,16 @@ void gather_cls(const float *seq, long long seqs, int len, float *cls, hipStream
     if (total <= 0) return;
     KernelTimer timer(kFamGlue, stream, 0.0, 8.0 * total);
     hipLaunchKernelGGL(gather_cls_kernel, grid_1d(total), dim3(256), 0, stream, seq, seqs, len, cls);
+    IRX_HIP(hipGetLastError());
+}
+
+void label_embeddings(const float *targets, long long n, const float *w, const float *b, int classes, int width,
+                      bool classifier, float *out, hipStream_t stream) {
+    if (n <= 0) return;
+    const long long count = n * width;
+    KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * (n + count));
+    hipLaunchKernelGGL(label_embedding_kernel, grid_1d(count), dim3(256), 0, stream, targets, n, w, b, classes, width,
+                       classifier, out);
     IRX_HIP(hipGetLastError());
 }
 

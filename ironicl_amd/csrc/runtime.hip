@@ -351,6 +351,10 @@ struct irx_weights {
     const float *cls = nullptr, *out_ln_w = nullptr, *out_ln_b = nullptr;
     const float *ln_w = nullptr, *ln_b = nullptr;
     Lin dec0, dec2;
+    // Label encoders (y_encoder) of the column and ICL stages, for builds
+    // given targets: weight [width, classes] (1 column for the regressor).
+    Lin ycol, yicl;
+    int classes = 0;
     std::vector<float> freqs_host;
 };
 
@@ -747,6 +751,12 @@ void weights_load(irx_weights *W, irx_tensor_lookup lookup, void *user) {
     const size_t width = W->width;
     L.take("icl_predictor.decoder.2.weight", width * 1024, &W->dec2.w);
     L.take("icl_predictor.decoder.2.bias", width, &W->dec2.b);
+    // y_encoder inputs: the classifier's 10 classes one-hot, the regressor's target (model.rs:777-836).
+    W->classes = W->task == IRX_TASK_CLASSIFIER ? 10 : 1;
+    L.take("col_embedder.y_encoder.weight", 128 * (size_t)W->classes, &W->ycol.w);
+    L.take("col_embedder.y_encoder.bias", 128, &W->ycol.b);
+    L.take("icl_predictor.y_encoder.weight", 512 * (size_t)W->classes, &W->yicl.w);
+    L.take("icl_predictor.y_encoder.bias", 512, &W->yicl.b);
     W->arena.alloc(L.host.size() * sizeof(float));
     IRX_HIP(hipMemcpy(W->arena.p, L.host.data(), L.host.size() * sizeof(float), hipMemcpyHostToDevice));
     W->bytes = W->arena.bytes;
@@ -868,7 +878,12 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     const irx_shape sh = in->shape;
     if (!shape_ok(&sh)) fail(IRX_INVALID_ARGUMENT, "build shape must be nonempty");
     if (sh.rows < 64) fail(IRX_DOES_NOT_FIT, "the device builds contexts of at least 64 training rows");
-    if (!in->x || !in->column_labels || !in->icl_labels || !in->rope_frequencies || !in->cls_tokens)
+    // Label embeddings come from the host (column_labels and icl_labels, as the
+    // reference's BuildInputs carry them) or, when both are null, from the
+    // targets through the resident y_encoder weights.
+    const bool device_labels = !in->column_labels && !in->icl_labels;
+    if (!in->x || (device_labels ? !in->targets : (!in->column_labels || !in->icl_labels)) || !in->rope_frequencies ||
+        !in->cls_tokens)
         fail(IRX_INVALID_ARGUMENT, "build inputs are missing");
     for (int i = 0; i < kColumnBlocks; ++i)
         if (!in->inducing_queries[i]) fail(IRX_INVALID_ARGUMENT, "inducing queries are missing");
@@ -938,6 +953,7 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     upload(d_cos, cos_t.data(), cos_t.size() * 4, s);
     upload(d_sin, sin_t.data(), sin_t.size() * 4, s);
     float *d_x = ws.take((size_t)N * H), *d_ylab = ws.take((size_t)N * 128), *d_yicl = ws.take((size_t)N * 512);
+    float *d_targets = device_labels ? ws.take((size_t)N) : nullptr;
     float *d_state = ws.take((size_t)H * N * 128);
     // Cached values that are not finite (in FP16 for the FP16 cache) are counted here.
     unsigned *counter = reinterpret_cast<unsigned *>(ws.take(64));
@@ -948,7 +964,14 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     for (int e = 0; e < B; ++e) {
         ws.used = mark;
         upload(d_x, in->x + (size_t)e * N * H, (size_t)N * H * 4, s);
-        upload(d_ylab, in->column_labels + (size_t)e * N * 128, (size_t)N * 128 * 4, s);
+        if (device_labels) {
+            const bool clf = W->task == IRX_TASK_CLASSIFIER;
+            upload(d_targets, in->targets + (size_t)e * N, (size_t)N * 4, s);
+            label_embeddings(d_targets, N, W->ycol.w, W->ycol.b, W->classes, 128, clf, d_ylab, s);
+            label_embeddings(d_targets, N, W->yicl.w, W->yicl.b, W->classes, 512, clf, d_yicl, s);
+        } else {
+            upload(d_ylab, in->column_labels + (size_t)e * N * 128, (size_t)N * 128 * 4, s);
+        }
         // Column stage, chunk by chunk of features (column_stream + isab, cpu.rs:1132-1207).
         {
             const size_t cmark = ws.used;
@@ -992,9 +1015,11 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
             }
             ws.used = cmark;
         }
-        if (e > 0) IRX_HIP(hipStreamWaitEvent(side.s, side.free, 0));
-        upload(d_yicl, in->icl_labels + (size_t)e * N * 512, (size_t)N * 512 * 4, side.s);
-        IRX_HIP(hipEventRecord(side.ready, side.s));
+        if (!device_labels) {
+            if (e > 0) IRX_HIP(hipStreamWaitEvent(side.s, side.free, 0));
+            upload(d_yicl, in->icl_labels + (size_t)e * N * 512, (size_t)N * 512 * 4, side.s);
+            IRX_HIP(hipEventRecord(side.ready, side.s));
+        }
         // Row stage in runs, into the ICL row states.
         float *rows = ws.take((size_t)N * 512);
         {
@@ -1011,9 +1036,9 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
             }
             ws.used = rmark;
         }
-        IRX_HIP(hipStreamWaitEvent(s, side.ready, 0));
+        if (!device_labels) IRX_HIP(hipStreamWaitEvent(s, side.ready, 0));
         add_inplace(rows, d_yicl, (long long)N * 512, s);
-        IRX_HIP(hipEventRecord(side.free, s));
+        if (!device_labels) IRX_HIP(hipEventRecord(side.free, s));
         // ICL stage: each block's K/V from the training rows, then their queries.
         {
             Stages::IclBuffers ib = Stages::icl_buffers(ws, N, 1, N, N, cus, f16);

@@ -40,7 +40,8 @@ class Shape(ctypes.Structure):
 class BuildInputs(ctypes.Structure):
     _fields_ = [("shape", Shape), ("x", _CF), ("column_labels", _CF), ("icl_labels", _CF),
                 ("inducing_queries", _CF * 3), ("base_scales", _CF * 12), ("rope_frequencies", _CF),
-                ("cls_tokens", _CF), ("budget", _sz), ("progress", PROGRESS), ("progress_user", ctypes.c_void_p)]
+                ("cls_tokens", _CF), ("budget", _sz), ("progress", PROGRESS), ("progress_user", ctypes.c_void_p),
+                ("targets", _CF)]
 
 
 class BuildOutputs(ctypes.Structure):

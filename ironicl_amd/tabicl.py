@@ -3,10 +3,12 @@ surface over the C ABI.
 
 This mirrors how src/models/tabicl_v2/cpu.rs drives its CUDA backend
 (``build_tensors_cuda`` cpu.rs:737-804, ``with_cuda`` cpu.rs:1855-1910,
-``predict_logits`` cpu.rs:2057-2108): the host embeds the labels, computes
-the QASSMax base scales and the column stage's inducing queries, hands every
-array to ``irx_build`` / ``irx_predictor_*`` and post-processes logits
-(probability aggregation, regression quantiles).
+``predict_logits`` cpu.rs:2057-2108): the host computes the QASSMax base
+scales and the column stage's inducing queries, hands every array to
+``irx_build`` / ``irx_predictor_*`` and post-processes logits (probability
+aggregation, regression quantiles). The label embeddings, which the
+reference's host computes, are computed by the device from the targets
+(``Executor.device_labels``).
 
 Nothing here computes the model on the CPU: rows the device flags for the
 CPU path (a grouped all-missing -100 triple) come back as NaN logits and are
@@ -91,6 +93,12 @@ class Prediction:
 class Executor:
     """An official TabICLv2 model with its weights resident on the GPU
     (Executor, cpu.rs:290-296; ModelWeights::new, cuda/weights.rs:299)."""
+
+    # Builds hand the device the [B, N] targets, which it embeds through its
+    # y_encoder weights (irx_build_inputs.targets). False: the host computes
+    # the [B, N, 128] and [B, N, 512] embeddings and uploads them, as the
+    # reference's BuildInputs carry them (the two give the same bits).
+    device_labels = True
 
     def __init__(self, task: str, weights: dict[str, np.ndarray], device: hip.Device | None = None,
                  source_sha256: str | None = None):
@@ -343,12 +351,18 @@ class Executor:
     def _build(self, x, y_train, meta: cf.Metadata, download: bool, progress, device_limit: int,
                precision: int = hip.PRECISION_FP32) -> "StaticExecutor":
         b, n, h = x.shape
-        col_labels, icl_labels = self.label_embeddings(y_train)
         ind_q, bases = self._row_count_constants(n)
         freqs, cls = self.rope_frequencies(), self.cls_tokens()
         inp = hip.BuildInputs()
         inp.shape = hip.Shape(b, h, n, self.width)
-        inp.x, inp.column_labels, inp.icl_labels = hip.fptr(x), hip.fptr(col_labels), hip.fptr(icl_labels)
+        inp.x = hip.fptr(x)
+        if self.device_labels:
+            # The device embeds the targets through its y_encoder weights.
+            targets = np.ascontiguousarray(y_train, np.float32)
+            inp.targets = hip.fptr(targets)
+        else:
+            col_labels, icl_labels = self.label_embeddings(y_train)
+            inp.column_labels, inp.icl_labels = hip.fptr(col_labels), hip.fptr(icl_labels)
         for i in range(3):
             inp.inducing_queries[i] = hip.fptr(ind_q[i])
         for i in range(12):

@@ -270,6 +270,29 @@ def test_regressor_quantiles(device, reg_weights):
         np.testing.assert_array_equal(g, want)
 
 
+@pytest.mark.parametrize("task", ["classifier", "regressor"])
+def test_device_label_embeddings_equal_the_host_ones(device, clf_weights, reg_weights, task):
+    """Builds from targets (the device embeds them through its y_encoder
+    weights) and from host-computed embeddings (the reference's BuildInputs)
+    give the same context and logits, bit for bit: an 8-estimator classifier
+    with class shifts and a regressor with real-valued targets."""
+    weights = clf_weights if task == "classifier" else reg_weights
+    ex = tabicl.Executor(task, weights, device)
+    w = S.WORKLOADS["clf-200k" if task == "classifier" else "reg-20k"]
+    x, y, xt, meta = S.workload_data(w, train_rows=700, test_rows=20, features=11)
+    perms = meta.get("class_permutations")
+    out = []
+    for device_labels in (True, False):
+        ex.device_labels = device_labels
+        st = ex.build_context(x, y, class_permutations=perms, download=True)
+        out.append((st.context, st.predict_logits(xt).logits))
+    (ctx_d, lg_d), (ctx_h, lg_h) = out
+    for part_d, part_h in zip(ctx_d, ctx_h):
+        for a, b in zip(part_d, part_h):
+            np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(lg_d, lg_h)
+
+
 def test_ensemble_with_feature_permutations(clf, clf_oracle):
     w = S.WORKLOADS["clf-200k"]
     x, y, xt, meta = S.workload_data(w, train_rows=200, test_rows=30, features=9)
