@@ -299,6 +299,61 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
     }
 }
 
+// Products of at most eight rows (passes of 1-8 rows: the ICL blocks'
+// out-projection and FFN down, the decoder's last layer). A workgroup stages
+// the rows in LDS once; each of its waves' four 16-lane groups takes one
+// output column, lane i of a group the floats 64j + 4i .. 64j + 4i + 3 of K
+// (so the group's weight loads and LDS reads are contiguous 256-byte runs),
+// with every weight load of the wave in flight before the products; the
+// group's 16 partial sums are reduced by shuffles and lane m writes row m.
+// At one row a launch is one round trip for its weights instead of
+// split-K's eight dependent steps.
+template <int M, int EPI, int KPL>  // KPL: K / 16 floats per lane
+__global__ __launch_bounds__(256) void gemm_rows_kernel(GemmArgs p) {
+    constexpr int K = 16 * KPL;
+    __shared__ __attribute__((aligned(16))) float xs[M * K];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = lane >> 4, i = lane & 15;
+    const int col = blockIdx.x * 16 + wave * 4 + grp;
+    const float *wr = p.w + (long long)min(col, p.n - 1) * K + 4 * i;
+    f32x4 w[KPL / 4];
+#pragma unroll
+    for (int j = 0; j < KPL / 4; ++j) w[j] = *reinterpret_cast<const f32x4 *>(wr + 64 * j);
+    for (int idx = tid; idx < M * K / 4; idx += 256) {
+        const int m = idx / (K / 4), k4 = idx - m * (K / 4);
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (m < p.m) v = *reinterpret_cast<const f32x4 *>(p.a + (long long)m * p.lda + 4 * k4);
+        *reinterpret_cast<f32x4 *>(&xs[m * K + 4 * k4]) = v;
+    }
+    __syncthreads();
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < KPL / 4; ++j) {
+            const f32x4 xv = *reinterpret_cast<const f32x4 *>(&xs[m * K + 64 * j + 4 * i]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a = fmaf(xv[e], w[j][e], a);
+        }
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) a += __shfl_xor(a, off, 16);
+        acc[m] = a;
+    }
+    if (col >= p.n) return;
+    const long long coff = col_offset(p.out, col);
+    const float bias = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        if (m == i && m < p.m) {
+            float v = acc[m] + bias;
+            if constexpr (EPI == kEpiGelu) v = gelu_erf(v);
+            if constexpr (EPI == kEpiResidual) v += p.residual[(long long)m * p.ldr + col];
+            p.c[(long long)m * p.out.ldc + coff] = v;
+        }
+    }
+}
+
 // Compute units of the current device, looked up once per device ordinal.
 int device_compute_units() {
     constexpr int kMaxDevices = 64;
@@ -371,6 +426,39 @@ void launch(const GemmArgs &args, hipStream_t stream) {
     dispatch_epilogue<Tiled<BM, BN, BK>::template K>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
 }
 
+// gemm_rows_kernel for m <= 8 rows and K = 128, 256, 512 or 1,024 (plain
+// epilogues, ungrouped rows); false when the shape is not one of those.
+bool launch_rows(const GemmArgs &args, hipStream_t stream) {
+    if (args.m > 8 || args.out.rows_per_group < args.m || (args.epilogue & kEpiQass)) return false;
+    const int m = args.m <= 1 ? 1 : args.m <= 2 ? 2 : args.m <= 4 ? 4 : 8;
+    const dim3 grid(ceil_div(args.n, 16)), block(256);
+    bool launched = false;
+    auto go = [&]<int M, int KPL>() {
+        if (m != M || args.k != 16 * KPL) return;
+        const Flops f = work(args);
+        KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
+        if (args.epilogue == kEpiNone)
+            hipLaunchKernelGGL((gemm_rows_kernel<M, kEpiNone, KPL>), grid, block, 0, stream, args);
+        else if (args.epilogue == kEpiGelu)
+            hipLaunchKernelGGL((gemm_rows_kernel<M, kEpiGelu, KPL>), grid, block, 0, stream, args);
+        else
+            hipLaunchKernelGGL((gemm_rows_kernel<M, kEpiResidual, KPL>), grid, block, 0, stream, args);
+        IRX_HIP(hipGetLastError());
+        launched = true;
+    };
+    auto each_k = [&]<int M>() {
+        go.template operator()<M, 8>();
+        go.template operator()<M, 16>();
+        go.template operator()<M, 32>();
+        go.template operator()<M, 64>();
+    };
+    each_k.template operator()<1>();
+    each_k.template operator()<2>();
+    each_k.template operator()<4>();
+    each_k.template operator()<8>();
+    return launched;
+}
+
 void launch_splitk(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, 32), tiles_n = (int)ceil_div(args.n, 32);
     int per_xcd = (tiles_m * tiles_n + 7) / 8;
@@ -393,7 +481,7 @@ void gemm(const GemmArgs &args, hipStream_t stream) {
     const long long small_tiles = (long long)ceil_div(args.m, 64) * ceil_div(args.n, 64);
     const long long big_tiles = (long long)ceil_div(args.m, 128) * ceil_div(args.n, 128);
     if (small_tiles < 256) {
-        launch_splitk(args, stream);
+        if (!launch_rows(args, stream)) launch_splitk(args, stream);
     } else if (big_tiles >= 1024 || (args.epilogue == kEpiGelu && big_tiles >= 512)) {
         // 128 x 128 tiles: 16-deep K steps (40 KB of LDS, 128 registers: four
         // workgroups per CU) when there are at least two such rounds of

@@ -12,6 +12,7 @@
 //            cpu.rs:3798-3853; qassmax_f32, reference.rs:417-428).
 // It replaces, per ICL block of a prediction pass, LayerNorm + Q projection +
 // two QASS products (four launches), and LayerNorm + FFN up (two launches).
+// Passes of at most eight rows take ln_rows512_kernel instead.
 //
 // A workgroup of four waves computes 16 rows x 64 columns; wave w reduces over
 // K = 128 w .. 128 w + 127 on v_mfma_f32_16x16x4f32 with the product
@@ -154,6 +155,142 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
     }
 }
 
+// Passes of at most eight rows (M = 1, 2, 4 or 8 after rounding up). The
+// 16-row MFMA tiles above would spend 128 serial MFMAs per wave on one or two
+// real rows; here every weight load is issued first, the rows' LayerNorms
+// are taken under those loads (row r by wave r % waves, two-pass statistics
+// over a wave's 64 lanes) and staged in LDS, and each 16-lane group owns one
+// output column: lane i multiplies K floats 64 j + 4 i .. 64 j + 4 i + 3 and
+// the group's partial sums are reduced by shuffles. kLnGelu: 16 columns per
+// 256-thread workgroup, lane m of a group writes row m. kLnQass: a
+// 1,024-thread workgroup per head, whose 64 groups then take the head's
+// query MLP the same way (one column of h, then of g, per group, K = 64 over
+// the group's lanes) through LDS.
+template <int M, int EPI>
+__global__ __launch_bounds__(EPI == kLnQass ? 1024 : 256) void ln_rows512_kernel(LnLinear p) {
+    constexpr int kThreads = EPI == kLnQass ? 1024 : 256, kCols = kThreads / 16, kWaves = kThreads / 64;
+    __shared__ __attribute__((aligned(16))) float xs[M * 512];
+    __shared__ __attribute__((aligned(16))) float qh[EPI == kLnQass ? 2 : 1][M][64];  // QASS: q, then h
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 15, c = tid >> 4;
+    const int col = blockIdx.x * kCols + c;
+
+    const float *wr = p.w + (long long)min(col, p.n - 1) * 512 + 4 * i;
+    f32x4 w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = *reinterpret_cast<const f32x4 *>(wr + 64 * j);
+    f32x4 m0w, m2w;
+    if constexpr (EPI == kLnQass) {
+        m0w = *reinterpret_cast<const f32x4 *>(p.qm0w + c * 64 + 4 * i);
+        m2w = *reinterpret_cast<const f32x4 *>(p.qm2w + c * 64 + 4 * i);
+    }
+
+    for (int r = wave; r < M; r += kWaves) {
+        f32x4 *dst = reinterpret_cast<f32x4 *>(&xs[r * 512]);
+        if (r >= p.m) {
+            dst[lane] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dst[64 + lane] = f32x4{0.f, 0.f, 0.f, 0.f};
+            continue;
+        }
+        const float *xr = p.x + (long long)r * p.ldx;
+        f32x4 v[2] = {*reinterpret_cast<const f32x4 *>(xr + 4 * lane),
+                      *reinterpret_cast<const f32x4 *>(xr + 256 + 4 * lane)};
+        float s = ((v[0][0] + v[0][1]) + (v[0][2] + v[0][3])) + ((v[1][0] + v[1][1]) + (v[1][2] + v[1][3]));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+        const float mean = s / 512.f;
+        float sq = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = v[h][e] - mean;
+                sq = fmaf(d, d, sq);
+            }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
+        const float rstd = 1.0f / sqrtf(sq / 512.f + 1e-5f);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const f32x4 lw = *reinterpret_cast<const f32x4 *>(p.lnw + 256 * h + 4 * lane);
+            const f32x4 lb = *reinterpret_cast<const f32x4 *>(p.lnb + 256 * h + 4 * lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[h][e] = (v[h][e] - mean) * rstd * lw[e] + lb[e];
+            dst[64 * h + lane] = v[h];
+        }
+    }
+    __syncthreads();
+
+    // acc[m]: row m of this group's column, identical in all 16 lanes.
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const f32x4 xv = *reinterpret_cast<const f32x4 *>(&xs[m * 512 + 64 * j + 4 * i]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a = fmaf(xv[e], w[j][e], a);
+        }
+#pragma unroll
+        for (int off = 8; off >= 1; off >>= 1) a += __shfl_xor(a, off, 16);
+        acc[m] = a;
+    }
+    if constexpr (EPI == kLnGelu) {
+        if (col >= p.n) return;
+        const float bias = p.b[col];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            if (m == i && m < p.m) p.out[(long long)m * p.ldo + col] = gelu_erf(acc[m] + bias);
+    } else {
+        // One head per workgroup (n = 512): column c of the head is col.
+        const int head = blockIdx.x;
+        const float bias = p.b[col];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            if (m == i) qh[0][m][c] = acc[m] + bias;
+        __syncthreads();
+        auto mlp = [&](const f32x4 &wt, int src, int m) {
+            const f32x4 xv = *reinterpret_cast<const f32x4 *>(&qh[src][m][4 * i]);
+            float a = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a = fmaf(xv[e], wt[e], a);
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1) a += __shfl_xor(a, off, 16);
+            return a;
+        };
+        float hv[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) hv[m] = gelu_erf(mlp(m0w, 0, m) + p.qm0b[c]);
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            if (m == i) qh[1][m][c] = hv[m];
+        __syncthreads();
+        const float base = p.base[head * 64 + c];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float g = mlp(m2w, 1, m) + p.qm2b[c];
+            if (m == i && m < p.m) {
+                const int b = m / p.rows, rr = m - b * p.rows;
+                p.out[(((long long)b * kHeads + head) * p.rows + rr) * 64 + c] = qh[0][m][c] * base * (1.0f + tanhf(g));
+            }
+        }
+    }
+}
+
+template <int EPI>
+void launch_rows(const LnLinear &a, hipStream_t stream) {
+    const dim3 grid(EPI == kLnQass ? kHeads : a.n / 16), block(EPI == kLnQass ? 1024 : 256);
+    if (a.m <= 1)
+        hipLaunchKernelGGL((ln_rows512_kernel<1, EPI>), grid, block, 0, stream, a);
+    else if (a.m <= 2)
+        hipLaunchKernelGGL((ln_rows512_kernel<2, EPI>), grid, block, 0, stream, a);
+    else if (a.m <= 4)
+        hipLaunchKernelGGL((ln_rows512_kernel<4, EPI>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((ln_rows512_kernel<8, EPI>), grid, block, 0, stream, a);
+}
+
 }  // namespace
 
 void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream) {
@@ -168,7 +305,12 @@ void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream) {
     const double flops = 2.0 * m * n * 512 + (epilogue == kLnQass ? 2.0 * 2.0 * m * 8 * 64 * 64 : 0.0);
     KernelTimer timer(kFamGemm, stream, flops, 4.0 * (m * 512 + n * 512 + m * n));
     const dim3 grid((unsigned)ceil_div((size_t)a.m, kRows), (unsigned)(a.n / 64));
-    if (epilogue == kLnQass)
+    if (a.m <= 8) {
+        if (epilogue == kLnQass)
+            launch_rows<kLnQass>(a, stream);
+        else
+            launch_rows<kLnGelu>(a, stream);
+    } else if (epilogue == kLnQass)
         hipLaunchKernelGGL(ln_linear512_kernel<kLnQass>, grid, dim3(256), 0, stream, a);
     else
         hipLaunchKernelGGL(ln_linear512_kernel<kLnGelu>, grid, dim3(256), 0, stream, a);

@@ -42,7 +42,8 @@ def gelu64(x):
 
 
 @pytest.mark.parametrize("m,n,k,n2", [(65, 64, 64, 64), (300, 512, 512, 10), (513, 1024, 512, 512),
-                                      (128, 512, 1024, 512), (4096, 384, 128, 128), (7, 1024, 512, 999)])
+                                      (128, 512, 1024, 512), (4096, 384, 128, 128), (7, 1024, 512, 999),
+                                      (1, 512, 512, 512), (3, 128, 256, 128), (8, 1024, 512, 512)])
 def test_products_match_float64(device, m, n, k, n2):
     gen = values if m * k < 300_000 else fast_values
     x = gen(m * k, 1)
@@ -274,7 +275,8 @@ def ln64(x, w, b):
     return (x - x.mean(1, keepdims=True)) / np.sqrt(x.var(1, keepdims=True) + 1e-5) * w + b
 
 
-@pytest.mark.parametrize("m,n", [(1, 512), (17, 1024), (512, 1024), (1000, 512)])
+@pytest.mark.parametrize("m,n", [(1, 512), (2, 1024), (3, 1024), (8, 512), (9, 1024), (17, 1024), (512, 1024),
+                                 (1000, 512)])
 def test_ln_linear_gelu_matches_float64(device, m, n):
     """LN2 + FFN up (and the decoder's LN + first layer) in one kernel."""
     x = fast_values(m * 512, 1, 3.0) + 0.25
@@ -288,7 +290,7 @@ def test_ln_linear_gelu_matches_float64(device, m, n):
     np.testing.assert_allclose(out.reshape(m, n), want, rtol=1e-4, atol=2e-5)
 
 
-@pytest.mark.parametrize("estimators,rows", [(1, 1), (1, 5), (2, 250), (3, 17)])
+@pytest.mark.parametrize("estimators,rows", [(1, 1), (1, 2), (1, 5), (8, 1), (4, 2), (3, 3), (2, 250), (3, 17)])
 def test_ln_linear_qass_matches_float64(device, estimators, rows):
     """LN1 + Q projection + QASSMax (query MLP and gate per head), head-major."""
     m = estimators * rows
