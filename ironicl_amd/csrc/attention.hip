@@ -1903,9 +1903,12 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
     if (args.kv_rows <= kShortKeys) {
         // Matrix cores: 16 * qb queries per wave; about 8192 waves in flight.
         // Long query sets share each item's staged keys among four waves.
-        const int qb = args.q_rows <= 16 ? 1 : (args.q_rows <= 80 ? 5 : 4);
-        const int kb = args.kv_rows <= 80 ? 5 : 8;
+        // With few items (passes of a few rows) every 16-query block gets a
+        // wave of its own, which stages the item's keys again.
         const long long items = (long long)args.seqs * args.heads;
+        const int qb = (args.q_rows <= 16 || items * ceil_div(args.q_rows, 80) < 1024) ? 1
+                       : (args.q_rows <= 80 ? 5 : 4);
+        const int kb = args.kv_rows <= 80 ? 5 : 8;
         const long long chunks = ceil_div(args.q_rows, 16 * qb);
         const int waves = (qb == 4 && chunks >= 4) ? 4 : 1;
         const long long groups = std::max<long long>(

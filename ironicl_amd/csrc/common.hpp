@@ -120,10 +120,16 @@ struct GemmArgs {
     OutMap out;
     int m, n, k;
     int epilogue;
+    // Optional LayerNorm of A's rows taken in the product's prologue (K = 128,
+    // products for which gemm_fuses_ln holds): ln_w [128], ln_b [128] or null.
+    const float *ln_w, *ln_b;
 };
 
 // C = epilogue(A W^T + bias) on FP32 MFMA. K must be a multiple of 64.
 void gemm(const GemmArgs &args, hipStream_t stream);
+// Whether gemm takes a LayerNorm prologue (GemmArgs::ln_w) for an
+// m x n product with K = 128 and plain row-major output.
+bool gemm_fuses_ln(long long m, int n);
 
 // Post-attention half of a 128-wide block in one kernel (cpu.rs:1555-1601):
 // s1 = state + (att Wo^T + bo); state = s1 + (gelu(LN2(s1) W1^T + b1) W2^T + b2).

@@ -38,6 +38,27 @@ __device__ __forceinline__ long long col_offset(const OutMap &o, int n) {
     return plane * o.plane_stride + head * o.head_stride + within;
 }
 
+// LayerNorm of one 128-wide row by a half-wave, lane c4 holding columns
+// 4 c4 .. 4 c4 + 3 (layer_norm_f32, reference.rs:223-252: two-pass mean and
+// variance, eps 1e-5), in the arithmetic of the standalone 128-wide LayerNorm.
+__device__ __forceinline__ f32x4 layer_norm128_lanes(f32x4 v, const float *w, const float *b, int c4) {
+    auto half_wave_sum = [](float x) {
+#pragma unroll
+        for (int offset = 16; offset >= 1; offset >>= 1) x += __shfl_xor(x, offset, 64);
+        return x;
+    };
+    const float mean = half_wave_sum((v[0] + v[1]) + (v[2] + v[3])) / 128.0f;
+    const f32x4 d = v - mean;
+    float sq = d[0] * d[0];
+    sq = fmaf(d[1], d[1], sq);
+    sq = fmaf(d[2], d[2], sq);
+    sq = fmaf(d[3], d[3], sq);
+    const float rstd = 1.0f / sqrtf(half_wave_sum(sq) / 128.0f + 1e-5f);
+    f32x4 o = d * rstd * *reinterpret_cast<const f32x4 *>(w + 4 * c4);
+    if (b) o += *reinterpret_cast<const f32x4 *>(b + 4 * c4);
+    return o;
+}
+
 // Epilogue of one accumulator value at (row, col): bias, then GELU, residual
 // or the QASS gate, then the output map. EPI and GROUPED are compile-time so
 // each instantiation is straight-line code.
@@ -221,9 +242,13 @@ __global__ __launch_bounds__(256, BK == 16 ? 3 : 2) void gemm_kernel(GemmArgs p,
 // waves each take a quarter of K, reading their operands straight from L2 in
 // MFMA order (one 16-deep step ahead), then reduce through LDS; each wave
 // finishes four of the sixteen accumulator registers.
-template <int EPI, bool GROUPED>
+// LN: A's rows are LayerNormed first (K = 128), the tile's 32 rows staged in
+// LDS by the workgroup's eight half-waves, and the A operands read from there.
+template <int EPI, bool GROUPED, bool LN = false>
 __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
+    constexpr int kLnStride = 132;
     __shared__ float red[4][16][64];
+    __shared__ __attribute__((aligned(16))) float xs[LN ? 32 * kLnStride : 4];
     const int bid = blockIdx.x;
     const int tile = (bid % 8) * per_xcd + bid / 8;
     if (tile >= tiles_m * tiles_n) return;
@@ -234,19 +259,36 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
     const int kq = p.k / 4;
     const float *a = p.a + (long long)min(m0 + r32, p.m - 1) * p.lda + wave * kq + 8 * half;
     const float *b = p.w + (long long)min(n0 + r32, p.n - 1) * p.k + wave * kq + 8 * half;
+    const int a_lds = r32 * kLnStride + wave * kq + 8 * half;
+    auto load_a = [&](int off) {
+        if constexpr (LN)
+            return *reinterpret_cast<const f32x4 *>(&xs[a_lds + off]);
+        else
+            return *reinterpret_cast<const f32x4 *>(a + off);
+    };
 
+    f32x4 b0 = *reinterpret_cast<const f32x4 *>(b), b1 = *reinterpret_cast<const f32x4 *>(b + 4);
+    if constexpr (LN) {
+        const int hw = tid >> 5;
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int r = 8 * pass + hw;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(p.a + (long long)min(m0 + r, p.m - 1) * p.lda + 4 * r32);
+            *reinterpret_cast<f32x4 *>(&xs[r * kLnStride + 4 * r32]) = layer_norm128_lanes(v, p.ln_w, p.ln_b, r32);
+        }
+        __syncthreads();
+    }
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    f32x4 a0 = *reinterpret_cast<const f32x4 *>(a), a1 = *reinterpret_cast<const f32x4 *>(a + 4);
-    f32x4 b0 = *reinterpret_cast<const f32x4 *>(b), b1 = *reinterpret_cast<const f32x4 *>(b + 4);
+    f32x4 a0 = load_a(0), a1 = load_a(4);
     const int steps = kq / 16;
     for (int s = 0; s < steps; ++s) {
         f32x4 na0 = a0, na1 = a1, nb0 = b0, nb1 = b1;
         if (s + 1 < steps) {
             const int off = 16 * (s + 1);
-            na0 = *reinterpret_cast<const f32x4 *>(a + off);
-            na1 = *reinterpret_cast<const f32x4 *>(a + off + 4);
+            na0 = load_a(off);
+            na1 = load_a(off + 4);
             nb0 = *reinterpret_cast<const f32x4 *>(b + off);
             nb1 = *reinterpret_cast<const f32x4 *>(b + off + 4);
         }
@@ -308,9 +350,11 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
 // group's 16 partial sums are reduced by shuffles and lane m writes row m.
 // At one row a launch is one round trip for its weights instead of
 // split-K's eight dependent steps.
-template <int M, int EPI, int KPL>  // KPL: K / 16 floats per lane
+// LN (K = 128): row m is LayerNormed by half-wave m as it is staged.
+template <int M, int EPI, int KPL, bool LN = false>  // KPL: K / 16 floats per lane
 __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmArgs p) {
     constexpr int K = 16 * KPL;
+    static_assert(!LN || (K == 128 && M <= 8), "the LayerNorm prologue stages at most eight 128-wide rows");
     __shared__ __attribute__((aligned(16))) float xs[M * K];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 4, i = lane & 15;
@@ -319,11 +363,22 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmArgs p) {
     f32x4 w[KPL / 4];
 #pragma unroll
     for (int j = 0; j < KPL / 4; ++j) w[j] = *reinterpret_cast<const f32x4 *>(wr + 64 * j);
-    for (int idx = tid; idx < M * K / 4; idx += 256) {
-        const int m = idx / (K / 4), k4 = idx - m * (K / 4);
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (m < p.m) v = *reinterpret_cast<const f32x4 *>(p.a + (long long)m * p.lda + 4 * k4);
-        *reinterpret_cast<f32x4 *>(&xs[m * K + 4 * k4]) = v;
+    if constexpr (LN) {
+        const int m = tid >> 5, c4 = tid & 31;
+        if (m < M) {
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (m < p.m)
+                v = layer_norm128_lanes(*reinterpret_cast<const f32x4 *>(p.a + (long long)m * p.lda + 4 * c4),
+                                        p.ln_w, p.ln_b, c4);
+            *reinterpret_cast<f32x4 *>(&xs[m * K + 4 * c4]) = v;
+        }
+    } else {
+        for (int idx = tid; idx < M * K / 4; idx += 256) {
+            const int m = idx / (K / 4), k4 = idx - m * (K / 4);
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (m < p.m) v = *reinterpret_cast<const f32x4 *>(p.a + (long long)m * p.lda + 4 * k4);
+            *reinterpret_cast<f32x4 *>(&xs[m * K + 4 * k4]) = v;
+        }
     }
     __syncthreads();
     float acc[M];
@@ -419,6 +474,11 @@ struct SplitK {
     static constexpr auto kernel = gemm_splitk_kernel<E, G>;
 };
 
+template <int E, bool G>
+struct SplitKLn {
+    static constexpr auto kernel = gemm_splitk_kernel<E, G, true>;
+};
+
 template <int BM, int BN, int BK = kBK>
 void launch(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, BM), tiles_n = (int)ceil_div(args.n, BN);
@@ -437,6 +497,19 @@ bool launch_rows(const GemmArgs &args, hipStream_t stream) {
         if (m != M || args.k != 16 * KPL) return;
         const Flops f = work(args);
         KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
+        if constexpr (KPL == 8) {
+            if (args.ln_w) {
+                if (args.epilogue == kEpiNone)
+                    hipLaunchKernelGGL((gemm_rows_kernel<M, kEpiNone, 8, true>), grid, block, 0, stream, args);
+                else if (args.epilogue == kEpiGelu)
+                    hipLaunchKernelGGL((gemm_rows_kernel<M, kEpiGelu, 8, true>), grid, block, 0, stream, args);
+                else
+                    hipLaunchKernelGGL((gemm_rows_kernel<M, kEpiResidual, 8, true>), grid, block, 0, stream, args);
+                IRX_HIP(hipGetLastError());
+                launched = true;
+                return;
+            }
+        }
         if (args.epilogue == kEpiNone)
             hipLaunchKernelGGL((gemm_rows_kernel<M, kEpiNone, KPL>), grid, block, 0, stream, args);
         else if (args.epilogue == kEpiGelu)
@@ -462,13 +535,26 @@ bool launch_rows(const GemmArgs &args, hipStream_t stream) {
 void launch_splitk(const GemmArgs &args, hipStream_t stream) {
     int tiles_m = (int)ceil_div(args.m, 32), tiles_n = (int)ceil_div(args.n, 32);
     int per_xcd = (tiles_m * tiles_n + 7) / 8;
-    dispatch_epilogue<SplitK>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
+    if (args.ln_w)
+        dispatch_epilogue<SplitKLn>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
+    else
+        dispatch_epilogue<SplitK>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
 }
+
+// Products with fewer than 256 tiles of 64 x 64 take split-K or, at up to
+// eight rows, the small-row kernel.
+bool small_product(long long m, long long n) { return ceil_div(m, 64) * ceil_div(n, 64) < 256; }
 
 }  // namespace
 
+bool gemm_fuses_ln(long long m, int n) { return m > 0 && n > 0 && small_product(m, n); }
+
 void gemm(const GemmArgs &args, hipStream_t stream) {
     if (args.m <= 0 || args.n <= 0) return;
+    if (args.ln_w && (args.k != 128 || !gemm_fuses_ln(args.m, args.n) || args.out.rows_per_group < args.m ||
+                      args.epilogue == kEpiQass || (reinterpret_cast<uintptr_t>(args.ln_w) & 15) ||
+                      (reinterpret_cast<uintptr_t>(args.ln_b) & 15)))
+        fail(3, "gemm: a LayerNorm prologue needs K = 128, a small product and plain rows");
     if (args.k <= 0 || args.k % 64 != 0 || args.lda % 4 != 0 ||
         (reinterpret_cast<uintptr_t>(args.a) & 15) || (reinterpret_cast<uintptr_t>(args.w) & 15))
         fail(3, "gemm: K must be a positive multiple of 64 with 16-byte aligned rows");
@@ -478,9 +564,8 @@ void gemm(const GemmArgs &args, hipStream_t stream) {
     // with four or more 128 x 128 tiles per CU take them (GELU ones, whose
     // epilogue is long, from two per CU), the rest 64 x 64 (measured on the
     // prediction pass's products).
-    const long long small_tiles = (long long)ceil_div(args.m, 64) * ceil_div(args.n, 64);
     const long long big_tiles = (long long)ceil_div(args.m, 128) * ceil_div(args.n, 128);
-    if (small_tiles < 256) {
+    if (small_product(args.m, args.n)) {
         if (!launch_rows(args, stream)) launch_splitk(args, stream);
     } else if (big_tiles >= 1024 || (args.epilogue == kEpiGelu && big_tiles >= 512)) {
         // 128 x 128 tiles: 16-deep K steps (40 KB of LDS, 128 registers: four

@@ -443,6 +443,22 @@ struct Stages {
         gemm(g, s);
     }
 
+    // LayerNorm of 128-wide rows x [m, 128] and the product that reads it:
+    // taken in the product's prologue when the product is prediction-sized,
+    // else written to `norm` first.
+    void ln_linear128(const float *x, long long m, const float *lnw, const float *lnb, float *norm, const float *wt,
+                      const float *b, int n, float *c, long long ldc, int epi = kEpiNone) const {
+        if (gemm_fuses_ln(m, n)) {
+            GemmArgs g{};
+            g.a = x, g.lda = 128, g.w = wt, g.bias = b, g.c = c, g.out = OutMap::row_major(n, ldc);
+            g.m = (int)m, g.n = n, g.k = 128, g.epilogue = epi, g.ln_w = lnw, g.ln_b = lnb;
+            gemm(g, s);
+            return;
+        }
+        layer_norm(x, 128, lnw, lnb, norm, 128, m, 128, s);
+        linear(norm, 128, m, 128, wt, b, n, c, ldc, epi);
+    }
+
     // LN1 + the in_proj rows [head_row0, head_row0 + 16 head_nb) of a 128-wide
     // block into out [m, ldo]: one fused launch from 16384 rows (as the tail),
     // else LayerNorm into `norm` and a product.
@@ -455,8 +471,8 @@ struct Stages {
             head128(h, s);
             return;
         }
-        layer_norm(x, 128, bw.n1w, bw.n1b, norm, 128, m, 128, s);
-        linear(norm, 128, m, 128, bw.in_w + (size_t)bw.head_row0 * 128, bw.in_b + bw.head_row0, n, out, ldo);
+        ln_linear128(x, m, bw.n1w, bw.n1b, norm, bw.in_w + (size_t)bw.head_row0 * 128, bw.in_b + bw.head_row0, n,
+                     out, ldo);
     }
 
     void linear_map(const float *a, long long lda, long long m, int k, const float *wt, const float *b, int n,
@@ -497,8 +513,12 @@ struct Stages {
             return;
         }
         linear(att, d, m, d, bw.out.w, bw.out.b, d, state, d, kEpiResidual, state, d);
-        layer_norm(state, d, bw.n2w, bw.n2b, norm, d, m, d, s);
-        linear(norm, d, m, d, bw.l1.w, bw.l1.b, 2 * d, hid, 2 * d, kEpiGelu);
+        if (d == 128) {
+            ln_linear128(state, m, bw.n2w, bw.n2b, norm, bw.l1.w, bw.l1.b, 2 * d, hid, 2 * d, kEpiGelu);
+        } else {
+            layer_norm(state, d, bw.n2w, bw.n2b, norm, d, m, d, s);
+            linear(norm, d, m, d, bw.l1.w, bw.l1.b, 2 * d, hid, 2 * d, kEpiGelu);
+        }
         linear(hid, 2 * d, m, 2 * d, bw.l2.w, bw.l2.b, d, state, d, kEpiResidual, state, d);
     }
 
@@ -565,8 +585,7 @@ struct Stages {
         const long long mc = seqs * kReserved;
         gather_cls(r.seq, seqs, len, r.cls, s);
         head(bw, r.seq, m, r.norm, r.qkv, 256);
-        layer_norm(r.cls, 128, bw.n1w, bw.n1b, r.cnorm, 128, mc, 128, s);
-        linear(r.cnorm, 128, mc, 128, bw.in_w, bw.in_b, 128, r.cq, 128);
+        ln_linear128(r.cls, mc, bw.n1w, bw.n1b, r.cnorm, bw.in_w, bw.in_b, 128, r.cq, 128);
         SmallAttention a{};
         a.q = r.cq, a.q_seq = kReserved * 128, a.q_group = 0, a.q_row = 128, a.q_head = kColumnHead;
         a.k = r.qkv, a.v = r.qkv + 128, a.k_seq = a.v_seq = (long long)len * 256, a.k_group = a.v_group = 0;
@@ -2165,7 +2184,7 @@ namespace {
 // Heads [heads, rows, 16] of one sequence; RoPE tables [max(query_rows, rows), 16] or null.
 void test_small_attention(irx_device *device, const float *q, const float *k, const float *v, const float *cos_t,
                           const float *sin_t, size_t heads, size_t query_rows, size_t rows, float *out) {
-    if (!device || !q || !k || !v || !out || !heads || !query_rows || !rows || heads > 64 ||
+    if (!device || !q || !k || !v || !out || !heads || !query_rows || !rows || heads > 4096 ||
         query_rows > (1u << 20) || rows > (1u << 24) || (!cos_t) != (!sin_t))
         fail(IRX_INVALID_ARGUMENT, "small attention shapes do not match");
     set_device(device);

@@ -236,10 +236,12 @@ def block_tail64(att, state, wo, bo, n2w, n2b, w1, b1, w2, b2):
     return s1 + (h @ w2.astype(np.float64).T + b2)
 
 
-@pytest.mark.parametrize("rows,outputs", [(1, 128), (65, 384), (1000, 256), (16411, 384), (17000, 128)])
+@pytest.mark.parametrize("rows,outputs", [(1, 128), (3, 384), (8, 256), (65, 384), (1000, 256), (16411, 384),
+                                          (17000, 128)])
 @pytest.mark.parametrize("fused", [0, 1])
 def test_block_head_matches_float64(device, rows, outputs, fused):
-    """LN1 + in_proj of a 128-wide block: the fused kernel and the two launches."""
+    """LN1 + in_proj of a 128-wide block: the fused kernel, and the product
+    with the LayerNorm in its prologue (small products) or before it."""
     x = fast_values(rows * 128, 21, 3.0) + 0.2
     lnw, lnb = fast_values(128, 22, 0.2) + 1.0, fast_values(128, 23, 0.1)
     w, b = fast_values(outputs * 128, 24, 0.09), fast_values(outputs, 25, 0.1)
@@ -251,7 +253,7 @@ def test_block_head_matches_float64(device, rows, outputs, fused):
     np.testing.assert_allclose(out.reshape(rows, outputs), want, rtol=1e-4, atol=1e-5)
 
 
-@pytest.mark.parametrize("rows", [1, 17, 64, 65, 1000, 16411])
+@pytest.mark.parametrize("rows", [1, 5, 17, 64, 65, 1000, 16411])
 @pytest.mark.parametrize("fused", [0, 1])
 def test_block_tail_matches_float64(device, rows, fused):
     att = fast_values(rows * 128, 1, 2.0)
@@ -352,6 +354,21 @@ def test_small_attention_many_keys_matches_float64(device, query_rows, rows, qsc
     q = fast_values(heads * query_rows * 16, 4, qscale).reshape(heads, query_rows, 16)
     k = fast_values(heads * rows * 16, 5).reshape(heads, rows, 16)
     v = fast_values(heads * rows * 16, 6).reshape(heads, rows, 16)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_small_attention(device.handle, F(q), F(k), F(v), heads, query_rows, rows,
+                                                 F(out)))
+    worst = max(np.abs(out[h] - attention64(q[h], k[h], v[h], 0.25)).max() for h in range(heads))
+    assert worst < 1e-5, worst
+
+
+@pytest.mark.parametrize("heads,query_rows,rows", [(1024, 68, 68), (512, 100, 128), (1024, 16, 80)])
+def test_small_attention_many_items_matches_float64(device, heads, query_rows, rows):
+    """As many (sequence, head) items as a 128-row pass has, where waves take
+    several 16-query blocks each (few items give every block its own wave)."""
+    q = fast_values(heads * query_rows * 16, 10, 3.0).reshape(heads, query_rows, 16)
+    k = fast_values(heads * rows * 16, 11).reshape(heads, rows, 16)
+    v = fast_values(heads * rows * 16, 12).reshape(heads, rows, 16)
     out = np.zeros_like(q)
     F = hip.fptr
     hip.check(hip.lib().irx_test_small_attention(device.handle, F(q), F(k), F(v), heads, query_rows, rows,
