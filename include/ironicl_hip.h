@@ -380,8 +380,9 @@ int irx_test_block_head(irx_device *device, int fused, const float *x, size_t ro
                         const float *lnb, const float *w, const float *b, size_t outputs, float *out);
 /* The post-attention half of a 128-wide block (cpu.rs:1555-1601) on `rows`
  * rows: s1 = state + (att wo^T + bo); out = s1 + (gelu(LN2(s1) w1^T + b1) w2^T + b2),
- * LN2 with n2w / n2b. fused = 1 runs the one-kernel tail, 0 the separate
- * products and LayerNorm. wo [128,128], w1 [256,128], w2 [128,256]. With
+ * LN2 with n2w / n2b. fused = 1 runs the one-kernel tail, 2 its
+ * small-pass form (16 rows per workgroup), 0 the separate products and
+ * LayerNorm. wo [128,128], w1 [256,128], w2 [128,256]. With
  * repeats > 1 the tail is applied again repeats - 1 times after `out` is
  * read (for timing with irx_profile_read). */
 int irx_test_block_tail(irx_device *device, int fused, const float *att, const float *state, size_t rows,

@@ -146,7 +146,8 @@ struct Tail128 {
     long long m;
 };
 void tail128_pack(const float *wo, const float *w1, const float *w2, float *out);
-void tail128(const Tail128 &t, hipStream_t stream);
+// rows16: the small-pass form (16 rows per workgroup, bitwise the same results).
+void tail128(const Tail128 &t, hipStream_t stream, bool rows16 = false);
 
 // Pre-attention head of a 128-wide block in one kernel: out = LN1(x) W^T + b
 // for nb = 8, 16 or 24 blocks of 16 outputs (W [16 nb, 128], packed by

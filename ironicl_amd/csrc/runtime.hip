@@ -485,15 +485,17 @@ struct Stages {
 
     // Post-attention half of a block: out-projection + residual into `state`,
     // then LN2, FFN (GELU) and residual (cpu.rs:1555-1601).
-    // A 128-wide block's tail runs fused (tail128) once its rows fill the
-    // chip: one wave carries 16 rows through the whole chain, so with fewer
-    // than 16384 rows (256 workgroups) the four separate launches, which
-    // spread each product over every CU, finish first. fused: -1 chooses,
-    // 0 / 1 force.
+    // A 128-wide block's tail runs fused: tail128 once its rows fill the chip
+    // (one wave carries 16 rows through the whole chain, 256 workgroups at
+    // 16384 rows), below that its 16-rows-per-workgroup form, whose four
+    // waves split each product. fused: -1 chooses; 0 forces the four
+    // separate launches, 1 tail128, 2 the small-pass form.
     void tail(const BlockW &bw, float *state, long long m, const float *att, float *norm, float *hid,
               int fused = -1) const {
         const int d = bw.dim;
-        const bool use_fused = fused < 0 ? (d == 128 && bw.tail_pack && m >= 16384) : fused == 1;
+        const bool packed = d == 128 && bw.tail_pack;
+        const bool use_fused = fused < 0 ? packed : fused >= 1;
+        const bool rows16 = fused < 0 ? m < 16384 : fused == 2;
         if (d == 512 && m <= kLnLinearRows) {
             // Prediction-sized 512-wide blocks: LN2 fused into the FFN's first product.
             linear(att, d, m, d, bw.out.w, bw.out.b, d, state, d, kEpiResidual, state, d);
@@ -509,7 +511,7 @@ struct Stages {
             Tail128 t{};
             t.att = att, t.lda = d, t.state = state, t.ldx = d, t.pack = bw.tail_pack, t.m = m;
             t.bo = bw.out.b, t.n2w = bw.n2w, t.n2b = bw.n2b, t.b1 = bw.l1.b, t.b2 = bw.l2.b;
-            tail128(t, s);
+            tail128(t, s, rows16);
             return;
         }
         linear(att, d, m, d, bw.out.w, bw.out.b, d, state, d, kEpiResidual, state, d);
@@ -2092,7 +2094,7 @@ int irx_test_block_tail(irx_device *device, int fused, const float *att, const f
                         const float *b1, const float *w2, const float *b2, size_t repeats, float *out) {
     return guarded("irx_test_block_tail", [&] {
         if (!device || !att || !state || !wo || !bo || !n2w || !n2b || !w1 || !b1 || !w2 || !b2 || !out || !rows ||
-            (fused != 0 && fused != 1) || !repeats)
+            fused < 0 || fused > 2 || !repeats)
             fail(IRX_INVALID_ARGUMENT, "block tail arguments do not match");
         set_device(device);
         const size_t n = rows * 128;

@@ -205,6 +205,162 @@ __global__ __launch_bounds__(256, 3) void tail128_kernel(Tail128 p) {
     }
 }
 
+// The same tail for small passes (a few thousand rows or fewer), where
+// tail128's 64-row workgroups would leave most CUs idle and each wave would
+// carry its rows through all 320 products alone: one workgroup per 16 rows,
+// wave w producing output blocks 2 w and 2 w + 1 (of the out-projection and
+// of the FFN's second layer) and hidden slices 2 w and 2 w + 1. The waves
+// swap s1 and the GELU layer through LDS; every wave takes LN2 of the whole
+// rows itself. Fragments are read from the tail128 pack in global memory
+// (320 KB, shared by every workgroup through L2), each wave's W1 fragments
+// issued with its first loads. Every accumulator takes its products in
+// tail128's order, so the results are tail128's bit for bit.
+__global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
+    constexpr int kS1Stride = 132, kHidStride = 260;
+    __shared__ __attribute__((aligned(16))) float s1s[16 * kS1Stride];
+    __shared__ __attribute__((aligned(16))) float hs[16 * kHidStride];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
+    const long long row = (long long)blockIdx.x * 16 + m16;
+    const bool live = row < p.m;
+    const long long r = live ? row : p.m - 1;
+    const float *pk = p.pack + lane * 4;
+    // Fragment (k-block kb, output block ob) of Wo; (kb, hb) of slice c's W1
+    // rows; (hidden block 2 c + j, ob) of W2 (tail128_pack's order).
+    auto wo_frag = [&](int kb, int ob) { return *reinterpret_cast<const f32x4 *>(pk + kb * 2048 + ob * 256); };
+    auto w1_frag = [&](int c, int kb, int hb) {
+        return *reinterpret_cast<const f32x4 *>(pk + (2 + c) * kChunkFloats + (kb * 2 + hb) * 256);
+    };
+    auto w2_frag = [&](int c, int j, int ob) {
+        return *reinterpret_cast<const f32x4 *>(pk + (2 + c) * kChunkFloats + 4096 + (j * 8 + ob) * 256);
+    };
+
+    f32x4 fo[8][2], x[8], s1[2];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fo[kb][j] = wo_frag(kb, 2 * w + j);
+    const float *att = p.att + r * p.lda + 4 * g;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(att + 16 * b);
+    const float *st = p.state + r * p.ldx + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) s1[j] = *reinterpret_cast<const f32x4 *>(st + 16 * (2 * w + j));
+    f32x4 f1[2][8][2];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) f1[sl][kb][hb] = w1_frag(2 * w + sl, kb, hb);
+
+    // Out-projection of output blocks 2 w + j; s1 = state + (acc + bo) to LDS.
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[j] = mfma(fo[kb][j][e], x[kb][e], acc[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int c0 = 16 * (2 * w + j) + 4 * g;
+        const f32x4 bo = *reinterpret_cast<const f32x4 *>(p.bo + c0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s1[j][e] = s1[j][e] + (acc[j][e] + bo[e]);
+        *reinterpret_cast<f32x4 *>(&s1s[m16 * kS1Stride + c0]) = s1[j];
+    }
+    __syncthreads();
+
+    // LN2 of the 16 rows (as tail128: row m's features over lanes m, m + 16,
+    // m + 32, m + 48).
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(&s1s[m16 * kS1Stride + 16 * b + 4 * g]);
+    float sum = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += x[b][e];
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float mean = sum / 128.f;
+    float sq = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float d = x[b][e] - mean;
+            sq = fmaf(d, d, sq);
+        }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 nw = *reinterpret_cast<const f32x4 *>(p.n2w + 16 * b + 4 * g);
+        const f32x4 nb = *reinterpret_cast<const f32x4 *>(p.n2b + 16 * b + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[b][e] = (x[b][e] - mean) * rstd * nw[e] + nb[e];
+    }
+
+    // Hidden slices c = 2 w + sl: gelu(W1 x + b1) to LDS.
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+        const int c = 2 * w + sl;
+        f32x4 h[2][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i >> 1][i & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) h[hb][kb & 1] = mfma(f1[sl][kb][hb][e], x[kb][e], h[hb][kb & 1]);
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const f32x4 b1 = *reinterpret_cast<const f32x4 *>(p.b1 + 32 * c + 16 * hb + 4 * g);
+            f32x4 hg;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hg[e] = gelu_erf((h[hb][0][e] + h[hb][1][e]) + b1[e]);
+            *reinterpret_cast<f32x4 *>(&hs[m16 * kHidStride + 32 * c + 16 * hb + 4 * g]) = hg;
+        }
+    }
+    // This wave's W2 fragments (output blocks 2 w + j), in flight over the barrier.
+    f32x4 f2[8][2][2];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int ob = 0; ob < 2; ++ob) f2[c][j][ob] = w2_frag(c, j, 2 * w + ob);
+    __syncthreads();
+
+    // FFN down over the 256 hidden units, slice by slice as tail128 does.
+    f32x4 acc2[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f32x4 hv = *reinterpret_cast<const f32x4 *>(&hs[m16 * kHidStride + 32 * c + 16 * j + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ob = 0; ob < 2; ++ob) acc2[ob] = mfma(f2[c][j][ob][e], hv[e], acc2[ob]);
+        }
+    if (!live) return;
+    float *out = p.state + row * p.ldx + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int c0 = 16 * (2 * w + j);
+        const f32x4 b2 = *reinterpret_cast<const f32x4 *>(p.b2 + c0 + 4 * g);
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (acc2[j][e] + b2[e]) + s1[j][e];
+        *reinterpret_cast<f32x4 *>(out + c0) = v;
+    }
+}
+
 // The head of a 128-wide block: y = LN1(x) W^T + b over 16 NB outputs,
 // written row-major; the same per-wave layout as tail128, the fragments of W
 // in (k-block, output block) order streamed through the same LDS buffers.
@@ -341,7 +497,7 @@ void tail128_pack(const float *wo, const float *w1, const float *w2, float *out)
     }
 }
 
-void tail128(const Tail128 &t, hipStream_t stream) {
+void tail128(const Tail128 &t, hipStream_t stream, bool rows16) {
     if (t.m <= 0) return;
     if (!t.att || !t.state || !t.pack || !t.bo || !t.n2w || !t.n2b || !t.b1 || !t.b2)
         fail(3, "tail128: missing tensor");
@@ -351,7 +507,10 @@ void tail128(const Tail128 &t, hipStream_t stream) {
     const double m = (double)t.m;
     // Products 2 m (128*128 + 2 * 128*256); bytes: att and state in, state out, weights.
     KernelTimer timer(kFamGemm, stream, m * 2.0 * (128.0 * 128 + 2 * 128.0 * 256), m * 128 * 4 * 3.0 + kTail128PackFloats * 4.0);
-    hipLaunchKernelGGL(tail128_kernel, dim3((unsigned)ceil_div(t.m, (long long)kTailRows)), dim3(256), 0, stream, t);
+    if (rows16)
+        hipLaunchKernelGGL(tail128_rows16_kernel, dim3((unsigned)ceil_div(t.m, 16LL)), dim3(256), 0, stream, t);
+    else
+        hipLaunchKernelGGL(tail128_kernel, dim3((unsigned)ceil_div(t.m, (long long)kTailRows)), dim3(256), 0, stream, t);
     IRX_HIP(hipGetLastError());
 }
 

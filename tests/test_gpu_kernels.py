@@ -254,7 +254,7 @@ def test_block_head_matches_float64(device, rows, outputs, fused):
 
 
 @pytest.mark.parametrize("rows", [1, 5, 17, 64, 65, 1000, 16411])
-@pytest.mark.parametrize("fused", [0, 1])
+@pytest.mark.parametrize("fused", [0, 1, 2])
 def test_block_tail_matches_float64(device, rows, fused):
     att = fast_values(rows * 128, 1, 2.0)
     state = fast_values(rows * 128, 2, 3.0)
@@ -270,6 +270,26 @@ def test_block_tail_matches_float64(device, rows, fused):
                         w1.reshape(256, 128), b1, w2.reshape(128, 256), b2)
     np.testing.assert_allclose(out.reshape(rows, 128), want, rtol=1e-4, atol=1e-5)
     assert np.abs(out.reshape(rows, 128) - want).max() < 2e-5
+
+
+@pytest.mark.parametrize("rows", [1, 16, 33, 1000])
+def test_block_tail_small_pass_form_equals_tail128(device, rows):
+    """The 16-rows-per-workgroup tail takes every product in tail128's order:
+    the same bits, on rows that are not a multiple of either's tile."""
+    att = fast_values(rows * 128, 11, 2.0)
+    state = fast_values(rows * 128, 12, 3.0)
+    wo, bo = fast_values(128 * 128, 13, 0.09), fast_values(128, 14, 0.1)
+    n2w, n2b = fast_values(128, 15, 0.2) + 1.0, fast_values(128, 16, 0.1)
+    w1, b1 = fast_values(256 * 128, 17, 0.09), fast_values(256, 18, 0.1)
+    w2, b2 = fast_values(128 * 256, 19, 0.06), fast_values(128, 20, 0.1)
+    outs = []
+    F = hip.fptr
+    for fused in (1, 2):
+        out = np.zeros_like(state)
+        hip.check(hip.lib().irx_test_block_tail(device.handle, fused, F(att), F(state), rows, F(wo), F(bo), F(n2w),
+                                                F(n2b), F(w1), F(b1), F(w2), F(b2), 1, F(out)))
+        outs.append(out)
+    np.testing.assert_array_equal(outs[0], outs[1])
 
 
 def ln64(x, w, b):
