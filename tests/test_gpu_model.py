@@ -98,6 +98,23 @@ def test_pass_rows_and_device_path_do_not_change_results(lcg):
     np.testing.assert_array_equal(dl.to_host(), whole)
 
 
+@pytest.mark.parametrize("rows", [1, 2, 4, 5])
+def test_passes_of_few_rows_match_the_oracle(clf, clf_oracle, lcg, rows):
+    """Calls of 1-5 test rows over two estimators: passes of at most eight
+    (estimator, row) pairs take the small-row products, LayerNorm + linear
+    kernels and 16-row block tails, five rows the split-K products. Checked
+    against the oracle on its own context and against the 512-row passes."""
+    x, y, xt, shifts, ctx_cpu, ctx_gpu = lcg
+    few = np.ascontiguousarray(xt[:, :rows])
+    st = clf.load_context_tensors(ctx_cpu, x.shape, 3, shifts)
+    gpu = st.predict_raw(few).logits
+    cpu = clf_oracle.predict_cached(ctx_cpu, few)
+    assert_parity(gpu, cpu, f"{rows} rows on the oracle context")
+    assert np.array_equal(gpu[..., :3].argmax(-1), cpu[..., :3].argmax(-1))
+    whole = ctx_gpu.predict_raw(xt).logits
+    np.testing.assert_allclose(ctx_gpu.predict_raw(few).logits, whole[:, :rows], atol=1e-6, rtol=1e-6)
+
+
 def test_stream_counts_give_identical_results(lcg):
     *_, ctx_gpu = lcg
     xt = lcg[2]
