@@ -1191,12 +1191,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
 
 // Merge of split partials by their log2-sum-exp, into tokens [b * q_rows +
 // row, head * 64 + d]. Partial outputs are [splits, pairs, q_padded, 64],
-// followed by the log2-sum-exps [splits, pairs, q_padded]. One wave per
-// (pair, row): lane = split group (lane / 16, every fourth split) x four dims.
-// Each round loads eight splits per group at once and folds them into the
-// lane's running reference; the four groups are combined at the end.
-__global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int splits, int q_padded) {
-    const long long pq = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+// followed by the log2-sum-exps [splits, pairs, q_padded]. One single-wave
+// workgroup per (pair, row), so even a one-row pass's eight merges spread
+// over eight CUs: lane = split group (lane / 16, every fourth split) x four
+// dims. Each round loads sixteen splits per group at once (the 64 splits of
+// a decode pass in one round) and folds them into the lane's running
+// reference; the four groups are combined at the end.
+constexpr int kMergePerGroup = 16;
+__global__ __launch_bounds__(64) void icl_merge_kernel(IclAttention p, int splits, int q_padded) {
+    const long long pq = blockIdx.x;
     if (pq >= (long long)p.pairs * p.q_rows) return;
     const int lane = threadIdx.x & 63, sg = lane >> 4, d = (lane & 15) * 4;
     const int qrow = (int)(pq % p.q_rows);
@@ -1206,11 +1209,11 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
     const float *lse = p.partial + (long long)splits * step * 64 + row0;
     float m_run = -INFINITY, den = 0.f;
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = sg; s0 < splits; s0 += 32) {
-        float l8[8];
-        f32x4 v8[8];
+    for (int s0 = sg; s0 < splits; s0 += 4 * kMergePerGroup) {
+        float l8[kMergePerGroup];
+        f32x4 v8[kMergePerGroup];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < kMergePerGroup; ++j) {
             const int s = s0 + 4 * j;
             if (s < splits) {
                 l8[j] = lse[s * step];
@@ -1222,11 +1225,11 @@ __global__ __launch_bounds__(256) void icl_merge_kernel(IclAttention p, int spli
         }
         float m_new = m_run;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) m_new = fmaxf(m_new, l8[j]);
+        for (int j = 0; j < kMergePerGroup; ++j) m_new = fmaxf(m_new, l8[j]);
         const float a = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while m_run is -inf
         num *= a, den *= a;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < kMergePerGroup; ++j) {
             const float w = __builtin_amdgcn_exp2f(l8[j] - m_new);
             num += w * v8[j];
             den += w;
@@ -1859,7 +1862,7 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
             hipLaunchKernelGGL(icl_merge_rows_kernel<16>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args,
                                g.splits, g.q_padded);
         else
-            hipLaunchKernelGGL(icl_merge_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, args, g.splits,
+            hipLaunchKernelGGL(icl_merge_kernel, dim3((unsigned)rows), dim3(64), 0, stream, args, g.splits,
                                g.q_padded);
         IRX_HIP(hipGetLastError());
     }
