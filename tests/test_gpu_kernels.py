@@ -297,8 +297,8 @@ def ln64(x, w, b):
     return (x - x.mean(1, keepdims=True)) / np.sqrt(x.var(1, keepdims=True) + 1e-5) * w + b
 
 
-@pytest.mark.parametrize("m,n", [(1, 512), (2, 1024), (3, 1024), (8, 512), (9, 1024), (17, 1024), (512, 1024),
-                                 (1000, 512)])
+@pytest.mark.parametrize("m,n", [(1, 512), (2, 1024), (3, 1024), (8, 512), (9, 1024), (16, 512), (17, 1024),
+                                 (512, 1024), (1000, 512)])
 def test_ln_linear_gelu_matches_float64(device, m, n):
     """LN2 + FFN up (and the decoder's LN + first layer) in one kernel."""
     x = fast_values(m * 512, 1, 3.0) + 0.25
@@ -312,7 +312,8 @@ def test_ln_linear_gelu_matches_float64(device, m, n):
     np.testing.assert_allclose(out.reshape(m, n), want, rtol=1e-4, atol=2e-5)
 
 
-@pytest.mark.parametrize("estimators,rows", [(1, 1), (1, 2), (1, 5), (8, 1), (4, 2), (3, 3), (2, 250), (3, 17)])
+@pytest.mark.parametrize("estimators,rows", [(1, 1), (1, 2), (1, 5), (8, 1), (4, 2), (3, 3), (1, 16), (2, 8),
+                                             (3, 5), (2, 250), (3, 17)])
 def test_ln_linear_qass_matches_float64(device, estimators, rows):
     """LN1 + Q projection + QASSMax (query MLP and gate per head), head-major."""
     m = estimators * rows

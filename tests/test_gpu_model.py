@@ -98,12 +98,13 @@ def test_pass_rows_and_device_path_do_not_change_results(lcg):
     np.testing.assert_array_equal(dl.to_host(), whole)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 4, 5])
+@pytest.mark.parametrize("rows", [1, 2, 4, 5, 8])
 def test_passes_of_few_rows_match_the_oracle(clf, clf_oracle, lcg, rows):
-    """Calls of 1-5 test rows over two estimators: passes of at most eight
-    (estimator, row) pairs take the small-row products, LayerNorm + linear
-    kernels and 16-row block tails, five rows the split-K products. Checked
-    against the oracle on its own context and against the 512-row passes."""
+    """Calls of 1-8 test rows over two estimators: passes of at most eight
+    (estimator, row) pairs take the small-row products and LayerNorm + linear
+    kernels, sixteen pairs the split-K products and 16-row MFMA tiles, and all
+    of them the 16-row block tails. Checked against the oracle on its own
+    context and against the 512-row passes."""
     x, y, xt, shifts, ctx_cpu, ctx_gpu = lcg
     few = np.ascontiguousarray(xt[:, :rows])
     st = clf.load_context_tensors(ctx_cpu, x.shape, 3, shifts)
