@@ -321,6 +321,20 @@ def test_ensemble_with_feature_permutations(clf, clf_oracle):
     assert_parity(gpu, cpu, "3 estimators")
 
 
+@pytest.mark.parametrize("features", [1, 2, 3])
+def test_contexts_of_one_to_three_features(clf, clf_oracle, features):
+    """Feature counts where the column inputs' (f + 1, f + 2, f + 4) mod H
+    neighbours repeat or are the feature itself, and the row transformer sees
+    5-7 tokens (cpu.rs:818-823 accepts any H >= 1): build and predict on the
+    GPU against the oracle's uncached forward."""
+    x, y, xt, shifts = reference_lcg_data(1, 128, 6, features)
+    ctx = clf.build_context(x, y, class_permutations=shifts)
+    gpu = ctx.predict_raw(xt).logits
+    cpu = clf_oracle.predict_uncached(x, y, xt)
+    assert_parity(gpu, cpu, f"{features} features")
+    assert np.array_equal(gpu[..., :3].argmax(-1), cpu[..., :3].argmax(-1))
+
+
 def test_progress_hook_can_interrupt(clf):
     x, y, xt, _ = reference_lcg_data(2, 128, 8, 5)
     calls = []
