@@ -335,6 +335,23 @@ def test_contexts_of_one_to_three_features(clf, clf_oracle, features):
     assert np.array_equal(gpu[..., :3].argmax(-1), cpu[..., :3].argmax(-1))
 
 
+@pytest.mark.parametrize("classes", [2, 10])
+def test_two_and_ten_classes(clf, clf_oracle, classes):
+    """The fewest and the most classes the classifier takes (label
+    embeddings, logits over `classes` of the 10 outputs, probability
+    aggregation with per-estimator class shifts), two estimators: build and
+    predict on the GPU against the oracle's uncached forward."""
+    x, y, xt, shifts = reference_lcg_data(2, 160, 12, 6, classes=classes)
+    ctx = clf.build_context(x, y, class_permutations=shifts)
+    gpu = ctx.predict_raw(xt).logits
+    cpu = clf_oracle.predict_uncached(x, y, xt)
+    assert_parity(gpu, cpu, f"{classes} classes")
+    assert np.array_equal(gpu[..., :classes].argmax(-1), cpu[..., :classes].argmax(-1))
+    probs = ctx.predict_probabilities(xt)
+    ref = O.aggregate(np.ascontiguousarray(cpu[..., :classes]), shifts)
+    np.testing.assert_allclose(probs, ref, atol=1e-5)
+
+
 def test_progress_hook_can_interrupt(clf):
     x, y, xt, _ = reference_lcg_data(2, 128, 8, 5)
     calls = []
