@@ -86,15 +86,21 @@ def test_gpu_equals_the_closed_form(device, clf_weights, reg_weights, task, name
 
 
 def test_conditioned_weights_end_to_end_1k(device, clf_weights):
-    """1,024 training rows x 54 features, 7 classes, 8 test rows."""
+    """1,024 training rows x 54 features, 7 classes, 8 test rows: one pass of
+    eight rows, then calls of one and three rows (the small-pass kernels'
+    one- and four-row forms) on peaked softmaxes."""
     w = C.conditioned_weights(clf_weights)
     x, y, xt, _ = S.workload_data(S.WORKLOADS["clf-1k"])
     print("conditioned weights, 1,024 x 54", flush=True)
-    gpu = tabicl.Executor("classifier", w, device).build_context(x, y).predict_logits(xt).logits
+    ctx = tabicl.Executor("classifier", w, device).build_context(x, y)
+    gpu = ctx.predict_logits(xt).logits
     O.set_threads(16)
     cpu = O.OracleModel("classifier", w, O.EXACT).predict_uncached(x, y, xt)[..., :7]
     assert_parity(gpu, cpu, "conditioned clf-1k")
     assert np.array_equal(gpu.argmax(-1), cpu.argmax(-1))
+    for rows in (slice(0, 1), slice(1, 4)):
+        part = ctx.predict_logits(np.ascontiguousarray(xt[:, rows])).logits
+        assert_parity(part, cpu[:, rows], f"conditioned clf-1k, rows {rows.start}-{rows.stop - 1}")
 
 
 @pytest.fixture(scope="module")
