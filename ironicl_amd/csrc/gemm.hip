@@ -341,6 +341,63 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
     }
 }
 
+// Small products with K = 512 or 1,024 and a few dozen rows (the 512-wide
+// out-projection and FFN down of passes of 9-64 rows): the split-K tile over
+// eight waves, each taking an eighth of K with all of its operand loads
+// issued before the first product, so a tile costs one memory round trip
+// rather than one per 16-deep step (the four-wave kernel's 8-16 dependent
+// steps). Each wave finishes two of the
+// sixteen accumulator registers: rows (2w % 4) + 8 (w / 2) + 4 half + rr.
+template <int EPI, bool GROUPED, int KW>  // KW: K per wave
+__global__ __launch_bounds__(512) void gemm_splitk8_kernel(GemmArgs p, int tiles_m, int tiles_n, int per_xcd) {
+    constexpr int S = KW / 16;
+    __shared__ float red[8][16][64];
+    const int bid = blockIdx.x;
+    const int tile = (bid % 8) * per_xcd + bid / 8;
+    if (tile >= tiles_m * tiles_n) return;
+    const int tm = tile / tiles_n, tn = tile - (tile / tiles_n) * tiles_n;
+    const int m0 = tm * 32, n0 = tn * 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = lane >> 5, r32 = lane & 31;
+    const float *a = p.a + (long long)min(m0 + r32, p.m - 1) * p.lda + wave * KW + 8 * half;
+    const float *b = p.w + (long long)min(n0 + r32, p.n - 1) * p.k + wave * KW + 8 * half;
+    f32x4 av[S][2], bv[S][2];
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+        av[st][0] = *reinterpret_cast<const f32x4 *>(a + 16 * st);
+        av[st][1] = *reinterpret_cast<const f32x4 *>(a + 16 * st + 4);
+        bv[st][0] = *reinterpret_cast<const f32x4 *>(b + 16 * st);
+        bv[st][1] = *reinterpret_cast<const f32x4 *>(b + 16 * st + 4);
+    }
+    // Left to itself the compiler would sink each load down to its product.
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[st][h][t], bv[st][h][t], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    const int col = n0 + r32;
+    if (col >= p.n) return;
+    const long long coff = col_offset(p.out, col);
+    const float bias = p.bias ? p.bias[col] : 0.f;
+    const int row0 = m0 + (2 * wave) % 4 + 8 * (wave / 2) + 4 * half;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+        const int r = 2 * wave + rr;
+        float v = red[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) v += red[w][r][lane];
+        if (row0 + rr < p.m) store_out<EPI, GROUPED>(p, row0 + rr, col, coff, bias, v);
+    }
+}
+
 // Products of at most eight rows (passes of 1-8 rows: the ICL blocks'
 // out-projection and FFN down, the decoder's last layer). A workgroup stages
 // the rows in LDS once; each of its waves' four 16-lane groups takes one
@@ -440,16 +497,17 @@ Flops work(const GemmArgs &args) {
 
 // Kernel of one epilogue kind and output map.
 template <template <int, bool> class K>
-void dispatch_epilogue(const GemmArgs &args, dim3 grid, hipStream_t stream, int tiles_m, int tiles_n, int per_xcd) {
+void dispatch_epilogue(const GemmArgs &args, dim3 grid, hipStream_t stream, int tiles_m, int tiles_n, int per_xcd,
+                       int threads = 256) {
     const bool grouped = args.out.rows_per_group < args.m;
     const Flops f = work(args);
     KernelTimer timer(kFamGemm, stream, f.flops, f.bytes);
 #define IRX_GEMM_CASE(E)                                                                                         \
     if (args.epilogue == E) {                                                                                    \
         if (grouped)                                                                                             \
-            hipLaunchKernelGGL((K<E, true>::kernel), grid, dim3(256), 0, stream, args, tiles_m, tiles_n, per_xcd); \
+            hipLaunchKernelGGL((K<E, true>::kernel), grid, dim3(threads), 0, stream, args, tiles_m, tiles_n, per_xcd); \
         else                                                                                                     \
-            hipLaunchKernelGGL((K<E, false>::kernel), grid, dim3(256), 0, stream, args, tiles_m, tiles_n, per_xcd); \
+            hipLaunchKernelGGL((K<E, false>::kernel), grid, dim3(threads), 0, stream, args, tiles_m, tiles_n, per_xcd); \
         IRX_HIP(hipGetLastError());                                                                              \
         return;                                                                                                  \
     }
@@ -477,6 +535,20 @@ struct SplitK {
 template <int E, bool G>
 struct SplitKLn {
     static constexpr auto kernel = gemm_splitk_kernel<E, G, true>;
+};
+
+// Rows up to which K = 512 and 1,024 products take the eight-wave split-K:
+// passes of a few dozen rows gain (16-row pass 1.29 -> 1.27 ms), but beside
+// the other stream's attention a 512-row pass's 512-thread, 150-register
+// workgroups cost more than they save (the two-stream step 43.8 -> 46.5 ms).
+constexpr int kSplitK8Rows = 64;
+
+template <int KW>
+struct SplitK8 {
+    template <int E, bool G>
+    struct K {
+        static constexpr auto kernel = gemm_splitk8_kernel<E, G, KW>;
+    };
 };
 
 template <int BM, int BN, int BK = kBK>
@@ -537,6 +609,10 @@ void launch_splitk(const GemmArgs &args, hipStream_t stream) {
     int per_xcd = (tiles_m * tiles_n + 7) / 8;
     if (args.ln_w)
         dispatch_epilogue<SplitKLn>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
+    else if (args.m <= kSplitK8Rows && args.k == 512)
+        dispatch_epilogue<SplitK8<64>::template K>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd, 512);
+    else if (args.m <= kSplitK8Rows && args.k == 1024)
+        dispatch_epilogue<SplitK8<128>::template K>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd, 512);
     else
         dispatch_epilogue<SplitK>(args, dim3(per_xcd * 8), stream, tiles_m, tiles_n, per_xcd);
 }
