@@ -33,15 +33,18 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, const f32x4 &acc) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
 }
 
-template <int EPI>
+// OB: 16-column output blocks per workgroup (4, or 2 for the GELU form of
+// passes of at most 32 rows, which then spread over twice the workgroups).
+template <int EPI, int OB = 4>
 __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
+    static_assert(OB == 4 || (OB == 2 && EPI == kLnGelu), "QASS needs a whole 64-wide head per workgroup");
     __shared__ float red[2][4][kRows];
     __shared__ __attribute__((aligned(16))) float part[4][kRows][68];
     __shared__ __attribute__((aligned(16))) float tile[2][kRows][68];  // QASS: q, then the hidden layer
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int m16 = lane & 15, g = lane >> 4;
     const long long row0 = (long long)blockIdx.x * kRows;
-    const int col0 = 64 * blockIdx.y;
+    const int col0 = 16 * OB * blockIdx.y;
     const long long row = row0 + m16;
     const long long r = row < p.m ? row : p.m - 1;
     const int k0 = 128 * w;
@@ -49,7 +52,7 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
     // x[row][k0 + 16 kb + 4 g + e], and every weight fragment of this wave's
     // quarter up front (columns col0 + 16 ob + lane % 16): the loads' latency
     // is paid once, under the LayerNorm.
-    f32x4 x[8], wf[8][4];
+    f32x4 x[8], wf[8][OB];
     const float *xr = p.x + r * p.ldx + k0 + 4 * g;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) x[kb] = *reinterpret_cast<const f32x4 *>(xr + 16 * kb);
@@ -57,7 +60,7 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
-        for (int ob = 0; ob < 4; ++ob) wf[kb][ob] = *reinterpret_cast<const f32x4 *>(wr + ob * 16 * 512 + 16 * kb);
+        for (int ob = 0; ob < OB; ++ob) wf[kb][ob] = *reinterpret_cast<const f32x4 *>(wr + ob * 16 * 512 + 16 * kb);
     float s = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) s += (x[kb][0] + x[kb][1]) + (x[kb][2] + x[kb][3]);
@@ -89,23 +92,24 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
     }
 
     // This wave's quarter of the product: columns col0 + 16 ob + n, n = lane % 16.
-    f32x4 acc[4];
+    f32x4 acc[OB];
 #pragma unroll
-    for (int ob = 0; ob < 4; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ob = 0; ob < OB; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-            for (int ob = 0; ob < 4; ++ob) acc[ob] = mfma(wf[kb][ob][e], x[kb][e], acc[ob]);
+            for (int ob = 0; ob < OB; ++ob) acc[ob] = mfma(wf[kb][ob][e], x[kb][e], acc[ob]);
 #pragma unroll
-    for (int ob = 0; ob < 4; ++ob)
+    for (int ob = 0; ob < OB; ++ob)
         *reinterpret_cast<f32x4 *>(&part[w][m16][16 * ob + 4 * g]) = acc[ob];
     __syncthreads();
 
     // Thread t finishes row t / 16, columns 4 (t % 16) .. +3.
     const int om = tid >> 4, oc = 4 * (tid & 15);
     const long long orow = row0 + om;
+    if (oc >= 16 * OB) return;  // OB = 2: only the GELU form, which has no barrier after this
     f32x4 v = (*reinterpret_cast<const f32x4 *>(&part[0][om][oc]) + *reinterpret_cast<const f32x4 *>(&part[1][om][oc])) +
               (*reinterpret_cast<const f32x4 *>(&part[2][om][oc]) + *reinterpret_cast<const f32x4 *>(&part[3][om][oc]));
     v += *reinterpret_cast<const f32x4 *>(p.b + col0 + oc);
@@ -310,10 +314,14 @@ void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream) {
             launch_rows<kLnQass>(a, stream);
         else
             launch_rows<kLnGelu>(a, stream);
-    } else if (epilogue == kLnQass)
+    } else if (epilogue == kLnQass) {
         hipLaunchKernelGGL(ln_linear512_kernel<kLnQass>, grid, dim3(256), 0, stream, a);
-    else
+    } else if (a.m <= 32) {
+        const dim3 narrow((unsigned)ceil_div((size_t)a.m, kRows), (unsigned)(a.n / 32));
+        hipLaunchKernelGGL((ln_linear512_kernel<kLnGelu, 2>), narrow, dim3(256), 0, stream, a);
+    } else {
         hipLaunchKernelGGL(ln_linear512_kernel<kLnGelu>, grid, dim3(256), 0, stream, a);
+    }
     IRX_HIP(hipGetLastError());
 }
 
