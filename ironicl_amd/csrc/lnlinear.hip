@@ -33,13 +33,27 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, const f32x4 &acc) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
 }
 
+// Sum of a[0..W-1] as a pairwise tree ((a0 + a1) + (a2 + a3)) + ...
+template <int W, typename F>
+__device__ __forceinline__ auto tree_sum(F a) {
+    if constexpr (W == 4)
+        return (a(0) + a(1)) + (a(2) + a(3));
+    else
+        return ((a(0) + a(1)) + (a(2) + a(3))) + ((a(4) + a(5)) + (a(6) + a(7)));
+}
+
 // OB: 16-column output blocks per workgroup (4, or 2 for the GELU form of
 // passes of at most 32 rows, which then spread over twice the workgroups).
-template <int EPI, int OB = 4>
-__global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
+// W: waves, each taking 512 / W of K (8 for the QASS form of passes of at
+// most 32 rows: half the products and weight loads per wave; waves 4-7 then
+// only pass the barriers of the epilogue).
+template <int EPI, int OB = 4, int W = 4>
+__global__ __launch_bounds__(64 * W) void ln_linear512_kernel(LnLinear p) {
     static_assert(OB == 4 || (OB == 2 && EPI == kLnGelu), "QASS needs a whole 64-wide head per workgroup");
-    __shared__ float red[2][4][kRows];
-    __shared__ __attribute__((aligned(16))) float part[4][kRows][68];
+    static_assert(W == 4 || W == 8, "four or eight waves");
+    constexpr int KB = 32 / W;  // 16-wide k-blocks per wave
+    __shared__ float red[2][W][kRows];
+    __shared__ __attribute__((aligned(16))) float part[W][kRows][68];
     __shared__ __attribute__((aligned(16))) float tile[2][kRows][68];  // QASS: q, then the hidden layer
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int m16 = lane & 15, g = lane >> 4;
@@ -47,31 +61,31 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
     const int col0 = 16 * OB * blockIdx.y;
     const long long row = row0 + m16;
     const long long r = row < p.m ? row : p.m - 1;
-    const int k0 = 128 * w;
+    const int k0 = 16 * KB * w;
 
     // x[row][k0 + 16 kb + 4 g + e], and every weight fragment of this wave's
     // quarter up front (columns col0 + 16 ob + lane % 16): the loads' latency
     // is paid once, under the LayerNorm.
-    f32x4 x[8], wf[8][OB];
+    f32x4 x[KB], wf[KB][OB];
     const float *xr = p.x + r * p.ldx + k0 + 4 * g;
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) x[kb] = *reinterpret_cast<const f32x4 *>(xr + 16 * kb);
+    for (int kb = 0; kb < KB; ++kb) x[kb] = *reinterpret_cast<const f32x4 *>(xr + 16 * kb);
     const float *wr = p.w + (long long)(col0 + m16) * 512 + k0 + 4 * g;
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int ob = 0; ob < OB; ++ob) wf[kb][ob] = *reinterpret_cast<const f32x4 *>(wr + ob * 16 * 512 + 16 * kb);
     float s = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) s += (x[kb][0] + x[kb][1]) + (x[kb][2] + x[kb][3]);
+    for (int kb = 0; kb < KB; ++kb) s += (x[kb][0] + x[kb][1]) + (x[kb][2] + x[kb][3]);
     s += __shfl_xor(s, 16, 64);
     s += __shfl_xor(s, 32, 64);
     if (g == 0) red[0][w][m16] = s;
     __syncthreads();
-    const float mean = ((red[0][0][m16] + red[0][1][m16]) + (red[0][2][m16] + red[0][3][m16])) / 512.f;
+    const float mean = tree_sum<W>([&](int i) { return red[0][i][m16]; }) / 512.f;
     float sq = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float d = x[kb][e] - mean;
@@ -81,10 +95,10 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
     sq += __shfl_xor(sq, 32, 64);
     if (g == 0) red[1][w][m16] = sq;
     __syncthreads();
-    const float var = ((red[1][0][m16] + red[1][1][m16]) + (red[1][2][m16] + red[1][3][m16])) / 512.f;
+    const float var = tree_sum<W>([&](int i) { return red[1][i][m16]; }) / 512.f;
     const float rstd = 1.0f / sqrtf(var + 1e-5f);
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
         const f32x4 lw = *reinterpret_cast<const f32x4 *>(p.lnw + k0 + 16 * kb + 4 * g);
         const f32x4 lb = *reinterpret_cast<const f32x4 *>(p.lnb + k0 + 16 * kb + 4 * g);
 #pragma unroll
@@ -96,7 +110,7 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
 #pragma unroll
     for (int ob = 0; ob < OB; ++ob) acc[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -106,29 +120,32 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
         *reinterpret_cast<f32x4 *>(&part[w][m16][16 * ob + 4 * g]) = acc[ob];
     __syncthreads();
 
-    // Thread t finishes row t / 16, columns 4 (t % 16) .. +3.
-    const int om = tid >> 4, oc = 4 * (tid & 15);
+    // Threads 0-255 finish row t / 16, columns 4 (t % 16) .. +3.
+    const int om = (tid >> 4) & (kRows - 1), oc = 4 * (tid & 15);
+    const bool finisher = tid < 16 * kRows;
     const long long orow = row0 + om;
     if (oc >= 16 * OB) return;  // OB = 2: only the GELU form, which has no barrier after this
-    f32x4 v = (*reinterpret_cast<const f32x4 *>(&part[0][om][oc]) + *reinterpret_cast<const f32x4 *>(&part[1][om][oc])) +
-              (*reinterpret_cast<const f32x4 *>(&part[2][om][oc]) + *reinterpret_cast<const f32x4 *>(&part[3][om][oc]));
+    f32x4 v = tree_sum<W>([&](int i) { return *reinterpret_cast<const f32x4 *>(&part[i][om][oc]); });
     v += *reinterpret_cast<const f32x4 *>(p.b + col0 + oc);
     if constexpr (EPI == kLnGelu) {
-        if (orow < p.m) {
+        if (finisher && orow < p.m) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
             *reinterpret_cast<f32x4 *>(p.out + orow * p.ldo + col0 + oc) = v;
         }
     } else {
-        // The head's query tile, then its MLP: wave w computes columns 16 w .. 16 w + 15
-        // of each layer from the whole previous tile.
+        // The head's query tile, then its MLP: wave w < 4 computes columns
+        // 16 w .. 16 w + 15 of each layer from the whole previous tile (with
+        // eight waves, waves 4-7 only pass the barriers).
+        const bool mlp = w < 4;
+        const int wq = w & 3;
         f32x4 mw[2][4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            mw[0][kb] = *reinterpret_cast<const f32x4 *>(p.qm0w + (16 * w + m16) * 64 + 16 * kb + 4 * g);
-            mw[1][kb] = *reinterpret_cast<const f32x4 *>(p.qm2w + (16 * w + m16) * 64 + 16 * kb + 4 * g);
+            mw[0][kb] = *reinterpret_cast<const f32x4 *>(p.qm0w + (16 * wq + m16) * 64 + 16 * kb + 4 * g);
+            mw[1][kb] = *reinterpret_cast<const f32x4 *>(p.qm2w + (16 * wq + m16) * 64 + 16 * kb + 4 * g);
         }
-        *reinterpret_cast<f32x4 *>(&tile[0][om][oc]) = v;
+        if (finisher) *reinterpret_cast<f32x4 *>(&tile[0][om][oc]) = v;
         __syncthreads();
         auto layer = [&](const f32x4 *wt, const float *bias, int src) {
             f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -138,16 +155,18 @@ __global__ __launch_bounds__(256) void ln_linear512_kernel(LnLinear p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) a = mfma(wt[kb][e], xf[e], a);
             }
-            return a + *reinterpret_cast<const f32x4 *>(bias + 16 * w + 4 * g);
+            return a + *reinterpret_cast<const f32x4 *>(bias + 16 * wq + 4 * g);
         };
-        f32x4 h = layer(mw[0], p.qm0b, 0);
+        if (mlp) {
+            f32x4 h = layer(mw[0], p.qm0b, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = gelu_erf(h[e]);
-        *reinterpret_cast<f32x4 *>(&tile[1][m16][16 * w + 4 * g]) = h;
+            for (int e = 0; e < 4; ++e) h[e] = gelu_erf(h[e]);
+            *reinterpret_cast<f32x4 *>(&tile[1][m16][16 * wq + 4 * g]) = h;
+        }
         __syncthreads();
-        const f32x4 gm = layer(mw[1], p.qm2b, 1);
-        if (row < p.m) {
-            const int head = blockIdx.y, col = 16 * w + 4 * g;
+        if (mlp && row < p.m) {
+            const f32x4 gm = layer(mw[1], p.qm2b, 1);
+            const int head = blockIdx.y, col = 16 * wq + 4 * g;
             const f32x4 q = *reinterpret_cast<const f32x4 *>(&tile[0][m16][col]);
             const f32x4 base = *reinterpret_cast<const f32x4 *>(p.base + head * 64 + col);
             f32x4 o;
@@ -314,6 +333,8 @@ void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream) {
             launch_rows<kLnQass>(a, stream);
         else
             launch_rows<kLnGelu>(a, stream);
+    } else if (epilogue == kLnQass && a.m <= 32) {
+        hipLaunchKernelGGL((ln_linear512_kernel<kLnQass, 4, 8>), grid, dim3(512), 0, stream, a);
     } else if (epilogue == kLnQass) {
         hipLaunchKernelGGL(ln_linear512_kernel<kLnQass>, grid, dim3(256), 0, stream, a);
     } else if (a.m <= 32) {

@@ -313,7 +313,7 @@ def test_ln_linear_gelu_matches_float64(device, m, n):
 
 
 @pytest.mark.parametrize("estimators,rows", [(1, 1), (1, 2), (1, 5), (8, 1), (4, 2), (3, 3), (1, 16), (2, 8),
-                                             (3, 5), (2, 250), (3, 17)])
+                                             (3, 5), (1, 32), (4, 8), (3, 11), (2, 250), (3, 17)])
 def test_ln_linear_qass_matches_float64(device, estimators, rows):
     """LN1 + Q projection + QASSMax (query MLP and gate per head), head-major."""
     m = estimators * rows
