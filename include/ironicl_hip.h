@@ -421,6 +421,16 @@ int irx_test_small_attention(irx_device *device, const float *q, const float *k,
 int irx_test_small_attention_rope(irx_device *device, const float *q, const float *k, const float *v,
                                   const float *rope_cos, const float *rope_sin, size_t heads, size_t query_rows,
                                   size_t rows, float *out);
+/* Token-major sequences q [seqs, query_rows, heads, 16], k and v [seqs, rows,
+ * heads, 16] (a token's heads adjacent, as in the row transformer), RoPE
+ * tables as above or null, through the kernel `method` picks: 0 the
+ * library's choice, 1 the per-wave and long-range kernels, 2 the staged
+ * kernel (every key of an item in LDS once; more than 16 queries, at most 512
+ * keys). With reps > 0 the launch is then repeated reps times on the null
+ * stream and *ms_per_launch receives the mean launch time from HIP events. */
+int irx_test_small_attention_tokens(irx_device *device, int method, const float *q, const float *k, const float *v,
+                                    const float *rope_cos, const float *rope_sin, size_t seqs, size_t heads,
+                                    size_t query_rows, size_t rows, float *out, int reps, float *ms_per_launch);
 
 #ifdef __cplusplus
 }

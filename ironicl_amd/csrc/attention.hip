@@ -48,6 +48,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+// This file builds with IEEE mode off (-mno-amdgpu-ieee), which the device
+// library's work-item functions were not built with, so they would stay
+// out-of-line calls returning ids in VGPRs: ids come from the builtins.
+__device__ __forceinline__ int tid_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int bid_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int bdim_x() { return (int)__builtin_amdgcn_workgroup_size_x(); }
+
 constexpr int kKeyTile = 64;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -94,7 +101,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
     __shared__ __attribute__((aligned(16))) IclTile tiles[2];
 
     const int total = g.qtiles * p.pairs * g.splits;
-    const int bid = blockIdx.x;
+    const int bid = bid_x();
     const int t_id = (bid % 8) * g.per_xcd + bid / 8;
     if (t_id >= total) return;
     const int qt = t_id % g.qtiles;
@@ -105,7 +112,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
     const int k_begin = __builtin_amdgcn_readfirstlane(split * g.keys_per_split);
     const int k_end = __builtin_amdgcn_readfirstlane(min(p.kv_rows, k_begin + g.keys_per_split));
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = tid_x(), lane = tid & 63, wave = tid >> 6;
     const int half = lane >> 5, r32 = lane & 31;
     // Query block j of this wave holds rows qrow0 + 32 j.
     const int qrow0 = qt * kIclQueries + wave * 64 + r32;
@@ -439,7 +446,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
     __shared__ __attribute__((aligned(16))) std::conditional_t<FP8, IclTile8, IclTile16> tiles[2];
 
     const int total = g.qtiles * p.pairs * g.splits;
-    const int bid = blockIdx.x;
+    const int bid = bid_x();
     const int t_id = (bid % 8) * g.per_xcd + bid / 8;
     if (t_id >= total) return;
     const int qt = t_id % g.qtiles;
@@ -450,7 +457,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
     const int k_end = __builtin_amdgcn_readfirstlane(min(p.kv_rows, k_begin + g.keys_per_split));
     const int n_pad = (p.kv_rows + kKeyTile - 1) / kKeyTile * kKeyTile;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = tid_x(), lane = tid & 63, wave = tid >> 6;
     const int half = lane >> 5, r32 = lane & 31;
     const int qrow0 = qt * kIclQueries + wave * 64 + r32;
 
@@ -697,13 +704,13 @@ __global__ __launch_bounds__(256) void pack_icl16_kernel(const T *k, const T *v,
                                                          unsigned short *k16, unsigned short *v16, unsigned *bad) {
     __shared__ float tile[64][65];
     const int tiles = (int)((rows + kKeyTile - 1) / kKeyTile);
-    const int pair = blockIdx.x / tiles, tix = blockIdx.x % tiles;
+    const int pair = bid_x() / tiles, tix = bid_x() % tiles;
     const long long n_pad = (long long)tiles * kKeyTile;
     const long long k0 = (long long)tix * kKeyTile;
     const T *ks = k + (long long)pair * rows * 64, *vs = v + (long long)pair * rows * 64;
     unsigned short *kd = k16 + ((long long)pair * n_pad + k0) * 64, *vd = v16 + ((long long)pair * n_pad + k0) * 64;
     unsigned local_bad = 0;
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    for (int i = tid_x(); i < 64 * 64; i += 256) {
         const int key = i / 64, d = i % 64;
         const bool in = k0 + key < rows;
         const float kv = in ? (float)ks[(k0 + key) * 64 + d] : 0.f;
@@ -716,7 +723,7 @@ __global__ __launch_bounds__(256) void pack_icl16_kernel(const T *k, const T *v,
     __syncthreads();
     // V^T: row d holds the tile's keys in the stored order (positions 4..7 and
     // 8..11 of each 16-key group swapped).
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    for (int i = tid_x(); i < 64 * 64; i += 256) {
         const int d = i / 64, pos = i % 64;
         const int q16 = pos & 15, swap = (q16 >= 4 && q16 < 8) ? 4 : (q16 >= 8 && q16 < 12 ? -4 : 0);
         const int key = (pos & ~15) + q16 + swap;
@@ -730,11 +737,11 @@ __global__ __launch_bounds__(256) void unpack_icl16_kernel(const unsigned short 
                                                            long long rows, int pairs, unsigned short *k,
                                                            unsigned short *v) {
     const int tiles = (int)((rows + kKeyTile - 1) / kKeyTile);
-    const int pair = blockIdx.x / tiles, tix = blockIdx.x % tiles;
+    const int pair = bid_x() / tiles, tix = bid_x() % tiles;
     const long long n_pad = (long long)tiles * kKeyTile, k0 = (long long)tix * kKeyTile;
     const unsigned short *ks = k16 + ((long long)pair * n_pad + k0) * 64;
     const unsigned short *vs = v16 + ((long long)pair * n_pad + k0) * 64;
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    for (int i = tid_x(); i < 64 * 64; i += 256) {
         const int key = i / 64, d = i % 64;
         if (k0 + key >= rows) continue;
         const int q16 = key & 15, swap = (q16 >= 4 && q16 < 8) ? 4 : (q16 >= 8 && q16 < 12 ? -4 : 0);
@@ -769,8 +776,8 @@ template <int QG, bool SPLIT>
 __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAttention p, IclLaunch g) {
     __shared__ float red_o[kDecodeWaves][QG * 16 * kDecodeOStride];
     __shared__ float red_m[kDecodeWaves][QG * 16], red_l[kDecodeWaves][QG * 16];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 4, i16 = lane & 15;
-    const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
+    const int wave = tid_x() >> 6, lane = tid_x() & 63, grp = lane >> 4, i16 = lane & 15;
+    const int split = bid_x() % g.splits, pair = bid_x() / g.splits;
     const int k_begin = split * g.keys_per_split;
     const int k_end = min(p.kv_rows, k_begin + g.keys_per_split);
 
@@ -914,7 +921,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
     // A wave that got no block has reference -inf and sum 0.
 #pragma unroll
     for (int j = 0; j < QG; ++j) {
-        const int qi = (threadIdx.x >> 4) + 16 * j, d = 4 * (threadIdx.x & 15);
+        const int qi = (tid_x() >> 4) + 16 * j, d = 4 * (tid_x() & 15);
         if (qi >= p.q_rows) continue;
         float mx = -INFINITY;
 #pragma unroll
@@ -959,8 +966,8 @@ template <int QG, bool SPLIT, bool FP8 = false>
 __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclAttention p, IclLaunch g) {
     __shared__ float red_o[kDecodeWaves][QG * 16 * kDecodeOStride];
     __shared__ float red_m[kDecodeWaves][QG * 16], red_l[kDecodeWaves][QG * 16];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane >> 4, i16 = lane & 15;
-    const int split = blockIdx.x % g.splits, pair = blockIdx.x / g.splits;
+    const int wave = tid_x() >> 6, lane = tid_x() & 63, grp = lane >> 4, i16 = lane & 15;
+    const int split = bid_x() % g.splits, pair = bid_x() / g.splits;
     const int k_begin = split * g.keys_per_split;
     const int k_end = min(p.kv_rows, k_begin + g.keys_per_split);
     const int n_pad = (p.kv_rows + kKeyTile - 1) / kKeyTile * kKeyTile;
@@ -1163,7 +1170,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < QG; ++j) {
-        const int qi = (threadIdx.x >> 4) + 16 * j, d = 4 * (threadIdx.x & 15);
+        const int qi = (tid_x() >> 4) + 16 * j, d = 4 * (tid_x() & 15);
         if (qi >= p.q_rows) continue;
         float mx = -INFINITY;
 #pragma unroll
@@ -1199,9 +1206,9 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
 // reference; the four groups are combined at the end.
 constexpr int kMergePerGroup = 16;
 __global__ __launch_bounds__(64) void icl_merge_kernel(IclAttention p, int splits, int q_padded) {
-    const long long pq = blockIdx.x;
+    const long long pq = bid_x();
     if (pq >= (long long)p.pairs * p.q_rows) return;
-    const int lane = threadIdx.x & 63, sg = lane >> 4, d = (lane & 15) * 4;
+    const int lane = tid_x() & 63, sg = lane >> 4, d = (lane & 15) * 4;
     const int qrow = (int)(pq % p.q_rows);
     const int pair = (int)(pq / p.q_rows);
     const long long step = (long long)p.pairs * q_padded;  // rows between splits
@@ -1264,9 +1271,9 @@ __global__ __launch_bounds__(64) void icl_merge_kernel(IclAttention p, int split
 // at 2.7 TB/s).
 template <int MAXS>
 __global__ __launch_bounds__(256) void icl_merge_rows_kernel(IclAttention p, int splits, int q_padded) {
-    const long long pq = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const long long pq = (long long)bid_x() * 16 + (tid_x() >> 4);
     if (pq >= (long long)p.pairs * p.q_rows) return;
-    const int d = (threadIdx.x & 15) * 4;
+    const int d = (tid_x() & 15) * 4;
     const int qrow = (int)(pq % p.q_rows);
     const int pair = (int)(pq / p.q_rows);
     const long long step = (long long)p.pairs * q_padded;
@@ -1376,9 +1383,9 @@ __global__ __launch_bounds__(64 * kLongWaves) void small_attention_long_kernel(S
                                                                                int splits, int keys_per_split) {
     __shared__ __attribute__((aligned(16))) float red_o[kLongWaves][QG * 16 * kLongOStride];
     __shared__ float red_m[kLongWaves][QG * 16], red_l[kLongWaves][QG * 16];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
-    const int split = blockIdx.x % splits;
-    const int unit = blockIdx.x / splits;
+    const int wave = tid_x() >> 6, lane = tid_x() & 63, g = lane >> 4, l16 = lane & 15;
+    const int split = bid_x() % splits;
+    const int unit = bid_x() / splits;
     const int qc = unit % qchunks, item = unit / qchunks;
     const int head = item % p.heads, seq = item / p.heads;
     const int gs = seq / p.group, sq = seq - gs * p.group;
@@ -1513,7 +1520,7 @@ __global__ __launch_bounds__(64 * kLongWaves) void small_attention_long_kernel(S
     __syncthreads();
     // Merge: thread t takes query t / 2 of the chunk, dims 8 (t % 2) .. +7. A
     // wave that got no block has reference -inf and sum 0; wave 0 always has one.
-    const int qi = threadIdx.x >> 1, d0 = 8 * (threadIdx.x & 1);
+    const int qi = tid_x() >> 1, d0 = 8 * (tid_x() & 1);
     const int row = q0 + qi;
     if (qi >= QG * 16 || row >= p.q_rows) return;
     float mx = -INFINITY;
@@ -1545,7 +1552,7 @@ __global__ __launch_bounds__(64 * kLongWaves) void small_attention_long_kernel(S
 // and head, query, four dims).
 __global__ __launch_bounds__(256) void small_merge_kernel(SmallAttention p, int splits) {
     const long long items = (long long)p.seqs * p.heads;
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long idx = (long long)bid_x() * 256 + tid_x();
     const int c = (int)(idx & 3);
     const long long unit = idx >> 2;
     if (unit >= items * p.q_rows) return;
@@ -1593,9 +1600,9 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
     __shared__ __attribute__((aligned(16))) float Vt[16 * VSTRIDE];
     // Workgroup j of a (sequence, head) item: its WAVES waves take query chunks
     // (j * WAVES + wave) + k * groups_per_seq * WAVES and share the staged keys.
-    const int item = blockIdx.x / groups_per_seq;
-    const int wave = threadIdx.x >> 6;
-    const int c_first = (blockIdx.x - item * groups_per_seq) * WAVES + wave;
+    const int item = bid_x() / groups_per_seq;
+    const int wave = tid_x() >> 6;
+    const int c_first = (bid_x() - item * groups_per_seq) * WAVES + wave;
     const int c_step = groups_per_seq * WAVES;
     const int head = item % p.heads, seq = item / p.heads;
     const int gq = seq / p.group, sq = seq - gq * p.group;
@@ -1603,12 +1610,12 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
     const float *kb = p.k + gq * p.k_group + sq * p.k_seq + head * p.k_head;
     const float *vb = p.v + gq * p.v_group + sq * p.v_seq + head * p.v_head;
     float *ob = p.o + gq * p.o_group + sq * p.o_seq + head * p.o_head;
-    const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+    const int lane = tid_x() & 63, g = lane >> 4, l16 = lane & 15;
     const int kv = p.kv_rows;
     const int kblocks = (kv + 15) / 16;
 
     // Stage K (rotated) as [key][20] and V transposed as [dim][KEYS + 4]; keys past kv are zero.
-    for (int key = threadIdx.x; key < kblocks * 16; key += 64 * WAVES) {
+    for (int key = tid_x(); key < kblocks * 16; key += 64 * WAVES) {
         float kr[16], vr[16];
         if (key < kv) {
 #pragma unroll
@@ -1757,6 +1764,206 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
     }
 }
 
+// ---- 16-wide heads, every key staged once per item, query blocks over waves ----
+//
+// The row transformer's self-attention (row_embedding, cpu.rs:1226-1266:
+// H + 4 tokens per row, RoPE on queries and keys) and the CLS block's four
+// queries over every token. One workgroup of W waves per (sequence, head,
+// chunk of W * NG query blocks of 16): its threads stage the item's keys once
+// (RoPE applied, rows padded to 20 floats) and the values transposed into
+// LDS, then wave w takes the chunk's blocks w, w + W, ... (NG of them) over
+// every key, with the lazy running softmax of the long kernel: the scores
+// are exp2 against a reference that moves only when a lane's four
+// probabilities would sum past 2^64. The first key block sets the reference
+// from its own maxima, so no block is computed twice unless a score rises
+// 64 (log2 units) above it. A wave ends with its queries' final outputs: no
+// merge between waves or workgroups. Products on v_mfma_f32_16x16x4f32 in
+// the long kernel's transposed layout (S^T = K Q^T, O^T = V^T P^T).
+// Workgroups of one XCD take consecutive items, so the 8 heads of a
+// sequence, which share each token's 128-byte lines, are read into one L2.
+constexpr int kStagedKStride = 20;
+
+template <int NG, int KMAX, bool ROPE>
+__global__ __launch_bounds__(1024, NG == 1 ? 8 : NG == 2 ? 6 : 4) void staged_attention_kernel(SmallAttention p, int chunks, int per_xcd) {
+    constexpr int VSTRIDE = KMAX + 4;
+    __shared__ __attribute__((aligned(16))) float Ks[KMAX * kStagedKStride];
+    __shared__ __attribute__((aligned(16))) float Vt[16 * VSTRIDE];
+    // Index arithmetic in 32 bits (the launcher caps units below 2^31), with
+    // shifts for the row transformer's 8 heads and one chunk per item.
+    const int unit = (int)(bid_x() & 7) * per_xcd + (int)(bid_x() >> 3);
+    if (unit >= p.seqs * p.heads * chunks) return;
+    const int chunk = chunks == 1 ? 0 : unit % chunks;
+    const int item = chunks == 1 ? unit : unit / chunks;
+    const int head = p.heads == 8 ? (item & 7) : item % p.heads;
+    const int seq = p.heads == 8 ? (item >> 3) : item / p.heads;
+    const int gs = p.group >= p.seqs ? 0 : seq / p.group, sq = seq - gs * p.group;
+    const float *qb = p.q + gs * p.q_group + sq * p.q_seq + head * p.q_head;
+    const float *kb = p.k + gs * p.k_group + sq * p.k_seq + head * p.k_head;
+    const float *vb = p.v + gs * p.v_group + sq * p.v_seq + head * p.v_head;
+    float *ob = p.o + gs * p.o_group + sq * p.o_seq + head * p.o_head;
+    const int waves = bdim_x() >> 6, wave = tid_x() >> 6;
+    const int lane = tid_x() & 63, g = lane >> 4, l16 = lane & 15;
+    const int kv = p.kv_rows, kblocks = (kv + 15) >> 4;
+    const int first_block = chunk * waves * NG + wave;
+
+    // Stage K (rotated) as [key][20] and V^T as [dim][KMAX + 4]; keys past kv
+    // are zero. Thread t takes dims 4 c .. +3 (c = t / 16 % 4) of key
+    // 16 (t / 64) + t % 16: each 16-lane phase of a store covers 16
+    // consecutive keys of one chunk, which no two lanes' banks share in
+    // either layout. RoPE pairs dim d with d ^ 8, chunk c with c ^ 2.
+    // Offsets within an item are 32-bit (the launcher checks), added to the
+    // workgroup-uniform bases.
+    const unsigned k_row = (unsigned)p.k_row, v_row = (unsigned)p.v_row;
+    const unsigned q_row = (unsigned)p.q_row, o_row = (unsigned)p.o_row;
+    for (int t = tid_x(); t < kblocks * 64; t += bdim_x()) {
+        const unsigned key = ((t >> 6) << 4) | (t & 15), c = (t >> 4) & 3;
+        f32x4 kc = {0.f, 0.f, 0.f, 0.f}, vc = kc;
+        if (key < (unsigned)kv) {
+            kc = *reinterpret_cast<const f32x4 *>(kb + (key * k_row + 4 * c));
+            vc = *reinterpret_cast<const f32x4 *>(vb + (key * v_row + 4 * c));
+            if constexpr (ROPE) {
+                const f32x4 kp = *reinterpret_cast<const f32x4 *>(kb + (key * k_row + 4 * (c ^ 2)));
+                const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_cos + (key * 16 + 4 * c));
+                const f32x4 sn = *reinterpret_cast<const f32x4 *>(p.rope_sin + (key * 16 + 4 * c));
+                kc = kc * cs + kp * sn;
+            }
+        }
+        *reinterpret_cast<f32x4 *>(&Ks[key * kStagedKStride + 4 * c]) = kc;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Vt[(4 * c + e) * VSTRIDE + key] = vc[e];
+    }
+
+    // This wave's queries, rotated and scaled into the exp2 domain: lane
+    // (j, g) holds dims 4 g .. +3 of query 16 (first_block + n waves) + j.
+    f32x4 qf[NG];
+    {
+        const float scale = p.scale * kLog2e;
+#pragma unroll
+        for (int n = 0; n < NG; ++n) {
+            const unsigned row = 16 * (first_block + n * waves) + l16;
+            f32x4 q = {0.f, 0.f, 0.f, 0.f};
+            if (row < (unsigned)p.q_rows) {
+                q = *reinterpret_cast<const f32x4 *>(qb + (row * q_row + 4 * g));
+                if constexpr (ROPE) {
+                    const f32x4 qp = *reinterpret_cast<const f32x4 *>(qb + (row * q_row + 4 * (g ^ 2)));
+                    const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_cos + (row * 16 + 4 * g));
+                    const f32x4 sn = *reinterpret_cast<const f32x4 *>(p.rope_sin + (row * 16 + 4 * g));
+                    q = q * cs + qp * sn;
+                }
+            }
+            qf[n] = q * scale;
+        }
+    }
+    __syncthreads();
+
+    f32x4 o[NG], neg[NG];
+    float l_run[NG];
+    constexpr float kLazyLimit = 18446744073709551616.0f;  // 2^64
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    // Maximum / sum over the four lanes l16 + 16 g that share a query.
+    auto quad_max = [](float m) {
+        auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+        m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+        auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+        return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    };
+    auto quad_sum = [](float m) {
+        auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+        m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+        auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+        return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+    };
+    const float *k_lane = &Ks[l16 * kStagedKStride + 4 * g], *v_lane = &Vt[l16 * VSTRIDE + 4 * g];
+    auto load_k = [&](int b) { return *reinterpret_cast<const f32x4 *>(k_lane + b * (16 * kStagedKStride)); };
+    auto load_v = [&](int b) { return *reinterpret_cast<const f32x4 *>(v_lane + b * 16); };
+    // Key block b with operands kf, vf. FIRST: the reference is this block's
+    // maximum. MASK: keys at or past kv score -inf (only the last block can
+    // hold them).
+    auto block = [&]<bool FIRST, bool MASK>(int b, const f32x4 &kf, const f32x4 &vf) {
+        auto scores = [&](int n, const f32x4 &init) {
+            f32x4 s = init;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[n][st], s, 0, 0, 0);
+            if constexpr (MASK) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (16 * b + 4 * g + r >= kv) s[r] = -INFINITY;
+            }
+            return s;
+        };
+#pragma unroll
+        for (int n = 0; n < NG; ++n) {
+            f32x4 s;
+            if constexpr (FIRST) {
+                const f32x4 t = scores(n, zero4);
+                const float m = quad_max(fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])));
+                neg[n] = f32x4{-m, -m, -m, -m};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] = __builtin_amdgcn_exp2f(t[r] - m);
+                l_run[n] = (s[0] + s[1]) + (s[2] + s[3]);
+            } else {
+                s = scores(n, neg[n]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] = __builtin_amdgcn_exp2f(s[r]);
+                float lsum = (s[0] + s[1]) + (s[2] + s[3]);
+                if (__any(!(lsum <= kLazyLimit))) {
+                    const f32x4 t = scores(n, zero4);
+                    const float m_old = -neg[n][0];
+                    const float m_new = fmaxf(m_old, quad_max(fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]))));
+                    const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);
+                    l_run[n] *= alpha;
+                    o[n] *= alpha;
+                    neg[n] = f32x4{-m_new, -m_new, -m_new, -m_new};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[r] = __builtin_amdgcn_exp2f(t[r] - m_new);
+                    lsum = (s[0] + s[1]) + (s[2] + s[3]);
+                }
+                l_run[n] += lsum;
+            }
+            f32x4 acc = FIRST ? zero4 : o[n];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[i], s[i], acc, 0, 0, 0);
+            o[n] = acc;
+        }
+    };
+    const bool ragged = kv < kblocks * 16;
+    if (kblocks == 1) {
+        if (ragged)
+            block.template operator()<true, true>(0, load_k(0), load_v(0));
+        else
+            block.template operator()<true, false>(0, load_k(0), load_v(0));
+    } else {
+        // Each block's operands are read from LDS a block ahead, into two
+        // register sets in turn: (ka, va) holds block b's at the loop's top.
+        f32x4 ka = load_k(1), va = load_v(1);
+        block.template operator()<true, false>(0, load_k(0), load_v(0));
+        const int full_end = ragged ? kblocks - 1 : kblocks;
+        int b = 1;
+        for (; b + 2 <= full_end; b += 2) {
+            const f32x4 kb2 = load_k(b + 1), vb2 = load_v(b + 1);
+            block.template operator()<false, false>(b, ka, va);
+            const int nb = min(b + 2, kblocks - 1);
+            ka = load_k(nb), va = load_v(nb);
+            block.template operator()<false, false>(b + 1, kb2, vb2);
+        }
+        if (b < full_end) {
+            block.template operator()<false, false>(b, ka, va);
+            ++b;
+            ka = load_k(min(b, kblocks - 1)), va = load_v(min(b, kblocks - 1));
+        }
+        if (ragged) block.template operator()<false, true>(kblocks - 1, ka, va);
+    }
+
+    // Lane (j, g) holds O[query][dims 4 g .. +3]; the query's sum is over its four lanes.
+#pragma unroll
+    for (int n = 0; n < NG; ++n) {
+        const float l = quad_sum(l_run[n]);
+        const unsigned row = 16 * (first_block + n * waves) + l16;
+        if (row < (unsigned)p.q_rows)
+            *reinterpret_cast<f32x4 *>(ob + (row * o_row + 4 * g)) = o[n] * __builtin_amdgcn_rcpf(l);
+    }
+}
+
 }  // namespace
 
 int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units, bool f16) {
@@ -1891,6 +2098,67 @@ LongPlan plan_long(const SmallAttention &a) {
     return p;
 }
 
+// Launch shape of staged_attention_kernel: one chunk of query blocks per item
+// where a workgroup of at most 16 waves holds them (one block per wave up to
+// 16 blocks, two up to 32), else chunks of 64 blocks (16 waves of four).
+struct StagedPlan {
+    int ng, waves, chunks, kmax;
+};
+
+StagedPlan plan_staged(const SmallAttention &a) {
+    StagedPlan p{};
+    const int groups = (int)ceil_div(a.q_rows, 16);
+    if (groups <= 16) {
+        p.ng = 1, p.waves = groups, p.chunks = 1;
+    } else if (groups <= 32) {
+        p.ng = 2, p.waves = (int)ceil_div(groups, 2), p.chunks = 1;
+    } else {
+        p.ng = 4, p.waves = 16, p.chunks = (int)ceil_div(groups, 64);
+    }
+    const int kp = (int)ceil_div(a.kv_rows, 16) * 16;
+    p.kmax = kp <= 80 ? 80 : kp <= 128 ? 128 : kp <= 256 ? 256 : kp <= 512 ? 512 : 0;
+    return p;
+}
+
+// The staged kernel serves self-attention-shaped items: more than one query
+// block and at most 512 keys.
+bool staged_applies(const SmallAttention &a) { return a.q_rows > 16 && a.kv_rows <= 512; }
+
+void launch_staged(const SmallAttention &a, hipStream_t stream) {
+    const StagedPlan plan = plan_staged(a);
+    const long long units = (long long)a.seqs * a.heads * plan.chunks;
+    const long long per_xcd = ceil_div(units, 8);
+    if (per_xcd * 8 > 0x7fffffffLL) fail(3, "small attention grid is too large");
+    const long long span = std::max<long long>({(long long)a.q_rows * a.q_row, (long long)a.kv_rows * a.k_row,
+                                                (long long)a.kv_rows * a.v_row, (long long)a.q_rows * a.o_row});
+    if (span + 64 > 0x7fffffffLL) fail(3, "small attention rows are too far apart for the staged kernel");
+    const dim3 blocks((unsigned)(per_xcd * 8)), threads(64 * plan.waves);
+    const bool rope = a.rope_cos != nullptr;
+#define IRX_STAGED_CASE(NG, KMAX)                                                                               \
+    if (plan.ng == NG && plan.kmax == KMAX) {                                                                   \
+        if (rope)                                                                                               \
+            hipLaunchKernelGGL((staged_attention_kernel<NG, KMAX, true>), blocks, threads, 0, stream, a,        \
+                               plan.chunks, (int)per_xcd);                                                      \
+        else                                                                                                    \
+            hipLaunchKernelGGL((staged_attention_kernel<NG, KMAX, false>), blocks, threads, 0, stream, a,       \
+                               plan.chunks, (int)per_xcd);                                                      \
+    }
+    IRX_STAGED_CASE(1, 80)
+    IRX_STAGED_CASE(1, 128)
+    IRX_STAGED_CASE(1, 256)
+    IRX_STAGED_CASE(1, 512)
+    IRX_STAGED_CASE(2, 80)
+    IRX_STAGED_CASE(2, 128)
+    IRX_STAGED_CASE(2, 256)
+    IRX_STAGED_CASE(2, 512)
+    IRX_STAGED_CASE(4, 80)
+    IRX_STAGED_CASE(4, 128)
+    IRX_STAGED_CASE(4, 256)
+    IRX_STAGED_CASE(4, 512)
+#undef IRX_STAGED_CASE
+    IRX_HIP(hipGetLastError());
+}
+
 void small_attention(const SmallAttention &args, hipStream_t stream) {
     if (args.seqs <= 0 || args.q_rows <= 0) return;
     if (args.kv_rows <= 0 || args.group <= 0) fail(3, "small attention needs keys and a group size");
@@ -1900,9 +2168,15 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
           args.q_group | args.k_group | args.v_group | args.o_group | args.q_head | args.k_head | args.v_head |
           args.o_head) & 3))
         fail(3, "small attention operands must be 16-byte aligned");
+    if (args.method < 0 || args.method > 2) fail(3, "small attention method must be 0, 1 or 2");
     const double sh = (double)args.seqs * args.heads;
     KernelTimer timer(kFamSmall, stream, 4.0 * sh * args.q_rows * args.kv_rows * 16.0,
                       4.0 * sh * 32.0 * (args.q_rows + args.kv_rows));
+    if (args.method == 2 && !staged_applies(args)) fail(3, "the staged kernel needs more than 16 queries and at most 512 keys");
+    if (args.method == 2 || (args.method == 0 && staged_applies(args) && args.rope_cos != nullptr)) {
+        launch_staged(args, stream);
+        return;
+    }
     if (args.kv_rows <= kShortKeys) {
         // Matrix cores: 16 * qb queries per wave; about 8192 waves in flight.
         // Long query sets share each item's staged keys among four waves.

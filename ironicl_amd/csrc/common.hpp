@@ -236,6 +236,9 @@ struct SmallAttention {
     // split); small_attention_partial_floats gives the size that allows them.
     float *partial;
     long long partial_floats;
+    // 0 chooses the kernel; 1 keeps the per-wave / long kernels; 2 forces the
+    // staged kernel (every key in LDS once per item) where it applies.
+    int method;
 };
 void small_attention(const SmallAttention &args, hipStream_t stream);
 long long small_attention_partial_floats(const SmallAttention &args);

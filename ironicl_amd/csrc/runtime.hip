@@ -2219,7 +2219,72 @@ void test_small_attention(irx_device *device, const float *q, const float *k, co
     IRX_HIP(hipMemcpy(out, dout.p, qn * 4, hipMemcpyDeviceToHost));
 }
 
+// Token-major sequences [seqs, rows, heads, 16] (the row transformer's layout:
+// a token's heads adjacent) through the kernel `method` selects; with reps > 0
+// the launch is also timed reps times after a warm-up, the mean in *ms.
+void test_small_attention_tokens(irx_device *device, int method, const float *q, const float *k, const float *v,
+                                 const float *cos_t, const float *sin_t, size_t seqs, size_t heads,
+                                 size_t query_rows, size_t rows, float *out, int reps, float *ms) {
+    if (!device || !q || !k || !v || !out || !seqs || !heads || !query_rows || !rows || heads > 64 ||
+        seqs > (1u << 24) || query_rows > (1u << 16) || rows > (1u << 16) || (!cos_t) != (!sin_t) || reps < 0 ||
+        reps > 1000 || (reps > 0 && !ms) || seqs * heads * std::max(query_rows, rows) * 16 > (size_t(1) << 31))
+        fail(IRX_INVALID_ARGUMENT, "small attention shapes do not match");
+    set_device(device);
+    const size_t qn = seqs * query_rows * heads * 16, kn = seqs * rows * heads * 16;
+    const size_t tn = std::max(query_rows, rows) * 16;
+    DevBuf dq(qn * 4), dk(kn * 4), dv(kn * 4), dout(qn * 4), dcos, dsin;
+    IRX_HIP(hipMemcpy(dq.p, q, qn * 4, hipMemcpyHostToDevice));
+    IRX_HIP(hipMemcpy(dk.p, k, kn * 4, hipMemcpyHostToDevice));
+    IRX_HIP(hipMemcpy(dv.p, v, kn * 4, hipMemcpyHostToDevice));
+    SmallAttention a{};
+    if (cos_t) {
+        dcos.alloc(tn * 4), dsin.alloc(tn * 4);
+        IRX_HIP(hipMemcpy(dcos.p, cos_t, tn * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dsin.p, sin_t, tn * 4, hipMemcpyHostToDevice));
+        a.rope_cos = dcos.f(), a.rope_sin = dsin.f();
+    }
+    const long long w = (long long)heads * 16;
+    a.q = dq.f(), a.k = dk.f(), a.v = dv.f(), a.o = dout.f();
+    a.q_seq = (long long)query_rows * w, a.q_group = 0, a.q_row = w, a.q_head = 16;
+    a.k_seq = (long long)rows * w, a.k_group = 0, a.k_row = w, a.k_head = 16;
+    a.v_seq = a.k_seq, a.v_group = 0, a.v_row = w, a.v_head = 16;
+    a.o_seq = a.q_seq, a.o_group = 0, a.o_row = w, a.o_head = 16;
+    a.group = (int)seqs, a.seqs = (int)seqs, a.heads = (int)heads, a.q_rows = (int)query_rows;
+    a.kv_rows = (int)rows, a.scale = 0.25f, a.method = method;
+    DevBuf part;
+    if (const long long pf = small_attention_partial_floats(a)) {
+        part.alloc((size_t)pf * 4);
+        a.partial = part.f(), a.partial_floats = pf;
+    }
+    small_attention(a, nullptr);
+    IRX_HIP(hipDeviceSynchronize());
+    if (reps > 0) {
+        hipEvent_t e0, e1;
+        IRX_HIP(hipEventCreate(&e0));
+        IRX_HIP(hipEventCreate(&e1));
+        IRX_HIP(hipEventRecord(e0, nullptr));
+        for (int r = 0; r < reps; ++r) small_attention(a, nullptr);
+        IRX_HIP(hipEventRecord(e1, nullptr));
+        IRX_HIP(hipEventSynchronize(e1));
+        float total = 0.f;
+        IRX_HIP(hipEventElapsedTime(&total, e0, e1));
+        *ms = total / (float)reps;
+        IRX_HIP(hipEventDestroy(e0));
+        IRX_HIP(hipEventDestroy(e1));
+    }
+    IRX_HIP(hipMemcpy(out, dout.p, qn * 4, hipMemcpyDeviceToHost));
+}
+
 }  // namespace
+
+int irx_test_small_attention_tokens(irx_device *device, int method, const float *q, const float *k, const float *v,
+                                    const float *rope_cos, const float *rope_sin, size_t seqs, size_t heads,
+                                    size_t query_rows, size_t rows, float *out, int reps, float *ms_per_launch) {
+    return guarded("irx_test_small_attention_tokens", [&] {
+        test_small_attention_tokens(device, method, q, k, v, rope_cos, rope_sin, seqs, heads, query_rows, rows, out,
+                                    reps, ms_per_launch);
+    });
+}
 
 int irx_test_small_attention(irx_device *device, const float *q, const float *k, const float *v, size_t heads,
                              size_t query_rows, size_t rows, float *out) {

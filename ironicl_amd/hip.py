@@ -124,6 +124,8 @@ SIGNATURES = {
     "irx_test_copy": (ctypes.c_int, [ctypes.c_void_p, _sz]),
     "irx_test_small_attention": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
     "irx_test_small_attention_rope": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
+    "irx_test_small_attention_tokens": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _CF, _CF, _CF, _CF, _sz,
+                                                       _sz, _sz, _sz, _F, ctypes.c_int, _F]),
 }
 
 _lib = None

@@ -428,6 +428,61 @@ def test_small_attention_rope_matches_float64(device, query_rows, rows):
     assert worst < 1e-5, worst
 
 
+def rope_tables(n):
+    """The row stage's tables: cos twice and [-sin, sin] of position x
+    100000^(-i/8) (docs/model.md:33)."""
+    freqs = 1.0 / (100000.0 ** (np.arange(8) / 8.0))
+    angle = np.arange(n)[:, None] * freqs[None, :]
+    return (np.concatenate([np.cos(angle), np.cos(angle)], 1).astype(np.float32),
+            np.concatenate([-np.sin(angle), np.sin(angle)], 1).astype(np.float32))
+
+
+@pytest.mark.parametrize("seqs,query_rows,rows,rope,qscale", [
+    (3, 58, 58, True, 3.0), (3, 68, 68, True, 3.0), (2, 104, 104, True, 3.0), (2, 204, 204, True, 3.0),
+    (1, 504, 504, True, 3.0), (2, 17, 17, True, 3.0), (2, 32, 33, True, 3.0), (1, 600, 512, True, 3.0),
+    (2, 1100, 128, False, 3.0), (4, 68, 68, True, 40.0), (2, 204, 204, True, 40.0), (1, 300, 257, False, 40.0)])
+@pytest.mark.parametrize("method", [1, 2])
+def test_small_attention_tokens_match_float64(device, seqs, query_rows, rows, rope, qscale, method):
+    """Token-major sequences (a token's 8 heads adjacent, as the row
+    transformer stores them) through the staged kernel (every key of an item
+    in LDS once, query blocks over waves; method 2) and the per-wave and
+    long-range kernels (method 1): the row transformer's lengths (H + 4 at
+    54, 64, 100, 200 and 500 features), one- and two-block sequences, more
+    query blocks than a workgroup holds at once, and peaked scores
+    (qscale 40) that move the lazy softmax reference."""
+    heads = 8
+    q = fast_values(seqs * query_rows * heads * 16, 31, qscale).reshape(seqs, query_rows, heads, 16)
+    k = fast_values(seqs * rows * heads * 16, 32).reshape(seqs, rows, heads, 16)
+    v = fast_values(seqs * rows * heads * 16, 33).reshape(seqs, rows, heads, 16)
+    cos_t, sin_t = rope_tables(max(query_rows, rows)) if rope else (None, None)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_small_attention_tokens(device.handle, method, F(q), F(k), F(v),
+                                                        F(cos_t) if rope else None, F(sin_t) if rope else None,
+                                                        seqs, heads, query_rows, rows, F(out), 0, None))
+    worst = 0.0
+    for s_ in range(seqs):
+        for h in (0, 3, 7):
+            qq, kk = q[s_, :, h], k[s_, :, h]
+            if rope:
+                qq, kk = rope64(qq, cos_t, sin_t), rope64(kk, cos_t, sin_t)
+            worst = max(worst, np.abs(out[s_, :, h] - attention64(qq, kk, v[s_, :, h], 0.25)).max())
+    assert worst < 1e-5, worst
+
+
+def test_staged_attention_rejects_what_it_cannot_take(device):
+    z = np.zeros(16 * 8 * 600, np.float32)
+    out = np.zeros_like(z)
+    F = hip.fptr
+    # 16 queries (one block) and 513 keys are both outside the staged kernel.
+    assert hip.lib().irx_test_small_attention_tokens(device.handle, 2, F(z), F(z), F(z), None, None, 1, 8, 16, 16,
+                                                     F(out), 0, None) == hip.INVALID_ARGUMENT
+    assert hip.lib().irx_test_small_attention_tokens(device.handle, 2, F(z), F(z), F(z), None, None, 1, 1, 20, 513,
+                                                     F(out), 0, None) == hip.INVALID_ARGUMENT
+    assert hip.lib().irx_test_small_attention_tokens(device.handle, 3, F(z), F(z), F(z), None, None, 1, 1, 20, 20,
+                                                     F(out), 0, None) == hip.INVALID_ARGUMENT
+
+
 def test_harness_rejects_bad_shapes(device):
     z = np.zeros(64, np.float32)
     F = hip.fptr
