@@ -377,3 +377,22 @@ def test_build_rejects_missing_marker_and_tiny_contexts(clf):
     with pytest.raises(hip.HipError) as e:
         clf.build_context(x, y)
     assert e.value.status == hip.DOES_NOT_FIT
+
+
+def test_builds_reuse_the_devices_kept_workspace(clf, lcg):
+    """A device keeps its last build's workspace for the next build. A context
+    rebuilt after a larger build in between (whose data the kept workspace
+    then holds) is bitwise the first one: no stage reads workspace memory it
+    has not written."""
+    x, y, xt, shifts, _, ctx_gpu = lcg
+    first = ctx_gpu.predict_raw(xt).logits
+    rng = np.random.default_rng(5)
+    xb = rng.normal(size=(1, 700, 9)).astype(np.float32)
+    yb = (np.arange(700) % 4).astype(np.float32)[None]
+    big = clf.build_context(xb, yb)
+    assert np.isfinite(big.predict_raw(xb[:, :16]).logits).all()
+    del big
+    again = clf.build_context(x, y, class_permutations=shifts, download=True)
+    np.testing.assert_array_equal(again.predict_raw(xt).logits, first)
+    for blk in range(12):
+        np.testing.assert_array_equal(again.context[2][blk], ctx_gpu.context[2][blk])
