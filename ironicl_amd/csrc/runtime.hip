@@ -14,6 +14,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -852,7 +853,8 @@ BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus, int precision 
     int run = (int)std::min<long long>(n, 16384);
     while (run > 64 && row_run_floats(run, len) * 4 > cap) run /= 2;
     p.row_run = run;
-    size_t fixed = ((size_t)n * h + n * 128 + n * 512 + 6 * 128 * 128 + 12 * 512 + 2 * len * 16) * 4;
+    // x, label embeddings and targets of one estimator; inducing queries, base scales, RoPE tables.
+    size_t fixed = ((size_t)n * h + n * 128 + n * 512 + n + 6 * 128 * 128 + 12 * 512 + 2 * len * 16) * 4;
     size_t state = (size_t)h * n * 128 * 4;  // all features' column states of one estimator
     size_t icl = ((size_t)n * 512 * 7 + n * 1024) * 4 +
                  icl_attention_partial_floats(kHeads, (int)n, icl_attention_splits(kHeads, (int)n, (int)n, cus, f16),
@@ -890,12 +892,30 @@ bool has_missing_marker(const float *x, long long rows, int h) {
         scan(0, rows);
         return found.load();
     }
+    // Threads already started are joined even when starting another throws
+    // (a thread left joinable would terminate the process); rows no thread
+    // took are scanned here.
     std::vector<std::thread> pool;
+    struct Joiner {
+        std::vector<std::thread> &p;
+        ~Joiner() {
+            for (auto &th : p)
+                if (th.joinable()) th.join();
+        }
+    } joiner{pool};
     const long long per = (rows + threads - 1) / threads;
+    long long started = 0;
     for (int t = 0; t < threads; ++t) {
         const long long r0 = t * per, r1 = std::min(rows, r0 + per);
-        if (r0 < r1) pool.emplace_back(scan, r0, r1);
+        if (r0 >= r1) break;
+        try {
+            pool.emplace_back(scan, r0, r1);
+        } catch (const std::system_error &) {
+            break;
+        }
+        started = r1;
     }
+    if (started < rows) scan(started, rows);
     for (auto &th : pool) th.join();
     return found.load();
 }
@@ -925,6 +945,19 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
     for (int i = 0; i < kIclBlocks; ++i)
         if (!in->base_scales[i]) fail(IRX_INVALID_ARGUMENT, "base scales are missing");
     const int B = (int)sh.ensembles, H = (int)sh.features, N = (int)sh.rows, L = H + kReserved;
+    // Targets the device embeds are checked as the reference checks labels
+    // and targets (validate_labels / validate_targets, cpu.rs:1684-1688,
+    // 4717-4740): a classifier's are class indices 0..9, a regressor's finite.
+    if (device_labels) {
+        const bool clf = W->task == IRX_TASK_CLASSIFIER;
+        const float *t = in->targets;
+        for (size_t i = 0, n = (size_t)B * N; i < n; ++i) {
+            const float v = t[i];
+            if (clf ? !(v >= 0.f && v <= 9.f && v == std::floor(v)) : !std::isfinite(v))
+                fail(IRX_INVALID_ARGUMENT, clf ? "classifier targets must be integers in 0..=9"
+                                               : "regression targets must be finite");
+        }
+    }
     // A grouped all-missing triple is the CPU path's (has_missing_marker,
     // cpu.rs:4072-4084): the caller routes such a context to its CPU build.
     if (has_missing_marker(in->x, (long long)B * N, H))

@@ -36,10 +36,13 @@ import numpy as np
 
 
 def spot_checks(task, weights, width, ctx, x, y, xt, logits, features=4, train_rows=16, test_rows=32,
-                float64_rows=4, members=None, log=print) -> dict:
+                float64_rows=4, members=None, log=print, tests=None, more_logits=None) -> dict:
     """Report of the checks on estimators `members` (default 0 and B-1) of the
     GPU context `ctx` (a StaticExecutor) built from x [B,N,H], y [B,N], with
-    GPU logits [B,Q,>=width] of xt [B,Q,H]; report["ok"] is the verdict."""
+    GPU logits [B,Q,>=width] of xt [B,Q,H]; report["ok"] is the verdict.
+    `tests` fixes the sampled test rows; `more_logits` maps a name to other
+    GPU logits [B, len(tests), >=width] of those rows (another pass size), each
+    checked like `logits` against the same oracle rows."""
     import oracle as O
     from reference_np import Model
 
@@ -52,7 +55,7 @@ def spot_checks(task, weights, width, ctx, x, y, xt, logits, features=4, train_r
     rng = np.random.default_rng(7)
     feats = np.sort(rng.choice(h, min(h, features), replace=False))
     rows = np.sort(rng.choice(n, min(n, train_rows), replace=False))
-    tests = np.sort(rng.choice(q, min(q, test_rows), replace=False))
+    tests = np.sort(rng.choice(q, min(q, test_rows), replace=False)) if tests is None else np.asarray(tests)
     f64_rows = rows[:float64_rows]
 
     def excess(gpu, cpu):
@@ -96,6 +99,15 @@ def spot_checks(task, weights, width, ctx, x, y, xt, logits, features=4, train_r
         note("logits", gpu, cpu)
         if task == "classifier":
             argmax_ok &= bool(np.array_equal(gpu.argmax(-1), cpu.argmax(-1)))
+        for name, other in (more_logits or {}).items():
+            got = other[e:e + 1, :, :width]
+            ex_o, d_o = excess(got, cpu)
+            r = report.setdefault(f"logits_{name}", {"max_abs_diff_vs_oracle": 0.0, "strict_ok": True})
+            r["strict_ok"] &= ex_o <= 0
+            r["max_abs_diff_vs_oracle"] = max(r["max_abs_diff_vs_oracle"], d_o)
+            if task == "classifier":
+                r["argmax_identical"] = r.get("argmax_identical", True) and bool(
+                    np.array_equal(got.argmax(-1), cpu.argmax(-1)))
         log(f"estimator {e}: oracle checks in {time.perf_counter() - t0:.1f} s")
         if excess(gpu, cpu)[0] > 0:
             t0 = time.perf_counter()

@@ -165,6 +165,33 @@ def test_clf_50k_context_spot_checks_and_predictions(device, clf_weights):
     assert report["logits"]["strict_ok"] and report["logits"]["argmax_identical"], report
 
 
+def test_clf_50k_conditioned_weights_full_size(device, clf_weights):
+    """The benchmark's workload with sharpened attention (the conditioned
+    weights of tests/conditioned.py, whose ICL softmaxes keep about a sixth of
+    the sources effective where random-init keeps all): all 4,096 test rows in
+    512-row passes (the 512-query attention over 16 key ranges), and 32
+    sampled rows again in calls of 1, 14 and 17 rows (the decode kernel over 64
+    key ranges, one and two query groups, and the small-row products), each
+    against the oracle's cached prediction on the GPU-built context at the
+    strict bar, with the oracle's spot checks of the context."""
+    from conditioned import conditioned_weights
+
+    w = S.WORKLOADS["clf-50k"]
+    x, y, xt, _ = S.workload_data(w)
+    weights = conditioned_weights(clf_weights)
+    st = tabicl.Executor("classifier", weights, device).build_context(x, y)
+    gpu = st.predict_logits(xt).logits
+    assert gpu.shape == (1, 4096, 10) and np.isfinite(gpu).all()
+    tests = sample(32, xt.shape[1], 11)
+    small = np.concatenate([st.predict_logits(np.ascontiguousarray(xt[:, tests[a:b]])).logits
+                            for a, b in ((0, 1), (1, 15), (15, 32))], axis=1)
+    report = full_size.spot_checks("classifier", weights, 10, st, x, y, xt, gpu, features=2, train_rows=4,
+                                   test_rows=32, float64_rows=2, tests=tests, more_logits={"small_passes": small})
+    assert report["logits"]["strict_ok"] and report["logits"]["argmax_identical"], report
+    assert report["logits_small_passes"]["strict_ok"] and report["logits_small_passes"]["argmax_identical"], report
+    assert report["column_kv"]["ok"] and report["icl_kv"]["ok"], report
+
+
 @pytest.mark.timeout(1200)
 def test_clf_200k_ensemble_full_size(device, clf_weights):
     """8 estimators x 200,000 training rows x 500 features, 16,384 test rows

@@ -43,8 +43,14 @@ def gelu64(x):
 
 @pytest.mark.parametrize("m,n,k,n2", [(65, 64, 64, 64), (300, 512, 512, 10), (513, 1024, 512, 512),
                                       (128, 512, 1024, 512), (4096, 384, 128, 128), (7, 1024, 512, 999),
-                                      (1, 512, 512, 512), (3, 128, 256, 128), (8, 1024, 512, 512)])
+                                      (1, 512, 512, 512), (3, 128, 256, 128), (8, 1024, 512, 512),
+                                      (17, 1024, 512, 999), (40, 512, 1024, 512), (64, 1024, 512, 512),
+                                      (9, 512, 512, 512), (32, 1024, 1024, 512)])
 def test_products_match_float64(device, m, n, k, n2):
+    """Each product family: tiled GEMMs, split-K over four waves, the eight-wave
+    split-K of 9-64 rows at K = 512 / 1,024 (ragged N = 999 included; the
+    second product adds its input as residual when n2 == n), and the small-row
+    products of at most eight rows."""
     gen = values if m * k < 300_000 else fast_values
     x = gen(m * k, 1)
     w1, b1 = gen(n * k, 2), gen(n, 3)
@@ -111,6 +117,43 @@ def test_icl_attention_matches_float64(device, rows):
             want = attention64(q[pair, rows_sel], k[pair], v[pair], 0.125)
             worst = max(worst, np.abs(out[pair, rows_sel] - want).max())
         assert worst < 1e-5, (rows, query_rows, worst)
+
+
+@pytest.fixture(scope="module")
+def keys_50k():
+    """K and V of one estimator's 8 heads over 50,000 cached rows, the
+    benchmark's context size."""
+    pairs, rows = 8, 50_000
+    return (fast_values(pairs * rows * 64, 41).reshape(pairs, rows, 64),
+            fast_values(pairs * rows * 64, 42).reshape(pairs, rows, 64))
+
+
+@pytest.mark.parametrize("query_rows", [512, 1, 16, 17, 32])
+@pytest.mark.parametrize("peaked", [False, True])
+def test_icl_attention_at_the_benchmarks_launch_shapes(device, keys_50k, query_rows, peaked):
+    """The headline's exact launches: 8 pairs (one estimator's heads) over
+    50,000 keys, at 512 queries (the 512-row pass: 16 key ranges per query
+    tile, merged) and at 1, 16, 17 and 32 queries (passes of at most 32 rows:
+    the decode kernel over 64 key ranges, one or two query groups). Queries
+    scaled by 3, or peaked: each query 40 times a key spread over the whole
+    key range, so one key dominates and the running reference moves in the
+    range that holds it."""
+    k, v = keys_50k
+    pairs, rows = k.shape[0], k.shape[1]
+    if peaked:
+        at = np.linspace(0, rows - 1, query_rows).astype(np.int64)
+        q = np.ascontiguousarray(k[:, at] * np.float32(40.0))
+    else:
+        q = fast_values(pairs * query_rows * 64, 43, scale=3.0).reshape(pairs, query_rows, 64)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_icl_attention(device.handle, F(q), F(k), F(v), pairs, query_rows, rows, F(out)))
+    sel = sorted({0, 1, query_rows // 2, query_rows - 1}) if query_rows > 32 else list(range(query_rows))
+    worst = 0.0
+    for pair in (0, 3, 7):
+        want = attention64(q[pair, sel], k[pair], v[pair], 0.125)
+        worst = max(worst, np.abs(out[pair, sel] - want).max())
+    assert worst < 1e-5, (query_rows, peaked, worst)
 
 
 @pytest.mark.parametrize("rows", [1, 63, 64, 65, 2000, 10007])

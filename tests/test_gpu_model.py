@@ -396,3 +396,32 @@ def test_builds_reuse_the_devices_kept_workspace(clf, lcg):
     np.testing.assert_array_equal(again.predict_raw(xt).logits, first)
     for blk in range(12):
         np.testing.assert_array_equal(again.context[2][blk], ctx_gpu.context[2][blk])
+
+
+@pytest.mark.parametrize("bad", [3.5, -1.0, 10.0, float("nan"), float("inf")])
+def test_build_rejects_bad_classifier_targets_at_the_abi(clf, bad):
+    """Targets handed straight to irx_build (past the Python checks) are
+    checked as the reference checks labels (cpu.rs:4717-4740)."""
+    rng = np.random.default_rng(2)
+    x = rng.normal(size=(1, 80, 6)).astype(np.float32)
+    y = (np.arange(80) % 3).astype(np.float32)[None]
+    meta, xf, yf = clf._unhashed_metadata(x, y, None, None)
+    y_bad = yf.copy()
+    y_bad[0, 17] = bad
+    with pytest.raises(hip.HipError) as e:
+        clf._build(xf, y_bad, meta, False, None, 0)
+    assert e.value.status == hip.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("bad", [float("nan"), float("inf"), -float("inf")])
+def test_build_rejects_non_finite_regression_targets_at_the_abi(device, reg_weights, bad):
+    reg = tabicl.Executor("regressor", reg_weights, device)
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(1, 80, 6)).astype(np.float32)
+    y = rng.normal(size=(1, 80)).astype(np.float32)
+    meta, xf, yf = reg._unhashed_metadata(x, y, None, None)
+    y_bad = yf.copy()
+    y_bad[0, 5] = bad
+    with pytest.raises(hip.HipError) as e:
+        reg._build(xf, y_bad, meta, False, None, 0)
+    assert e.value.status == hip.INVALID_ARGUMENT
