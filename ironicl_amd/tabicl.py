@@ -414,6 +414,16 @@ class Executor:
                               base_scales=self.icl_base_scales(n), metadata=meta, keep_alive=context,
                               precision=_precision(stored))
 
+    def predict_input_bundle(self, bundle) -> Prediction:
+        """Uncached prediction of an IRINPUT bundle (Executor::predict_logits,
+        cpu.rs:970-1030): each estimator's first N of its T rows are the
+        training rows, the other T - N are predicted; logits [B, T - N, C]."""
+        if self.task != mf.CLASSIFIER:
+            raise ValueError("IRINPUT bundles carry classifier inputs")
+        b, t, h, n = bundle.shape
+        ctx = self.build_context(np.ascontiguousarray(bundle.x[:, :n]), bundle.y_train)
+        return ctx.predict_logits(np.ascontiguousarray(bundle.x[:, n:]))
+
     def load_context(self, path, optimize: str | None = None) -> "StaticExecutor":
         """Load a persisted IRCNTXT context, verify it against this model and
         upload it to HBM (Executor::load_context, cpu.rs:397-406)."""
@@ -665,6 +675,24 @@ class StaticExecutor:
             raise ValueError(f"rows {p.cpu_rows[:8]} hold the all-missing marker, which this backend does not "
                              "predict; use predict_logits and the CPU path for them")
         return aggregate_classifier_probabilities(p.logits, self.class_permutations, temperature, average_logits)
+
+    def _check_bundle(self, query) -> None:
+        meta = self.metadata
+        if meta is None or query.model_sha256 != meta.model_sha256 or query.context_sha256 != meta.context_sha256:
+            raise ValueError("query bundle model or context identity does not match the static context")
+
+    def predict_bundle(self, query) -> Prediction:
+        """Logits [B, Q, C] of an IRQUERY bundle made for exactly this context:
+        its model and context identities must be this context's
+        (StaticExecutor::predict_bundle, cpu.rs:2356-2373)."""
+        self._check_bundle(query)
+        return self.predict_logits(query.x)
+
+    def predict_bundle_probabilities(self, query, temperature: float = 0.9, average_logits: bool = True):
+        """Aggregated class probabilities [Q, C] of an IRQUERY bundle
+        (StaticExecutor::predict_bundle_probabilities, cpu.rs:2373-2385)."""
+        self._check_bundle(query)
+        return self.predict_probabilities(query.x, temperature, average_logits)
 
     def predict_regression(self, x: np.ndarray, alphas=(0.05, 0.5, 0.95)):
         """(mean [Q], quantiles [Q, len(alphas)]) in standardized target units

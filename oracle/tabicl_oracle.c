@@ -9,6 +9,7 @@
  */
 #include "tabicl_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <omp.h>
 #include <stdarg.h>
@@ -169,13 +170,26 @@ static void softmax_numerators(int math, float *scores, size_t n, float maximum,
         for (size_t i = 0; i < n; ++i) *denominator += (scores[i] = expf(scores[i] - maximum));
         return;
     }
-    float lanes[16] = {0};
+    /* vector_exp_negative on 16 lanes at once: the same clamp, ties-to-even
+     * exponent, fused remainder, polynomial and exponent bits per lane. */
+    const __m512 vmax = _mm512_set1_ps(maximum), lo = _mm512_set1_ps(-87.0f);
+    const __m512 log2e = _mm512_set1_ps(ORA_LOG2E), ln2 = _mm512_set1_ps(ORA_LN2);
+    const float coef[7] = {1.0f / 720.0f, 1.0f / 120.0f, 1.0f / 24.0f, 1.0f / 6.0f, 0.5f, 1.0f, 1.0f};
+    __m512 acc = _mm512_setzero_ps();
     size_t body = n / 16 * 16;
-    for (size_t i = 0; i < body; i += 16)
-        for (int l = 0; l < 16; ++l) {
-            float x = scores[i + l] - maximum;
-            lanes[l] += (scores[i + l] = vector_exp_negative(x));
-        }
+    for (size_t i = 0; i < body; i += 16) {
+        const __m512 v = _mm512_max_ps(_mm512_sub_ps(_mm512_loadu_ps(scores + i), vmax), lo);
+        const __m512 e = _mm512_roundscale_ps(_mm512_mul_ps(v, log2e), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+        const __m512 r = _mm512_fnmadd_ps(e, ln2, v);
+        __m512 poly = _mm512_set1_ps(1.0f / 5040.0f);
+        for (int c = 0; c < 7; ++c) poly = _mm512_fmadd_ps(poly, r, _mm512_set1_ps(coef[c]));
+        const __m512i bits = _mm512_slli_epi32(_mm512_add_epi32(_mm512_cvtps_epi32(e), _mm512_set1_epi32(127)), 23);
+        const __m512 num = _mm512_mul_ps(poly, _mm512_castsi512_ps(bits));
+        _mm512_storeu_ps(scores + i, num);
+        acc = _mm512_add_ps(acc, num);
+    }
+    float lanes[16];
+    _mm512_storeu_ps(lanes, acc);
     for (int w = 8; w >= 1; w >>= 1)
         for (int l = 0; l < w; ++l) lanes[l] += lanes[l + w];
     float total = lanes[0];
@@ -201,10 +215,53 @@ static inline float dot16(const float *a, const float *b, size_t n) {
     return acc[0] + tail;
 }
 
-/* affine_f32: reference.rs:83-120. weight [out,in] (PyTorch layout). */
+/* dot16's lane reduction on a vector: lanes l and l + 8, then l + 4, l + 2,
+ * l + 1, the same additions in the same order. */
+static inline float reduce16(__m512 acc) {
+    const __m256 s8 = _mm256_add_ps(_mm512_castps512_ps256(acc), _mm512_extractf32x8_ps(acc, 1));
+    const __m128 s4 = _mm_add_ps(_mm256_castps256_ps128(s8), _mm256_extractf128_ps(s8, 1));
+    const __m128 s2 = _mm_add_ps(s4, _mm_movehl_ps(s4, s4));
+    return _mm_cvtss_f32(_mm_add_ss(s2, _mm_shuffle_ps(s2, s2, 1)));
+}
+
+/* affine_f32: reference.rs:83-120. weight [out,in] (PyTorch layout).
+ * Register-blocked as affine_avx512 runs it (x86_64.rs:1639-1780): four input
+ * rows by four outputs share each 16-wide load; every output is still dot16's
+ * arithmetic (16 lane chains over the input, reduced pairwise, then the tail,
+ * then the bias), so the blocking changes no bit. */
 void ora_affine(const float *input, size_t rows, size_t in_dim, const float *weight,
                 const float *bias, size_t out_dim, float *output) {
-    for (size_t r = 0; r < rows; ++r) {
+    const size_t body = in_dim / 16 * 16;
+    size_t r = 0;
+    for (; r + 4 <= rows && body; r += 4) {
+        const float *x0 = input + r * in_dim;
+        size_t o = 0;
+        for (; o + 4 <= out_dim; o += 4) {
+            __m512 acc[4][4];
+            for (int i = 0; i < 4; ++i)
+                for (int c = 0; c < 4; ++c) acc[i][c] = _mm512_setzero_ps();
+            for (size_t k = 0; k < body; k += 16) {
+                __m512 w[4];
+                for (int c = 0; c < 4; ++c) w[c] = _mm512_loadu_ps(weight + (o + c) * in_dim + k);
+                for (int i = 0; i < 4; ++i) {
+                    const __m512 xv = _mm512_loadu_ps(x0 + i * in_dim + k);
+                    for (int c = 0; c < 4; ++c) acc[i][c] = _mm512_fmadd_ps(w[c], xv, acc[i][c]);
+                }
+            }
+            for (int i = 0; i < 4; ++i)
+                for (int c = 0; c < 4; ++c) {
+                    const float *wr = weight + (o + c) * in_dim, *xr = x0 + i * in_dim;
+                    float tail = 0.0f;
+                    for (size_t k = body; k < in_dim; ++k) tail = fmaf(wr[k], xr[k], tail);
+                    output[(r + i) * out_dim + o + c] = (bias ? bias[o + c] : 0.0f) + (reduce16(acc[i][c]) + tail);
+                }
+        }
+        for (; o < out_dim; ++o)
+            for (int i = 0; i < 4; ++i)
+                output[(r + i) * out_dim + o] =
+                    (bias ? bias[o] : 0.0f) + dot16(weight + o * in_dim, x0 + i * in_dim, in_dim);
+    }
+    for (; r < rows; ++r) {
         const float *x = input + r * in_dim;
         float *y = output + r * out_dim;
         for (size_t o = 0; o < out_dim; ++o)
@@ -344,24 +401,37 @@ static int attention_heads(int math, const float *query, size_t query_rows, cons
                  * so the tile loop has constant bounds (one register per row). */
                 for (size_t d = 0; d < head_dim; ++d)
                     for (size_t r = 0; r < QUERY_BLOCK; ++r) qd[d * QUERY_BLOCK + r] = r < rows ? qt[r * head_dim + d] : 0.0f;
+                /* One 16-source score vector per query row, in registers: each
+                 * lane a fused chain over the dimensions, then times the scale. */
+                const __m512 vscale = _mm512_set1_ps(scale);
                 for (size_t s = 0; s < ps; s += 16) {
-                    float acc[QUERY_BLOCK][16];
-                    memset(acc, 0, sizeof acc);
+                    __m512 acc[QUERY_BLOCK];
+                    for (int r = 0; r < QUERY_BLOCK; ++r) acc[r] = _mm512_setzero_ps();
                     for (size_t d = 0; d < head_dim; ++d) {
-                        const float *kd = packed + d * ps + s;
+                        const __m512 kd = _mm512_loadu_ps(packed + d * ps + s);
                         const float *qv = qd + d * QUERY_BLOCK;
-                        for (int r = 0; r < QUERY_BLOCK; ++r)
-                            for (int l = 0; l < 16; ++l) acc[r][l] = fmaf(kd[l], qv[r], acc[r][l]);
+                        for (int r = 0; r < QUERY_BLOCK; ++r) acc[r] = _mm512_fmadd_ps(kd, _mm512_set1_ps(qv[r]), acc[r]);
                     }
                     const size_t lanes = ns - s < 16 ? ns - s : 16;
+                    const __mmask16 keep = (__mmask16)((1u << lanes) - 1u);
                     for (size_t r = 0; r < rows; ++r)
-                        for (size_t l = 0; l < lanes; ++l) scores[r * ns + s + l] = acc[r][l] * scale;
+                        _mm512_mask_storeu_ps(scores + r * ns + s, keep, _mm512_mul_ps(acc[r], vscale));
                 }
                 for (size_t r = 0; r < rows; ++r) {
                     float *sc = scores + r * ns;
                     const size_t state = h * query_rows + q0 + r;
-                    float tile_max = -INFINITY;
-                    for (size_t s = 0; s < ns; ++s) {
+                    /* The tile's maximum (and whether any score is NaN), 16 at a time. */
+                    __m512 vmax = _mm512_set1_ps(-INFINITY);
+                    __mmask16 nan = 0;
+                    size_t s = 0;
+                    for (; s + 16 <= ns; s += 16) {
+                        const __m512 x = _mm512_loadu_ps(sc + s);
+                        nan |= _mm512_cmp_ps_mask(x, x, _CMP_UNORD_Q);
+                        vmax = _mm512_max_ps(vmax, x);
+                    }
+                    float tile_max = _mm512_reduce_max_ps(vmax);
+                    if (nan) status = -1;
+                    for (; s < ns; ++s) {
                         if (sc[s] != sc[s]) status = -1;
                         if (sc[s] > tile_max) tile_max = sc[s];
                     }
@@ -378,7 +448,47 @@ static int attention_heads(int math, const float *query, size_t query_rows, cons
                     maximum[state] = mx;
                 }
                 if (status) break;
-                for (size_t r = 0; r < rows; ++r) {
+                /* The value tile: per output element one fused multiply-add per
+                 * source, in source order. Four rows at a time share each value
+                 * row's loads, their 64-dim outputs held in registers. */
+                size_t r = 0;
+                if (head_dim == 64) {
+                    for (; r + 4 <= rows; r += 4) {
+                        float *o = output + (h * query_rows + q0 + r) * 64;
+                        __m512 acc[4][4];
+                        for (int i = 0; i < 4; ++i)
+                            for (int c = 0; c < 4; ++c) acc[i][c] = _mm512_loadu_ps(o + i * 64 + 16 * c);
+                        const float *w0 = scores + r * ns;
+                        for (size_t s = 0; s < ns; ++s) {
+                            const float *v = vt + s * 64;
+                            const __m512 v0 = _mm512_loadu_ps(v), v1 = _mm512_loadu_ps(v + 16);
+                            const __m512 v2 = _mm512_loadu_ps(v + 32), v3 = _mm512_loadu_ps(v + 48);
+                            for (int i = 0; i < 4; ++i) {
+                                const __m512 ws = _mm512_set1_ps(w0[i * ns + s]);
+                                acc[i][0] = _mm512_fmadd_ps(ws, v0, acc[i][0]);
+                                acc[i][1] = _mm512_fmadd_ps(ws, v1, acc[i][1]);
+                                acc[i][2] = _mm512_fmadd_ps(ws, v2, acc[i][2]);
+                                acc[i][3] = _mm512_fmadd_ps(ws, v3, acc[i][3]);
+                            }
+                        }
+                        for (int i = 0; i < 4; ++i)
+                            for (int c = 0; c < 4; ++c) _mm512_storeu_ps(o + i * 64 + 16 * c, acc[i][c]);
+                    }
+                }
+                if (head_dim == 16 && r < rows) {
+                    /* 16-wide heads: the block's rows in one register each. */
+                    __m512 acc[QUERY_BLOCK];
+                    float *o = output + (h * query_rows + q0) * 16;
+                    for (size_t i = r; i < rows; ++i) acc[i] = _mm512_loadu_ps(o + i * 16);
+                    for (size_t s = 0; s < ns; ++s) {
+                        const __m512 v = _mm512_loadu_ps(vt + s * 16);
+                        for (size_t i = r; i < rows; ++i)
+                            acc[i] = _mm512_fmadd_ps(_mm512_set1_ps(scores[i * ns + s]), v, acc[i]);
+                    }
+                    for (size_t i = r; i < rows; ++i) _mm512_storeu_ps(o + i * 16, acc[i]);
+                    r = rows;
+                }
+                for (; r < rows; ++r) {
                     float *o = output + (h * query_rows + q0 + r) * head_dim;
                     const float *w = scores + r * ns;
                     for (size_t s = 0; s < ns; ++s) {
