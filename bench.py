@@ -597,6 +597,39 @@ def bench_workload(name: str, args) -> dict:
     }
 
 
+def profile_rows(args) -> dict:
+    """The row transformer at every workload's row length L = H + 4 (58, 104,
+    68, 204, 504 tokens), for a profiler: per workload, one estimator's build
+    of a 4,096-row context with its feature count (the row stage runs all
+    4,096 training rows as sequences of L tokens) and single-stream passes of
+    512 test rows, every launch traced. The column and ICL stages run too, at
+    this N."""
+    from ironicl_amd import hip, hipmem, synthetic, tabicl
+
+    device = hip.Device(0)
+    executors = {task: tabicl.Executor(task, synthetic.random_weights(task), device)
+                 for task in ("classifier", "regressor")}
+    out = {}
+    for name, w in synthetic.WORKLOADS.items():
+        x, y, xt, _ = synthetic.workload_data(w, train_rows=4096, test_rows=512)
+        x, y, xt = x[:1], y[:1], xt[:1]
+        ex = executors[w.task]
+        ctx = ex.build_context(x, y)
+        ctx.set_streams(1)
+        ctx.set_graphs(False)
+        dx = hipmem.DeviceArray.from_host(np.ascontiguousarray(xt))
+        dl = hipmem.DeviceArray((1, xt.shape[1], ex.width))
+
+        def call():
+            hip.check(hip.lib().irx_predictor_predict_device(ctx.handle, dx.ptr, xt.shape[1], dl.ptr, None))
+
+        stats = latency_stats(timed_calls(call, args.warmup, args.steps))
+        out[name] = {"row_tokens": x.shape[2] + 4, "pass_ms_p50": stats["p50_ms"]}
+        log(f"profile leg rows: {name} (L = {x.shape[2] + 4}), 512-row pass p50 {stats['p50_ms']:.3f} ms")
+        del ctx
+    return {"profile_leg": "rows", "steps": args.steps, "by_workload": out}
+
+
 def profile_leg(args) -> dict:
     """The kernels of the headline's prediction alone, for a profiler's
     per-kernel statistics: one build, then single-stream prediction steps (or
@@ -604,6 +637,8 @@ def profile_leg(args) -> dict:
     or ("build") `warmup` untimed builds, then `steps` timed builds."""
     from ironicl_amd import hip, hipmem, synthetic, tabicl
 
+    if args.profile_leg == "rows":
+        return profile_rows(args)
     w = synthetic.WORKLOADS[WORKLOAD]
     x, y, xt, _ = synthetic.workload_data(w)
     q = xt.shape[1]
@@ -648,10 +683,11 @@ def main() -> int:
     ap.add_argument("--workload", default=WORKLOAD,
                     help="clf-50k (default, the full report) or another configuration at full size: clf-1k, "
                          "clf-10k, reg-20k, clf-200k (build, rows/s, build kernels, oracle parity on samples)")
-    ap.add_argument("--profile-leg", choices=["predict", "small", "build"], default=None,
+    ap.add_argument("--profile-leg", choices=["predict", "small", "build", "rows"], default=None,
                     help="only the leg a profiler reads: one build, then --steps single-stream prediction steps "
                          "of the 4,096 rows (predict) or passes of 1, 8, 16 and 32 rows (small), kernels launched "
-                         "one by one; or --warmup untimed then --steps timed builds (build)")
+                         "one by one; or --warmup untimed then --steps timed builds (build); or (rows) every "
+                         "workload's row length: a 4,096-row build and 512-row passes per feature count")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel over BYTES (reference for traffic counters)")
     args = ap.parse_args()
