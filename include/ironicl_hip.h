@@ -393,7 +393,10 @@ int irx_test_block_tail(irx_device *device, int fused, const float *att, const f
  * epilogue 1 (GELU): out [m, n] = gelu(LN(x) w^T + b); epilogue 2 (QASS, the
  * ICL query path, n = 512): q = LN(x) w^T + b, then per head
  * q * base[head] * (1 + tanh(gelu(q qm0w^T + qm0b) qm2w^T + qm2b)), into out
- * head-major [m / rows, 8, rows, 64] (StaticExecutor::qass, cpu.rs:3798-3853). */
+ * head-major [m / rows, 8, rows, 64] (StaticExecutor::qass, cpu.rs:3798-3853);
+ * epilogue 3: the same result as the build computes it for many query rows
+ * (LayerNorm, a tiled head-major Q projection, then the QASS MLP and gate
+ * over the projected rows). */
 int irx_test_ln_linear(irx_device *device, int epilogue, const float *x, size_t m, size_t rows,
                        const float *lnw, const float *lnb, const float *w, const float *b, size_t n,
                        const float *qm0w, const float *qm0b, const float *qm2w, const float *qm2b,

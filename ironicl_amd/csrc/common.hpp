@@ -213,6 +213,22 @@ struct LnLinear {
 };
 void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream);
 
+// The QASS query MLP and gate over already projected head-major query rows q
+// [m, 64] (m = estimators x 8 heads x rows): out = q * base[head] * (1 +
+// tanh(gelu(q Wm0^T + bm0) Wm2^T + bm2)), head = (row / rows) % 8
+// (qassmax_f32, reference.rs:417-428), with kLnQass's arithmetic. For the
+// build's N-row queries.
+struct QassRows {
+    const float *q;                  // [m, 64]
+    const float *w0, *b0, *w2, *b2;  // [64, 64], [64] each
+    const float *base;               // [8, 64]
+    float *out;                      // [m, 64]
+    long long m;
+    int rows;                        // rows per (estimator, head)
+    int compute_units;
+};
+void qass_rows(const QassRows &a, hipStream_t stream);
+
 // LayerNorm over `width` (128 or 512), eps 1e-5, two passes (reference.rs:223-252).
 void layer_norm(const float *x, long long ldx, const float *weight, const float *bias, float *y,
                 long long ldy, long long rows, int width, hipStream_t stream);

@@ -22,6 +22,8 @@
 // waves through LDS, and the partial products are summed there too.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace irx {
 namespace {
 
@@ -301,6 +303,88 @@ __global__ __launch_bounds__(EPI == kLnQass ? 1024 : 256) void ln_rows512_kernel
     }
 }
 
+// The QASS query MLP and gate over head-major query rows that are already
+// projected (the build's N-row queries, whose Q projection is a tiled
+// product): out = q * base[head] * (1 + tanh(gelu(q Wm0^T + bm0) Wm2^T +
+// bm2)). Each wave holds both 64 x 64 weights in its registers as A-operand
+// fragments (w[ob][kb] = W[16 ob + m][16 kb + 4 g .. +3]) and takes a
+// contiguous share of the 16-row tasks, loading the next task's rows while
+// it computes one. Rows are the B operand in the layout of the kLnQass
+// epilogue above (lane (m, g) holds row m's columns 16 b + 4 g + r in
+// register r of block b), which is also the layout the products return, so
+// the hidden layer goes from the first product to the second in registers.
+// Every output takes its sixteen products in that epilogue's order, then
+// the same bias, GELU, tanh and gate arithmetic: the two paths agree bit for
+// bit on the same queries.
+__global__ __launch_bounds__(256, 2) void qass_rows_kernel(QassRows p, long long tasks) {
+    const int lane = threadIdx.x & 63, m16 = lane & 15, g = lane >> 4;
+    const long long waves = (long long)gridDim.x * 4;
+    const long long wave = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const long long t_begin = wave * tasks / waves, t_end = (wave + 1) * tasks / waves;
+    if (t_begin >= t_end) return;
+
+    f32x4 w0[4][4], w2[4][4];
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            w0[ob][kb] = *reinterpret_cast<const f32x4 *>(p.w0 + (16 * ob + m16) * 64 + 16 * kb + 4 * g);
+            w2[ob][kb] = *reinterpret_cast<const f32x4 *>(p.w2 + (16 * ob + m16) * 64 + 16 * kb + 4 * g);
+        }
+    auto load = [&](long long t, f32x4 *x) {
+        const long long row = min(16 * t + m16, p.m - 1);
+        const float *src = p.q + row * 64 + 4 * g;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) x[kb] = *reinterpret_cast<const f32x4 *>(src + 16 * kb);
+    };
+    f32x4 x[4], xn[4];
+    load(t_begin, x);
+    for (long long t = t_begin; t < t_end; ++t) {
+        if (t + 1 < t_end) load(t + 1, xn);
+        // Four independent accumulators, each summed over (kb, e) in order.
+        f32x4 h[4];
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) h[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ob = 0; ob < 4; ++ob) h[ob] = mfma(w0[ob][kb][e], x[kb][e], h[ob]);
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) {
+            h[ob] += *reinterpret_cast<const f32x4 *>(p.b0 + 16 * ob + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[ob][e] = gelu_erf(h[ob][e]);
+        }
+        f32x4 a[4];
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) a[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ob = 0; ob < 4; ++ob) a[ob] = mfma(w2[ob][kb][e], h[kb][e], a[ob]);
+        const long long row = 16 * t + m16;
+        const int head = (int)((row / p.rows) % kHeads);
+        if (row < p.m) {
+            float *dst = p.out + row * 64 + 4 * g;
+#pragma unroll
+            for (int ob = 0; ob < 4; ++ob) {
+                const f32x4 gm = a[ob] + *reinterpret_cast<const f32x4 *>(p.b2 + 16 * ob + 4 * g);
+                const f32x4 base = *reinterpret_cast<const f32x4 *>(p.base + head * 64 + 16 * ob + 4 * g);
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = x[ob][e] * base[e] * (1.0f + tanhf(gm[e]));
+                *reinterpret_cast<f32x4 *>(dst + 16 * ob) = o;
+            }
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) x[kb] = xn[kb];
+    }
+}
+
 template <int EPI>
 void launch_rows(const LnLinear &a, hipStream_t stream) {
     const dim3 grid(EPI == kLnQass ? kHeads : a.n / 16), block(EPI == kLnQass ? 1024 : 256);
@@ -343,6 +427,23 @@ void ln_linear512(const LnLinear &a, int epilogue, hipStream_t stream) {
     } else {
         hipLaunchKernelGGL(ln_linear512_kernel<kLnGelu>, grid, dim3(256), 0, stream, a);
     }
+    IRX_HIP(hipGetLastError());
+}
+
+void qass_rows(const QassRows &a, hipStream_t stream) {
+    if (a.m <= 0) return;
+    if (a.rows <= 0) fail(3, "qass_rows: rows per head must be positive");
+    if ((reinterpret_cast<uintptr_t>(a.q) & 15) || (reinterpret_cast<uintptr_t>(a.out) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.w0) & 15) || (reinterpret_cast<uintptr_t>(a.w2) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.b0) & 15) || (reinterpret_cast<uintptr_t>(a.b2) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.base) & 15))
+        fail(3, "qass_rows: operands must be 16-byte aligned");
+    const long long tasks = (long long)ceil_div((size_t)a.m, 16);
+    // Two workgroups of four waves per CU, each wave a contiguous share of the tasks.
+    const long long groups = std::min<long long>(ceil_div((size_t)tasks, 4), 2LL * std::max(1, a.compute_units));
+    const double m = (double)a.m;
+    KernelTimer timer(kFamGemm, stream, 2.0 * 2.0 * m * 64 * 64, 4.0 * (2.0 * m * 64 + 2.0 * 64 * 64));
+    hipLaunchKernelGGL(qass_rows_kernel, dim3((unsigned)groups), dim3(256), 0, stream, a, tasks);
     IRX_HIP(hipGetLastError());
 }
 

@@ -617,12 +617,12 @@ struct Stages {
     }
 
     struct IclBuffers {
-        float *norm, *qh, *qhid, *qg, *att, *hid, *partial;
+        float *norm, *qh, *qg, *att, *hid, *partial;
         size_t partial_floats;
     };
     static IclBuffers icl_buffers(Arena &a, long long rows, int b, int q_rows, int kv_rows, int cus, bool f16 = false) {
         IclBuffers r{};
-        r.norm = a.take(rows * 512), r.qh = a.take(rows * 512), r.qhid = a.take(rows * 512);
+        r.norm = a.take(rows * 512), r.qh = a.take(rows * 512);
         r.qg = a.take(rows * 512), r.att = a.take(rows * 512), r.hid = a.take(rows * 1024);
         int splits = icl_attention_splits(b * kHeads, q_rows, kv_rows, cus, f16);
         r.partial_floats = icl_attention_partial_floats(b * kHeads, q_rows, splits, f16);
@@ -632,10 +632,12 @@ struct Stages {
 
     // Query half of ICL block `blk` (cached_block with QASS, cpu.rs:2587-2850,
     // 3798-3853) for `b` estimators x `rows` query rows [b*rows, 512], against
-    // K/V [b, 8, kv_rows, 64] (or the FP16 cache k16 / v16).
+    // K/V [b, 8, kv_rows, 64] (or the FP16 cache k16 / v16). normed: r.norm
+    // already holds LN1(x) (the build's K/V projection read it); only taken
+    // by queries too many for the fused LayerNorm form.
     void icl_queries(int blk, float *x, int b, int rows, const float *k, const float *v, int kv_rows,
                      const float *base, const IclBuffers &r, const unsigned short *k16 = nullptr,
-                     const unsigned short *v16 = nullptr, const Icl8Block *c8 = nullptr) const {
+                     const unsigned short *v16 = nullptr, const Icl8Block *c8 = nullptr, bool normed = false) const {
         const BlockW &bw = w.icl[blk];
         const long long m = (long long)b * rows;
         if (m <= kLnLinearRows) {
@@ -646,17 +648,15 @@ struct Stages {
             f.base = base, f.rows = rows;
             ln_linear512(f, kLnQass, s);
         } else {
-            layer_norm(x, 512, bw.n1w, bw.n1b, r.norm, 512, m, 512, s);
+            if (!normed) layer_norm(x, 512, bw.n1w, bw.n1b, r.norm, 512, m, 512, s);
             // Q, head-major [b, 8, rows, 64].
             OutMap qmap{64, kHeads, 0, (long long)rows * 64, rows, (long long)kHeads * rows * 64, 64};
             linear_map(r.norm, 512, m, 512, bw.in_w, bw.in_b, 512, r.qh, qmap);
             // QASSMax: q * base * (1 + tanh(MLP(q))) per head (reference.rs:417-428).
-            linear(r.qh, 64, m * kHeads, 64, bw.qm0.w, bw.qm0.b, 64, r.qhid, 64, kEpiGelu);
-            GemmArgs g{};
-            g.a = r.qhid, g.lda = 64, g.w = bw.qm2.w, g.bias = bw.qm2.b, g.residual = r.qh, g.ldr = 64;
-            g.qass_base = base, g.qass_rows = rows, g.c = r.qg, g.out = OutMap::row_major(64, 64);
-            g.m = (int)(m * kHeads), g.n = 64, g.k = 64, g.epilogue = kEpiQass;
-            gemm(g, s);
+            QassRows qa{};
+            qa.q = r.qh, qa.w0 = bw.qm0.w, qa.b0 = bw.qm0.b, qa.w2 = bw.qm2.w, qa.b2 = bw.qm2.b, qa.base = base;
+            qa.out = r.qg, qa.m = m * kHeads, qa.rows = rows, qa.compute_units = cus;
+            qass_rows(qa, s);
         }
         IclAttention at{};
         at.q = r.qg, at.q_pair_stride = (long long)rows * 64, at.k = k, at.v = v;
@@ -856,7 +856,7 @@ BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus, int precision 
     // x, label embeddings and targets of one estimator; inducing queries, base scales, RoPE tables.
     size_t fixed = ((size_t)n * h + n * 128 + n * 512 + n + 6 * 128 * 128 + 12 * 512 + 2 * len * 16) * 4;
     size_t state = (size_t)h * n * 128 * 4;  // all features' column states of one estimator
-    size_t icl = ((size_t)n * 512 * 7 + n * 1024) * 4 +
+    size_t icl = ((size_t)n * 512 * 6 + n * 1024) * 4 +
                  icl_attention_partial_floats(kHeads, (int)n, icl_attention_splits(kHeads, (int)n, (int)n, cus, f16),
                                               f16) * 4 +
                  (f16 ? (size_t)2 * kHeads * n * 64 * 4 : 0);  // FP32 K/V of a block before packing
@@ -1157,7 +1157,8 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
                     st.linear_map(ib.norm, 512, N, 512, bw.in_w + 512 * 512, bw.in_b + 512, 1024, kc, kvmap);
                     // The last block's row states are never read: only its K/V are kept.
                     if (blk + 1 < kIclBlocks)
-                        st.icl_queries(blk, rows, 1, N, kc, kc + icl_plane, N, d_base + blk * 512, ib);
+                        st.icl_queries(blk, rows, 1, N, kc, kc + icl_plane, N, d_base + blk * 512, ib, nullptr,
+                                       nullptr, nullptr, true);
                 } else {
                     // FP32 K/V of this estimator, then packed into its part of the FP16 cache.
                     const long long p32 = (long long)kHeads * N * 64;
@@ -1167,7 +1168,8 @@ void build_impl(irx_weights *W, const irx_build_inputs *in, irx_build_outputs *o
                     unsigned short *v16 = k16 + plane16;
                     pack_icl16(kv32, kv32 + p32, false, N, kHeads, k16, v16, counter, s);
                     if (blk + 1 < kIclBlocks)
-                        st.icl_queries(blk, rows, 1, N, nullptr, nullptr, N, d_base + blk * 512, ib, k16, v16);
+                        st.icl_queries(blk, rows, 1, N, nullptr, nullptr, N, d_base + blk * 512, ib, k16, v16,
+                                       nullptr, true);
                 }
             }
         }
@@ -2214,7 +2216,7 @@ int irx_test_ln_linear(irx_device *device, int epilogue, const float *x, size_t 
                        const float *lnb, const float *w, const float *b, size_t n, const float *qm0w,
                        const float *qm0b, const float *qm2w, const float *qm2b, const float *base, float *out) {
     return guarded("irx_test_ln_linear", [&] {
-        const bool qass = epilogue == kLnQass;
+        const bool tiled = epilogue == 3, qass = epilogue == kLnQass || tiled;
         if (!device || !x || !m || !lnw || !lnb || !w || !b || !out || (epilogue != kLnGelu && !qass) ||
             (qass && (n != 512 || !rows || m % rows || !qm0w || !qm0b || !qm2w || !qm2b || !base)) || !n || n % 64)
             fail(IRX_INVALID_ARGUMENT, "LN-linear arguments do not match");
@@ -2232,7 +2234,24 @@ int irx_test_ln_linear(irx_device *device, int epilogue, const float *x, size_t 
         f.x = dx.f(), f.ldx = 512, f.lnw = dlw.f(), f.lnb = dlb.f(), f.w = dw.f(), f.b = db.f(), f.out = dout.f();
         f.ldo = (long long)n, f.m = (int)m, f.n = (int)n;
         if (qass) f.qm0w = d0w.f(), f.qm0b = d0b.f(), f.qm2w = d2w.f(), f.qm2b = d2b.f(), f.base = dbase.f(), f.rows = (int)rows;
-        ln_linear512(f, epilogue, nullptr);
+        if (tiled) {
+            // The build's form (Stages::icl_queries with more rows than the fused form takes).
+            DevBuf dnorm(m * 512 * 4), dq(m * 512 * 4);
+            layer_norm(dx.f(), 512, dlw.f(), dlb.f(), dnorm.f(), 512, (long long)m, 512, nullptr);
+            GemmArgs g{};
+            g.a = dnorm.f(), g.lda = 512, g.w = dw.f(), g.bias = db.f(), g.c = dq.f();
+            const long long hr = (long long)rows;
+            g.out = OutMap{64, kHeads, 0, hr * 64, (int)hr, (long long)kHeads * hr * 64, 64};
+            g.m = (int)m, g.n = 512, g.k = 512, g.epilogue = kEpiNone;
+            gemm(g, nullptr);
+            QassRows qa{};
+            qa.q = dq.f(), qa.w0 = d0w.f(), qa.b0 = d0b.f(), qa.w2 = d2w.f(), qa.b2 = d2b.f(), qa.base = dbase.f();
+            qa.out = dout.f(), qa.m = (long long)m * kHeads, qa.rows = (int)rows, qa.compute_units = device->compute_units;
+            qass_rows(qa, nullptr);
+            IRX_HIP(hipDeviceSynchronize());
+        } else {
+            ln_linear512(f, epilogue, nullptr);
+        }
         IRX_HIP(hipDeviceSynchronize());
         IRX_HIP(hipMemcpy(out, dout.p, m * n * 4, hipMemcpyDeviceToHost));
     });

@@ -355,10 +355,15 @@ def test_ln_linear_gelu_matches_float64(device, m, n):
     np.testing.assert_allclose(out.reshape(m, n), want, rtol=1e-4, atol=2e-5)
 
 
-@pytest.mark.parametrize("estimators,rows", [(1, 1), (1, 2), (1, 5), (8, 1), (4, 2), (3, 3), (1, 16), (2, 8),
-                                             (3, 5), (1, 32), (4, 8), (3, 11), (2, 250), (3, 17)])
-def test_ln_linear_qass_matches_float64(device, estimators, rows):
-    """LN1 + Q projection + QASSMax (query MLP and gate per head), head-major."""
+@pytest.mark.parametrize("form,estimators,rows", [(2, 1, 1), (2, 1, 2), (2, 1, 5), (2, 8, 1), (2, 4, 2), (2, 3, 3),
+                                                  (2, 1, 16), (2, 2, 8), (2, 3, 5), (2, 1, 32), (2, 4, 8), (2, 3, 11),
+                                                  (2, 2, 250), (2, 3, 17), (3, 1, 1), (3, 3, 5), (3, 2, 250),
+                                                  (3, 1, 2049), (3, 3, 1001)])
+def test_ln_linear_qass_matches_float64(device, form, estimators, rows):
+    """LN1 + Q projection + QASSMax (query MLP and gate per head), head-major:
+    form 2 the prediction's fused kernel, form 3 the build's (LayerNorm, tiled
+    projection, then the MLP and gate over the projected rows, whose waves each
+    take a contiguous share of 16-row tasks; 3 x 1001 x 8 rows end mid-task)."""
     m = estimators * rows
     x = fast_values(m * 512, 6, 3.0) - 0.1
     lnw, lnb = fast_values(512, 7, 0.2) + 1.0, fast_values(512, 8, 0.1)
@@ -368,7 +373,7 @@ def test_ln_linear_qass_matches_float64(device, estimators, rows):
     base = fast_values(512, 15, 0.5) + 1.0
     out = np.zeros(m * 512, np.float32)
     F = hip.fptr
-    hip.check(hip.lib().irx_test_ln_linear(device.handle, 2, F(x), m, rows, F(lnw), F(lnb), F(w), F(b), 512,
+    hip.check(hip.lib().irx_test_ln_linear(device.handle, form, F(x), m, rows, F(lnw), F(lnb), F(w), F(b), 512,
                                            F(m0w), F(m0b), F(m2w), F(m2b), F(base), F(out)))
     q = ln64(x.reshape(m, 512), lnw, lnb) @ w.reshape(512, 512).T.astype(np.float64) + b
     q = q.reshape(estimators, rows, 8, 64).transpose(0, 2, 1, 3)  # head-major
