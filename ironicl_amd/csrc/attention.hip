@@ -60,6 +60,12 @@ constexpr float kLog2e = 1.44269504088896340736f;
 
 struct IclLaunch {
     int qtiles, splits, keys_per_split, per_xcd, q_padded;
+    // FP32 wide kernel only. count: workgroup units of this launch. A tail
+    // launch (tail_units > 0) takes units unit0 .. unit0 + tail_units - 1 of
+    // the (query tile, pair) units, each split over `splits` key ranges, with
+    // its partials compacted to [splits, tail_units * 256] rows.
+    int count, unit0, tail_units;
+    long long part_rows;  // partial rows per split
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -94,20 +100,51 @@ __device__ __forceinline__ float halves_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Long key ranges (FLUSH) accumulate in two levels: every kFlushTiles tiles
+// the register accumulators (O^T and the row sums) are added into totals the
+// lane keeps in LDS and restart from zero. A single FP32 accumulator over
+// tens of thousands of keys loses the contributions that arrive after a
+// dominant one (each addend below half an ulp of the sum is rounded away);
+// with peaked attention over 50,000 keys that cost 3e-4 of the output.
+constexpr int kFlushTiles = 64;
+constexpr int kFlushFloats = kIclWaves * 2 * 2 * 16 * 64;  // [j][b][r / 4][thread][r % 4]
+
 // SPLIT: the keys are split over workgroups and each writes a partial output
 // and its log2-sum-exp, merged afterwards; otherwise the output is final.
-template <bool SPLIT>
+template <bool SPLIT, bool FLUSH>
 __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAttention p, IclLaunch g) {
-    __shared__ __attribute__((aligned(16))) IclTile tiles[2];
+    // One LDS object: the K/V tiles, then (FLUSH) each thread's O^T totals
+    // and its row-sum totals [j][thread]. (As a second LDS object the totals
+    // made the compiler wait for the in-flight tile loads before every read
+    // of the current tile.)
+    struct LdsPlain {
+        IclTile tiles[2];
+    };
+    struct LdsFlush {
+        IclTile tiles[2];
+        float totals[kFlushFloats + kIclWaves * 2 * 64];
+    };
+    __shared__ __attribute__((aligned(16))) std::conditional_t<FLUSH, LdsFlush, LdsPlain> lds;
+    IclTile *tiles = lds.tiles;
+    float *totals = nullptr;
+    if constexpr (FLUSH) totals = lds.totals;
 
-    const int total = g.qtiles * p.pairs * g.splits;
     const int bid = bid_x();
     const int t_id = (bid % 8) * g.per_xcd + bid / 8;
-    if (t_id >= total) return;
-    const int qt = t_id % g.qtiles;
-    const int rest = t_id / g.qtiles;
-    const int split = rest % g.splits;
-    const int pair = rest / g.splits;
+    if (t_id >= g.count) return;
+    // Units (query tile qt of pair `pair`) in order qt + qtiles * pair. A
+    // tail launch's workgroups take its units split-major, so the units that
+    // share a key range are consecutive (and on one XCD).
+    int qt, split, pair, tail_unit = 0;
+    if (g.tail_units) {
+        tail_unit = t_id % g.tail_units, split = t_id / g.tail_units;
+        const int unit = g.unit0 + tail_unit;
+        qt = unit % g.qtiles, pair = unit / g.qtiles;
+    } else {
+        qt = t_id % g.qtiles;
+        const int rest = t_id / g.qtiles;
+        split = rest % g.splits, pair = rest / g.splits;
+    }
     // Workgroup-uniform; read into scalars so the key loop runs on scalar registers.
     const int k_begin = __builtin_amdgcn_readfirstlane(split * g.keys_per_split);
     const int k_end = __builtin_amdgcn_readfirstlane(min(p.kv_rows, k_begin + g.keys_per_split));
@@ -201,9 +238,28 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
     // block 1 (keys 32..63) is 512 floats further.
     const int kfrag = (8 * half + (r32 >> 4)) * 256 + (r32 & 15) * 4;
 
+    // FLUSH: the keys run in chunks of kFlushTiles tiles, each chunk's
+    // accumulators added into the lane's LDS totals after it (flushed: some
+    // chunk was; workgroup-uniform). The totals' addresses are formed where
+    // they are used, so nothing extra stays live through the tile loop.
+    bool flushed = false;
+    // Rescales owed to the totals since the last flush (the reference moved):
+    // applied when the totals are next read, so the tile loop touches no LDS
+    // besides its tiles.
+    float tot_scale[2] = {1.f, 1.f};
+    // O^T totals as [j][b][r / 4][thread] groups of four: one 16-byte LDS
+    // access per group of a lane's four consecutive registers.
+    auto o_tot = [&](int j, int b, int q) -> f32x4 & {
+        return *reinterpret_cast<f32x4 *>(&totals[(((j * 2 + b) * 4 + q) * 64 * kIclWaves + tid_x()) * 4]);
+    };
+    auto l_tot = [&](int j) -> float & { return totals[kFlushFloats + tid_x() + j * 64 * kIclWaves]; };
+    const int chunk = FLUSH ? kFlushTiles * kKeyTile : k_end - k_begin;
+
     issue_tile(k_begin, 0);
     int buf = 0;
-    for (int k0 = k_begin; k0 < k_end; k0 = __builtin_amdgcn_readfirstlane(k0 + kKeyTile)) {
+    for (int c0 = k_begin; c0 < k_end; c0 = __builtin_amdgcn_readfirstlane(c0 + chunk)) {
+    const int c1 = __builtin_amdgcn_readfirstlane(min(k_end, c0 + chunk));
+    for (int k0 = c0; k0 < c1; k0 = __builtin_amdgcn_readfirstlane(k0 + kKeyTile)) {
         wait_loads();
         __syncthreads();
         if (k0 + kKeyTile < k_end) issue_tile(k0 + kKeyTile, buf ^ 1);
@@ -301,6 +357,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
                     s[j][1][r] = __builtin_amdgcn_exp2f(t1[r] - m_new);
                     lsum += s[j][0][r] + s[j][1][r];
                 }
+                if constexpr (FLUSH) tot_scale[j] *= alpha;  // the totals are in the old scale too
                 m_ref[j] = m_new;
             }
             l_run[j] += lsum;
@@ -332,6 +389,49 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
         }
         buf ^= 1;
     }
+    if constexpr (FLUSH) {
+        if (c1 < k_end) {
+            // Each lane moves only its own values: no barrier.
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float ts = tot_scale[j];
+                l_tot(j) = flushed ? l_tot(j) * ts + l_run[j] : l_run[j];
+                l_run[j] = 0.f;
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        f32x4 t = flushed ? o_tot(j, b, q) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            t[e] = flushed ? t[e] * ts + o[j][b][4 * q + e] : o[j][b][4 * q + e];
+                            o[j][b][4 * q + e] = 0.f;
+                        }
+                        o_tot(j, b, q) = t;
+                    }
+                tot_scale[j] = 1.f;
+            }
+            flushed = true;
+        }
+    }
+    }
+    if constexpr (FLUSH) {
+        if (flushed) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float ts = tot_scale[j];
+                l_run[j] += l_tot(j) * ts;
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x4 t = o_tot(j, b, q);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[j][b][4 * q + e] += t[e] * ts;
+                    }
+            }
+        }
+    }
 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -344,9 +444,11 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
             const int b = pair / kHeads, head = pair - b * kHeads;
             dst = p.o + ((long long)b * p.q_rows + qrow) * p.ldo + head * 64;
         } else {
-            const long long row = ((long long)split * p.pairs + pair) * g.q_padded + qrow;
+            const long long row =
+                g.tail_units ? split * g.part_rows + (long long)tail_unit * kIclQueries + (qrow - qt * kIclQueries)
+                             : split * g.part_rows + (long long)pair * g.q_padded + qrow;
             dst = p.partial + row * 64;
-            if (half == 0) p.partial[(long long)g.splits * p.pairs * g.q_padded * 64 + row] = m_ref[j] + log2f(l_tot);
+            if (half == 0) p.partial[(long long)g.splits * g.part_rows * 64 + row] = m_ref[j] + log2f(l_tot);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -1219,16 +1321,14 @@ __global__ __launch_bounds__(64) void icl_merge_kernel(IclAttention p, int split
     for (int s0 = sg; s0 < splits; s0 += 4 * kMergePerGroup) {
         float l8[kMergePerGroup];
         f32x4 v8[kMergePerGroup];
+        // Slots past the splits re-read the last split and get weight 0
+        // (unconditional loads, as in icl_merge_rows_kernel).
 #pragma unroll
         for (int j = 0; j < kMergePerGroup; ++j) {
-            const int s = s0 + 4 * j;
-            if (s < splits) {
-                l8[j] = lse[s * step];
-                v8[j] = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + s * step) * 64 + d);
-            } else {
-                l8[j] = -INFINITY;
-                v8[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            const int s = s0 + 4 * j, sl = min(s, splits - 1);
+            const float ls = lse[sl * step];
+            v8[j] = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + sl * step) * 64 + d);
+            l8[j] = s < splits ? ls : -INFINITY;
         }
         float m_new = m_run;
 #pragma unroll
@@ -1269,27 +1369,37 @@ __global__ __launch_bounds__(64) void icl_merge_kernel(IclAttention p, int split
 // contiguous 4 KB run. A wave per row (icl_merge_kernel) leaves too few bytes
 // in flight for these launches (the build's 5-split merge of 50,000 rows ran
 // at 2.7 TB/s).
+// pq0: the first (pair, query row) to merge, pair * q_rows + row (a tail
+// launch's partials cover only the rows from its first unit on).
 template <int MAXS>
-__global__ __launch_bounds__(256) void icl_merge_rows_kernel(IclAttention p, int splits, int q_padded) {
-    const long long pq = (long long)bid_x() * 16 + (tid_x() >> 4);
+__global__ __launch_bounds__(256) void icl_merge_rows_kernel(IclAttention p, IclLaunch g, long long pq0) {
+    const long long pq = pq0 + (long long)bid_x() * 16 + (tid_x() >> 4);
     if (pq >= (long long)p.pairs * p.q_rows) return;
+    const int splits = g.splits;
     const int d = (tid_x() & 15) * 4;
     const int qrow = (int)(pq % p.q_rows);
     const int pair = (int)(pq / p.q_rows);
-    const long long step = (long long)p.pairs * q_padded;
-    const long long row0 = (long long)pair * q_padded + qrow;
+    const long long step = g.part_rows;
+    long long row0;
+    if (g.tail_units) {
+        const int qt = qrow / kIclQueries;
+        row0 = (long long)(pair * g.qtiles + qt - g.unit0) * kIclQueries + (qrow - qt * kIclQueries);
+    } else {
+        row0 = (long long)pair * g.q_padded + qrow;
+    }
     const float *lse = p.partial + (long long)splits * step * 64 + row0;
+    // Branch-free loads: slots past the splits re-read the last split (a
+    // cache hit) and get weight 0, so every slot is one unconditional load
+    // (with a branch per slot the compiler duplicated the code per split
+    // count and needed 212 registers at MAXS = 8).
     float l[MAXS];
     f32x4 v[MAXS];
 #pragma unroll
     for (int s = 0; s < MAXS; ++s) {
-        if (s < splits) {
-            l[s] = lse[s * step];
-            v[s] = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + s * step) * 64 + d);
-        } else {
-            l[s] = -INFINITY;
-            v[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+        const int sl = min(s, splits - 1);
+        const float ls = lse[sl * step];
+        v[s] = *reinterpret_cast<const f32x4 *>(p.partial + (row0 + sl * step) * 64 + d);
+        l[s] = s < splits ? ls : -INFINITY;
     }
     float m = l[0];
 #pragma unroll
@@ -1325,6 +1435,8 @@ IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units, bool f
         g.keys_per_split = per;
         g.splits = (int)ceil_div(kv_rows, per);
         g.per_xcd = 0;
+        g.count = pairs * g.splits;
+        g.part_rows = (long long)pairs * g.q_padded;
         return g;
     }
     g.qtiles = (int)ceil_div(q_rows, kIclQueries);
@@ -1350,7 +1462,46 @@ IclLaunch plan_icl(int pairs, int q_rows, int kv_rows, int compute_units, bool f
     g.keys_per_split = per;
     g.splits = (int)ceil_div(kv_rows, per);
     g.per_xcd = (int)ceil_div((long long)g.qtiles * pairs * g.splits, 8);
+    g.count = g.qtiles * pairs * g.splits;
+    g.part_rows = (long long)pairs * g.q_padded;
     return g;
+}
+
+// The FP32 wide kernel's plan. When its (query tile, pair) units fill at
+// least one round of workgroups (one per CU), the whole rounds run every
+// key in one workgroup each (final outputs: no partials, no merge) and the
+// units left over, fewer than a round, are split over key ranges so that
+// they fill one more round (the build's 50,000-row self-attention: 1,568
+// units = six rounds and 32 units in 8 splits, where one plan for all units
+// needed 5 splits, 30.6 rounds and a merge of every row). Otherwise the
+// units are split as plan_icl says. tail.count = 0: no tail launch.
+struct IclPlan {
+    IclLaunch main, tail;
+};
+
+IclPlan plan_icl_fp32(int pairs, int q_rows, int kv_rows, int compute_units) {
+    IclPlan pl{};
+    pl.main = plan_icl(pairs, q_rows, kv_rows, compute_units, false);
+    if (q_rows <= kDecodeQueries) return pl;
+    const long long units = (long long)pl.main.qtiles * pairs, slots = std::max(1, compute_units);
+    if (units < slots) return pl;
+    const long long full = units / slots * slots, rest = units - full;
+    IclLaunch &m = pl.main;
+    m.splits = 1, m.keys_per_split = kv_rows, m.count = (int)full, m.per_xcd = (int)ceil_div(full, 8);
+    if (rest > 0) {
+        IclLaunch &t = pl.tail;
+        t = m;
+        // At most 16 splits: the rows merge kernel's limit.
+        const long long max_splits = std::min(16, std::max(1, kv_rows / 512));
+        const int want = (int)std::max<long long>(1, std::min(slots / rest, max_splits));
+        t.keys_per_split = (int)ceil_div(ceil_div(kv_rows, want), kKeyTile) * kKeyTile;
+        t.splits = (int)ceil_div(kv_rows, t.keys_per_split);
+        t.unit0 = (int)full, t.tail_units = (int)rest;
+        t.count = (int)(rest * t.splits);
+        t.per_xcd = (int)ceil_div(t.count, 8);
+        t.part_rows = rest * kIclQueries;
+    }
+    return pl;
 }
 
 // ---- 16-wide heads on matrix cores, many keys ----
@@ -1966,15 +2117,14 @@ __global__ __launch_bounds__(1024, NG == 1 ? 8 : NG == 2 ? 6 : 4) void staged_at
 
 }  // namespace
 
-int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units, bool f16) {
-    return plan_icl(pairs, q_rows, kv_rows, compute_units, f16).splits;
-}
-
-size_t icl_attention_partial_floats(int pairs, int q_rows, int splits, bool f16) {
-    if (splits <= 1) return 0;
-    size_t q_padded = q_rows <= kDecodeQueries ? (size_t)kDecodeQueries
-                                                : ceil_div(q_rows, kIclQueries) * (size_t)kIclQueries;
-    return (size_t)splits * pairs * q_padded * 65;
+size_t icl_attention_partial_floats(int pairs, int q_rows, int kv_rows, int compute_units, bool f16) {
+    if (pairs <= 0 || q_rows <= 0 || kv_rows <= 0) return 0;
+    auto floats = [](const IclLaunch &g) { return g.splits > 1 ? (size_t)g.splits * g.part_rows * 65 : (size_t)0; };
+    if (!f16) {
+        const IclPlan pl = plan_icl_fp32(pairs, q_rows, kv_rows, compute_units);
+        return std::max(floats(pl.main), pl.tail.count ? floats(pl.tail) : (size_t)0);
+    }
+    return floats(plan_icl(pairs, q_rows, kv_rows, compute_units, true));
 }
 
 void icl_attention(const IclAttention &args, hipStream_t stream) {
@@ -1994,10 +2144,16 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         fail(3, "ICL attention FP8 cache and scales must be 16-byte aligned");
     // The FP8 cache uses the FP16 cache's tiling.
     const bool f16 = args.k16 != nullptr || fp8;
-    IclLaunch g = plan_icl(args.pairs, args.q_rows, args.kv_rows, args.compute_units, f16);
-    if (g.splits > 1) {
-        size_t need = icl_attention_partial_floats(args.pairs, args.q_rows, g.splits, f16);
-        if (!args.partial || args.partial_floats < need) fail(3, "ICL attention partial buffer is too small");
+    IclPlan pl{};
+    if (f16)
+        pl.main = plan_icl(args.pairs, args.q_rows, args.kv_rows, args.compute_units, true);
+    else
+        pl = plan_icl_fp32(args.pairs, args.q_rows, args.kv_rows, args.compute_units);
+    const IclLaunch &g = pl.main;
+    const bool tail = pl.tail.count > 0;
+    {
+        const size_t need = icl_attention_partial_floats(args.pairs, args.q_rows, args.kv_rows, args.compute_units, f16);
+        if (need && (!args.partial || args.partial_floats < need)) fail(3, "ICL attention partial buffer is too small");
     }
     {
         const double pairs = args.pairs, q = args.q_rows, kv = args.kv_rows;
@@ -2049,28 +2205,54 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
                 else
                     hipLaunchKernelGGL((icl_decode_kernel<2, false>), blocks, threads, 0, stream, args, g);
             }
-        } else if (g.splits > 1) {
-            hipLaunchKernelGGL((icl_attention_kernel<true>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
-                               args, g);
         } else {
-            hipLaunchKernelGGL((icl_attention_kernel<false>), dim3(g.per_xcd * 8), dim3(kIclWaves * 64), 0, stream,
-                               args, g);
+            // Ranges of more than 2 x kFlushTiles tiles accumulate in two levels.
+            auto wide = [&](const IclLaunch &l) {
+                const dim3 grid(l.per_xcd * 8), block(kIclWaves * 64);
+                const bool flush = l.keys_per_split > 2 * kFlushTiles * kKeyTile;
+                if (l.splits > 1 && flush)
+                    hipLaunchKernelGGL((icl_attention_kernel<true, true>), grid, block, 0, stream, args, l);
+                else if (l.splits > 1)
+                    hipLaunchKernelGGL((icl_attention_kernel<true, false>), grid, block, 0, stream, args, l);
+                else if (flush)
+                    hipLaunchKernelGGL((icl_attention_kernel<false, true>), grid, block, 0, stream, args, l);
+                else
+                    hipLaunchKernelGGL((icl_attention_kernel<false, false>), grid, block, 0, stream, args, l);
+            };
+            wide(g);
+            if (tail) wide(pl.tail);
         }
         IRX_HIP(hipGetLastError());
     }
-    if (g.splits > 1) {
-        long long rows = (long long)args.pairs * args.q_rows;
+    // Merge the split rows: every row, or the tail launch's rows from its
+    // first unit on.
+    const IclLaunch &split = tail ? pl.tail : g;
+    if (split.splits > 1) {
+        long long pq0 = 0;
+        if (tail) {
+            const int pair0 = split.unit0 / split.qtiles, qt0 = split.unit0 - pair0 * split.qtiles;
+            pq0 = (long long)pair0 * args.q_rows + (long long)qt0 * kIclQueries;
+        }
+        const long long rows = (long long)args.pairs * args.q_rows - pq0;
         KernelTimer timer(kFamIclMerge, stream, 0.0,
-                          4.0 * ((double)g.splits * rows * 65.0 + (double)rows * 64.0));
-        if (g.splits <= 8)
-            hipLaunchKernelGGL(icl_merge_rows_kernel<8>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args,
-                               g.splits, g.q_padded);
-        else if (g.splits <= 16)
-            hipLaunchKernelGGL(icl_merge_rows_kernel<16>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args,
-                               g.splits, g.q_padded);
+                          4.0 * ((double)split.splits * rows * 65.0 + (double)rows * 64.0));
+        if (split.splits <= 2)
+            hipLaunchKernelGGL(icl_merge_rows_kernel<2>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args, split,
+                               pq0);
+        else if (split.splits <= 4)
+            hipLaunchKernelGGL(icl_merge_rows_kernel<4>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args, split,
+                               pq0);
+        else if (split.splits <= 8)
+            hipLaunchKernelGGL(icl_merge_rows_kernel<8>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args, split,
+                               pq0);
+        else if (split.splits <= 16)
+            hipLaunchKernelGGL(icl_merge_rows_kernel<16>, dim3(ceil_div(rows, 16)), dim3(256), 0, stream, args, split,
+                               pq0);
+        else if (!tail)
+            hipLaunchKernelGGL(icl_merge_kernel, dim3((unsigned)rows), dim3(64), 0, stream, args, split.splits,
+                               split.q_padded);
         else
-            hipLaunchKernelGGL(icl_merge_kernel, dim3((unsigned)rows), dim3(64), 0, stream, args, g.splits,
-                               g.q_padded);
+            fail(3, "ICL attention tail split exceeds the merge's 16 splits");
         IRX_HIP(hipGetLastError());
     }
 }

@@ -104,7 +104,6 @@ enum Epilogue : int {
     kEpiNone = 0,
     kEpiGelu = 1,      // gelu(acc + bias)
     kEpiResidual = 2,  // acc + bias + residual[m, n]
-    kEpiQass = 4,      // residual[m, n] * base[(m / qass_rows) * N + n] * (1 + tanh(acc + bias))
 };
 
 struct GemmArgs {
@@ -114,8 +113,6 @@ struct GemmArgs {
     const float *bias;      // [N] or null
     const float *residual;  // [M, N] row-major with stride ldr, or null
     long long ldr;
-    const float *qass_base; // kEpiQass: [8 * N], head (row / qass_rows) % 8
-    int qass_rows;          // kEpiQass: rows per head
     float *c;
     OutMap out;
     int m, n, k;
@@ -283,8 +280,8 @@ struct IclAttention {
     const float *kscale, *vscale;
 };
 // Splits the ICL attention would use, and the partial floats it needs.
-int icl_attention_splits(int pairs, int q_rows, int kv_rows, int compute_units, bool f16 = false);
-size_t icl_attention_partial_floats(int pairs, int q_rows, int splits, bool f16 = false);
+// Floats of the split partials icl_attention needs for this shape (0: none).
+size_t icl_attention_partial_floats(int pairs, int q_rows, int kv_rows, int compute_units, bool f16 = false);
 void icl_attention(const IclAttention &args, hipStream_t stream);
 // Halves of one FP16 cache plane (K or V) for `pairs` x `rows` keys.
 inline size_t icl16_plane(long long pairs, long long rows) { return (size_t)pairs * ((rows + 63) / 64 * 64) * 64; }

@@ -59,8 +59,8 @@ __device__ __forceinline__ f32x4 layer_norm128_lanes(f32x4 v, const float *w, co
     return o;
 }
 
-// Epilogue of one accumulator value at (row, col): bias, then GELU, residual
-// or the QASS gate, then the output map. EPI and GROUPED are compile-time so
+// Epilogue of one accumulator value at (row, col): bias, then GELU or
+// residual, then the output map. EPI and GROUPED are compile-time so
 // each instantiation is straight-line code.
 template <int EPI, bool GROUPED>
 __device__ __forceinline__ void store_out(const GemmArgs &p, int row, int col, long long coff, float bias,
@@ -68,10 +68,6 @@ __device__ __forceinline__ void store_out(const GemmArgs &p, int row, int col, l
     float v = acc + bias;
     if constexpr (EPI == kEpiGelu) v = gelu_erf(v);
     if constexpr (EPI == kEpiResidual) v += p.residual[(long long)row * p.ldr + col];
-    if constexpr (EPI == kEpiQass) {
-        const int head = (row / p.qass_rows) % kHeads;
-        v = p.residual[(long long)row * p.ldr + col] * p.qass_base[head * p.n + col] * (1.0f + tanhf(v));
-    }
     long long roff;
     if constexpr (GROUPED) {
         int g = row / p.out.rows_per_group;
@@ -225,7 +221,7 @@ __global__ __launch_bounds__(256, BK == 16 ? 3 : 2) void gemm_kernel(GemmArgs p,
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
             const int row0 = m0 + wm * (BM / 2) + i * 32 + half * 4;
-            if constexpr (!GROUPED && EPI != kEpiQass) {
+            if constexpr (!GROUPED) {
                 store_rows<EPI>(p, row0, col, coff, bias, acc[i][j], m0 + BM <= p.m);
             } else {
 #pragma unroll
@@ -313,7 +309,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(GemmArgs p, int tiles_
         const int r = wave * 4 + rr;
         v16[rr] = red[0][r][lane] + red[1][r][lane] + red[2][r][lane] + red[3][r][lane];
     }
-    if constexpr (!GROUPED && EPI != kEpiQass) {
+    if constexpr (!GROUPED) {
         const long long ldc = p.out.ldc;
         float *dst = p.c + (long long)row0 * ldc + coff;
         const float *res = nullptr;
@@ -491,7 +487,7 @@ struct Flops {
 
 Flops work(const GemmArgs &args) {
     const double m = args.m, n = args.n, k = args.k;
-    const double resid = (args.epilogue & (kEpiResidual | kEpiQass)) ? m * n : 0.0;
+    const double resid = args.epilogue == kEpiResidual ? m * n : 0.0;
     return {2.0 * m * n * k, 4.0 * (m * k + n * k + m * n + resid)};
 }
 
@@ -514,7 +510,6 @@ void dispatch_epilogue(const GemmArgs &args, dim3 grid, hipStream_t stream, int 
     IRX_GEMM_CASE(kEpiNone)
     IRX_GEMM_CASE(kEpiGelu)
     IRX_GEMM_CASE(kEpiResidual)
-    IRX_GEMM_CASE(kEpiQass)
 #undef IRX_GEMM_CASE
     fail(3, "gemm: unknown epilogue");
 }
@@ -561,7 +556,7 @@ void launch(const GemmArgs &args, hipStream_t stream) {
 // gemm_rows_kernel for m <= 8 rows and K = 128, 256, 512 or 1,024 (plain
 // epilogues, ungrouped rows); false when the shape is not one of those.
 bool launch_rows(const GemmArgs &args, hipStream_t stream) {
-    if (args.m > 8 || args.out.rows_per_group < args.m || (args.epilogue & kEpiQass)) return false;
+    if (args.m > 8 || args.out.rows_per_group < args.m) return false;
     const int m = args.m <= 1 ? 1 : args.m <= 2 ? 2 : args.m <= 4 ? 4 : 8;
     const dim3 grid(ceil_div(args.n, 16)), block(256);
     bool launched = false;
@@ -628,13 +623,13 @@ bool gemm_fuses_ln(long long m, int n) { return m > 0 && n > 0 && small_product(
 void gemm(const GemmArgs &args, hipStream_t stream) {
     if (args.m <= 0 || args.n <= 0) return;
     if (args.ln_w && (args.k != 128 || !gemm_fuses_ln(args.m, args.n) || args.out.rows_per_group < args.m ||
-                      args.epilogue == kEpiQass || (reinterpret_cast<uintptr_t>(args.ln_w) & 15) ||
+                      (reinterpret_cast<uintptr_t>(args.ln_w) & 15) ||
                       (reinterpret_cast<uintptr_t>(args.ln_b) & 15)))
         fail(3, "gemm: a LayerNorm prologue needs K = 128, a small product and plain rows");
     if (args.k <= 0 || args.k % 64 != 0 || args.lda % 4 != 0 ||
         (reinterpret_cast<uintptr_t>(args.a) & 15) || (reinterpret_cast<uintptr_t>(args.w) & 15))
         fail(3, "gemm: K must be a positive multiple of 64 with 16-byte aligned rows");
-    if ((args.epilogue & (kEpiResidual | kEpiQass)) && !args.residual)
+    if (args.epilogue == kEpiResidual && !args.residual)
         fail(3, "gemm: residual epilogue without a residual");
     // Products with few 64 x 64 tiles split K over a workgroup's waves; those
     // with four or more 128 x 128 tiles per CU take them (GELU ones, whose
@@ -657,7 +652,7 @@ void gemm(const GemmArgs &args, hipStream_t stream) {
         const long long slots = (deep ? kDeepPerCu : kShallowPerCu) * cus;
         const long long tiles_n = ceil_div(args.n, 128);
         const long long main_tm = big_tiles / slots * slots / tiles_n;
-        const bool plain_rows = args.out.rows_per_group >= args.m && args.epilogue != kEpiQass;
+        const bool plain_rows = args.out.rows_per_group >= args.m;
         auto big = [&](const GemmArgs &a) {
             if (deep)
                 launch<128, 128, 32>(a, stream);

@@ -624,8 +624,7 @@ struct Stages {
         IclBuffers r{};
         r.norm = a.take(rows * 512), r.qh = a.take(rows * 512);
         r.qg = a.take(rows * 512), r.att = a.take(rows * 512), r.hid = a.take(rows * 1024);
-        int splits = icl_attention_splits(b * kHeads, q_rows, kv_rows, cus, f16);
-        r.partial_floats = icl_attention_partial_floats(b * kHeads, q_rows, splits, f16);
+        r.partial_floats = icl_attention_partial_floats(b * kHeads, q_rows, kv_rows, cus, f16);
         r.partial = r.partial_floats ? a.take(r.partial_floats) : nullptr;
         return r;
     }
@@ -857,8 +856,7 @@ BuildPlan plan_build(const irx_shape &sh, size_t budget, int cus, int precision 
     size_t fixed = ((size_t)n * h + n * 128 + n * 512 + n + 6 * 128 * 128 + 12 * 512 + 2 * len * 16) * 4;
     size_t state = (size_t)h * n * 128 * 4;  // all features' column states of one estimator
     size_t icl = ((size_t)n * 512 * 6 + n * 1024) * 4 +
-                 icl_attention_partial_floats(kHeads, (int)n, icl_attention_splits(kHeads, (int)n, (int)n, cus, f16),
-                                              f16) * 4 +
+                 icl_attention_partial_floats(kHeads, (int)n, (int)n, cus, f16) * 4 +
                  (f16 ? (size_t)2 * kHeads * n * 64 * 4 : 0);  // FP32 K/V of a block before packing
     p.ws_bytes = fixed + state + column_chunk_floats(chunk, n) * 4 + row_run_floats(run, len) * 4 + icl +
                  (size_t)64 * 256 * 40;
@@ -1268,8 +1266,7 @@ PassBuffers pass_layout(Arena &a, const irx_shape &sh, size_t R, int cus, bool f
     // A shorter pass may split the keys further; size the partials for the worst pass.
     size_t worst = 0;
     for (size_t rows = 32; rows <= R; rows += 32) {
-        int splits = icl_attention_splits((int)B * kHeads, (int)rows, (int)sh.rows, cus, f16);
-        worst = std::max(worst, icl_attention_partial_floats((int)B * kHeads, (int)rows, splits, f16));
+        worst = std::max(worst, icl_attention_partial_floats((int)B * kHeads, (int)rows, (int)sh.rows, cus, f16));
     }
     if (worst > p.ib.partial_floats) {
         p.ib.partial = a.take(worst);
@@ -1985,8 +1982,7 @@ int irx_test_icl_attention_precision(irx_device *device, int precision, const fl
         IRX_HIP(hipMemcpy(dq.p, q, qn * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(dk.p, k, kn * 4, hipMemcpyHostToDevice));
         IRX_HIP(hipMemcpy(dv.p, v, kn * 4, hipMemcpyHostToDevice));
-        int splits = icl_attention_splits((int)pairs, (int)query_rows, (int)rows, device->compute_units, f16);
-        size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, splits, f16);
+        size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, (int)rows, device->compute_units, f16);
         DevBuf part(pf * 4);
         DevBuf cache16(f16 ? 2 * icl16_plane((long long)pairs, (long long)rows) * 2 : 0), bad(f16 ? 4 : 0);
         DevBuf logical(fp8 ? 2 * kn * 2 : 0), block8(fp8 ? icl8_block_bytes((long long)pairs, (long long)rows) : 0);
@@ -2060,8 +2056,7 @@ int irx_icl_attention_noalloc(irx_device *device, const float *q, const float *k
         if (!device->scratch) fail(IRX_DEVICE_ERROR, "the device's scratch array was not set up");
         // The same split plan as irx_test_icl_attention on this device, so the
         // results are the same bit for bit; its partials must fit the scratch.
-        const int splits = icl_attention_splits((int)pairs, (int)query_rows, (int)rows, device->compute_units);
-        const size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, splits);
+        const size_t pf = icl_attention_partial_floats((int)pairs, (int)query_rows, (int)rows, device->compute_units);
         if (pf * sizeof(float) > kNoAllocScratchBytes)
             fail(IRX_INVALID_ARGUMENT, "ICL attention of " + std::to_string(pairs) + " pairs x " +
                                            std::to_string(query_rows) + " queries x " + std::to_string(rows) +

@@ -156,6 +156,47 @@ def test_icl_attention_at_the_benchmarks_launch_shapes(device, keys_50k, query_r
     assert worst < 1e-5, (query_rows, peaked, worst)
 
 
+@pytest.mark.parametrize("query_rows,rows", [(8193, 9000), (20000, 20000), (50000, 50000)])
+@pytest.mark.parametrize("peaked", [False, True])
+def test_icl_attention_whole_rounds_and_split_tail(device, query_rows, rows, peaked):
+    """Self-attention sized launches (the build's 20,000- and 50,000-row
+    shapes, and 8,193 queries over 9,000 keys): the (query tile, pair) units
+    that fill whole rounds of one workgroup per CU take every key, and the
+    units left over are split over key ranges and merged (on 256 CUs: 32
+    units in 8 ranges, 120 in 2, 8 in 16). Rows checked against float64 on
+    both sides of the boundary between the two launches."""
+    pairs = 8
+    k = fast_values(pairs * rows * 64, 51).reshape(pairs, rows, 64)
+    v = fast_values(pairs * rows * 64, 52).reshape(pairs, rows, 64)
+    if peaked:
+        at = np.linspace(0, rows - 1, query_rows).astype(np.int64)
+        q = np.ascontiguousarray(k[:, at] * np.float32(40.0))
+    else:
+        q = fast_values(pairs * query_rows * 64, 53, scale=3.0).reshape(pairs, query_rows, 64)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_icl_attention(device.handle, F(q), F(k), F(v), pairs, query_rows, rows, F(out)))
+    qtiles = -(-query_rows // 256)
+    units = qtiles * pairs
+    first_tail = units // 256 * 256  # first unit past the whole rounds (256 CUs)
+    # Three rows of the units at the boundary, one row of every tail unit and
+    # of every 37th unit before it.
+    check = {}
+    for unit in {0, first_tail - 1, first_tail, units - 1}:
+        pair, qt = divmod(unit, qtiles)
+        check.setdefault(pair, set()).update({qt * 256, min(qt * 256 + 129, query_rows - 1),
+                                              min(qt * 256 + 255, query_rows - 1)})
+    for unit in list(range(0, first_tail, 37)) + list(range(first_tail, units)):
+        pair, qt = divmod(unit, qtiles)
+        check.setdefault(pair, set()).add(min(qt * 256 + (unit * 97) % 256, query_rows - 1))
+    worst = 0.0
+    for pair, sel in check.items():
+        sel = sorted(sel)
+        want = attention64(q[pair, sel], k[pair], v[pair], 0.125)
+        worst = max(worst, np.abs(out[pair, sel] - want).max())
+    assert worst < 1e-5, (query_rows, rows, peaked, worst)
+
+
 @pytest.mark.parametrize("rows", [1, 63, 64, 65, 2000, 10007])
 def test_icl_attention_split_fp16_matches_float64(device, rows):
     """Split-FP16 products over the FP16 cache (optimize="auto"): against

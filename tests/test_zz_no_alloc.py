@@ -1,8 +1,9 @@
 """The no-allocation ICL attention (irx_icl_attention_noalloc) against the
 allocating kernel harness (irx_test_icl_attention) on the same device: two
-calls in a row, the second smaller, each bitwise equal; and a shape whose
-split-K partials exceed the library's scratch array refused before any work.
-Collected last: its entry point shares one scratch array per device."""
+calls in a row, the second smaller, each bitwise equal; the shape with the
+largest split-K partials the split plan makes on 256 CUs; and invalid calls
+refused before any work. Collected last: its entry point shares one scratch
+array per device."""
 
 import numpy as np
 import pytest
@@ -54,17 +55,28 @@ def test_no_alloc_attention_matches_the_harness(device, shapes):
         np.testing.assert_array_equal(got, want, err_msg=f"call {call}")
 
 
-def test_no_alloc_attention_refuses_what_its_scratch_cannot_hold(device):
-    """8 pairs x 8,448 queries x 4,096 keys splits its keys 8 ways: 8 x 8 x
-    8,448 x 65 partial floats (140 MB), past the 64 MiB scratch. Refused on the
-    host; the buffers are real and sized for the shape all the same."""
-    pairs, query_rows, rows = 8, 8448, 4096
-    q = hipmem.DeviceArray.from_host(np.zeros((pairs, query_rows, 64), np.float32))
-    kv = hipmem.DeviceArray.from_host(np.zeros((pairs, rows, 64), np.float32))
-    out = hipmem.DeviceArray((pairs // 8, query_rows, 512))
-    status = hip.lib().irx_icl_attention_noalloc(device.handle, q.ptr, kv.ptr, kv.ptr, pairs, query_rows, rows,
-                                                 out.ptr, None)
-    assert status == hip.INVALID_ARGUMENT
-    assert b"no-allocation entry point holds" in hip.lib().irx_last_error()
+def test_no_alloc_attention_at_the_largest_partials(device):
+    """The split plan's partials are largest just below one round of
+    (query tile, pair) units: 8 pairs x 7,936 queries (248 units on 256 CUs)
+    split 2 ways over 4,096 keys, 2 x 8 x 7,936 x 65 floats (33 MB), inside
+    the 64 MiB scratch. (At a full round or more, whole rounds run unsplit and
+    only the units left over are split, into at most one round: at most 17
+    MB.) Bitwise the harness's result."""
+    pairs, query_rows, rows = 8, 7936, 4096
+    print(f"no-alloc attention: pairs {pairs}, queries {query_rows}, keys {rows}", flush=True)
+    q = values(pairs * query_rows * 64, 31, 3.0).reshape(pairs, query_rows, 64)
+    k = values(pairs * rows * 64, 32).reshape(pairs, rows, 64)
+    v = values(pairs * rows * 64, 33).reshape(pairs, rows, 64)
+    np.testing.assert_array_equal(no_alloc(device, q, k, v), harness(device, q, k, v))
+
+
+def test_no_alloc_attention_refuses_invalid_calls(device):
+    """A null operand and an out-of-range shape are refused on the host with
+    IRX_INVALID_ARGUMENT, before any work."""
+    kv = hipmem.DeviceArray.from_host(np.zeros((8, 16, 64), np.float32))
+    out = hipmem.DeviceArray((1, 16, 512))
     assert hip.lib().irx_icl_attention_noalloc(device.handle, None, kv.ptr, kv.ptr, 8, 1, 1, out.ptr,
                                                None) == hip.INVALID_ARGUMENT
+    assert hip.lib().irx_icl_attention_noalloc(device.handle, kv.ptr, kv.ptr, kv.ptr, 8, 1 << 25, 16, out.ptr,
+                                               None) == hip.INVALID_ARGUMENT
+    assert b"out of range" in hip.lib().irx_last_error()
