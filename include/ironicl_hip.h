@@ -5,7 +5,7 @@
  * plugin point: the `Device` enum (src/models/tabicl_v2/mod.rs:15-41) and the
  * `cuda` module surface (src/models/tabicl_v2/cuda/mod.rs:47-52). A thin Rust
  * FFI crate wraps these entry points into a `rocm` module with the same
- * surface; INTEGRATION.md shows that binding.
+ * surface.
  *
  * Conventions
  *   - Every entry point returns an irx_status. On failure the calling thread's

@@ -26,11 +26,12 @@
 //    loads; only a range's last tile is clamped and masked. One workgroup of
 //    four waves per CU: each wave may use 512 registers.
 //
-//    Key ranges are split over workgroups to fill the chip (prediction passes)
-//    or to even out its last round (the build); each split writes its
-//    normalized partial output and log2-sum-exp, and a merge kernel combines
-//    them. Workgroups sharing a (pair, split) K/V range are placed on the same
-//    XCD so the range is read into one L2.
+//    Key ranges are split over workgroups to fill the chip (prediction
+//    passes); the build's many query tiles run whole rounds with every key
+//    and split only the tiles left over (plan_icl_fp32). Each split writes
+//    its normalized partial output and log2-sum-exp, and a merge kernel
+//    combines them. Workgroups sharing a (pair, split) K/V range are placed on
+//    the same XCD so the range is read into one L2.
 //
 // 2. Attention of 16-wide heads on the vector ALUs (column ISAB and row
 //    transformer), one thread per (sequence, head, query row), keys staged
@@ -2144,6 +2145,9 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
         fail(3, "ICL attention FP8 cache and scales must be 16-byte aligned");
     // The FP8 cache uses the FP16 cache's tiling.
     const bool f16 = args.k16 != nullptr || fp8;
+    // Workgroup indices and unit counts are 32-bit in the kernels.
+    if ((long long)ceil_div((size_t)args.q_rows, kIclQueries) * args.pairs * 64 > INT32_MAX)
+        fail(3, "ICL attention shape exceeds the kernels' 32-bit workgroup indices");
     IclPlan pl{};
     if (f16)
         pl.main = plan_icl(args.pairs, args.q_rows, args.kv_rows, args.compute_units, true);

@@ -3,8 +3,9 @@ unchanged (src/format/model.rs:19-30, 381-483 encode, 486-714 parse,
 869-885 profiles; common rules in src/format/mod.rs:1-26).
 
 Kept alike on purpose: it is the on-disk interchange format the backend's
-weights come from (the north star keeps it unchanged), so an artifact written
-here loads in the reference and one the reference writes loads here.
+weights come from (the reference's own artifacts must load unchanged), so an
+artifact written here loads in the reference and one the reference writes loads
+here.
 
 Layout, little-endian:
 

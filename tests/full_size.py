@@ -39,7 +39,7 @@ def spot_checks(task, weights, width, ctx, x, y, xt, logits, features=4, train_r
                 float64_rows=4, members=None, log=print, tests=None, more_logits=None) -> dict:
     """Report of the checks on estimators `members` (default 0 and B-1) of the
     GPU context `ctx` (a StaticExecutor) built from x [B,N,H], y [B,N], with
-    GPU logits [B,Q,>=width] of xt [B,Q,H]; report["ok"] is the verdict.
+    GPU logits [B,Q,>=width] of xt [B,Q,H]; report["ok"] is the outcome.
     `tests` fixes the sampled test rows; `more_logits` maps a name to other
     GPU logits [B, len(tests), >=width] of those rows (another pass size), each
     checked like `logits` against the same oracle rows."""

@@ -17,7 +17,7 @@ root after building the oracle:
     python tests/golden/make_end_to_end.py [--stats]
 
 --stats also prints the conditioned weights' attention statistics on the
-1,024-row, 54-feature workload (the figures DESIGN.md records).
+1,024-row, 54-feature workload.
 """
 
 from __future__ import annotations

@@ -15,7 +15,7 @@ ora_build_context in test_oracle_model.py):
 Predictions: every test row on the GPU, the oracle's cached prediction of
 sampled rows against the GPU-built context, the HBM-bound small-pass kernels
 against the 512-row pass, and (classifier) invariance under a permutation of
-the training rows. The bar is the north star's: |gpu - cpu| <= 1e-5 +
+the training rows. The parity bar: |gpu - cpu| <= 1e-5 +
 1e-4 |cpu| with identical argmax. The benchmark's 50,000-row workload and
 the 8 x 200,000 x 500 ensemble run the same checks (tests/full_size.py)."""
 

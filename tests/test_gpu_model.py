@@ -1,6 +1,6 @@
 """Whole-model parity of the GPU path against the oracle, through the C ABI.
 
-The bar (north star): every logit / regression output within
+The parity bar: every logit / regression output within
 |gpu - cpu| <= 1e-5 + 1e-4 |cpu| of the oracle's FP32 CPU path on identical
 inputs and weights, with identical argmax."""
 
