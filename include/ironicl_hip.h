@@ -402,6 +402,9 @@ int irx_test_ln_linear(irx_device *device, int epilogue, const float *x, size_t 
                        const float *lnw, const float *lnb, const float *w, const float *b, size_t n,
                        const float *qm0w, const float *qm0b, const float *qm2w, const float *qm2b,
                        const float *base, float *out);
+/* GELU, 0.5 x (1 + erf(x / sqrt 2)), of count floats as every kernel here
+ * computes it (src/kernels/reference.rs:52-54). */
+int irx_test_gelu(irx_device *device, const float *x, size_t count, float *out);
 /* LayerNorm over width (128 or 512), eps 1e-5. */
 int irx_test_layer_norm(irx_device *device, const float *x, const float *weight, const float *bias,
                         size_t rows, size_t width, float *out);

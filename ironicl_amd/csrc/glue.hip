@@ -194,6 +194,11 @@ __global__ __launch_bounds__(256) void label_embedding_kernel(const float *targe
     }
 }
 
+__global__ __launch_bounds__(256) void gelu_kernel(const float *x, float *y, long long count) {
+    for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long long)gridDim.x * 256)
+        y[idx] = gelu_erf(x[idx]);
+}
+
 __global__ __launch_bounds__(256) void add_kernel(float *y, const float *x, long long count) {
     for (long long idx = (long long)blockIdx.x * 256 + threadIdx.x; idx < count; idx += (long long)gridDim.x * 256)
         y[idx] += x[idx];
@@ -294,6 +299,12 @@ void label_embeddings(const float *targets, long long n, const float *w, const f
     KernelTimer timer(kFamGlue, stream, 0.0, 4.0 * (n + count));
     hipLaunchKernelGGL(label_embedding_kernel, grid_1d(count), dim3(256), 0, stream, targets, n, w, b, classes, width,
                        classifier, out);
+    IRX_HIP(hipGetLastError());
+}
+
+void gelu_apply(const float *x, float *y, long long count, hipStream_t stream) {
+    if (count <= 0) return;
+    hipLaunchKernelGGL(gelu_kernel, grid_1d(count), dim3(256), 0, stream, x, y, count);
     IRX_HIP(hipGetLastError());
 }
 

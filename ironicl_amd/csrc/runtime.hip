@@ -2269,6 +2269,18 @@ int irx_test_layer_norm(irx_device *device, const float *x, const float *weight,
     });
 }
 
+int irx_test_gelu(irx_device *device, const float *x, size_t count, float *out) {
+    return guarded("irx_test_gelu", [&] {
+        if (!device || !x || !out || !count) fail(IRX_INVALID_ARGUMENT, "GELU arguments do not match");
+        set_device(device);
+        DevBuf dx(count * 4), dy(count * 4);
+        IRX_HIP(hipMemcpy(dx.p, x, count * 4, hipMemcpyHostToDevice));
+        gelu_apply(dx.f(), dy.f(), (long long)count, nullptr);
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(out, dy.p, count * 4, hipMemcpyDeviceToHost));
+    });
+}
+
 int irx_test_copy(irx_device *device, size_t floats) {
     return guarded("irx_test_copy", [&] {
         if (!device || !floats || floats % 4) fail(IRX_INVALID_ARGUMENT, "copy size must be a multiple of 4 floats");

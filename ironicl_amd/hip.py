@@ -121,6 +121,7 @@ SIGNATURES = {
     "irx_test_ln_linear": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _sz, _sz, _CF, _CF, _CF, _CF, _sz, _CF,
                                           _CF, _CF, _CF, _CF, _F]),
     "irx_test_layer_norm": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _F]),
+    "irx_test_gelu": (ctypes.c_int, [ctypes.c_void_p, _CF, _sz, _F]),
     "irx_test_copy": (ctypes.c_int, [ctypes.c_void_p, _sz]),
     "irx_test_small_attention": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _sz, _F]),
     "irx_test_small_attention_rope": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _CF, _CF, _sz, _sz, _sz, _F]),

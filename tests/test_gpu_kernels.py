@@ -424,6 +424,28 @@ def test_ln_linear_qass_matches_float64(device, form, estimators, rows):
     np.testing.assert_allclose(out.reshape(estimators, 8, rows, 64), want, rtol=1e-4, atol=2e-5)
 
 
+def test_gelu_matches_float64(device):
+    """The GELU every kernel computes (erfc from one fitted polynomial of log2
+    erfc and one exponential) against float64 0.5 x (1 + erf(x / sqrt 2)) on a
+    dense grid over [-12, 12], the fit's end at |x| = 4 sqrt 2, tiny and huge
+    magnitudes: within 1.2e-7 (1 + |x|); +inf stays inf and NaN stays NaN."""
+    from scipy.special import erf
+    grid = np.linspace(-12.0, 12.0, 2_000_001)
+    edge = 4.0 * math.sqrt(2.0) + np.linspace(-1e-4, 1e-4, 2001)
+    extra = np.array([0.0, -0.0, 1e-30, -1e-30, 1e-7, -1e-7, 30.0, -30.0, 1e6, -1e6, 3.4e38, -3.4e38])
+    x = np.concatenate([grid, edge, -edge, extra]).astype(np.float32)
+    out = np.zeros_like(x)
+    hip.check(hip.lib().irx_test_gelu(device.handle, hip.fptr(x), x.size, hip.fptr(out)))
+    x64 = x.astype(np.float64)
+    want = 0.5 * x64 * (1.0 + erf(x64 / math.sqrt(2.0)))
+    err = np.abs(out.astype(np.float64) - want)
+    assert (err <= 1.2e-7 * (1.0 + np.abs(x64))).all(), (x[err.argmax()], err.max())
+    special = np.array([np.inf, np.nan], np.float32)
+    got = np.zeros_like(special)
+    hip.check(hip.lib().irx_test_gelu(device.handle, hip.fptr(special), 2, hip.fptr(got)))
+    assert got[0] == np.inf and np.isnan(got[1])
+
+
 @pytest.mark.parametrize("rows,width", [(1, 128), (333, 128), (1000, 512), (4, 512)])
 def test_layer_norm_matches_float64(device, rows, width):
     x = fast_values(rows * width, 4, 3.0) + 0.5
