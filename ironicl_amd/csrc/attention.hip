@@ -221,19 +221,21 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][0][r] = 0.f, o[j][1][r] = 0.f;
     // Softmax reference m_ref[j] per query (shared by the lane pair l, l ^ 32):
-    // probabilities are exp2(s - m_ref). It is raised, and the tile redone,
-    // only when a tile's probabilities could exceed 2^64 or when it is still
-    // unset (-inf, the first tile), so most tiles skip the maximum reduction;
-    // -m_ref is the products' initial accumulator, which folds the subtraction
-    // into the MFMA. Relative to the true running maximum a probability is at
-    // most 2^64 and anything below 2^-126 of the maximum is lost, as in the
-    // exact online softmax.
+    // probabilities are exp2(s - m_ref). The range's first tile sets it to
+    // that tile's maxima (its products start from zero); after that it is
+    // raised, and the tile redone, only when a tile's probabilities could
+    // exceed 2^64, so most tiles skip the maximum reduction; -m_ref is the
+    // products' initial accumulator, which folds the subtraction into the
+    // MFMA. Relative to the true running maximum a probability is at most
+    // 2^64 and anything below 2^-126 of the maximum is lost, as in the exact
+    // online softmax.
     float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     f32x16 neg_ref[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) neg_ref[j][r] = INFINITY;
+        for (int r = 0; r < 16; ++r) neg_ref[j][r] = 0.f;
+    bool fresh = true;  // workgroup-uniform: no tile of the range done yet
     constexpr float kLazyLimit = 18446744073709551616.0f;  // 2^64
     // K fragment of chunk 8*half + cc for key r32 of block 0 is at kfrag + (cc >> 2) * 1024 + (cc & 3) * 64;
     // block 1 (keys 32..63) is 512 floats further.
@@ -308,6 +310,24 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
                 }
             }
         }
+        if (fresh) {
+            // The range's first tile: its scores (from a zero accumulator)
+            // give the reference.
+            fresh = false;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float mt = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(s[j][0][r], s[j][1][r]));
+                const float m = halves_max(mt);
+                m_ref[j] = m;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    neg_ref[j][r] = -m;
+                    s[j][0][r] -= m, s[j][1][r] -= m;
+                }
+            }
+        }
         // Softmax per query block (exp2 domain) against the lazy reference.
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -319,7 +339,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_kernel(IclAtt
                 lsum += s[j][0][r] + s[j][1][r];
             }
             if (__any(!(lsum <= kLazyLimit))) {
-                // The reference is unset or too low for this tile: recompute the
+                // The reference is too low for this tile: recompute the
                 // block's scores from zero and raise it to the running maximum.
                 f32x16 t0, t1;
 #pragma unroll
@@ -653,11 +673,14 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[d][j][r] = 0.f;
+    // The lazy reference as in icl_attention_kernel: set from the range's
+    // first tile, raised when a tile's probabilities could pass the limit.
     float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     f32x16 neg_ref[2], zero;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) neg_ref[0][r] = INFINITY, neg_ref[1][r] = INFINITY, zero[r] = 0.f;
+    for (int r = 0; r < 16; ++r) neg_ref[0][r] = 0.f, neg_ref[1][r] = 0.f, zero[r] = 0.f;
     constexpr float kLazyLimit16 = 32768.0f;  // 2^15: probabilities stay FP16-representable
+    bool fresh = true;  // workgroup-uniform: no tile of the range done yet
 
     // One tile at k0 from LDS buffer `buf`. Only a range's last tile can hold
     // keys past it (RAGGED): full tiles carry no masking code at all (left to
@@ -695,6 +718,19 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             scores(j, neg_ref[j], s[j][0], s[j][1]);
+            if (fresh) {
+                // The range's first tile (scores from a zero accumulator).
+                float mt = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mt = fmaxf(mt, fmaxf(s[j][0][r], s[j][1][r]));
+                const float m = halves_max(mt);
+                m_ref[j] = m;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    neg_ref[j][r] = -m;
+                    s[j][0][r] -= m, s[j][1][r] -= m;
+                }
+            }
             float lsum = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -724,6 +760,7 @@ __global__ __launch_bounds__(kIclWaves * 64, 1) void icl_attention_split_kernel(
             }
             l_run[j] += lsum;
         }
+        fresh = false;
         // O^T += V^T P^T over the tile's four 16-key steps.
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -926,10 +963,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
     for (int gq = 0; gq < QG; ++gq) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) o[gq][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        neg_ref[gq] = INFINITY, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
+        neg_ref[gq] = 0.f, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
     }
     constexpr float kLazyLimit = 18446744073709551616.0f;  // 2^64
     constexpr int kStride = 16 * kDecodeWaves;
+    // The wave's first block sets the reference from its own maxima (its
+    // scores start from zero); later blocks redo theirs only when their
+    // probabilities could exceed 2^64.
+    bool fresh = true;
 
     // One 16-key block at kk (kk < k_end): scores, lazy softmax, output.
     auto process = [&](int kk, const f32x4 *kf, const f32x4 *vf) {
@@ -944,6 +985,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
                 for (int r = 0; r < 4; ++r)
                     if (kk + 4 * grp + r >= k_end) s[r] = -INFINITY;
             }
+            if (fresh) {
+                float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+                mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+                mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                neg_ref[gq] = -mt;
+                m_ref[gq] = mt;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] -= mt;
+            }
             float lsum = 0.f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -951,7 +1001,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
                 lsum += s[r];
             }
             if (__any(!(lsum <= kLazyLimit))) {
-                // Unset or too low a reference: redo this block's scores from zero.
+                // Too low a reference: redo this block's scores from zero.
                 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int m = 0; m < 16; ++m)
@@ -985,6 +1035,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
                 for (int t = 0; t < 4; ++t)
                     o[gq][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r][t], s[r], o[gq][t], 0, 0, 0);
         }
+        fresh = false;
     };
 
     // Two register sets in turn: the next block's loads are always issued
@@ -1154,11 +1205,12 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
     for (int gq = 0; gq < QG; ++gq) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) o[gq][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-        neg_ref[gq] = INFINITY, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
+        neg_ref[gq] = 0.f, m_ref[gq] = -INFINITY, l_run[gq] = 0.f;
     }
     constexpr float kLazyLimit16 = 32768.0f;
     constexpr int kStride = 32 * kDecodeWaves;
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    bool fresh = true;  // the wave's first block sets the reference (as icl_decode_kernel)
 
     auto process = [&](int kk, const u32x4 *kf, const u32x4 *vf) {
         const bool tail = kk + 32 > k_end;
@@ -1188,6 +1240,16 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
             const f32x4 nr = {neg_ref[gq], neg_ref[gq], neg_ref[gq], neg_ref[gq]};
             f32x4 s0, s1;
             scores(nr, s0, s1);
+            if (fresh) {
+                float mt = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                 fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+                mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+                mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+                neg_ref[gq] = -mt;
+                m_ref[gq] = mt;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s0[r] -= mt, s1[r] -= mt;
+            }
             float lsum = 0.f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -1233,6 +1295,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode16_kernel(IclA
                 if constexpr (!FP8) o[gq][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[gq][d], 0, 0, 0);
             }
         }
+        fresh = false;
     };
 
     // Two register sets in turn; loads past the range re-read the range's
