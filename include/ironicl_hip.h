@@ -390,6 +390,19 @@ int irx_test_block_tail(irx_device *device, int fused, const float *att, const f
                         const float *wo, const float *bo, const float *n2w, const float *n2b,
                         const float *w1, const float *b1, const float *w2, const float *b2,
                         size_t repeats, float *out);
+/* A cached column block (multihead_attn2 of a column ISAB block and its
+ * feed-forward half, cpu.rs:2587-2850; the reference's column_block_f32,
+ * kernels.rs:1342) on `cols` columns of `rows` rows, state [cols, rows, 128]
+ * updated into out: LN1 (lnw / lnb), q = LN1(state) wq^T + bq (wq [128, 128]),
+ * attention of 8 heads of 16 (scale 1/4) to the column's cached inducing keys
+ * and values k, v [cols, 8, 128, 16], then the tail of irx_test_block_tail
+ * (same weights). fused = 1 runs the one-kernel block, 0 the head, 16-wide
+ * attention and tail launches. repeats as irx_test_block_tail. */
+int irx_test_column_block(irx_device *device, int fused, const float *state, size_t cols, size_t rows,
+                          const float *k, const float *v, const float *lnw, const float *lnb, const float *wq,
+                          const float *bq, const float *wo, const float *bo, const float *n2w, const float *n2b,
+                          const float *w1, const float *b1, const float *w2, const float *b2, size_t repeats,
+                          float *out);
 /* LayerNorm fused into a 512-wide product, x [m, 512], w [n, 512]:
  * epilogue 1 (GELU): out [m, n] = gelu(LN(x) w^T + b); epilogue 2 (QASS, the
  * ICL query path, n = 512): q = LN(x) w^T + b, then per head

@@ -57,7 +57,6 @@ __device__ __forceinline__ int bid_x() { return (int)__builtin_amdgcn_workgroup_
 __device__ __forceinline__ int bdim_x() { return (int)__builtin_amdgcn_workgroup_size_x(); }
 
 constexpr int kKeyTile = 64;
-constexpr float kLog2e = 1.44269504088896340736f;
 
 struct IclLaunch {
     int qtiles, splits, keys_per_split, per_xcd, q_padded;

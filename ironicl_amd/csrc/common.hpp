@@ -25,6 +25,8 @@ constexpr int kColumnHead = kColumnDim / kHeads;  // 16
 constexpr int kIclHead = kIclDim / kHeads;         // 64
 // One column's cached inducing K (or V): 8 heads x 128 points x 16 dims.
 constexpr int kColumnCache = kHeads * kInducing * kColumnHead;
+// Softmaxes run in the exp2 domain: scores are scaled by log2(e).
+constexpr float kLog2e = 1.44269504088896340736f;
 
 // A failed HIP call or argument check. The C ABI turns it into a status code
 // and the thread's last-error message.
@@ -186,6 +188,30 @@ struct Head128 {
 size_t head128_pack_floats(int outputs);
 void head128_pack(const float *w, int outputs, float *out);
 void head128(const Head128 &h, hipStream_t stream);
+
+// A cached column block in one kernel (multihead_attn2 of a column ISAB block
+// with its feed-forward half, cached_block, cpu.rs:2587-2850; the reference's
+// one-launch column_block_f32, kernels.rs:1342): for the states x of `cols`
+// columns of `rows` rows,
+//   q = LN1(x) Wq^T + bq, att = softmax(q K^T / 4) V per head of 16 against
+//   the column's 128 cached inducing keys and values,
+// then the tail128 chain on (att, x). Bitwise the results of head128 (8
+// blocks), the 16-wide attention and tail128 run in turn.
+struct ColumnBlock {
+    float *state;  // [cols, rows, 128], updated in place
+    long long rows;
+    int cols;
+    // Column c's keys [8][128][16] at k + (c / group) * group_stride + (c % group) * kColumnCache (values at v + ...).
+    const float *k, *v;
+    int group;
+    long long group_stride;
+    const float *lnw, *lnb;  // LN1 [128]
+    const float *qpack;      // head128_pack of in_proj rows 0..127
+    const float *qb;         // their bias [128]
+    const float *pack;       // tail128_pack of the block
+    const float *bo, *n2w, *n2b, *b1, *b2;
+};
+void column_block(const ColumnBlock &c, hipStream_t stream);
 
 // Regression outputs of decoded quantiles [b, q, k] (k <= 4096) on the device
 // (quantiles::summarize, quantiles.rs:80-213): per query row, averaged over

@@ -443,6 +443,9 @@ void set_device(const irx_device *d) { IRX_HIP(hipSetDevice(d->ordinal)); }
 // them (prediction passes); larger products (the build's N rows) keep the
 // tiled GEMMs, whose large tiles reuse the weights across rows.
 constexpr long long kLnLinearRows = 8192;
+// States (columns x rows) from which a cached column block runs as one
+// kernel (column_block) rather than three launches.
+constexpr long long kColumnFusedRows = 16384;
 
 struct Stages {
     const irx_weights &w;
@@ -543,10 +546,24 @@ struct Stages {
     // states [cols, rows, 128] against cached inducing K/V: column c reads
     // kcache + (c / group) * group_stride + (c % group) * 16384
     // (cached_block, cpu.rs:2587-2850; column_block_f32, kernels.rs:1342).
+    // fused: -1 chooses, 0 the three launches (head, 16-wide attention,
+    // tail), 1 column_block's one kernel (the head128 / tail128 arithmetic:
+    // bitwise the three launches from 16384 rows).
     void column_attend(int blk, float *state, int cols, int rows, const float *kcache, const float *vcache,
-                       int group, long long group_stride, float *norm, float *q, float *att, float *hid) const {
+                       int group, long long group_stride, float *norm, float *q, float *att, float *hid,
+                       int fused = -1) const {
         const BlockW &bw = w.col2[blk];
         const long long m = (long long)cols * rows;
+        const bool packed = bw.head_pack && bw.head_nb == 8 && bw.head_row0 == 0 && bw.tail_pack;
+        if (fused == 1 || (fused < 0 && packed && m >= kColumnFusedRows)) {
+            if (!packed) fail(IRX_INVALID_ARGUMENT, "the fused column block needs packed weights");
+            ColumnBlock c{};
+            c.state = state, c.rows = rows, c.cols = cols, c.k = kcache, c.v = vcache, c.group = group;
+            c.group_stride = group_stride, c.lnw = bw.n1w, c.lnb = bw.n1b, c.qpack = bw.head_pack, c.qb = bw.in_b;
+            c.pack = bw.tail_pack, c.bo = bw.out.b, c.n2w = bw.n2w, c.n2b = bw.n2b, c.b1 = bw.l1.b, c.b2 = bw.l2.b;
+            column_block(c, s);
+            return;
+        }
         head(bw, state, m, norm, q, kColumnDim);
         SmallAttention a{};
         a.q = q, a.q_seq = (long long)rows * kColumnDim, a.q_group = (long long)group * rows * kColumnDim;
@@ -2203,6 +2220,57 @@ int irx_test_block_tail(irx_device *device, int fused, const float *att, const f
         IRX_HIP(hipMemcpy(out, dstate.p, n * 4, hipMemcpyDeviceToHost));
         // Further applications (timing only) update the same state.
         for (size_t i = 1; i < repeats; ++i) st.tail(bw, dstate.f(), (long long)rows, datt.f(), dnorm.f(), dhid.f(), fused);
+        IRX_HIP(hipDeviceSynchronize());
+    });
+}
+
+int irx_test_column_block(irx_device *device, int fused, const float *state, size_t cols, size_t rows,
+                          const float *k, const float *v, const float *lnw, const float *lnb, const float *wq,
+                          const float *bq, const float *wo, const float *bo, const float *n2w, const float *n2b,
+                          const float *w1, const float *b1, const float *w2, const float *b2, size_t repeats,
+                          float *out) {
+    return guarded("irx_test_column_block", [&] {
+        if (!device || !state || !k || !v || !lnw || !lnb || !wq || !bq || !wo || !bo || !n2w || !n2b || !w1 ||
+            !b1 || !w2 || !b2 || !out || !cols || !rows || (fused != 0 && fused != 1) || !repeats ||
+            cols > (1u << 20) || rows > (1u << 24))
+            fail(IRX_INVALID_ARGUMENT, "column block arguments do not match");
+        set_device(device);
+        const size_t n = cols * rows * 128;
+        std::vector<float> host;
+        const size_t hpack = head128_pack_floats(128);
+        const size_t sizes[] = {128,         128, 128 * 128, 128, 128 * 128, 128, 128, 128, 256 * 128, 256,
+                                128 * 256,   128, hpack,     kTail128PackFloats};
+        const float *srcs[] = {lnw, lnb, wq, bq, wo, bo, n2w, n2b, w1, b1, w2, b2, nullptr, nullptr};
+        constexpr int kParts = 14;
+        size_t offs[kParts], total = 0;
+        for (int i = 0; i < kParts; ++i) offs[i] = total, total += (sizes[i] + 63) / 64 * 64;
+        host.assign(total, 0.f);
+        for (int i = 0; i < 12; ++i) std::memcpy(host.data() + offs[i], srcs[i], sizes[i] * 4);
+        head128_pack(wq, 128, host.data() + offs[12]);
+        tail128_pack(wo, w1, w2, host.data() + offs[13]);
+        DevBuf dw(total * 4), dstate(n * 4), dk(cols * kColumnCache * 4), dv(cols * kColumnCache * 4);
+        DevBuf dnorm(n * 4), dq(n * 4), datt(n * 4), dhid(2 * n * 4);
+        IRX_HIP(hipMemcpy(dw.p, host.data(), total * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dstate.p, state, n * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dk.p, k, cols * kColumnCache * 4, hipMemcpyHostToDevice));
+        IRX_HIP(hipMemcpy(dv.p, v, cols * kColumnCache * 4, hipMemcpyHostToDevice));
+        const float *f = dw.f();
+        irx_weights none;
+        BlockW &bw = none.col2[0];
+        bw.dim = 128, bw.n1w = f + offs[0], bw.n1b = f + offs[1], bw.in_w = f + offs[2], bw.in_b = f + offs[3];
+        bw.out = {f + offs[4], f + offs[5]}, bw.n2w = f + offs[6], bw.n2b = f + offs[7];
+        bw.l1 = {f + offs[8], f + offs[9]}, bw.l2 = {f + offs[10], f + offs[11]};
+        bw.head_pack = f + offs[12], bw.head_nb = 8, bw.head_row0 = 0, bw.tail_pack = f + offs[13];
+        Stages st{none, nullptr, device->compute_units};
+        auto run = [&] {
+            st.column_attend(0, dstate.f(), (int)cols, (int)rows, dk.f(), dv.f(), (int)cols, 0, dnorm.f(), dq.f(),
+                             datt.f(), dhid.f(), fused);
+        };
+        run();
+        IRX_HIP(hipDeviceSynchronize());
+        IRX_HIP(hipMemcpy(out, dstate.p, n * 4, hipMemcpyDeviceToHost));
+        // Further applications (timing only) update the same state.
+        for (size_t i = 1; i < repeats; ++i) run();
         IRX_HIP(hipDeviceSynchronize());
     });
 }

@@ -53,6 +53,131 @@ __device__ __forceinline__ f32x4 mfma(float a, float b, const f32x4 &acc) {
 
 __device__ __forceinline__ f32x4 lds4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
 
+// The chain after a 128-wide block's attention (cpu.rs:1555-1601): x holds
+// the row's attention output and s1 its state, in the per-wave layout above;
+// the packed weights arrive as half-chunks h0 .. h0 + 19 from next(h), which
+// returns the lane's base in the half's LDS buffer. The new state goes to
+// out (the lane's first feature, 4 g) when the row is live.
+template <class Next>
+__device__ __forceinline__ void tail_chain(f32x4 (&x)[8], f32x4 (&s1)[8], Next &&next, int h0, const Tail128 &t,
+                                           float *out, bool live, int g) {
+    f32x4 acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Out-projection: half-chunks 0 .. 3 hold k-blocks 2 hc and 2 hc + 1,
+    // each with the eight output blocks' fragments. The second k-block's
+    // fragments are read while the first one's 32 products (8 independent
+    // accumulators) run.
+#pragma unroll
+    for (int hc = 0; hc < 4; ++hc) {
+        const float *frag = next(h0 + hc);
+        f32x4 fa[2][8];
+#pragma unroll
+        for (int ob = 0; ob < 8; ++ob) fa[0][ob] = lds4(frag + ob * 256);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            if (kb == 0) {
+#pragma unroll
+                for (int ob = 0; ob < 8; ++ob) fa[1][ob] = lds4(frag + (8 + ob) * 256);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(fa[kb][ob][e], x[2 * hc + kb][e], acc[ob]);
+        }
+    }
+
+    // s1 = state + (acc + bo), then LN2 over the row's 128 features, held by
+    // lanes m, m + 16, m + 32, m + 48.
+    float sum = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 bo = *reinterpret_cast<const f32x4 *>(t.bo + 16 * b + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            s1[b][e] = s1[b][e] + (acc[b][e] + bo[e]);
+            sum += s1[b][e];
+        }
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float mean = sum / 128.f;
+    float sq = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float d = s1[b][e] - mean;
+            sq = fmaf(d, d, sq);
+        }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 w = *reinterpret_cast<const f32x4 *>(t.n2w + 16 * b + 4 * g);
+        const f32x4 bb = *reinterpret_cast<const f32x4 *>(t.n2b + 16 * b + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[b][e] = (s1[b][e] - mean) * rstd * w[e] + bb[e];
+        acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // FFN, 32 hidden units per slice c: h = gelu(W1 x + b1) for units 32 c +
+    // 16 hb + 4 g + e from half-chunk 4 + 2 c (even and odd k-blocks in
+    // separate accumulators, four independent chains), then acc += W2 h from
+    // half-chunk 5 + 2 c.
+#pragma unroll 1
+    for (int c = 0; c < 8; ++c) {
+        const float *frag = next(h0 + 4 + 2 * c);
+        f32x4 h[2][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i >> 1][i & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 fw[2][2];
+        fw[0][0] = lds4(frag), fw[0][1] = lds4(frag + 256);
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            if (kb < 7) {
+                fw[(kb + 1) & 1][0] = lds4(frag + ((kb + 1) * 2) * 256);
+                fw[(kb + 1) & 1][1] = lds4(frag + ((kb + 1) * 2 + 1) * 256);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) h[hb][kb & 1] = mfma(fw[kb & 1][hb][e], x[kb][e], h[hb][kb & 1]);
+        }
+        f32x4 hg[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const f32x4 b1 = *reinterpret_cast<const f32x4 *>(t.b1 + 32 * c + 16 * hb + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hg[hb][e] = gelu_erf((h[hb][0][e] + h[hb][1][e]) + b1[e]);
+        }
+        const float *frag2 = next(h0 + 5 + 2 * c);
+        f32x4 f2[2][8];
+#pragma unroll
+        for (int ob = 0; ob < 8; ++ob) f2[0][ob] = lds4(frag2 + ob * 256);
+#pragma unroll
+        for (int ob = 0; ob < 8; ++ob) f2[1][ob] = lds4(frag2 + (8 + ob) * 256);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(f2[j][ob][e], hg[j][e], acc[ob]);
+    }
+
+    if (!live) return;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const f32x4 b2 = *reinterpret_cast<const f32x4 *>(t.b2 + 16 * b + 4 * g);
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (acc[b][e] + b2[e]) + s1[b][e];
+        *reinterpret_cast<f32x4 *>(out + 16 * b) = v;
+    }
+}
+
 __global__ __launch_bounds__(256, 3) void tail128_kernel(Tail128 p) {
     __shared__ __attribute__((aligned(16))) float buf[2][kHalfFloats];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -81,128 +206,172 @@ __global__ __launch_bounds__(256, 3) void tail128_kernel(Tail128 p) {
     issue(0);
 
     // x: row m's features 16 kb + 4 g + e (att now, LN2(s1) later).
-    f32x4 x[8], s1[8], acc[8];
+    f32x4 x[8], s1[8];
     const float *att = p.att + r * p.lda + 4 * g;
     const float *st = p.state + r * p.ldx + 4 * g;
 #pragma unroll
     for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(att + 16 * b);
 #pragma unroll
     for (int b = 0; b < 8; ++b) s1[b] = *reinterpret_cast<const f32x4 *>(st + 16 * b);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    tail_chain(x, s1, next, 0, p, p.state + r * p.ldx + 4 * g, live, g);
+}
 
-    // Out-projection: half-chunks 0 .. 3 hold k-blocks 2 hc and 2 hc + 1,
-    // each with the eight output blocks' fragments. The second k-block's
-    // fragments are read while the first one's 32 products (8 independent
-    // accumulators) run.
+// A cached column block in one kernel: 64 rows of one column per workgroup,
+// wave w carrying rows 16 w .. 16 w + 15 through LN1, the query projection
+// (head128's order), the attention of its 8 heads to the column's 128 cached
+// inducing keys and values (the 16-wide attention kernel's exact softmax and
+// order) and tail128's chain, so q and the attention output never leave
+// registers. 32 half-chunks of 16 KB stream through two LDS buffers: 0..3 the
+// query rows' fragments, 4..11 head h's keys (fragment order, 8 KB) and values
+// (8 KB: per 16-key block, four planes of 64 lanes, lane (d, g) of plane r
+// holding key 16 kb + 4 g + r's dim d, gathered by 4-byte loads from the
+// cache's [key][16] rows), 12..31 tail128's pack. Workgroups of one XCD take
+// consecutive units, so a column's tiles share its K/V in one L2.
+constexpr int kColumnHalves = 32;
+
+__global__ __launch_bounds__(256, 2) void column_block_kernel(ColumnBlock p, int tiles, int per_xcd) {
+    __shared__ __attribute__((aligned(16))) float buf[2][kHalfFloats];
+    const int unit = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    if (unit >= p.cols * tiles) return;  // workgroup-uniform, before any barrier
+    const int col = unit / tiles, tile = unit - col * tiles;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
+    const long long row = (long long)tile * kTailRows + wv * 16 + m16;
+    const bool live = row < p.rows;
+    const long long r = live ? row : p.rows - 1;
+    float *xrow = p.state + ((long long)col * p.rows + r) * 128 + 4 * g;
+    const long long coff = (long long)(col / p.group) * p.group_stride + (long long)(col % p.group) * kColumnCache;
+    const float *kcol = p.k + coff, *vcol = p.v + coff;
+
+    auto issue = [&](int h) {
+        float *dst = buf[h & 1];
+        if (h < 4 || h >= 12) {
+            const float *src = (h < 4 ? p.qpack + h * kHalfFloats : p.pack + (h - 12) * kHalfFloats) + (4 * wv) * 256 +
+                               lane * 4;
 #pragma unroll
-    for (int hc = 0; hc < 4; ++hc) {
-        const float *frag = next(hc);
-        f32x4 fa[2][8];
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_global_load_lds(src + i * 256, (lds_void *)&dst[(4 * wv + i) * 256], 16, 0, 0);
+        } else {
+            // Head h - 4: wave w moves key blocks 2 w and 2 w + 1.
+            const float *kh = kcol + (h - 4) * (kInducing * kColumnHead), *vh = vcol + (h - 4) * (kInducing * kColumnHead);
 #pragma unroll
-        for (int ob = 0; ob < 8; ++ob) fa[0][ob] = lds4(frag + ob * 256);
+            for (int i = 0; i < 2; ++i) {
+                const int kb = 2 * wv + i;
+                __builtin_amdgcn_global_load_lds(kh + (16 * kb + m16) * 16 + 4 * g, (lds_void *)&dst[kb * 256], 16, 0, 0);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            if (kb == 0) {
-#pragma unroll
-                for (int ob = 0; ob < 8; ++ob) fa[1][ob] = lds4(frag + (8 + ob) * 256);
+                for (int rr = 0; rr < 4; ++rr)
+                    __builtin_amdgcn_global_load_lds(vh + (16 * kb + 4 * g + rr) * 16 + m16,
+                                                     (lds_void *)&dst[2048 + (kb * 4 + rr) * 64], 4, 0, 0);
             }
+        }
+    };
+    // Half h's buffer once its loads are done and every wave is past half
+    // h - 1 (whose buffer half h + 1 then overwrites).
+    auto next = [&](int h) {
+        wait_vm();
+        __syncthreads();
+        if (h + 1 < kColumnHalves) issue(h + 1);
+        return &buf[h & 1][0];
+    };
+    issue(0);
+
+    // The rows' states (kept for the residual) and LN1, as head128.
+    f32x4 s1[8], x[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+    for (int b = 0; b < 8; ++b) s1[b] = *reinterpret_cast<const f32x4 *>(xrow + 16 * b);
+    {
+        float sum = 0.f;
 #pragma unroll
-                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(fa[kb][ob][e], x[2 * hc + kb][e], acc[ob]);
+        for (int b = 0; b < 8; ++b) sum += (s1[b][0] + s1[b][1]) + (s1[b][2] + s1[b][3]);
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        const float mean = sum / 128.f;
+        float sq = 0.f;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = s1[b][e] - mean;
+                sq = fmaf(d, d, sq);
+            }
+        sq += __shfl_xor(sq, 16, 64);
+        sq += __shfl_xor(sq, 32, 64);
+        const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const f32x4 w = *reinterpret_cast<const f32x4 *>(p.lnw + 16 * b + 4 * g);
+            const f32x4 bb = *reinterpret_cast<const f32x4 *>(p.lnb + 16 * b + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[b][e] = (s1[b][e] - mean) * rstd * w[e] + bb[e];
         }
     }
 
-    // s1 = state + (acc + bo), then LN2 over the row's 128 features, held by
-    // lanes m, m + 16, m + 32, m + 48.
-    float sum = 0.f;
+    // q: lane (m, g) holds head h's dims 4 g .. 4 g + 3 of row m in q[h],
+    // scaled into the exp2 domain (1 / sqrt(16) = 0.25).
+    f32x4 q[8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const f32x4 bo = *reinterpret_cast<const f32x4 *>(p.bo + 16 * b + 4 * g);
+    for (int ob = 0; ob < 8; ++ob) q[ob] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            s1[b][e] = s1[b][e] + (acc[b][e] + bo[e]);
-            sum += s1[b][e];
+    for (int c = 0; c < 4; ++c) {
+        const float *frag = next(c) + lane * 4;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int f = 16 * c + i, kb = f / 8, ob = f % 8;
+            const f32x4 a = lds4(frag + i * 256);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[ob] = mfma(a[e], x[kb][e], q[ob]);
         }
     }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    const float mean = sum / 128.f;
-    float sq = 0.f;
+    const float scale = 0.25f * kLog2e;
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float d = s1[b][e] - mean;
-            sq = fmaf(d, d, sq);
-        }
-    sq += __shfl_xor(sq, 16, 64);
-    sq += __shfl_xor(sq, 32, 64);
-    const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const f32x4 w = *reinterpret_cast<const f32x4 *>(p.n2w + 16 * b + 4 * g);
-        const f32x4 bb = *reinterpret_cast<const f32x4 *>(p.n2b + 16 * b + 4 * g);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[b][e] = (s1[b][e] - mean) * rstd * w[e] + bb[e];
-        acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int ob = 0; ob < 8; ++ob) q[ob] = (q[ob] + *reinterpret_cast<const f32x4 *>(p.qb + 16 * ob + 4 * g)) * scale;
 
-    // FFN, 32 hidden units per slice c: h = gelu(W1 x + b1) for units 32 c +
-    // 16 hb + 4 g + e from half-chunk 4 + 2 c (even and odd k-blocks in
-    // separate accumulators, four independent chains), then acc += W2 h from
-    // half-chunk 5 + 2 c.
-#pragma unroll 1
-    for (int c = 0; c < 8; ++c) {
-        const float *frag = next(4 + 2 * c);
-        f32x4 h[2][2];
+    // Per head: S^T = K Q^T (lane (m, g) holds keys 16 kb + 4 g + r of row
+    // m), the exact softmax over the 128 keys, O^T = V^T P^T, which leaves
+    // head h's output in tail128's layout for feature block h.
+    f32x4 att[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i >> 1][i & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        f32x4 fw[2][2];
-        fw[0][0] = lds4(frag), fw[0][1] = lds4(frag + 256);
+    for (int h = 0; h < 8; ++h) {
+        const float *hb = next(4 + h);
+        f32x4 s[8];
 #pragma unroll
         for (int kb = 0; kb < 8; ++kb) {
-            if (kb < 7) {
-                fw[(kb + 1) & 1][0] = lds4(frag + ((kb + 1) * 2) * 256);
-                fw[(kb + 1) & 1][1] = lds4(frag + ((kb + 1) * 2 + 1) * 256);
+            const f32x4 kf = lds4(hb + kb * 256 + lane * 4);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) acc = mfma(kf[st], q[h][st], acc);
+            s[kb] = acc;
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) m = fmaxf(m, fmaxf(fmaxf(s[kb][0], s[kb][1]), fmaxf(s[kb][2], s[kb][3])));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float l = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                s[kb][rr] = __builtin_amdgcn_exp2f(s[kb][rr] - m);
+                l += s[kb][rr];
             }
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const float inv = 1.0f / l;
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+        for (int kb = 0; kb < 8; ++kb) {
+            const float *vp = hb + 2048 + kb * 256 + lane;
 #pragma unroll
-                for (int hb = 0; hb < 2; ++hb) h[hb][kb & 1] = mfma(fw[kb & 1][hb][e], x[kb][e], h[hb][kb & 1]);
+            for (int rr = 0; rr < 4; ++rr) o = mfma(vp[rr * 64], s[kb][rr], o);
         }
-        f32x4 hg[2];
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-            const f32x4 b1 = *reinterpret_cast<const f32x4 *>(p.b1 + 32 * c + 16 * hb + 4 * g);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) hg[hb][e] = gelu_erf((h[hb][0][e] + h[hb][1][e]) + b1[e]);
-        }
-        const float *frag2 = next(5 + 2 * c);
-        f32x4 f2[2][8];
-#pragma unroll
-        for (int ob = 0; ob < 8; ++ob) f2[0][ob] = lds4(frag2 + ob * 256);
-#pragma unroll
-        for (int ob = 0; ob < 8; ++ob) f2[1][ob] = lds4(frag2 + (8 + ob) * 256);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int ob = 0; ob < 8; ++ob) acc[ob] = mfma(f2[j][ob][e], hg[j][e], acc[ob]);
+        att[h] = o * inv;
     }
 
-    if (!live) return;
-    float *out = p.state + row * p.ldx + 4 * g;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const f32x4 b2 = *reinterpret_cast<const f32x4 *>(p.b2 + 16 * b + 4 * g);
-        f32x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (acc[b][e] + b2[e]) + s1[b][e];
-        *reinterpret_cast<f32x4 *>(out + 16 * b) = v;
-    }
+    Tail128 t{};
+    t.bo = p.bo, t.n2w = p.n2w, t.n2b = p.n2b, t.b1 = p.b1, t.b2 = p.b2;
+    tail_chain(att, s1, [&](int h) { return next(h) + lane * 4; }, 12, t, xrow, live, g);
 }
 
 // The same tail for small passes (a few thousand rows or fewer), where
@@ -511,6 +680,27 @@ void tail128(const Tail128 &t, hipStream_t stream, bool rows16) {
         hipLaunchKernelGGL(tail128_rows16_kernel, dim3((unsigned)ceil_div(t.m, 16LL)), dim3(256), 0, stream, t);
     else
         hipLaunchKernelGGL(tail128_kernel, dim3((unsigned)ceil_div(t.m, (long long)kTailRows)), dim3(256), 0, stream, t);
+    IRX_HIP(hipGetLastError());
+}
+
+void column_block(const ColumnBlock &c, hipStream_t stream) {
+    if (c.cols <= 0 || c.rows <= 0) return;
+    if (!c.state || !c.k || !c.v || !c.lnw || !c.lnb || !c.qpack || !c.qb || !c.pack || !c.bo || !c.n2w || !c.n2b ||
+        !c.b1 || !c.b2 || c.group <= 0)
+        fail(3, "column_block: missing tensor");
+    if ((reinterpret_cast<uintptr_t>(c.state) & 15) || (reinterpret_cast<uintptr_t>(c.k) & 15) ||
+        (reinterpret_cast<uintptr_t>(c.v) & 15) || (reinterpret_cast<uintptr_t>(c.qpack) & 15) ||
+        (reinterpret_cast<uintptr_t>(c.pack) & 15) || (c.group_stride & 3))
+        fail(3, "column_block: operands must be 16-byte aligned");
+    const long long tiles = (c.rows + kTailRows - 1) / kTailRows, units = tiles * c.cols;
+    const long long per_xcd = (units + 7) / 8;
+    if (per_xcd * 8 > 0x7fffffffLL) fail(3, "column_block: too many rows");
+    const double m = (double)c.cols * (double)c.rows;
+    // q, attention (scores and values over 128 keys x 8 heads of 16), the tail.
+    const double flops = m * 2.0 * (128.0 * 128 + 2.0 * 128 * 128 + 128.0 * 128 + 2 * 128.0 * 256);
+    KernelTimer timer(kFamGemm, stream, flops, m * 128 * 4 * 2.0 + (double)c.cols * kColumnCache * 8.0);
+    hipLaunchKernelGGL(column_block_kernel, dim3((unsigned)(per_xcd * 8)), dim3(256), 0, stream, c, (int)tiles,
+                       (int)per_xcd);
     IRX_HIP(hipGetLastError());
 }
 

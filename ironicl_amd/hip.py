@@ -118,6 +118,8 @@ SIGNATURES = {
     "irx_test_block_head": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _sz, _CF, _CF, _CF, _CF, _sz, _F]),
     "irx_test_block_tail": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _CF, _sz, _CF, _CF, _CF, _CF, _CF, _CF,
                                            _CF, _CF, _sz, _F]),
+    "irx_test_column_block": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _sz, _sz, _CF, _CF, _CF, _CF, _CF,
+                                             _CF, _CF, _CF, _CF, _CF, _CF, _CF, _CF, _CF, _sz, _F]),
     "irx_test_ln_linear": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _CF, _sz, _sz, _CF, _CF, _CF, _CF, _sz, _CF,
                                           _CF, _CF, _CF, _CF, _F]),
     "irx_test_layer_norm": (ctypes.c_int, [ctypes.c_void_p, _CF, _CF, _CF, _sz, _sz, _F]),

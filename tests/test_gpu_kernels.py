@@ -376,6 +376,81 @@ def test_block_tail_small_pass_form_equals_tail128(device, rows):
     np.testing.assert_array_equal(outs[0], outs[1])
 
 
+def column_weights(seed):
+    """LN1, the query rows of in_proj and the tail's weights of a cached column block."""
+    shapes = {"lnw": (128,), "lnb": (128,), "wq": (128, 128), "bq": (128,), "wo": (128, 128), "bo": (128,),
+              "n2w": (128,), "n2b": (128,), "w1": (256, 128), "b1": (256,), "w2": (128, 256), "b2": (128,)}
+    scales = {"lnw": 0.2, "lnb": 0.1, "wq": 0.09, "bq": 0.1, "wo": 0.09, "bo": 0.1, "n2w": 0.2, "n2b": 0.1,
+              "w1": 0.09, "b1": 0.1, "w2": 0.06, "b2": 0.1}
+    out = {}
+    for i, (name, shape) in enumerate(shapes.items()):
+        out[name] = fast_values(int(np.prod(shape)), seed + i, scales[name]).reshape(shape)
+    out["lnw"] = out["lnw"] + np.float32(1.0)
+    out["n2w"] = out["n2w"] + np.float32(1.0)
+    return out
+
+
+def column_block64(state, k, v, wt):
+    """cached_block (cpu.rs:2587-2850) in float64 for [cols, rows, 128] states
+    against [cols, 8, 128, 16] cached inducing keys and values."""
+    cols, rows = state.shape[:2]
+    x = state.astype(np.float64).reshape(-1, 128)
+    q = (ln64(x, wt["lnw"], wt["lnb"]) @ wt["wq"].T.astype(np.float64) + wt["bq"]).reshape(cols, rows, 128)
+    att = np.zeros((cols, rows, 128))
+    for h in range(8):
+        s = np.matmul(q[..., 16 * h:16 * h + 16], np.swapaxes(k[:, h].astype(np.float64), 1, 2)) * 0.25
+        s = np.exp(s - s.max(-1, keepdims=True))
+        att[..., 16 * h:16 * h + 16] = np.matmul(s / s.sum(-1, keepdims=True), v[:, h].astype(np.float64))
+    return block_tail64(att.reshape(-1, 128), x, wt["wo"], wt["bo"], wt["n2w"], wt["n2b"], wt["w1"], wt["b1"],
+                        wt["w2"], wt["b2"]).reshape(cols, rows, 128)
+
+
+def run_column_block(device, fused, state, k, v, wt):
+    cols, rows = state.shape[:2]
+    out = np.zeros_like(state)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_column_block(device.handle, fused, F(state), cols, rows, F(k), F(v), F(wt["lnw"]),
+                                              F(wt["lnb"]), F(wt["wq"]), F(wt["bq"]), F(wt["wo"]), F(wt["bo"]),
+                                              F(wt["n2w"]), F(wt["n2b"]), F(wt["w1"]), F(wt["b1"]), F(wt["w2"]),
+                                              F(wt["b2"]), 1, F(out)))
+    return out
+
+
+def column_inputs(cols, rows, seed):
+    state = fast_values(cols * rows * 128, seed, 3.0).reshape(cols, rows, 128)
+    k = fast_values(cols * 8 * 128 * 16, seed + 1, 1.5).reshape(cols, 8, 128, 16)
+    v = fast_values(cols * 8 * 128 * 16, seed + 2, 1.0).reshape(cols, 8, 128, 16)
+    return state, k, v
+
+
+@pytest.mark.parametrize("cols,rows", [(1, 1), (3, 17), (2, 100), (64, 512), (5, 3333)])
+@pytest.mark.parametrize("fused", [0, 1])
+def test_column_block_matches_float64(device, cols, rows, fused):
+    """A cached column block (LN1, query projection, 8-head attention to the
+    column's 128 cached inducing K/V, tail), as one kernel and as three
+    launches, against float64; rows not a multiple of the kernel's 64."""
+    state, k, v = column_inputs(cols, rows, 31)
+    wt = column_weights(40)
+    out = run_column_block(device, fused, state, k, v, wt)
+    want = column_block64(state, k, v, wt)
+    np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-5)
+    assert np.abs(out - want).max() < 3e-5
+
+
+@pytest.mark.parametrize("cols,rows", [(64, 512), (37, 1000), (3, 6000)])
+def test_column_block_one_kernel_equals_three_launches(device, cols, rows):
+    """From 16,384 states the three launches are head128, the 16-wide
+    attention and tail128, whose arithmetic the one kernel repeats: the same
+    bits (peaked scores included: keys scaled up so one dominates)."""
+    state, k, v = column_inputs(cols, rows, 51)
+    wt = column_weights(60)
+    for kscale in (1.0, 12.0):
+        kk = (k * np.float32(kscale)).astype(np.float32)
+        one = run_column_block(device, 1, state, kk, v, wt)
+        three = run_column_block(device, 0, state, kk, v, wt)
+        np.testing.assert_array_equal(one, three)
+
+
 def ln64(x, w, b):
     x = x.astype(np.float64)
     return (x - x.mean(1, keepdims=True)) / np.sqrt(x.var(1, keepdims=True) + 1e-5) * w + b
