@@ -444,8 +444,10 @@ void set_device(const irx_device *d) { IRX_HIP(hipSetDevice(d->ordinal)); }
 // tiled GEMMs, whose large tiles reuse the weights across rows.
 constexpr long long kLnLinearRows = 8192;
 // States (columns x rows) from which a cached column block runs as one
-// kernel (column_block) rather than three launches.
-constexpr long long kColumnFusedRows = 16384;
+// kernel (column_block) rather than three launches. Measured per block at
+// 64 columns: 128 rows 56 against 80 us, 64 rows 54 against 43 us (the one
+// kernel streams 512 KB of weights and K/V through LDS per 64-row tile).
+constexpr long long kColumnFusedRows = 8192;
 
 struct Stages {
     const irx_weights &w;

@@ -226,10 +226,13 @@ __global__ __launch_bounds__(256, 3) void tail128_kernel(Tail128 p) {
 // (8 KB: per 16-key block, four planes of 64 lanes, lane (d, g) of plane r
 // holding key 16 kb + 4 g + r's dim d, gathered by 4-byte loads from the
 // cache's [key][16] rows), 12..31 tail128's pack. Workgroups of one XCD take
-// consecutive units, so a column's tiles share its K/V in one L2.
+// consecutive units, so a column's tiles share its K/V in one L2. Three
+// workgroups share a CU (168 registers, as tail128; the compiler keeps a few
+// values of the prologue in scratch until the epilogue): at two, the
+// build's 3.2M-row blocks ran 6% slower than the three launches.
 constexpr int kColumnHalves = 32;
 
-__global__ __launch_bounds__(256, 2) void column_block_kernel(ColumnBlock p, int tiles, int per_xcd) {
+__global__ __launch_bounds__(256, 3) void column_block_kernel(ColumnBlock p, int tiles, int per_xcd) {
     __shared__ __attribute__((aligned(16))) float buf[2][kHalfFloats];
     const int unit = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
     if (unit >= p.cols * tiles) return;  // workgroup-uniform, before any barrier
