@@ -396,8 +396,9 @@ int irx_test_block_tail(irx_device *device, int fused, const float *att, const f
  * updated into out: LN1 (lnw / lnb), q = LN1(state) wq^T + bq (wq [128, 128]),
  * attention of 8 heads of 16 (scale 1/4) to the column's cached inducing keys
  * and values k, v [cols, 8, 128, 16], then the tail of irx_test_block_tail
- * (same weights). fused = 1 runs the one-kernel block, 0 the head, 16-wide
- * attention and tail launches. repeats as irx_test_block_tail. */
+ * (same weights). fused = 1 runs the one-kernel block, 2 its small-pass form
+ * (16 rows per workgroup), 0 the head, 16-wide attention and tail launches.
+ * repeats as irx_test_block_tail. */
 int irx_test_column_block(irx_device *device, int fused, const float *state, size_t cols, size_t rows,
                           const float *k, const float *v, const float *lnw, const float *lnb, const float *wq,
                           const float *bq, const float *wo, const float *bo, const float *n2w, const float *n2b,

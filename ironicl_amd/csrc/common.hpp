@@ -211,7 +211,8 @@ struct ColumnBlock {
     const float *pack;       // tail128_pack of the block
     const float *bo, *n2w, *n2b, *b1, *b2;
 };
-void column_block(const ColumnBlock &c, hipStream_t stream);
+// rows16: the small-pass form (16 rows of a column per workgroup, the same bits).
+void column_block(const ColumnBlock &c, hipStream_t stream, bool rows16 = false);
 
 // Regression outputs of decoded quantiles [b, q, k] (k <= 4096) on the device
 // (quantiles::summarize, quantiles.rs:80-213): per query row, averaged over

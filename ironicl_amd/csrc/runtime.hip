@@ -444,10 +444,13 @@ void set_device(const irx_device *d) { IRX_HIP(hipSetDevice(d->ordinal)); }
 // tiled GEMMs, whose large tiles reuse the weights across rows.
 constexpr long long kLnLinearRows = 8192;
 // States (columns x rows) from which a cached column block runs as one
-// kernel (column_block) rather than three launches. Measured per block at
-// 64 columns: 128 rows 56 against 80 us, 64 rows 54 against 43 us (the one
-// kernel streams 512 KB of weights and K/V through LDS per 64-row tile).
-constexpr long long kColumnFusedRows = 8192;
+// kernel of 64-row tiles (column_block) rather than its small-pass form of
+// 16 rows per workgroup. Measured per block at 64 columns (the three
+// launches the one kernel replaced in brackets): 32 rows 53.6 / 20.8 (32.7)
+// us, 128 rows 55.7 / 37.8 (77.9) us, 256 rows 60.0 / 68.5 (77.2) us, 512
+// rows 101 / 122 (115) us; the tiled kernel streams 512 KB of weights and
+// K/V through LDS per tile.
+constexpr long long kColumnFusedRows = 12288;
 
 struct Stages {
     const irx_weights &w;
@@ -550,20 +553,22 @@ struct Stages {
     // (cached_block, cpu.rs:2587-2850; column_block_f32, kernels.rs:1342).
     // fused: -1 chooses, 0 the three launches (head, 16-wide attention,
     // tail), 1 column_block's one kernel (the head128 / tail128 arithmetic:
-    // bitwise the three launches from 16384 rows).
+    // bitwise the three launches from 16384 rows), 2 its small-pass form
+    // (the same bits).
     void column_attend(int blk, float *state, int cols, int rows, const float *kcache, const float *vcache,
                        int group, long long group_stride, float *norm, float *q, float *att, float *hid,
                        int fused = -1) const {
         const BlockW &bw = w.col2[blk];
         const long long m = (long long)cols * rows;
         const bool packed = bw.head_pack && bw.head_nb == 8 && bw.head_row0 == 0 && bw.tail_pack;
-        if (fused == 1 || (fused < 0 && packed && m >= kColumnFusedRows)) {
+        if (fused < 0) fused = !packed ? 0 : m >= kColumnFusedRows ? 1 : 2;
+        if (fused >= 1) {
             if (!packed) fail(IRX_INVALID_ARGUMENT, "the fused column block needs packed weights");
             ColumnBlock c{};
             c.state = state, c.rows = rows, c.cols = cols, c.k = kcache, c.v = vcache, c.group = group;
             c.group_stride = group_stride, c.lnw = bw.n1w, c.lnb = bw.n1b, c.qpack = bw.head_pack, c.qb = bw.in_b;
             c.pack = bw.tail_pack, c.bo = bw.out.b, c.n2w = bw.n2w, c.n2b = bw.n2b, c.b1 = bw.l1.b, c.b2 = bw.l2.b;
-            column_block(c, s);
+            column_block(c, s, fused == 2);
             return;
         }
         head(bw, state, m, norm, q, kColumnDim);
@@ -2233,7 +2238,7 @@ int irx_test_column_block(irx_device *device, int fused, const float *state, siz
                           float *out) {
     return guarded("irx_test_column_block", [&] {
         if (!device || !state || !k || !v || !lnw || !lnb || !wq || !bq || !wo || !bo || !n2w || !n2b || !w1 ||
-            !b1 || !w2 || !b2 || !out || !cols || !rows || (fused != 0 && fused != 1) || !repeats ||
+            !b1 || !w2 || !b2 || !out || !cols || !rows || fused < 0 || fused > 2 || !repeats ||
             cols > (1u << 20) || rows > (1u << 24))
             fail(IRX_INVALID_ARGUMENT, "column block arguments do not match");
         set_device(device);

@@ -387,46 +387,23 @@ __global__ __launch_bounds__(256, 3) void column_block_kernel(ColumnBlock p, int
 // (320 KB, shared by every workgroup through L2), each wave's W1 fragments
 // issued with its first loads. Every accumulator takes its products in
 // tail128's order, so the results are tail128's bit for bit.
-__global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
-    constexpr int kS1Stride = 132, kHidStride = 260;
-    __shared__ __attribute__((aligned(16))) float s1s[16 * kS1Stride];
-    __shared__ __attribute__((aligned(16))) float hs[16 * kHidStride];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int m16 = lane & 15, g = lane >> 4;
-    const long long row = (long long)blockIdx.x * 16 + m16;
-    const bool live = row < p.m;
-    const long long r = live ? row : p.m - 1;
-    const float *pk = p.pack + lane * 4;
-    // Fragment (k-block kb, output block ob) of Wo; (kb, hb) of slice c's W1
-    // rows; (hidden block 2 c + j, ob) of W2 (tail128_pack's order).
-    auto wo_frag = [&](int kb, int ob) { return *reinterpret_cast<const f32x4 *>(pk + kb * 2048 + ob * 256); };
-    auto w1_frag = [&](int c, int kb, int hb) {
-        return *reinterpret_cast<const f32x4 *>(pk + (2 + c) * kChunkFloats + (kb * 2 + hb) * 256);
-    };
+// tail128_rows16's chain from the out-projection on, for wave w of a
+// workgroup of 16 rows: x holds the lane's row's attention output (all eight
+// blocks), s1 its state's blocks 2 w and 2 w + 1, fo and f1 the wave's Wo and
+// W1 fragments; s1s and hs are the workgroup's LDS exchange buffers, pk the
+// lane's base in the tail128 pack. The new state's blocks 2 w, 2 w + 1 go to
+// out (the lane's first feature, 4 g) when the row is live.
+constexpr int kRows16S1Stride = 132, kRows16HidStride = 260;
+
+__device__ __forceinline__ void rows16_chain(const Tail128 &t, const f32x4 (&x)[8], f32x4 (&s1)[2],
+                                             const f32x4 (&fo)[8][2], const f32x4 (&f1)[2][8][2], float *s1s,
+                                             float *hs, const float *pk, int w, int m16, int g, float *out,
+                                             bool live) {
+    constexpr int kS1Stride = kRows16S1Stride, kHidStride = kRows16HidStride;
     auto w2_frag = [&](int c, int j, int ob) {
         return *reinterpret_cast<const f32x4 *>(pk + (2 + c) * kChunkFloats + 4096 + (j * 8 + ob) * 256);
     };
-
-    f32x4 fo[8][2], x[8], s1[2];
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) fo[kb][j] = wo_frag(kb, 2 * w + j);
-    const float *att = p.att + r * p.lda + 4 * g;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(att + 16 * b);
-    const float *st = p.state + r * p.ldx + 4 * g;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) s1[j] = *reinterpret_cast<const f32x4 *>(st + 16 * (2 * w + j));
-    f32x4 f1[2][8][2];
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
-#pragma unroll
-        for (int kb = 0; kb < 8; ++kb)
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb) f1[sl][kb][hb] = w1_frag(2 * w + sl, kb, hb);
-
+    f32x4 xn[8];
     // Out-projection of output blocks 2 w + j; s1 = state + (acc + bo) to LDS.
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -438,7 +415,7 @@ __global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int c0 = 16 * (2 * w + j) + 4 * g;
-        const f32x4 bo = *reinterpret_cast<const f32x4 *>(p.bo + c0);
+        const f32x4 bo = *reinterpret_cast<const f32x4 *>(t.bo + c0);
 #pragma unroll
         for (int e = 0; e < 4; ++e) s1[j][e] = s1[j][e] + (acc[j][e] + bo[e]);
         *reinterpret_cast<f32x4 *>(&s1s[m16 * kS1Stride + c0]) = s1[j];
@@ -448,12 +425,12 @@ __global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
     // LN2 of the 16 rows (as tail128: row m's features over lanes m, m + 16,
     // m + 32, m + 48).
 #pragma unroll
-    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(&s1s[m16 * kS1Stride + 16 * b + 4 * g]);
+    for (int b = 0; b < 8; ++b) xn[b] = *reinterpret_cast<const f32x4 *>(&s1s[m16 * kS1Stride + 16 * b + 4 * g]);
     float sum = 0.f;
 #pragma unroll
     for (int b = 0; b < 8; ++b)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum += x[b][e];
+        for (int e = 0; e < 4; ++e) sum += xn[b][e];
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     const float mean = sum / 128.f;
@@ -462,7 +439,7 @@ __global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
     for (int b = 0; b < 8; ++b)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float d = x[b][e] - mean;
+            const float d = xn[b][e] - mean;
             sq = fmaf(d, d, sq);
         }
     sq += __shfl_xor(sq, 16, 64);
@@ -470,10 +447,10 @@ __global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
     const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-        const f32x4 nw = *reinterpret_cast<const f32x4 *>(p.n2w + 16 * b + 4 * g);
-        const f32x4 nb = *reinterpret_cast<const f32x4 *>(p.n2b + 16 * b + 4 * g);
+        const f32x4 nw = *reinterpret_cast<const f32x4 *>(t.n2w + 16 * b + 4 * g);
+        const f32x4 nb = *reinterpret_cast<const f32x4 *>(t.n2b + 16 * b + 4 * g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[b][e] = (x[b][e] - mean) * rstd * nw[e] + nb[e];
+        for (int e = 0; e < 4; ++e) xn[b][e] = (xn[b][e] - mean) * rstd * nw[e] + nb[e];
     }
 
     // Hidden slices c = 2 w + sl: gelu(W1 x + b1) to LDS.
@@ -488,10 +465,10 @@ __global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int hb = 0; hb < 2; ++hb) h[hb][kb & 1] = mfma(f1[sl][kb][hb][e], x[kb][e], h[hb][kb & 1]);
+                for (int hb = 0; hb < 2; ++hb) h[hb][kb & 1] = mfma(f1[sl][kb][hb][e], xn[kb][e], h[hb][kb & 1]);
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) {
-            const f32x4 b1 = *reinterpret_cast<const f32x4 *>(p.b1 + 32 * c + 16 * hb + 4 * g);
+            const f32x4 b1 = *reinterpret_cast<const f32x4 *>(t.b1 + 32 * c + 16 * hb + 4 * g);
             f32x4 hg;
 #pragma unroll
             for (int e = 0; e < 4; ++e) hg[e] = gelu_erf((h[hb][0][e] + h[hb][1][e]) + b1[e]);
@@ -521,16 +498,198 @@ __global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
                 for (int ob = 0; ob < 2; ++ob) acc2[ob] = mfma(f2[c][j][ob][e], hv[e], acc2[ob]);
         }
     if (!live) return;
-    float *out = p.state + row * p.ldx + 4 * g;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int c0 = 16 * (2 * w + j);
-        const f32x4 b2 = *reinterpret_cast<const f32x4 *>(p.b2 + c0 + 4 * g);
+        const f32x4 b2 = *reinterpret_cast<const f32x4 *>(t.b2 + c0 + 4 * g);
         f32x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = (acc2[j][e] + b2[e]) + s1[j][e];
         *reinterpret_cast<f32x4 *>(out + c0) = v;
     }
+}
+
+__global__ __launch_bounds__(256) void tail128_rows16_kernel(Tail128 p) {
+    constexpr int kS1Stride = kRows16S1Stride, kHidStride = kRows16HidStride;
+    __shared__ __attribute__((aligned(16))) float s1s[16 * kS1Stride];
+    __shared__ __attribute__((aligned(16))) float hs[16 * kHidStride];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
+    const long long row = (long long)blockIdx.x * 16 + m16;
+    const bool live = row < p.m;
+    const long long r = live ? row : p.m - 1;
+    const float *pk = p.pack + lane * 4;
+    // Fragment (k-block kb, output block ob) of Wo; (kb, hb) of slice c's W1
+    // rows (tail128_pack's order).
+    auto wo_frag = [&](int kb, int ob) { return *reinterpret_cast<const f32x4 *>(pk + kb * 2048 + ob * 256); };
+    auto w1_frag = [&](int c, int kb, int hb) {
+        return *reinterpret_cast<const f32x4 *>(pk + (2 + c) * kChunkFloats + (kb * 2 + hb) * 256);
+    };
+
+    f32x4 fo[8][2], x[8], s1[2];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fo[kb][j] = wo_frag(kb, 2 * w + j);
+    const float *att = p.att + r * p.lda + 4 * g;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(att + 16 * b);
+    const float *st = p.state + r * p.ldx + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) s1[j] = *reinterpret_cast<const f32x4 *>(st + 16 * (2 * w + j));
+    f32x4 f1[2][8][2];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) f1[sl][kb][hb] = w1_frag(2 * w + sl, kb, hb);
+
+    rows16_chain(p, x, s1, fo, f1, s1s, hs, pk, w, m16, g, p.state + r * p.ldx + 4 * g, live);
+}
+
+// The cached column block for small passes: one workgroup per 16 rows of
+// one column, wave w taking query heads and output blocks 2 w and 2 w + 1
+// (tail128_rows16's split). Every wave takes LN1 of the whole rows; its
+// query fragments, its heads' keys (fragment order) and values (lane (d, g)
+// value r of key block kb = key 16 kb + 4 g + r's dim d) come straight from
+// global memory, all issued with its first loads, and the tail's Wo and W1
+// fragments follow while the attention runs. The attention outputs meet in
+// LDS for the out-projection; from there on this is tail128_rows16. The
+// arithmetic is column_block_kernel's, so the results are its bits.
+__global__ __launch_bounds__(256) void column_block_rows16_kernel(ColumnBlock p, int groups) {
+    constexpr int kS1Stride = kRows16S1Stride, kHidStride = kRows16HidStride;
+    __shared__ __attribute__((aligned(16))) float as[16 * kS1Stride];
+    __shared__ __attribute__((aligned(16))) float s1s[16 * kS1Stride];
+    __shared__ __attribute__((aligned(16))) float hs[16 * kHidStride];
+    const int unit = blockIdx.x;
+    const int col = unit / groups, grp = unit - col * groups;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m16 = lane & 15, g = lane >> 4;
+    const long long row = (long long)grp * 16 + m16;
+    const bool live = row < p.rows;
+    const long long r = live ? row : p.rows - 1;
+    float *xrow = p.state + ((long long)col * p.rows + r) * 128 + 4 * g;
+    const long long coff = (long long)(col / p.group) * p.group_stride + (long long)(col % p.group) * kColumnCache;
+    const float *kh = p.k + coff + (2 * w) * (kInducing * kColumnHead);
+    const float *vh = p.v + coff + (2 * w) * (kInducing * kColumnHead);
+    const float *qk = p.qpack + lane * 4, *pk = p.pack + lane * 4;
+
+    f32x4 x[8], fq[8][2], kf[2][8];
+    float vv[2][8][4];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(xrow + 16 * b);
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fq[kb][j] = *reinterpret_cast<const f32x4 *>(qk + (kb * 8 + 2 * w + j) * 256);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            kf[j][kb] = *reinterpret_cast<const f32x4 *>(kh + j * 2048 + (16 * kb + m16) * 16 + 4 * g);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) vv[j][kb][rr] = vh[j * 2048 + (16 * kb + 4 * g + rr) * 16 + m16];
+        }
+
+    // LN1 over the rows, as head128.
+    {
+        float sum = 0.f;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) sum += (x[b][0] + x[b][1]) + (x[b][2] + x[b][3]);
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        const float mean = sum / 128.f;
+        float sq = 0.f;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = x[b][e] - mean;
+                sq = fmaf(d, d, sq);
+            }
+        sq += __shfl_xor(sq, 16, 64);
+        sq += __shfl_xor(sq, 32, 64);
+        const float rstd = 1.0f / sqrtf(sq / 128.f + 1e-5f);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const f32x4 lw = *reinterpret_cast<const f32x4 *>(p.lnw + 16 * b + 4 * g);
+            const f32x4 lb = *reinterpret_cast<const f32x4 *>(p.lnb + 16 * b + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[b][e] = (x[b][e] - mean) * rstd * lw[e] + lb[e];
+        }
+    }
+    f32x4 q[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) q[j] = mfma(fq[kb][j][e], x[kb][e], q[j]);
+    const float scale = 0.25f * kLog2e;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) q[j] = (q[j] + *reinterpret_cast<const f32x4 *>(p.qb + 16 * (2 * w + j) + 4 * g)) * scale;
+
+    // The tail's fragments for this wave and its state blocks, in flight
+    // during the attention.
+    f32x4 fo[8][2], f1[2][8][2], s1[2];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fo[kb][j] = *reinterpret_cast<const f32x4 *>(pk + kb * 2048 + (2 * w + j) * 256);
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+                f1[sl][kb][hb] =
+                    *reinterpret_cast<const f32x4 *>(pk + (2 + 2 * w + sl) * kChunkFloats + (kb * 2 + hb) * 256);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) s1[j] = *reinterpret_cast<const f32x4 *>(xrow + 16 * (2 * w + j));
+
+    // Heads 2 w + j, as column_block_kernel.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        f32x4 s[8];
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) acc = mfma(kf[j][kb][st], q[j][st], acc);
+            s[kb] = acc;
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) m = fmaxf(m, fmaxf(fmaxf(s[kb][0], s[kb][1]), fmaxf(s[kb][2], s[kb][3])));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        float l = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                s[kb][rr] = __builtin_amdgcn_exp2f(s[kb][rr] - m);
+                l += s[kb][rr];
+            }
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const float inv = 1.0f / l;
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) o = mfma(vv[j][kb][rr], s[kb][rr], o);
+        *reinterpret_cast<f32x4 *>(&as[m16 * kS1Stride + 16 * (2 * w + j) + 4 * g]) = o * inv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = *reinterpret_cast<const f32x4 *>(&as[m16 * kS1Stride + 16 * b + 4 * g]);
+    Tail128 t{};
+    t.bo = p.bo, t.n2w = p.n2w, t.n2b = p.n2b, t.b1 = p.b1, t.b2 = p.b2;
+    rows16_chain(t, x, s1, fo, f1, s1s, hs, pk, w, m16, g, xrow, live);
 }
 
 // The head of a 128-wide block: y = LN1(x) W^T + b over 16 NB outputs,
@@ -686,7 +845,7 @@ void tail128(const Tail128 &t, hipStream_t stream, bool rows16) {
     IRX_HIP(hipGetLastError());
 }
 
-void column_block(const ColumnBlock &c, hipStream_t stream) {
+void column_block(const ColumnBlock &c, hipStream_t stream, bool rows16) {
     if (c.cols <= 0 || c.rows <= 0) return;
     if (!c.state || !c.k || !c.v || !c.lnw || !c.lnb || !c.qpack || !c.qb || !c.pack || !c.bo || !c.n2w || !c.n2b ||
         !c.b1 || !c.b2 || c.group <= 0)
@@ -702,8 +861,15 @@ void column_block(const ColumnBlock &c, hipStream_t stream) {
     // q, attention (scores and values over 128 keys x 8 heads of 16), the tail.
     const double flops = m * 2.0 * (128.0 * 128 + 2.0 * 128 * 128 + 128.0 * 128 + 2 * 128.0 * 256);
     KernelTimer timer(kFamGemm, stream, flops, m * 128 * 4 * 2.0 + (double)c.cols * kColumnCache * 8.0);
-    hipLaunchKernelGGL(column_block_kernel, dim3((unsigned)(per_xcd * 8)), dim3(256), 0, stream, c, (int)tiles,
-                       (int)per_xcd);
+    if (rows16) {
+        const long long groups = (c.rows + 15) / 16;
+        if (groups * c.cols > 0x7fffffffLL) fail(3, "column_block: too many rows");
+        hipLaunchKernelGGL(column_block_rows16_kernel, dim3((unsigned)(groups * c.cols)), dim3(256), 0, stream, c,
+                           (int)groups);
+    } else {
+        hipLaunchKernelGGL(column_block_kernel, dim3((unsigned)(per_xcd * 8)), dim3(256), 0, stream, c, (int)tiles,
+                           (int)per_xcd);
+    }
     IRX_HIP(hipGetLastError());
 }
 

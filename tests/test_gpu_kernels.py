@@ -424,11 +424,12 @@ def column_inputs(cols, rows, seed):
 
 
 @pytest.mark.parametrize("cols,rows", [(1, 1), (3, 17), (2, 100), (64, 512), (5, 3333)])
-@pytest.mark.parametrize("fused", [0, 1])
+@pytest.mark.parametrize("fused", [0, 1, 2])
 def test_column_block_matches_float64(device, cols, rows, fused):
     """A cached column block (LN1, query projection, 8-head attention to the
-    column's 128 cached inducing K/V, tail), as one kernel and as three
-    launches, against float64; rows not a multiple of the kernel's 64."""
+    column's 128 cached inducing K/V, tail), as one kernel (64-row tiles or
+    the small-pass form) and as three launches, against float64; rows not a
+    multiple of the kernels' 64 or 16."""
     state, k, v = column_inputs(cols, rows, 31)
     wt = column_weights(40)
     out = run_column_block(device, fused, state, k, v, wt)
@@ -449,6 +450,18 @@ def test_column_block_one_kernel_equals_three_launches(device, cols, rows):
         one = run_column_block(device, 1, state, kk, v, wt)
         three = run_column_block(device, 0, state, kk, v, wt)
         np.testing.assert_array_equal(one, three)
+
+
+@pytest.mark.parametrize("cols,rows", [(64, 1), (3, 17), (64, 32), (7, 300)])
+def test_column_block_small_pass_form_equals_one_kernel(device, cols, rows):
+    """The 16-rows-per-workgroup form repeats the one kernel's arithmetic:
+    the same bits at every pass size (peaked scores included)."""
+    state, k, v = column_inputs(cols, rows, 71)
+    wt = column_weights(80)
+    for kscale in (1.0, 12.0):
+        kk = (k * np.float32(kscale)).astype(np.float32)
+        np.testing.assert_array_equal(run_column_block(device, 2, state, kk, v, wt),
+                                      run_column_block(device, 1, state, kk, v, wt))
 
 
 def ln64(x, w, b):
