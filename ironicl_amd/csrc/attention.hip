@@ -1594,12 +1594,18 @@ constexpr int kLongOStride = 20;  // LDS rows of 16 outputs, padded
 
 template <int QG, bool ROPE>
 __global__ __launch_bounds__(64 * kLongWaves) void small_attention_long_kernel(SmallAttention p, int qchunks,
-                                                                               int splits, int keys_per_split) {
+                                                                               int splits, int keys_per_split,
+                                                                               int per_xcd, int count) {
     __shared__ __attribute__((aligned(16))) float red_o[kLongWaves][QG * 16 * kLongOStride];
     __shared__ float red_m[kLongWaves][QG * 16], red_l[kLongWaves][QG * 16];
     const int wave = tid_x() >> 6, lane = tid_x() & 63, g = lane >> 4, l16 = lane & 15;
-    const int split = bid_x() % splits;
-    const int unit = bid_x() / splits;
+    // Workgroups of one XCD take consecutive (split, chunk, head, sequence)
+    // units: a token's heads share its cache lines (two 16-wide heads per
+    // 128-byte line), which they then fetch into one L2.
+    const int t = (int)(bid_x() & 7) * per_xcd + (int)(bid_x() >> 3);
+    if (t >= count) return;
+    const int split = t % splits;
+    const int unit = t / splits;
     const int qc = unit % qchunks, item = unit / qchunks;
     const int head = item % p.heads, seq = item / p.heads;
     const int gs = seq / p.group, sq = seq - gs * p.group;
@@ -1804,7 +1810,8 @@ constexpr int kShortKeys = 128;     // keys the matrix-core path takes
 constexpr int kShortKStride = 20;   // K rows padded to 20 floats
 
 template <int QB, int KB, bool ROPE, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallAttention p, int groups_per_seq) {
+__global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallAttention p, int groups_per_seq,
+                                                                          int per_xcd, int count) {
     // Rows are padded against bank conflicts, except for 80 keys (the
     // 68-token rows of 64 features): unpadded, one item's K and V^T take
     // exactly 10 KB, so sixteen single-wave workgroups fit a CU's LDS and a
@@ -1814,9 +1821,13 @@ __global__ __launch_bounds__(64 * WAVES) void small_attention_mfma_kernel(SmallA
     __shared__ __attribute__((aligned(16))) float Vt[16 * VSTRIDE];
     // Workgroup j of a (sequence, head) item: its WAVES waves take query chunks
     // (j * WAVES + wave) + k * groups_per_seq * WAVES and share the staged keys.
-    const int item = bid_x() / groups_per_seq;
+    // Workgroups of one XCD take consecutive (group, head, sequence) units,
+    // so a token's heads fetch its cache lines into one L2.
+    const int t = (int)(bid_x() & 7) * per_xcd + (int)(bid_x() >> 3);
+    if (t >= count) return;
+    const int item = t / groups_per_seq;
     const int wave = tid_x() >> 6;
-    const int c_first = (bid_x() - item * groups_per_seq) * WAVES + wave;
+    const int c_first = (t - item * groups_per_seq) * WAVES + wave;
     const int c_step = groups_per_seq * WAVES;
     const int head = item % p.heads, seq = item / p.heads;
     const int gq = seq / p.group, sq = seq - gq * p.group;
@@ -2438,17 +2449,17 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
         const int waves = (qb == 4 && chunks >= 4) ? 4 : 1;
         const long long groups = std::max<long long>(
             1, std::min<long long>(ceil_div(chunks, waves), ceil_div(8192, items * waves)));
-        const long long blocks = items * groups;
-        if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
+        const long long blocks = items * groups, per_xcd = ceil_div(blocks, 8);
+        if (per_xcd * 8 > 0x7fffffffLL) fail(3, "small attention grid is too large");
         const bool rope = args.rope_cos != nullptr;
 #define IRX_SMALL_CASE(QB, KB, W)                                                                                 \
     if (qb == QB && kb == KB && waves == W) {                                                                    \
         if (rope)                                                                                                \
-            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, KB, true, W>), dim3((unsigned)blocks), dim3(64 * W), \
-                               0, stream, args, (int)groups);                                                    \
+            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, KB, true, W>), dim3((unsigned)(per_xcd * 8)),    \
+                               dim3(64 * W), 0, stream, args, (int)groups, (int)per_xcd, (int)blocks);          \
         else                                                                                                     \
-            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, KB, false, W>), dim3((unsigned)blocks),           \
-                               dim3(64 * W), 0, stream, args, (int)groups);                                      \
+            hipLaunchKernelGGL((small_attention_mfma_kernel<QB, KB, false, W>), dim3((unsigned)(per_xcd * 8)),   \
+                               dim3(64 * W), 0, stream, args, (int)groups, (int)per_xcd, (int)blocks);          \
     }
         IRX_SMALL_CASE(1, 5, 1)
         IRX_SMALL_CASE(1, 8, 1)
@@ -2464,18 +2475,20 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
         const bool split = plan.splits > 1 && args.partial && args.partial_floats >= plan.partial_floats;
         const int splits = split ? plan.splits : 1;
         const int per = split ? plan.keys_per_split : args.kv_rows;
-        const long long blocks = plan.units * splits;
-        if (blocks > 0x7fffffffLL) fail(3, "small attention grid is too large");
+        const long long blocks = plan.units * splits, per_xcd = ceil_div(blocks, 8);
+        if (per_xcd * 8 > 0x7fffffffLL) fail(3, "small attention grid is too large");
         const bool rope = args.rope_cos != nullptr;
         const int qg = args.q_rows >= kLongQueries ? 8 : (args.q_rows > 32 ? 4 : (args.q_rows > 16 ? 2 : 1));
 #define IRX_LONG_CASE(QG)                                                                                      \
     if (qg == QG) {                                                                                            \
         if (rope)                                                                                              \
-            hipLaunchKernelGGL((small_attention_long_kernel<QG, true>), dim3((unsigned)blocks),                \
-                               dim3(64 * kLongWaves), 0, stream, args, plan.qchunks, splits, per);             \
+            hipLaunchKernelGGL((small_attention_long_kernel<QG, true>), dim3((unsigned)(per_xcd * 8)),         \
+                               dim3(64 * kLongWaves), 0, stream, args, plan.qchunks, splits, per,              \
+                               (int)per_xcd, (int)blocks);                                                     \
         else                                                                                                   \
-            hipLaunchKernelGGL((small_attention_long_kernel<QG, false>), dim3((unsigned)blocks),               \
-                               dim3(64 * kLongWaves), 0, stream, args, plan.qchunks, splits, per);             \
+            hipLaunchKernelGGL((small_attention_long_kernel<QG, false>), dim3((unsigned)(per_xcd * 8)),        \
+                               dim3(64 * kLongWaves), 0, stream, args, plan.qchunks, splits, per,              \
+                               (int)per_xcd, (int)blocks);                                                     \
     }
         IRX_LONG_CASE(1)
         IRX_LONG_CASE(2)
