@@ -669,6 +669,28 @@ def test_small_attention_tokens_match_float64(device, seqs, query_rows, rows, ro
     assert worst < 1e-5, worst
 
 
+@pytest.mark.parametrize("qscale", [3.0, 40.0])
+def test_rope_attention_past_512_tokens_matches_float64(device, qscale):
+    """Rows of 604 tokens (600 features) are longer than the staged kernel
+    takes: the row transformer's self-attention with RoPE then runs on the
+    long-range kernel (method 0, as a build chooses)."""
+    seqs, heads, tokens = 2, 8, 604
+    q = fast_values(seqs * tokens * heads * 16, 34, qscale).reshape(seqs, tokens, heads, 16)
+    k = fast_values(seqs * tokens * heads * 16, 35).reshape(seqs, tokens, heads, 16)
+    v = fast_values(seqs * tokens * heads * 16, 36).reshape(seqs, tokens, heads, 16)
+    cos_t, sin_t = rope_tables(tokens)
+    out = np.zeros_like(q)
+    F = hip.fptr
+    hip.check(hip.lib().irx_test_small_attention_tokens(device.handle, 0, F(q), F(k), F(v), F(cos_t), F(sin_t),
+                                                        seqs, heads, tokens, tokens, F(out), 0, None))
+    worst = 0.0
+    for s_ in range(seqs):
+        for h in (0, 5, 7):
+            qq, kk = rope64(q[s_, :, h], cos_t, sin_t), rope64(k[s_, :, h], cos_t, sin_t)
+            worst = max(worst, np.abs(out[s_, :, h] - attention64(qq, kk, v[s_, :, h], 0.25)).max())
+    assert worst < 1e-5, worst
+
+
 def test_staged_attention_rejects_what_it_cannot_take(device):
     z = np.zeros(16 * 8 * 600, np.float32)
     out = np.zeros_like(z)

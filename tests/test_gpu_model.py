@@ -335,6 +335,19 @@ def test_contexts_of_one_to_three_features(clf, clf_oracle, features):
     assert np.array_equal(gpu[..., :3].argmax(-1), cpu[..., :3].argmax(-1))
 
 
+def test_rows_longer_than_the_staged_attention_takes(clf, clf_oracle):
+    """600 features: the row transformer's sequences are 604 tokens, past the
+    512 keys of the staged row attention, so its self-attention takes the
+    long-range kernel with RoPE (four waves per 128-query chunk, key ranges
+    merged), and the CLS block's four queries read 604 tokens."""
+    x, y, xt, shifts = reference_lcg_data(1, 96, 5, 600)
+    ctx = clf.build_context(x, y, class_permutations=shifts)
+    gpu = ctx.predict_raw(xt).logits
+    cpu = clf_oracle.predict_uncached(x, y, xt)
+    assert_parity(gpu, cpu, "600 features")
+    assert np.array_equal(gpu[..., :3].argmax(-1), cpu[..., :3].argmax(-1))
+
+
 @pytest.mark.parametrize("classes", [2, 10])
 def test_two_and_ten_classes(clf, clf_oracle, classes):
     """The fewest and the most classes the classifier takes (label
