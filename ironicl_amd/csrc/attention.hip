@@ -2032,30 +2032,38 @@ __global__ __launch_bounds__(1024, NG == 1 ? 8 : NG == 2 ? 6 : 4) void staged_at
     const int first_block = chunk * waves * NG + wave;
 
     // Stage K (rotated) as [key][20] and V^T as [dim][KMAX + 4]; keys past kv
-    // are zero. Thread t takes dims 4 c .. +3 (c = t / 16 % 4) of key
+    // (in the last block only) repeat key kv - 1, whose scores the last block
+    // masks. Thread t takes dims 4 c .. +3 (c = t / 16 % 4) of key
     // 16 (t / 64) + t % 16: each 16-lane phase of a store covers 16
     // consecutive keys of one chunk, which no two lanes' banks share in
     // either layout. RoPE pairs dim d with d ^ 8, chunk c with c ^ 2.
-    // Offsets within an item are 32-bit (the launcher checks), added to the
-    // workgroup-uniform bases.
-    const unsigned k_row = (unsigned)p.k_row, v_row = (unsigned)p.v_row;
-    const unsigned q_row = (unsigned)p.q_row, o_row = (unsigned)p.o_row;
-    for (int t = tid_x(); t < kblocks * 64; t += bdim_x()) {
+    // Offsets within an item are 32-bit byte offsets (the launcher checks)
+    // from the workgroup-uniform bases, so every load takes a scalar base.
+    const unsigned k_row = 4u * (unsigned)p.k_row, v_row = 4u * (unsigned)p.v_row;
+    const unsigned q_row = 4u * (unsigned)p.q_row, o_row = 4u * (unsigned)p.o_row;
+    auto ld4 = [](const float *base, unsigned bytes) {
+        return *reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(base) + bytes);
+    };
+    auto stage = [&](int t) {
         const unsigned key = ((t >> 6) << 4) | (t & 15), c = (t >> 4) & 3;
-        f32x4 kc = {0.f, 0.f, 0.f, 0.f}, vc = kc;
-        if (key < (unsigned)kv) {
-            kc = *reinterpret_cast<const f32x4 *>(kb + (key * k_row + 4 * c));
-            vc = *reinterpret_cast<const f32x4 *>(vb + (key * v_row + 4 * c));
-            if constexpr (ROPE) {
-                const f32x4 kp = *reinterpret_cast<const f32x4 *>(kb + (key * k_row + 4 * (c ^ 2)));
-                const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_cos + (key * 16 + 4 * c));
-                const f32x4 sn = *reinterpret_cast<const f32x4 *>(p.rope_sin + (key * 16 + 4 * c));
-                kc = kc * cs + kp * sn;
-            }
+        const unsigned src = min(key, (unsigned)kv - 1);
+        f32x4 kc = ld4(kb, src * k_row + 16 * c);
+        const f32x4 vc = ld4(vb, src * v_row + 16 * c);
+        if constexpr (ROPE) {
+            const f32x4 kp = ld4(kb, src * k_row + 16 * (c ^ 2));
+            const f32x4 cs = ld4(p.rope_cos, src * 64 + 16 * c);
+            const f32x4 sn = ld4(p.rope_sin, src * 64 + 16 * c);
+            kc = kc * cs + kp * sn;
         }
         *reinterpret_cast<f32x4 *>(&Ks[key * kStagedKStride + 4 * c]) = kc;
 #pragma unroll
         for (int e = 0; e < 4; ++e) Vt[(4 * c + e) * VSTRIDE + key] = vc[e];
+    };
+    if (kblocks * 64 <= (int)bdim_x()) {
+        // One pass covers every key (self-attention: a wave per 16-key block).
+        if (tid_x() < kblocks * 64) stage(tid_x());
+    } else {
+        for (int t = tid_x(); t < kblocks * 64; t += bdim_x()) stage(t);
     }
 
     // This wave's queries, rotated and scaled into the exp2 domain: lane
@@ -2065,16 +2073,14 @@ __global__ __launch_bounds__(1024, NG == 1 ? 8 : NG == 2 ? 6 : 4) void staged_at
         const float scale = p.scale * kLog2e;
 #pragma unroll
         for (int n = 0; n < NG; ++n) {
-            const unsigned row = 16 * (first_block + n * waves) + l16;
-            f32x4 q = {0.f, 0.f, 0.f, 0.f};
-            if (row < (unsigned)p.q_rows) {
-                q = *reinterpret_cast<const f32x4 *>(qb + (row * q_row + 4 * g));
-                if constexpr (ROPE) {
-                    const f32x4 qp = *reinterpret_cast<const f32x4 *>(qb + (row * q_row + 4 * (g ^ 2)));
-                    const f32x4 cs = *reinterpret_cast<const f32x4 *>(p.rope_cos + (row * 16 + 4 * g));
-                    const f32x4 sn = *reinterpret_cast<const f32x4 *>(p.rope_sin + (row * 16 + 4 * g));
-                    q = q * cs + qp * sn;
-                }
+            // Rows past q_rows repeat the last query (their outputs are not stored).
+            const unsigned row = min(16u * (first_block + n * waves) + l16, (unsigned)p.q_rows - 1);
+            f32x4 q = ld4(qb, row * q_row + 16 * g);
+            if constexpr (ROPE) {
+                const f32x4 qp = ld4(qb, row * q_row + 16 * (g ^ 2));
+                const f32x4 cs = ld4(p.rope_cos, row * 64 + 16 * g);
+                const f32x4 sn = ld4(p.rope_sin, row * 64 + 16 * g);
+                q = q * cs + qp * sn;
             }
             qf[n] = q * scale;
         }
@@ -2185,7 +2191,8 @@ __global__ __launch_bounds__(1024, NG == 1 ? 8 : NG == 2 ? 6 : 4) void staged_at
         const float l = quad_sum(l_run[n]);
         const unsigned row = 16 * (first_block + n * waves) + l16;
         if (row < (unsigned)p.q_rows)
-            *reinterpret_cast<f32x4 *>(ob + (row * o_row + 4 * g)) = o[n] * __builtin_amdgcn_rcpf(l);
+            *reinterpret_cast<f32x4 *>(reinterpret_cast<char *>(ob) + (row * o_row + 16 * g)) =
+                o[n] * __builtin_amdgcn_rcpf(l);
     }
 }
 
@@ -2390,7 +2397,7 @@ void launch_staged(const SmallAttention &a, hipStream_t stream) {
     if (per_xcd * 8 > 0x7fffffffLL) fail(3, "small attention grid is too large");
     const long long span = std::max<long long>({(long long)a.q_rows * a.q_row, (long long)a.kv_rows * a.k_row,
                                                 (long long)a.kv_rows * a.v_row, (long long)a.q_rows * a.o_row});
-    if (span + 64 > 0x7fffffffLL) fail(3, "small attention rows are too far apart for the staged kernel");
+    if (4 * (span + 64) > 0xffffffffLL) fail(3, "small attention rows are too far apart for the staged kernel");
     const dim3 blocks((unsigned)(per_xcd * 8)), threads(64 * plan.waves);
     const bool rope = a.rope_cos != nullptr;
 #define IRX_STAGED_CASE(NG, KMAX)                                                                               \
