@@ -944,15 +944,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64, 2) void icl_decode_kernel(IclAtt
     const float *vbase = p.v + pair * p.kv_pair_stride;
     // Block at k0: K dims 16 c + 4 grp .. +3 (c = 0..3) of key k0 + i16, and
     // V dims 4 i16 .. +3 of keys k0 + 4 grp + r. Keys past the range repeat
-    // its last key (masked below).
+    // its last key (masked below). Addresses are 32-bit byte offsets from the
+    // pair's uniform bases (the launcher checks that 256 bytes per key fit).
+    const char *kb8 = reinterpret_cast<const char *>(kbase), *vb8 = reinterpret_cast<const char *>(vbase);
     auto load = [&](int k0, f32x4 *kd, f32x4 *vd) {
-        const int key = min(k0 + i16, k_end - 1);
+        const unsigned key = (unsigned)min(k0 + i16, k_end - 1);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) kd[c] = *reinterpret_cast<const f32x4 *>(kbase + (long long)key * 64 + 16 * c + 4 * grp);
+        for (int c = 0; c < 4; ++c) kd[c] = *reinterpret_cast<const f32x4 *>(kb8 + (key * 256u + 64u * c + 16u * grp));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int vk = min(k0 + 4 * grp + r, k_end - 1);
-            vd[r] = *reinterpret_cast<const f32x4 *>(vbase + (long long)vk * 64 + 4 * i16);
+            const unsigned vk = (unsigned)min(k0 + 4 * grp + r, k_end - 1);
+            vd[r] = *reinterpret_cast<const f32x4 *>(vb8 + (vk * 256u + 16u * i16));
         }
     };
 
@@ -2277,6 +2279,7 @@ void icl_attention(const IclAttention &args, hipStream_t stream) {
             else
                 wide16.template operator()<false>();
         } else if (args.q_rows <= kDecodeQueries) {
+            if ((long long)args.kv_rows * 256 > 0xffffffffLL) fail(3, "ICL attention: too many keys for the decode kernel");
             const dim3 blocks((unsigned)((long long)args.pairs * g.splits)), threads(kDecodeWaves * 64);
             if (args.q_rows <= 16) {
                 if (g.splits > 1)
