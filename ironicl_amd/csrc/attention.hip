@@ -1643,18 +1643,23 @@ __global__ __launch_bounds__(64 * kLongWaves) void small_attention_long_kernel(S
 
     // Block at kk: K dims 4 g .. +3 of key kk + lane % 16, and V dim lane % 16
     // of keys kk + 4 g + i. Keys past the range repeat its last key (masked).
+    // Addresses are 32-bit byte offsets from the item's uniform bases (the
+    // launcher checks that the keys' rows fit).
+    const unsigned k_row = 4u * (unsigned)p.k_row, v_row = 4u * (unsigned)p.v_row;
+    const char *kb8 = reinterpret_cast<const char *>(kb), *vb8 = reinterpret_cast<const char *>(vb);
     auto load = [&](int kk, f32x4 &kd, f32x4 &vd) {
-        const int key = min(kk + l16, k_end - 1);
-        const float *ks = kb + (long long)key * p.k_row;
-        kd = *reinterpret_cast<const f32x4 *>(ks + 4 * g);
+        const unsigned key = (unsigned)min(kk + l16, k_end - 1);
+        const unsigned ks = key * k_row;
+        kd = *reinterpret_cast<const f32x4 *>(kb8 + (ks + 16u * g));
         if constexpr (ROPE) {
-            const f32x4 y = *reinterpret_cast<const f32x4 *>(ks + (4 * g ^ 8));
-            const f32x4 c = *reinterpret_cast<const f32x4 *>(p.rope_cos + key * 16 + 4 * g);
-            const f32x4 s = *reinterpret_cast<const f32x4 *>(p.rope_sin + key * 16 + 4 * g);
+            const f32x4 y = *reinterpret_cast<const f32x4 *>(kb8 + (ks + 4u * (4 * g ^ 8)));
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(p.rope_cos) + (key * 64u + 16u * g));
+            const f32x4 s = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const char *>(p.rope_sin) + (key * 64u + 16u * g));
             kd = kd * c + y * s;
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vd[i] = vb[(long long)min(kk + 4 * g + i, k_end - 1) * p.v_row + l16];
+        for (int i = 0; i < 4; ++i)
+            vd[i] = *reinterpret_cast<const float *>(vb8 + ((unsigned)min(kk + 4 * g + i, k_end - 1) * v_row + 4u * l16));
     };
 
     f32x4 o[QG];
@@ -2487,6 +2492,8 @@ void small_attention(const SmallAttention &args, hipStream_t stream) {
         const int per = split ? plan.keys_per_split : args.kv_rows;
         const long long blocks = plan.units * splits, per_xcd = ceil_div(blocks, 8);
         if (per_xcd * 8 > 0x7fffffffLL) fail(3, "small attention grid is too large");
+        if (4LL * ((long long)args.kv_rows * std::max(args.k_row, args.v_row) + 64) > 0xffffffffLL)
+            fail(3, "small attention keys are too far apart for the long-range kernel");
         const bool rope = args.rope_cos != nullptr;
         const int qg = args.q_rows >= kLongQueries ? 8 : (args.q_rows > 32 ? 4 : (args.q_rows > 16 ? 2 : 1));
 #define IRX_LONG_CASE(QG)                                                                                      \
